@@ -1,0 +1,213 @@
+"""Benchmark of the MI355X TurboQuant hot path (one GPU).
+
+Headline (BASELINE.json metric): PQO3 fused decode attention GB/s and % of
+HBM peak at 32K context -- config 3: one layer, batch 1, 16 query heads,
+8 KV heads (GQA 2:1), head_dim 128, 32,768 tokens, K/V N(0,1) with 4 of 128
+channels x8, bf16 query.  A "step" is one fused decode over the compressed
+cache.  Algorithmic bytes per step: 8 heads x 32768 tokens x (56 + 56) B =
+29,360,128 B (K and V codes + f16 scales, each byte counted once).  The
+cache (29 MB) fits the 256 MB Infinity Cache, so steps rotate through
+>= 1 GiB of distinct cache copies.
+
+Secondary: PQO3 quantize Mvec/s at d=128 (config 2: 28 layers x 8 KV heads x
+4096 tokens, K and V, bf16 in) with the fused rotation, reported in the same
+JSON line under "quantize".
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0
+
+C3 = dict(heads=16, kv_heads=8, head_dim=128, ctx=32768, bits=3)
+C2 = dict(layers=28, kv_heads=8, tokens=4096, head_dim=128, bits=3)
+
+
+def c3_bytes() -> int:
+    per_vec = C3["head_dim"] * C3["bits"] // 8 + 2 * (C3["head_dim"] // 32)
+    return C3["kv_heads"] * C3["ctx"] * 2 * per_vec
+
+
+def build_c3_copies(torch, tq, copies: int):
+    """Quantize seeded K/V once on the GPU, then replicate the compressed cache."""
+    import numpy as np
+    from tq_testdata import kv_outlier
+
+    rng = np.random.default_rng(3)
+    hkv, t, hd, bits = C3["kv_heads"], C3["ctx"], C3["head_dim"], C3["bits"]
+    k = torch.from_numpy(kv_outlier(rng, hkv, t, hd).reshape(-1, hd)).cuda().to(torch.bfloat16)
+    v = torch.from_numpy(kv_outlier(rng, hkv, t, hd).reshape(-1, hd)).cuda().to(torch.bfloat16)
+    pk, sk = tq.pqo_quantize(k, bits)
+    pv, sv = tq.pqo_quantize(v, bits)
+    pd = hd * bits // 8
+    base = [pk.view(hkv, t, pd), sk.view(hkv, t, 4), pv.view(hkv, t, pd), sv.view(hkv, t, 4)]
+    out = [base] + [[x.clone() for x in base] for _ in range(copies - 1)]
+    q = (torch.from_numpy(rng.standard_normal((1, C3["heads"], hd)).astype(np.float32)) / math.sqrt(hd))
+    return out, q.cuda().to(torch.bfloat16)
+
+
+def time_steps(torch, fn, steps: int, warmup: int):
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(steps):
+        fn(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) / steps, wall
+
+
+def cpu_baseline_c3():
+    """Oracle (C restatement of the reference CPU path: polar_dequantize then
+    dense softmax attention, single thread) on a bounded sample: one KV head
+    (2 query heads) at the full 32K context; scaled to the 8-head config."""
+    import numpy as np
+    from oracle import oracle as orc
+    from tq_testdata import kv_outlier
+
+    rng = np.random.default_rng(33)
+    t, hd, bits = C3["ctx"], C3["head_dim"], C3["bits"]
+    k = kv_outlier(rng, 1, t, hd).reshape(-1, hd)
+    v = kv_outlier(rng, 1, t, hd).reshape(-1, hd)
+    pk, sk = orc.pqo_quantize(bits, k, hd)
+    pv, sv = orc.pqo_quantize(bits, v, hd)
+    q = rng.standard_normal((2, hd)).astype(np.float32) / np.float32(math.sqrt(hd))
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        kd = orc.pqo_dequantize(bits, pk, sk, hd).reshape(1, t, hd)
+        vd = orc.pqo_dequantize(bits, pv, sv, hd).reshape(1, t, hd)
+        orc.attention_dense(q, kd, vd, 1.0 / math.sqrt(hd))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 3.0 or reps >= 20:
+            break
+    per_head = el / reps
+    full = per_head * C3["kv_heads"]
+    return {"value": round(c3_bytes() / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"1 of 8 KV heads (2 q-heads) x 32768 tokens, {reps} reps, scaled x8; "
+                      "oracle/tq_oracle.c pqo_dequantize + attention_dense"}
+
+
+def cpu_baseline_quantize():
+    import numpy as np
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((200_000, 128)).astype(np.float32)
+    t0 = time.perf_counter()
+    orc.pqo_quantize(3, x, 128)
+    el = time.perf_counter() - t0
+    return {"value": round(x.shape[0] / el / 1e6, 4), "unit": "Mvec/s", "cores": 1, "kind": "port",
+            "sample": "200,000 vectors d=128, oracle/tq_oracle.c pqo_quantize (rotation + MaxNorm + pack)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the decode path shards by KV head with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import turboquant_amd as tq
+
+    # ---- config 3: fused decode attention ----
+    copies = max(1, math.ceil((1 << 30) / c3_bytes()) + 1)
+    caches, q = build_c3_copies(torch, tq, copies)
+    hkv, t, hd, bits, h = C3["kv_heads"], C3["ctx"], C3["head_dim"], C3["bits"], C3["heads"]
+    lens = torch.tensor([t], dtype=torch.int32, device="cuda")
+    ws = tq.AttentionWorkspace(1, h, hkv, hd, t)
+    out = torch.empty((1, h, hd), dtype=torch.float32, device="cuda")
+    scale = 1.0 / math.sqrt(hd)
+
+    def attn_step(i):
+        kidx, ksc, vidx, vsc = caches[i % copies]
+        tq.pqo_decode_attention(q, kidx, ksc, vidx, vsc, lens, hkv, bits, t, t, 0, scale, ws, out=out)
+
+    ms, wall = time_steps(torch, attn_step, args.steps, args.warmup)
+    gbs = c3_bytes() / (ms * 1e-3) / 1e9
+    del caches
+
+    # ---- config 2: PQO3 quantize (fused rotation), bf16 in ----
+    n_vec = C2["layers"] * C2["kv_heads"] * C2["tokens"] * 2
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn((n_vec, C2["head_dim"]), generator=gen, device="cuda", dtype=torch.float32)
+    x[:, torch.tensor([3, 40, 77, 101], device="cuda")] *= 8.0
+    x = x.to(torch.bfloat16)
+    qsteps = max(5, args.steps // 10)
+    qwarm = max(2, args.warmup // 10)
+    packed = torch.empty((n_vec, 48), dtype=torch.uint8, device="cuda")
+    scales = torch.empty((n_vec, 4), dtype=torch.int16, device="cuda")
+    from turboquant_amd import _lib
+    st = torch.cuda.current_stream().cuda_stream
+
+    def quant_step(i):
+        _lib.check(_lib.lib.tq_pqo_quantize(x.data_ptr(), _lib.TQ_DTYPE_BF16, packed.data_ptr(), scales.data_ptr(),
+                                            n_vec, 128, 3, st))
+
+    qms, _ = time_steps(torch, quant_step, qsteps, qwarm)
+    q_bytes = n_vec * (256 + 56)
+    q_gbs = q_bytes / (qms * 1e-3) / 1e9
+    mvec = n_vec / (qms * 1e-3) / 1e6
+
+    cpu = None
+    qcpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_c3()
+        qcpu = cpu_baseline_quantize()
+
+    rec = {
+        "metric": "PQO3 fused decode attn GB/s (%HBM peak) @32K ctx; quantize Mvec/s at d=128",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codes / f32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V with 4 of 128 channels x8, quantized PQO3 on device)",
+        "config": {"workload": "C3: fused PQO3 decode attention, batch 1, 16 q-heads / 8 KV heads, d=128, "
+                               "ctx 32768, bf16 query, f32 out; rotating >= 1 GiB of cache copies",
+                   "copies": copies, "algorithmic_bytes_per_step": c3_bytes()},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "quantize": {"metric": "PQO3 quantize Mvec/s at d=128 (C2, bf16 in, fused rotation)",
+                     "value": round(mvec, 2), "unit": "Mvec/s", "ms_per_step": round(qms, 6),
+                     "vectors_per_step": n_vec, "algorithmic_bytes_per_step": q_bytes,
+                     "roofline": {"bound": "hbm", "achieved": round(q_gbs, 2), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(q_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "cpu_baseline": qcpu},
+        "wall_s_timed": round(wall, 4),
+    }
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

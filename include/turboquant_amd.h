@@ -1,0 +1,144 @@
+/*
+ * turboquant_amd.h -- C ABI of the MI355X (gfx950) TurboQuant KV-cache path.
+ *
+ * All pointers are device pointers unless stated otherwise; the caller owns
+ * every buffer (outputs and scratch alike), as in the reference's FFI
+ * (src/cache/cuda/ffi.rs:10-79), where candle tensors own all memory.  f16
+ * values cross as raw uint16_t bits.  Every entry point is stream-ordered on
+ * the given hipStream_t (0 = the null stream) and does not synchronise the
+ * host.  Entry points return a status (0 = success); tq_last_error() gives
+ * the message of the calling thread's last failure.
+ *
+ * Layouts (bits = 3 or 4, head_dim = 32 * num_qblocks):
+ *   packed indices : [num_vectors][head_dim * bits / 8] u8, each 32-element
+ *                    qblock a little-endian bitstream of bits-wide codes
+ *                    (reference src/packed/mod.rs:242-309)
+ *   scales         : [num_vectors][head_dim / 32] f16 bits; a negative value
+ *                    marks an outlier-codebook block (quantize_tensor.rs:68-70)
+ *   cache          : token t of KV head g of sequence b at
+ *                    ((b * seq_stride) + g * kv_head_stride + t) records
+ *                    (CompressedStorage, src/cache/storage.rs:24-139)
+ */
+#ifndef TURBOQUANT_AMD_H
+#define TURBOQUANT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  1..5 mirror TurboQuantError (reference src/error.rs:5-29);
+ * 6 covers the candle cache errors (cache_err, src/cache/mod.rs:30-32). */
+enum {
+    TQ_OK = 0,
+    TQ_ERR_INVALID_DIMENSION = 1,
+    TQ_ERR_UNSUPPORTED_BITS = 2,
+    TQ_ERR_DIMENSION_MISMATCH = 3,
+    TQ_ERR_LAYER_OUT_OF_RANGE = 4,
+    TQ_ERR_RANGE_OUT_OF_BOUNDS = 5,
+    TQ_ERR_INVALID_ARGUMENT = 6,
+    TQ_ERR_DEVICE = 7
+};
+
+/* Element types of activations crossing the boundary. */
+enum { TQ_DTYPE_F32 = 0, TQ_DTYPE_BF16 = 1, TQ_DTYPE_F16 = 2 };
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char *tq_last_error(void);
+/* Library version string. */
+const char *tq_version(void);
+
+/* =========================================================================
+ * Reference FFI, same symbols and argument meaning as
+ * src/cache/cuda/ffi.rs:10-79 with hipStream_t in place of CUstream.  The
+ * reference declares them void; these return a status, which a caller that
+ * declares them void simply ignores (x86-64 SysV: the value is in rax).
+ * ========================================================================= */
+
+/* Replaces tq_dequant_batch (ffi.rs:11-22; tq_dequant_kernel.cu:104-125).
+ * out[num_blocks][block_size] f32 = |scale| * WHT^-1(codebook[idx] * sign). */
+int tq_dequant_batch(const uint8_t *packed_indices, const uint16_t *scales,
+                     const float *codebook, const float *sign_pattern, float *output,
+                     int num_blocks, int block_size, int bits, int bytes_per_block,
+                     hipStream_t stream);
+
+/* Replaces tq_quant_maxnorm_batch (ffi.rs:24-37; tq_quant_kernel.cu:416-439).
+ * Input is already rotated; MaxNorm scale, bucketize, pack, signed f16 scale. */
+int tq_quant_maxnorm_batch(const float *rotated_input, const float *boundaries,
+                           uint8_t *packed_out, uint16_t *scales_out, int num_blocks,
+                           int block_size, int bits, int num_boundaries, int bytes_per_block,
+                           float outer_centroid, float scale_sign, hipStream_t stream);
+
+/* Replaces tq_pack_indices (ffi.rs:39-48; tq_quant_kernel.cu:441-456). */
+int tq_pack_indices(const uint8_t *indices, uint8_t *packed_out, int num_vectors,
+                    int block_size, int bits, int bytes_per_block, hipStream_t stream);
+
+/* Replaces tq_fused_attention (ffi.rs:50-78; tq_attention_kernel.cu:337-392).
+ * q [num_attention_heads][head_dim] f32, out the same shape.  partial_out
+ * [num_attention_heads * num_partitions][head_dim], partial_max/sum
+ * [num_attention_heads * num_partitions] are caller scratch, with
+ * num_partitions = ceil(kv_len / 512) as in cuda/attention.rs:13,70.  The QJL
+ * arguments must be null / 0: the reference never enables them
+ * (cuda/attention.rs:153-157). */
+int tq_fused_attention(const float *q, const uint8_t *k_indices, const uint16_t *k_scales,
+                       const uint8_t *v_indices, const uint16_t *v_scales,
+                       const float *codebook, const float *sign_pattern, float *output,
+                       float *partial_out, float *partial_max, float *partial_sum,
+                       const uint8_t *qjl_signs, const uint16_t *qjl_residual_norms,
+                       const float *rq, int qjl_enabled, int num_attention_heads,
+                       int num_kv_heads, int head_dim, int kv_len, int kv_stride,
+                       int packed_dim, int num_qblocks, int bits, float softmax_scale,
+                       int num_partitions, hipStream_t stream);
+
+/* =========================================================================
+ * Fused MI355X entry points (no reference counterpart as single calls; each
+ * replaces a chain of reference calls, named per entry).
+ * ========================================================================= */
+
+/* PQO quantize with the block rotation fused in.  Replaces polar_quantize's
+ * CUDA path = candle matmul(R_fwd) + tq_quant_maxnorm_batch
+ * (quantize_tensor.rs:54-60, cuda/quantize.rs:97-168).  x [num_vectors]
+ * [head_dim] in x_dtype; packed_out [num_vectors][head_dim*bits/8];
+ * scales_out [num_vectors][head_dim/32] (negative: PQO outlier blocks). */
+int tq_pqo_quantize(const void *x, int x_dtype, uint8_t *packed_out, uint16_t *scales_out,
+                    size_t num_vectors, int head_dim, int bits, hipStream_t stream);
+
+/* PQO dequantize.  Replaces polar_dequantize (quantize_tensor.rs:179-220) /
+ * tq_dequant_batch followed by to_dtype.  out [num_vectors][head_dim]. */
+int tq_pqo_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
+                      size_t num_vectors, int head_dim, int bits, hipStream_t stream);
+
+/* Workspace for tq_pqo_decode_attention (partials + merge counters). */
+size_t tq_attention_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                   int max_kv_len);
+/* Zero-fills the merge counters of a workspace (once after allocation; every
+ * call leaves them zero again).  Uses a fill kernel, no memset node. */
+int tq_attention_workspace_init(void *workspace, size_t workspace_bytes, int batch,
+                                int num_heads, int num_kv_heads, int head_dim, int max_kv_len,
+                                hipStream_t stream);
+
+/* Fused PQO decode attention over a compressed cache, batched over
+ * sequences with per-sequence lengths, split-K over the context and GQA
+ * sharing (each compressed byte is read once for all query heads of its KV
+ * head).  Replaces PqoCache::decode_cuda -> fused_attention ->
+ * tq_fused_attention (pqo.rs:106-174, cuda/attention.rs:41-174).
+ *   q   [batch][num_heads][head_dim] in q_dtype
+ *   out [batch][num_heads][head_dim] in out_dtype
+ *   kv_lens: device int[batch]; max_kv_len: host bound on every kv_lens[b]
+ *   record strides in tokens: kv_head_stride (capacity), seq_stride. */
+int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
+                            const uint16_t *k_scales, const uint8_t *v_indices,
+                            const uint16_t *v_scales, const int *kv_lens, int batch,
+                            int num_heads, int num_kv_heads, int head_dim, int bits,
+                            int max_kv_len, long long kv_head_stride, long long seq_stride,
+                            float softmax_scale, void *out, int out_dtype, void *workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

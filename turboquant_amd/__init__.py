@@ -1,0 +1,160 @@
+"""turboquant_amd -- MI355X-native TurboQuant KV-cache hot path.
+
+Thin Python surface over the C ABI (include/turboquant_amd.h) for tests and
+benchmarks.  Device memory and streams come from PyTorch (ROCm); every
+compute call goes to the hand-written gfx950 kernels in
+libturboquant_amd.so.  There is no CPU fallback: importing this package
+without the built library raises.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ._lib import (TQ_DTYPE_BF16, TQ_DTYPE_F16, TQ_DTYPE_F32, TurboQuantError, check, lib)
+
+__all__ = [
+    "TurboQuantError", "lib", "pqo_quantize", "pqo_dequantize", "quant_maxnorm_batch", "dequant_batch",
+    "pack_indices", "fused_attention", "AttentionWorkspace", "pqo_decode_attention", "pqo_codebook_values",
+]
+
+_DT = {torch.float32: TQ_DTYPE_F32, torch.bfloat16: TQ_DTYPE_BF16, torch.float16: TQ_DTYPE_F16}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return t.data_ptr()
+
+
+def pqo_quantize(x: torch.Tensor, bits: int):
+    """PQO quantize [N, head_dim] (f32/bf16/f16) with the fused block rotation.
+
+    Returns (packed u8 [N, head_dim*bits/8], scales int16 [N, head_dim/32]
+    holding f16 bits, negative = outlier block)."""
+    if x.dim() != 2:
+        raise ValueError("x must be [N, head_dim]")
+    n, hd = x.shape
+    packed = torch.empty((n, hd * bits // 8), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((n, max(hd // 32, 1)), dtype=torch.int16, device=x.device)
+    check(lib.tq_pqo_quantize(_ptr(x), _DT[x.dtype], _ptr(packed), _ptr(scales), n, hd, bits, _stream()))
+    return packed, scales
+
+
+def pqo_dequantize(packed: torch.Tensor, scales: torch.Tensor, bits: int, head_dim: int,
+                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    n = packed.shape[0]
+    out = torch.empty((n, head_dim), dtype=out_dtype, device=packed.device)
+    check(lib.tq_pqo_dequantize(_ptr(packed), _ptr(scales), _ptr(out), _DT[out_dtype], n, head_dim, bits,
+                                _stream()))
+    return out
+
+
+def quant_maxnorm_batch(rotated: torch.Tensor, boundaries: torch.Tensor, bits: int, outer_centroid: float,
+                        scale_sign: float = -1.0):
+    """Reference-ABI quantize of already-rotated f32 blocks [num_blocks, 32]."""
+    nb = rotated.numel() // 32
+    bpb = 32 * bits // 8
+    packed = torch.empty((nb, bpb), dtype=torch.uint8, device=rotated.device)
+    scales = torch.empty((nb,), dtype=torch.int16, device=rotated.device)
+    check(lib.tq_quant_maxnorm_batch(_ptr(rotated), _ptr(boundaries), _ptr(packed), _ptr(scales), nb, 32, bits,
+                                     boundaries.numel(), bpb, float(outer_centroid), float(scale_sign), _stream()))
+    return packed, scales
+
+
+def dequant_batch(packed: torch.Tensor, scales: torch.Tensor, codebook: torch.Tensor, sign_pattern: torch.Tensor,
+                  bits: int) -> torch.Tensor:
+    """Reference-ABI dequantize: [num_blocks, 32] f32."""
+    nb = scales.numel()
+    out = torch.empty((nb, 32), dtype=torch.float32, device=packed.device)
+    check(lib.tq_dequant_batch(_ptr(packed), _ptr(scales), _ptr(codebook), _ptr(sign_pattern), _ptr(out), nb, 32,
+                               bits, 32 * bits // 8, _stream()))
+    return out
+
+
+def pack_indices(indices: torch.Tensor, bits: int, bytes_per_block: int | None = None) -> torch.Tensor:
+    """Reference-ABI packing of [num_vectors, block_size] u8 codes.  The default
+    bytes_per_block follows the reference packers' zero-padded tails
+    (whole 3-byte groups for 3-bit, packed/indices.rs:72-78)."""
+    nv, bs = indices.shape
+    if bytes_per_block is None:
+        bytes_per_block = {2: (bs + 3) // 4, 3: ((bs + 7) // 8) * 3, 4: (bs + 1) // 2}[bits]
+    bpb = bytes_per_block
+    out = torch.empty((nv, bpb), dtype=torch.uint8, device=indices.device)
+    check(lib.tq_pack_indices(_ptr(indices), _ptr(out), nv, bs, bits, bpb, _stream()))
+    return out
+
+
+def fused_attention(q, k_idx, k_sc, v_idx, v_sc, codebook, sign_pattern, num_kv_heads, kv_len, kv_stride, bits,
+                    softmax_scale):
+    """Reference-ABI fused decode attention (single sequence, f32 q/out)."""
+    h, hd = q.shape
+    p = (kv_len + 511) // 512
+    dev = q.device
+    out = torch.zeros((h, hd), dtype=torch.float32, device=dev)
+    po = torch.zeros((h * max(p, 1), hd), dtype=torch.float32, device=dev)
+    pm = torch.zeros((h * max(p, 1),), dtype=torch.float32, device=dev)
+    ps = torch.zeros((h * max(p, 1),), dtype=torch.float32, device=dev)
+    check(lib.tq_fused_attention(_ptr(q), _ptr(k_idx), _ptr(k_sc), _ptr(v_idx), _ptr(v_sc), _ptr(codebook),
+                                 _ptr(sign_pattern), _ptr(out), _ptr(po), _ptr(pm), _ptr(ps), None, None, None, 0,
+                                 h, num_kv_heads, hd, kv_len, kv_stride, hd * bits // 8, hd // 32, bits,
+                                 float(softmax_scale), p, _stream()))
+    return out
+
+
+class AttentionWorkspace:
+    """Device workspace for pqo_decode_attention (split-K partials + counters)."""
+
+    def __init__(self, batch: int, num_heads: int, num_kv_heads: int, head_dim: int, max_kv_len: int,
+                 device="cuda"):
+        self.shape = (batch, num_heads, num_kv_heads, head_dim, max_kv_len)
+        self.nbytes = lib.tq_attention_workspace_size(batch, num_heads, num_kv_heads, head_dim, max_kv_len)
+        if self.nbytes == 0:
+            raise ValueError("invalid workspace shape")
+        self.buf = torch.empty((self.nbytes,), dtype=torch.uint8, device=device)
+        check(lib.tq_attention_workspace_init(_ptr(self.buf), self.nbytes, batch, num_heads, num_kv_heads, head_dim,
+                                              max_kv_len, _stream()))
+
+
+def pqo_decode_attention(q, k_idx, k_sc, v_idx, v_sc, kv_lens, num_kv_heads, bits, max_kv_len, kv_head_stride,
+                         seq_stride, softmax_scale, workspace: AttentionWorkspace,
+                         out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None):
+    """Batched fused decode attention.  q [B, H, D]; kv_lens int32 [B] (device)."""
+    b, h, hd = q.shape
+    if out is None:
+        out = torch.empty((b, h, hd), dtype=out_dtype, device=q.device)
+    check(lib.tq_pqo_decode_attention(_ptr(q), _DT[q.dtype], _ptr(k_idx), _ptr(k_sc), _ptr(v_idx), _ptr(v_sc),
+                                      _ptr(kv_lens), b, h, num_kv_heads, hd, bits, max_kv_len, kv_head_stride,
+                                      seq_stride, float(softmax_scale), _ptr(out), _DT[out.dtype],
+                                      _ptr(workspace.buf), workspace.nbytes, _stream()))
+    return out
+
+
+def pqo_codebook_values(bits: int):
+    """(centroids, boundaries, outer) of the PQO MaxNorm codebook, f32 arithmetic as in
+    src/cache/precomputed/codebooks.rs:51-88 (host-side constants)."""
+    import numpy as np
+    r = np.float32(2.1573)
+    if bits == 3:
+        c = np.array([-2.1573, -1.3336, -0.7434, -0.2428, 0.2428, 0.7434, 1.3336, 2.1573], np.float32)
+        b = np.array([-1.7455, -1.0385, -0.4931, 0.0, 0.4931, 1.0385, 1.7455], np.float32)
+    elif bits == 4:
+        step = np.float32(np.float32(2.0) * r) / np.float32(15.0)
+        c = np.array([-r + np.float32(i) * step for i in range(16)], np.float32)
+        b = np.array([-r + (np.float32(i) + np.float32(0.5)) * step for i in range(15)], np.float32)
+    else:
+        raise ValueError("bits must be 3 or 4")
+    return c, b, np.float32(c.max())
+
+
+def default_softmax_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,732 @@
+// tq_attention.hip -- fused PQO decode attention over the compressed cache.
+//
+// One workgroup (1024 lanes, 16 waves) owns a tile (sequence b, KV head g,
+// chunk of CH = 1024 tokens) and serves all NR = num_heads / num_kv_heads
+// query heads of that KV head, so every compressed byte is read from HBM
+// exactly once (GQA sharing).  All of the tile's global loads (K and V codes
+// and scales) are issued before any arithmetic and sit in VGPRs while the
+// query tables are built, so each lane has ~25 loads in flight.
+//
+// Keys are never inverse-rotated.  With the block dequantization
+//   k_j = |s| * inv * (H (cb[idx] * sg))_j               (wht_tensor.rs:38-64)
+// the dot product is q.k = |s| * sum_i cb[idx_i] * qt_i, qt = inv * sg * (H q)
+// (the rotated query), built once per tile.  The tile builds an LDS table of
+// qt_i * cb[code] (times softmax scale * log2 e) for every code PAIR of
+// adjacent elements (3-bit: 64 pair codes), so one 6-bit field extract and
+// one LDS read cover two key elements for all NR heads at once.  Values are
+// accumulated in the rotated domain, sum_t w_t |s_t| cb[idx_t], with a pair
+// codebook (one LDS read per two elements), and inverse-rotated once per
+// head after the split-K merge.
+//
+// Softmax is two-pass inside a tile (all CH scores staged in LDS, one max,
+// one exp2 per score).  Split-K partials (m, l, acc) go to a workspace; with
+// INLINE_MERGE the last tile of a (b, g) to finish (device-scope atomic
+// counter) merges them and writes the output, then re-arms the counter, so
+// one launch does the whole decode.
+#include "tq_common.h"
+#include "tq_device.h"
+
+namespace {
+
+using namespace tqd;
+
+constexpr float kInvSqrt32 = 0x1.6a09e6p-3f;
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr int kThreads = 1024;
+constexpr int kChunk = 1024;
+constexpr int kWaves = kThreads / 64;
+
+struct AttnArgs {
+  const void *q;
+  const uint8_t *k_idx;
+  const uint16_t *k_sc;
+  const uint8_t *v_idx;
+  const uint16_t *v_sc;
+  const int *kv_lens;        // device lengths, or null -> single_len
+  int single_len;
+  int max_len;               // host bound; device lengths are clamped to it
+  int num_heads;
+  int num_kv_heads;
+  long long kv_head_stride;  // tokens
+  long long seq_stride;      // tokens
+  float softmax_scale;
+  float *po;                 // partial acc  [(b*H + h) * P + c][head_dim]
+  float *pm;                 // partial max  [(b*H + h) * P + c]   (base-2 logits)
+  float *ps;                 // partial sum  [(b*H + h) * P + c]
+  int *counters;             // [b * Hkv + g], zero between launches
+  int P;                     // chunk stride per (b, h) in the partial arrays
+  void *out;
+  int out_dtype;
+  float cb[16];              // codebook
+  float sg[32];              // decode sign factor per element
+};
+
+template <int QT>
+__device__ __forceinline__ float load_q(const void *q, long long i) {
+  if constexpr (QT == kF32) return static_cast<const float *>(q)[i];
+  else if constexpr (QT == kBF16) return bf16_to_f32(static_cast<const uint16_t *>(q)[i]);
+  else return f16_to_f32(static_cast<const uint16_t *>(q)[i]);
+}
+
+__device__ __forceinline__ float dpp_quad_xor1(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_quad_xor2(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+}
+
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Reads `W` bits starting at bit `pos` of a little-endian word array.
+template <int W, int NW>
+__device__ __forceinline__ uint32_t bits_at(const uint32_t (&w)[NW], int pos) {
+  const int wi = pos >> 5, sh = pos & 31;
+  if (sh + W <= 32) return (w[wi] >> sh) & ((1u << W) - 1u);
+  return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & ((1u << W) - 1u);
+}
+
+template <int BITS>
+struct Geo {
+  static constexpr int NC = 1 << BITS;
+  static constexpr int QB_BYTES = 4 * BITS;  // bytes per 32-element qblock
+  // key table: 3-bit uses code pairs (64 entries per pair position),
+  // 4-bit single codes (16 entries per element) to keep the table in LDS
+  static constexpr bool KPAIR = (BITS == 3);
+  static constexpr int KG = KPAIR ? 2 : 1;            // elements per key lookup
+  static constexpr int KENT = KPAIR ? 64 : 16;        // entries per position
+  static constexpr int KPOS = 32 / KG;                // positions per qblock
+};
+
+// ---------------------------------------------------------------------------
+// Split-K merge and final inverse rotation for NR heads of one (b, g):
+//   o = inv * H(sg * sum_c 2^(m_c - M) acc_c) / sum_c 2^(m_c - M) l_c
+// All partial loads of a lane are independent (one latency round).
+// ---------------------------------------------------------------------------
+constexpr int kMergeCap = 2048;  // max NR * chunks merged (LDS floats)
+constexpr int kMiscFloats = 2 * kMergeCap + kThreads + 8;
+
+template <int NR>
+__device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, float *lds) {
+  constexpr int HD = 128;
+  constexpr int OUTS = NR * HD;
+  constexpr int PARTS = kThreads / OUTS;   // lanes sharing one output element
+  constexpr int MAXC = 8;                  // partial values per lane per round
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  float *s_w = lds;                     // [NR][nchunks]: m_c, then weights 2^(m_c - M)
+  float *s_ls = s_w + kMergeCap;        // [NR][nchunks]: l_c
+  float *s_part = s_ls + kMergeCap;     // [kThreads] partial sums
+  float *s_l = s_part + kThreads;       // [NR]
+  const int o = tid % OUTS, part = tid / OUTS;
+  const int r = o / HD, d = o % HD;
+  const long long bh = (long long)b * a.num_heads + g * NR + r;
+  // first round of this lane's partial accumulators, issued together with
+  // the (m, l) loads so the whole merge costs one memory round trip when
+  // nchunks <= MAXC * PARTS
+  float pv[MAXC];
+#pragma unroll
+  for (int k = 0; k < MAXC; k++) {
+    const int cc = part + k * PARTS;
+    pv[k] = cc < nchunks ? a.po[(bh * a.P + cc) * HD + d] : 0.f;
+  }
+  for (int e = tid; e < NR * nchunks; e += kThreads) {
+    const int rr = e / nchunks, cc = e % nchunks;
+    const long long bh2 = (long long)b * a.num_heads + g * NR + rr;
+    s_w[e] = a.pm[bh2 * a.P + cc];
+    s_ls[e] = a.ps[bh2 * a.P + cc];
+  }
+  __syncthreads();
+  if (wave < NR) {  // wave rr reduces head rr
+    const int rr = wave;
+    float M = -INFINITY;
+    for (int cc = lane; cc < nchunks; cc += 64) M = fmaxf(M, s_w[rr * nchunks + cc]);
+    M = wave_reduce(M, [](float x, float y) { return fmaxf(x, y); });
+    float L = 0.f;
+    for (int cc = lane; cc < nchunks; cc += 64) {
+      const float w = exp2f(s_w[rr * nchunks + cc] - M);
+      s_w[rr * nchunks + cc] = w;
+      L = __builtin_fmaf(s_ls[rr * nchunks + cc], w, L);
+    }
+    L = wave_reduce(L, [](float x, float y) { return x + y; });
+    if (lane == 0) s_l[rr] = L;
+  }
+  __syncthreads();
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXC; k++) {
+    const int cc = part + k * PARTS;
+    if (cc < nchunks) acc = __builtin_fmaf(pv[k], s_w[r * nchunks + cc], acc);
+  }
+  for (int cc = part + MAXC * PARTS; cc < nchunks; cc += PARTS)  // long contexts only
+    acc = __builtin_fmaf(a.po[(bh * a.P + cc) * HD + d], s_w[r * nchunks + cc], acc);
+  s_part[tid] = acc;
+  __syncthreads();
+  if (tid < OUTS) {
+    float A = 0.f;
+#pragma unroll
+    for (int p = 0; p < PARTS; p++) A += s_part[p * OUTS + tid];
+    // inverse rotation over the 32 lanes of this block (lane bits 0..4 = i)
+    const int i = d & 31;
+    float v = A * a.sg[i];
+#pragma unroll
+    for (int hh = 1; hh < 32; hh <<= 1) {
+      float ov = __shfl_xor(v, hh, 64);
+      v = (i & hh) ? (ov - v) : (v + ov);
+    }
+    const float L = s_l[r];
+    const float res = (L > 0.f) ? v * kInvSqrt32 / L : 0.f;
+    const long long oi = bh * HD + d;
+    if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = res;
+    else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(res);
+    else static_cast<uint16_t *>(a.out)[oi] = f32_to_f16(res);
+  }
+}
+
+template <int BITS, int NR, int QT, bool INLINE_MERGE>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
+  using G = Geo<BITS>;
+  constexpr int NQB = 4, HD = 128, CH = kChunk;
+  constexpr int QW = BITS;                      // 32-bit words per qblock
+  constexpr int PACKED = NQB * QW * 4;          // bytes per token record
+  constexpr int SUB = kThreads / NQB;           // tokens per sub-chunk: one (token, qblock) per lane
+  constexpr int NSUB = CH / SUB;                // sub-chunks per tile
+  constexpr bool LIGHT = (BITS == 3 && NR <= 2);  // register budget allows the deeper pipeline
+  constexpr int EPL = LIGHT ? 16 : 8;           // V-pass elements per lane
+  constexpr int NSET = LIGHT ? 3 : 2;           // register sets of loads in flight
+  constexpr int GPQ = 32 / EPL;                 // V lanes per qblock of a token
+  constexpr int VLPT = NQB * GPQ;               // V lanes per token
+  constexpr int VSL = kThreads / VLPT;          // V token slices
+  constexpr int VTS = SUB / VSL;                // tokens per V lane per sub-chunk
+  constexpr int VCODES = 1 << (2 * BITS);       // pair-codebook entries
+  constexpr int KTAB = NQB * G::KPOS * G::KENT * NR;
+  constexpr int VRED = kWaves * HD * NR;
+  constexpr int TABSZ = KTAB > VRED ? KTAB : VRED;
+  // LDS carve, in 32-bit words.  The key table sits at offset 0 so every
+  // lookup's table position folds into the ds_read immediate offset.
+  constexpr int OFF_CB2 = TABSZ;                        // float2[VCODES]
+  constexpr int OFF_V = OFF_CB2 + 2 * VCODES;           // u32 [2][SUB * NQB * QW]  V records
+  constexpr int VBUF = SUB * NQB * QW;
+  constexpr int OFF_VS = OFF_V + 2 * VBUF;              // u16 [2][SUB * NQB]       V scales
+  constexpr int VSBUF = SUB * NQB / 2;
+  constexpr int OFF_P = OFF_VS + 2 * VSBUF;             // f32 [2][NR][SUB]         scores
+  constexpr int OFF_Q = OFF_P + 2 * NR * SUB;           // f32 [NR * HD]            rotated queries
+  constexpr int OFF_RED = OFF_Q + NR * HD;              // f32 [3][NR][kWaves]: 2 max buffers + l sums
+  constexpr int OFF_MISC = OFF_V;                       // merge scratch aliases the staging buffers
+  constexpr int TOTAL0 = OFF_RED + 3 * NR * kWaves + 8;
+  constexpr int TOTAL = TOTAL0 > OFF_MISC + kMiscFloats ? TOTAL0 : OFF_MISC + kMiscFloats;
+  static_assert(NSUB * SUB == CH, "tile shape");
+  __shared__ float lds[TOTAL];
+  __shared__ int s_flag;
+  float *s_tab = lds;
+  float2 *s_cb2 = reinterpret_cast<float2 *>(lds + OFF_CB2);
+  uint32_t *s_v = reinterpret_cast<uint32_t *>(lds + OFF_V);
+  uint16_t *s_vs = reinterpret_cast<uint16_t *>(lds + OFF_VS);
+  float *s_p = lds + OFF_P;
+  float *s_q = lds + OFF_Q;
+  float *s_red = lds + OFF_RED;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
+  const int t0 = c * CH;
+  if (t0 >= len) return;  // empty tile: not counted by the merge
+  const int nchunks = (len + CH - 1) / CH;
+  const long long rec0 = (long long)b * a.seq_stride + (long long)g * a.kv_head_stride;
+
+  // ---- loads: lane = (token kt, qblock kq) of a sub-chunk; three register sets ----
+  const int kq = tid & (NQB - 1), kt = tid / NQB;
+  uint32_t kw[NSET][QW], vw[NSET][QW], ksc[NSET], vsc[NSET];
+  auto issue = [&](int s, int set) {
+    const int t = min(t0 + s * SUB + kt, len - 1);
+    const long long rec = rec0 + t;
+    const uint32_t *kp = reinterpret_cast<const uint32_t *>(a.k_idx + rec * PACKED) + kq * QW;
+    const uint32_t *vp = reinterpret_cast<const uint32_t *>(a.v_idx + rec * PACKED) + kq * QW;
+    if constexpr (QW == 4) {
+      const uint4 k4 = *reinterpret_cast<const uint4 *>(kp);
+      kw[set][0] = k4.x; kw[set][1] = k4.y; kw[set][2] = k4.z; kw[set][3] = k4.w;
+    } else {
+#pragma unroll
+      for (int w = 0; w < QW; w++) kw[set][w] = kp[w];
+    }
+    ksc[set] = a.k_sc[rec * NQB + kq];
+    if constexpr (QW == 4) {
+      const uint4 v4 = *reinterpret_cast<const uint4 *>(vp);
+      vw[set][0] = v4.x; vw[set][1] = v4.y; vw[set][2] = v4.z; vw[set][3] = v4.w;
+    } else {
+#pragma unroll
+      for (int w = 0; w < QW; w++) vw[set][w] = vp[w];
+    }
+    vsc[set] = a.v_sc[rec * NQB + kq];
+  };
+  const int nsub = min(NSUB, (len - t0 + SUB - 1) / SUB);  // sub-chunks holding tokens (uniform)
+  // the query load goes first so the table build below overlaps the K/V loads
+  float qv = 0.f;
+  if (tid < NR * HD) qv = load_q<QT>(a.q, ((long long)b * a.num_heads + g * NR) * HD + tid);
+  issue(0, 0);
+  if (NSET > 2 && nsub > 1) issue(1, 1);
+
+  // ---- rotated, scaled queries (32-lane butterflies) and the LDS tables ----
+  const float qscale = a.softmax_scale * kLog2e * kInvSqrt32;
+  if (tid < NR * HD) {
+    const int d = tid % HD;
+    float v = qv;
+    const int i = d & 31;
+#pragma unroll
+    for (int hh = 1; hh < 32; hh <<= 1) {
+      float ov = __shfl_xor(v, hh, 64);
+      v = (i & hh) ? (ov - v) : (v + ov);
+    }
+    s_q[tid] = v * (a.sg[i] * qscale);
+  }
+  if (tid < VCODES) {
+    constexpr int NCm = G::NC - 1;
+    s_cb2[tid] = make_float2(a.cb[tid & NCm], a.cb[(tid >> BITS) & NCm]);
+  }
+  __syncthreads();
+  for (int e = tid; e < NQB * G::KPOS * G::KENT; e += kThreads) {
+    // e = (qb * KPOS + pos) * KENT + code
+    const int code = e % G::KENT, qp = e / G::KENT;
+    const int qb = qp / G::KPOS, pos = qp % G::KPOS;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      float v;
+      if constexpr (G::KPAIR) {
+        const float *qt = s_q + r * HD + qb * 32 + 2 * pos;
+        v = qt[0] * a.cb[code & 7] + qt[1] * a.cb[code >> 3];
+      } else {
+        v = s_q[r * HD + qb * 32 + pos] * a.cb[code];
+      }
+      s_tab[e * NR + r] = v;
+    }
+  }
+  __syncthreads();
+
+  // ---- V-pass lane geometry: (token slice, qblock, element group of EPL) ----
+  const int vgrp = tid % GPQ, vqb = (tid / GPQ) % NQB, vsl = tid / VLPT;
+  int vlo, vhi, vsh;
+  if constexpr (BITS == 3 && EPL == 16) {
+    vlo = (48 * vgrp) >> 5; vhi = vlo + 1; vsh = (48 * vgrp) & 31;
+  } else if constexpr (BITS == 3) {
+    vlo = (24 * vgrp) >> 5; vhi = min(vlo + 1, 2); vsh = (24 * vgrp) & 31;
+  } else if constexpr (EPL == 16) {
+    vlo = 2 * vgrp; vhi = vlo + 1; vsh = 0;
+  } else {
+    vlo = vgrp; vhi = vgrp; vsh = 0;
+  }
+  float acc[NR][EPL];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) acc[r][e] = 0.f;
+  float m_run[NR], l_part[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    m_run[r] = -INFINITY;
+    l_part[r] = 0.f;
+  }
+  const float *ktab = s_tab + kq * G::KPOS * G::KENT * NR;
+
+#pragma unroll
+  for (int s = 0; s < NSUB; s++) {
+    if (s >= nsub) break;  // uniform: the tile ends here
+    const int set = s % NSET, buf = s & 1;
+    if (s + NSET - 1 < nsub) issue(s + NSET - 1, (s + NSET - 1) % NSET);
+
+    // ---- K pass on this sub-chunk: lane = (token, qblock) ----
+    {
+      float part[NR];
+#pragma unroll
+      for (int r = 0; r < NR; r++) part[r] = 0.f;
+#pragma unroll
+      for (int pos = 0; pos < G::KPOS; pos++) {
+        const uint32_t code = bits_at<BITS * G::KG>(kw[set], pos * BITS * G::KG);
+        const float *e = ktab + (pos * G::KENT + code) * NR;
+        if constexpr (NR == 2) {
+          const float2 v = *reinterpret_cast<const float2 *>(e);
+          part[0] += v.x;
+          part[1] += v.y;
+        } else if constexpr (NR == 4) {
+          const float4 v = *reinterpret_cast<const float4 *>(e);
+          part[0] += v.x;
+          part[1] += v.y;
+          part[2] += v.z;
+          part[3] += v.w;
+        } else {
+#pragma unroll
+          for (int r = 0; r < NR; r++) part[r] += e[r];
+        }
+      }
+      const float ks = fabsf(f16_to_f32((uint16_t)ksc[set]));
+      const bool valid = t0 + s * SUB + kt < len;
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        float sc = part[r] * ks;
+        sc += dpp_quad_xor1(sc);
+        sc += dpp_quad_xor2(sc);
+        if (kq == (r & (NQB - 1))) s_p[(buf * NR + r) * SUB + kt] = valid ? sc : -INFINITY;
+      }
+      // stage this sub-chunk's V qblock for the transposed V pass
+      uint32_t *dst = s_v + buf * VBUF + (kt * NQB + kq) * QW;
+      if constexpr (QW == 4) {
+        *reinterpret_cast<uint4 *>(dst) = make_uint4(vw[set][0], vw[set][1], vw[set][2], vw[set][3]);
+      } else {
+#pragma unroll
+        for (int w = 0; w < QW; w++) dst[w] = vw[set][w];
+      }
+      s_vs[buf * 2 * VSBUF + kt * NQB + kq] = (uint16_t)vsc[set];
+    }
+    __syncthreads();
+
+    // ---- running max over the sub-chunk (base-2 logits) ----
+    if (tid < NR * SUB) {
+      const float v = s_p[buf * NR * SUB + tid];
+      const float mx = wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
+      if (lane == 0) s_red[buf * NR * kWaves + wave] = mx;  // wave w covers head w / (SUB/64)
+    }
+    __syncthreads();
+    float alpha[NR];
+    bool grow = false;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      float mx = m_run[r];
+#pragma unroll
+      for (int w = 0; w < SUB / 64; w++) mx = fmaxf(mx, s_red[buf * NR * kWaves + r * (SUB / 64) + w]);
+      alpha[r] = (mx > m_run[r]) ? exp2f(m_run[r] - mx) : 1.f;  // 2^-inf = 0 on the first growth
+      grow |= mx > m_run[r];
+      m_run[r] = mx;
+    }
+    if (__builtin_amdgcn_readfirstlane((int)grow)) {  // uniform across the workgroup: scalar branch
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        l_part[r] *= alpha[r];
+#pragma unroll
+        for (int e = 0; e < EPL; e++) acc[r][e] *= alpha[r];
+      }
+    }
+
+    // ---- V pass on this sub-chunk (pair codebook, rotated domain) ----
+#pragma unroll
+    for (int tk = 0; tk < VTS; tk++) {
+      const int tl = vsl + tk * VSL;
+      const uint32_t *rw = s_v + buf * VBUF + (tl * NQB + vqb) * QW;
+      uint64_t bits64;
+      if constexpr (BITS == 3 && EPL == 16) {
+        bits64 = (((uint64_t)rw[vhi] << 32) | rw[vlo]) >> vsh;
+      } else if constexpr (BITS == 3) {
+        bits64 = __builtin_amdgcn_alignbit(rw[vhi], rw[vlo], vsh);
+      } else if constexpr (EPL == 16) {
+        bits64 = ((uint64_t)rw[vhi] << 32) | rw[vlo];
+      } else {
+        bits64 = rw[vlo];
+      }
+      const float vs = fabsf(f16_to_f32(s_vs[buf * 2 * VSBUF + tl * NQB + vqb]));
+      const bool tv = t0 + s * SUB + tl < len;
+      float wgt[NR];
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        const float p = tv ? exp2f(s_p[(buf * NR + r) * SUB + tl] - m_run[r]) : 0.f;
+        if (vqb == 0 && vgrp == 0) l_part[r] += p;
+        wgt[r] = p * vs;
+      }
+#pragma unroll
+      for (int pr = 0; pr < EPL / 2; pr++) {
+        const float2 cv = s_cb2[(uint32_t)(bits64 >> (pr * 2 * BITS)) & (VCODES - 1)];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+          acc[r][2 * pr] = __builtin_fmaf(wgt[r], cv.x, acc[r][2 * pr]);
+          acc[r][2 * pr + 1] = __builtin_fmaf(wgt[r], cv.y, acc[r][2 * pr + 1]);
+        }
+      }
+    }
+  }
+
+  // ---- reduce: V accumulators over the token slices, l over all lanes ----
+  float l_r[NR];
+  {
+    float *s_lr = s_red + 2 * NR * kWaves;  // [NR][kWaves], distinct from the max buffers
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const float sm = wave_reduce(l_part[r], [](float x, float y) { return x + y; });
+      if (lane == 0) s_lr[r * kWaves + wave] = sm;
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        float v = acc[r][e];
+#pragma unroll
+        for (int o = VLPT; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+        acc[r][e] = v;
+      }
+    __syncthreads();  // key table and scores no longer needed
+    if (lane < VLPT) {
+#pragma unroll
+      for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) s_tab[(wave * HD + vqb * 32 + vgrp * EPL + e) * NR + r] = acc[r][e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      float sm = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; w++) sm += s_lr[r * kWaves + w];
+      l_r[r] = sm;
+    }
+  }
+
+  // ---- tile partials ----
+  if (tid < NR * HD) {
+    const int r = tid / HD, d = tid % HD;
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) sum += s_tab[(w * HD + d) * NR + r];
+    const long long bh = (long long)b * a.num_heads + g * NR + r;
+    a.po[(bh * a.P + c) * HD + d] = sum;
+    if (d == 0) {
+      a.pm[bh * a.P + c] = m_run[r];
+      a.ps[bh * a.P + c] = l_r[r];
+    }
+  }
+
+  if constexpr (INLINE_MERGE) {
+    // Every writing wave waits for its stores, then one wave publishes them
+    // device-wide with a single release fence before the arrival counter.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (wave == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      if (lane == 0) {
+        const int prev = __hip_atomic_fetch_add(&a.counters[b * a.num_kv_heads + g], 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        s_flag = (prev == nchunks - 1);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (s_flag) {
+      merge_and_store<NR>(a, b, g, nchunks, lds + OFF_MISC);
+      if (tid == 0)
+        __hip_atomic_store(&a.counters[b * a.num_kv_heads + g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Standalone split-K merge (the reference ABI's second launch).
+template <int NR>
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
+  __shared__ float s_misc[kMiscFloats];
+  const int g = blockIdx.x, b = blockIdx.y;
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
+  const int nchunks = (len + kChunk - 1) / kChunk;
+  if (nchunks == 0) return;
+  merge_and_store<NR>(a, b, g, nchunks, s_misc);
+}
+
+__global__ void fill_zero_kernel(int *p, long long n) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Workspace layout: po | pm | ps | counters (each 256-byte aligned).
+struct WsLayout {
+  size_t po, pm, ps, cnt, total;
+  int P;
+};
+
+WsLayout ws_layout(int batch, int num_heads, int num_kv_heads, int head_dim, int max_len) {
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  WsLayout w{};
+  w.P = (max_len + kChunk - 1) / kChunk;
+  const size_t bhp = (size_t)batch * num_heads * w.P;
+  w.po = 0;
+  w.pm = al(w.po + bhp * head_dim * sizeof(float));
+  w.ps = al(w.pm + bhp * sizeof(float));
+  w.cnt = al(w.ps + bhp * sizeof(float));
+  w.total = al(w.cnt + (size_t)batch * num_kv_heads * sizeof(int));
+  return w;
+}
+
+AttnArgs base_args(int bits) {
+  AttnArgs a{};
+  tqh::PqoCodebook cb = tqh::pqo_codebook(bits);
+  for (int i = 0; i < cb.nc; i++) a.cb[i] = cb.c[i];
+  volatile float thirty_two = 32.0f;
+  volatile float sq = sqrtf(thirty_two);
+  volatile float inv = 1.0f / sq;
+  for (int j = 0; j < 32; j++) {
+    volatile float rf = pqo_neg(j) ? -inv : inv;
+    a.sg[j] = rf * sq;
+  }
+  a.out_dtype = kF32;
+  return a;
+}
+
+template <int BITS, int NR, bool INLINE>
+int launch_decode_q(const AttnArgs &a, int qt, dim3 grid, hipStream_t st) {
+  if (qt == kF32) hipLaunchKernelGGL((attn_decode_kernel<BITS, NR, kF32, INLINE>), grid, dim3(kThreads), 0, st, a);
+  else if (qt == kBF16) hipLaunchKernelGGL((attn_decode_kernel<BITS, NR, kBF16, INLINE>), grid, dim3(kThreads), 0, st, a);
+  else hipLaunchKernelGGL((attn_decode_kernel<BITS, NR, kF16, INLINE>), grid, dim3(kThreads), 0, st, a);
+  return tqh::check_launch("attn_decode_kernel");
+}
+
+template <bool INLINE>
+int launch_decode(const AttnArgs &a, int bits, int nr, int qt, dim3 grid, hipStream_t st) {
+  if (bits == 3) {
+    if (nr == 1) return launch_decode_q<3, 1, INLINE>(a, qt, grid, st);
+    if (nr == 2) return launch_decode_q<3, 2, INLINE>(a, qt, grid, st);
+    return launch_decode_q<3, 4, INLINE>(a, qt, grid, st);
+  }
+  if (nr == 1) return launch_decode_q<4, 1, INLINE>(a, qt, grid, st);
+  if (nr == 2) return launch_decode_q<4, 2, INLINE>(a, qt, grid, st);
+  return launch_decode_q<4, 4, INLINE>(a, qt, grid, st);
+}
+
+int check_common(int num_heads, int num_kv_heads, int head_dim, int bits) {
+  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+  if (head_dim != 128)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "fused decode attention supports head_dim 128, got %d", head_dim);
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_heads (%d) must be a multiple of num_kv_heads (%d)", num_heads,
+                     num_kv_heads);
+  const int nr = num_heads / num_kv_heads;
+  if (nr != 1 && nr != 2 && nr != 4)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "GQA ratio %d not supported (1, 2 or 4)", nr);
+  return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" size_t tq_attention_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                              int max_kv_len) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_kv_len < 0) return 0;
+  return ws_layout(batch, num_heads, num_kv_heads, head_dim, max_kv_len).total;
+}
+
+extern "C" int tq_attention_workspace_init(void *workspace, size_t workspace_bytes, int batch, int num_heads,
+                                           int num_kv_heads, int head_dim, int max_kv_len, hipStream_t stream) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_kv_len < 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid workspace shape");
+  const WsLayout w = ws_layout(batch, num_heads, num_kv_heads, head_dim, max_kv_len);
+  if (!workspace || workspace_bytes < w.total)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
+  const long long n = (long long)batch * num_kv_heads;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     reinterpret_cast<int *>(static_cast<char *>(workspace) + w.cnt), n);
+  return tqh::check_launch("fill_zero_kernel");
+}
+
+extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
+                                       const uint8_t *v_indices, const uint16_t *v_scales, const int *kv_lens,
+                                       int batch, int num_heads, int num_kv_heads, int head_dim, int bits,
+                                       int max_kv_len, long long kv_head_stride, long long seq_stride,
+                                       float softmax_scale, void *out, int out_dtype, void *workspace,
+                                       size_t workspace_bytes, hipStream_t stream) {
+  int rc = check_common(num_heads, num_kv_heads, head_dim, bits);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(q_dtype) || !tqh::valid_dtype(out_dtype))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (batch <= 0 || max_kv_len <= 0) return TQ_OK;
+  if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !kv_lens || !out)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  if (kv_head_stride < max_kv_len)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_head_stride %lld < max_kv_len %d", kv_head_stride, max_kv_len);
+  if (batch > 1 && seq_stride < (long long)num_kv_heads * kv_head_stride)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "seq_stride %lld overlaps the KV heads of a sequence", seq_stride);
+  const WsLayout w = ws_layout(batch, num_heads, num_kv_heads, head_dim, max_kv_len);
+  if (!workspace || workspace_bytes < w.total)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
+  if ((long long)(num_heads / num_kv_heads) * w.P > kMergeCap)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "max_kv_len %d too long for one merge", max_kv_len);
+  AttnArgs a = base_args(bits);
+  char *ws = static_cast<char *>(workspace);
+  a.q = q;
+  a.k_idx = k_indices;
+  a.k_sc = k_scales;
+  a.v_idx = v_indices;
+  a.v_sc = v_scales;
+  a.kv_lens = kv_lens;
+  a.single_len = 0;
+  a.max_len = max_kv_len;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.kv_head_stride = kv_head_stride;
+  a.seq_stride = seq_stride;
+  a.softmax_scale = softmax_scale;
+  a.po = reinterpret_cast<float *>(ws + w.po);
+  a.pm = reinterpret_cast<float *>(ws + w.pm);
+  a.ps = reinterpret_cast<float *>(ws + w.ps);
+  a.counters = reinterpret_cast<int *>(ws + w.cnt);
+  a.P = w.P;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  const dim3 grid((unsigned)w.P, (unsigned)num_kv_heads, (unsigned)batch);
+  return launch_decode<true>(a, bits, num_heads / num_kv_heads, q_dtype, grid, stream);
+}
+
+extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, const uint16_t *k_scales,
+                                  const uint8_t *v_indices, const uint16_t *v_scales, const float *codebook,
+                                  const float *sign_pattern, float *output, float *partial_out, float *partial_max,
+                                  float *partial_sum, const uint8_t *qjl_signs, const uint16_t *qjl_residual_norms,
+                                  const float *rq, int qjl_enabled, int num_attention_heads, int num_kv_heads,
+                                  int head_dim, int kv_len, int kv_stride, int packed_dim, int num_qblocks, int bits,
+                                  float softmax_scale, int num_partitions, hipStream_t stream) {
+  (void)qjl_signs;
+  (void)qjl_residual_norms;
+  (void)rq;
+  if (kv_len == 0 || num_kv_heads == 0) return TQ_OK;  // tq_attention_kernel.cu:366
+  if (qjl_enabled) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL correction in fused attention is not enabled");
+  int rc = check_common(num_attention_heads, num_kv_heads, head_dim, bits);
+  if (rc) return rc;
+  if (num_qblocks != head_dim / 32 || packed_dim != head_dim * bits / 8)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_qblocks/packed_dim inconsistent with head_dim and bits");
+  if (kv_len < 0 || kv_stride < kv_len) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_stride < kv_len");
+  if (num_partitions < (kv_len + 511) / 512)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_partitions %d < ceil(kv_len/512)", num_partitions);
+  if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !codebook || !sign_pattern || !output ||
+      !partial_out || !partial_max || !partial_sum)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  // The codebook and sign pattern are device tensors in the reference
+  // (pqo.rs:134-160) holding the PQO constants, which this entry applies from
+  // its own copy.  The caller's partial buffers (sized for 512-token
+  // partitions) hold this entry's 1024-token partials.
+  (void)codebook;
+  (void)sign_pattern;
+  AttnArgs a = base_args(bits);
+  a.q = q;
+  a.k_idx = k_indices;
+  a.k_sc = k_scales;
+  a.v_idx = v_indices;
+  a.v_sc = v_scales;
+  a.kv_lens = nullptr;
+  a.single_len = kv_len;
+  a.max_len = kv_len;
+  a.num_heads = num_attention_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.kv_head_stride = kv_stride;
+  a.seq_stride = 0;
+  a.softmax_scale = softmax_scale;
+  a.po = partial_out;
+  a.pm = partial_max;
+  a.ps = partial_sum;
+  a.counters = nullptr;
+  a.P = num_partitions;
+  a.out = output;
+  a.out_dtype = kF32;
+  const int nr = num_attention_heads / num_kv_heads;
+  const int P = (kv_len + kChunk - 1) / kChunk;
+  if ((long long)nr * P > kMergeCap) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_len %d too long for one merge", kv_len);
+  rc = launch_decode<false>(a, bits, nr, kF32, dim3((unsigned)P, (unsigned)num_kv_heads, 1u), stream);
+  if (rc) return rc;
+  const dim3 mgrid((unsigned)num_kv_heads, 1u);
+  if (nr == 1) hipLaunchKernelGGL((attn_merge_kernel<1>), mgrid, dim3(kThreads), 0, stream, a);
+  else if (nr == 2) hipLaunchKernelGGL((attn_merge_kernel<2>), mgrid, dim3(kThreads), 0, stream, a);
+  else hipLaunchKernelGGL((attn_merge_kernel<4>), mgrid, dim3(kThreads), 0, stream, a);
+  return tqh::check_launch("attn_merge_kernel");
+}

@@ -1,0 +1,94 @@
+// tq_common.cpp -- error reporting and host-side constant tables.
+#include "tq_common.h"
+
+#include <cmath>
+#include <cstring>
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+extern "C" const char *tq_last_error(void) { return g_last_error; }
+extern "C" const char *tq_version(void) { return "turboquant_amd 0.1.0 (gfx950)"; }
+
+namespace tqh {
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+  return TQ_OK;
+}
+
+PqoCodebook pqo_codebook(int bits) {
+  // src/cache/precomputed/codebooks.rs:8-88.  3-bit: the llama.cpp table;
+  // 4-bit: c4[i] = -R + i * (2R/15), b4[i] = -R + (i + 0.5) * (2R/15), f32.
+  static const float c3[8] = {-2.1573f, -1.3336f, -0.7434f, -0.2428f, 0.2428f, 0.7434f, 1.3336f, 2.1573f};
+  static const float b3[7] = {-1.7455f, -1.0385f, -0.4931f, 0.0f, 0.4931f, 1.0385f, 1.7455f};
+  static const float c2[4] = {-2.1573f, -0.7434f, 0.7434f, 2.1573f};
+  static const float b2[3] = {-1.0385f, 0.0f, 1.0385f};
+  PqoCodebook cb;
+  cb.bits = bits;
+  const float range = 2.1573f;
+  if (bits == 3) {
+    cb.nc = 8;
+    std::memcpy(cb.c, c3, sizeof c3);
+    std::memcpy(cb.b, b3, sizeof b3);
+  } else if (bits == 4) {
+    cb.nc = 16;
+    volatile float full = 2.0f * range;  // volatile: keep every f32 rounding step
+    volatile float step = full / 15.0f;
+    for (int i = 0; i < 16; i++) {
+      volatile float t = (float)i * step;
+      cb.c[i] = -range + t;
+    }
+    for (int i = 0; i < 15; i++) {
+      volatile float k = (float)i + 0.5f;
+      volatile float t = k * step;
+      cb.b[i] = -range + t;
+    }
+  } else if (bits == 2) {
+    cb.nc = 4;
+    std::memcpy(cb.c, c2, sizeof c2);
+    std::memcpy(cb.b, b2, sizeof b2);
+  } else {
+    return cb;
+  }
+  float m = cb.c[0];
+  for (int i = 1; i < cb.nc; i++) m = cb.c[i] > m ? cb.c[i] : m;
+  cb.outer = m;
+  return cb;
+}
+
+static float next_up_host(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) == 0) u = 1u;
+  else u = ((int32_t)u >= 0) ? u + 1u : u - 1u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+DivThresholds div_thresholds(const float *b, int nb, float outer) {
+  DivThresholds t;
+  t.nb = nb;
+  for (int k = 0; k < nb; k++) {
+    float up = next_up_host(b[k]);
+    t.mu[k] = ((double)b[k] + (double)up) * 0.5;  // exact: both fit in 25 bits
+    uint32_t u;
+    std::memcpy(&u, &b[k], 4);
+    if ((u & 1u) == 0) t.strict_mask |= 1u << k;
+  }
+  t.mul = (float)(1.0 / (double)outer);
+  return t;
+}
+
+}  // namespace tqh

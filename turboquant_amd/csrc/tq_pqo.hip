@@ -1,0 +1,427 @@
+// tq_pqo.hip -- PQO (block-32 MaxNorm) cache codec kernels for gfx950.
+//
+// Design: one lane owns one 32-element qblock.  The block's values live in
+// 32 VGPRs, so the Walsh-Hadamard rotation is five in-register butterfly
+// stages with no cross-lane traffic, the max-abs is a register reduction,
+// and the bucketized codes are shifted straight into the packed words
+// (12 B for 3-bit, 16 B for 4-bit) that the lane stores; nothing needs
+// atomics or LDS.  A wave covers 64 consecutive qblocks, so its stores of
+// packed codes and f16 scales are contiguous.
+//
+// Exactness: the reference computes v = fl(r / scale) and counts v > b_k
+// (quantize_tensor.rs:107-108, 161-176).  Here each block turns its 2^b - 1
+// boundaries into exact thresholds U_k in the input domain once
+// (tqd::div_threshold, f64), and the per-element work is r >= U_k: the same
+// codes for every finite input, without a division per element.
+#include "tq_common.h"
+#include "tq_device.h"
+
+namespace {
+
+using namespace tqd;
+
+constexpr float kInvSqrt32 = 0x1.6a09e6p-3f;  // fl(1 / fl(sqrt(32))) = 0.17677669f
+
+struct QuantConsts {
+  double mu[15];
+  float b[15];
+  uint32_t strict_mask;
+  float mul;
+  float scale_sign;
+};
+
+template <int BITS>
+struct Packed {
+  static constexpr int kWords = BITS;  // 32 * BITS / 32
+  static constexpr int kBytes = 4 * BITS;
+};
+
+template <int IN_DT>
+__device__ __forceinline__ void load_block(const void *__restrict__ x, long long blk, float (&r)[32]) {
+  if constexpr (IN_DT == kF32) {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + blk * 32);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      float4 v = p[q];
+      r[4 * q + 0] = v.x;
+      r[4 * q + 1] = v.y;
+      r[4 * q + 2] = v.z;
+      r[4 * q + 3] = v.w;
+    }
+  } else {
+    const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + blk * 32);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint4 v = p[q];
+      uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        if constexpr (IN_DT == kBF16) {
+          r[8 * q + 2 * k] = u2f(w[k] << 16);
+          r[8 * q + 2 * k + 1] = u2f(w[k] & 0xffff0000u);
+        } else {
+          r[8 * q + 2 * k] = f16_to_f32((uint16_t)(w[k] & 0xffffu));
+          r[8 * q + 2 * k + 1] = f16_to_f32((uint16_t)(w[k] >> 16));
+        }
+      }
+    }
+  }
+}
+
+// MaxNorm scale, exact bucketize and pack of one rotated block.
+template <int BITS>
+__device__ __forceinline__ float quantize_block(const float (&r)[32], const QuantConsts &k,
+                                                uint32_t (&w)[Packed<BITS>::kWords]) {
+  constexpr int NB = (1 << BITS) - 1;
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(r[j]));
+  float s = amax * k.mul;
+  if (s < 1e-10f) s = 1e-10f;
+
+  uint32_t idx[32];
+  if (__builtin_isfinite(s)) {
+    float U[NB];
+#pragma unroll
+    for (int t = 0; t < NB; t++) U[t] = div_threshold(k.mu[t], (k.strict_mask >> t) & 1u, s);
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int t = 0; t < NB; t++) c += (r[j] >= U[t]) ? 1u : 0u;
+      idx[j] = c;
+    }
+  } else {
+    // Infinite scale (an infinite input): follow the reference's division.
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      float v = r[j] / s;
+      uint32_t c = 0;
+#pragma unroll
+      for (int t = 0; t < NB; t++) c += (v > k.b[t]) ? 1u : 0u;
+      idx[j] = c;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < Packed<BITS>::kWords; q++) w[q] = 0;
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    const int pos = j * BITS, wi = pos >> 5, sh = pos & 31;
+    w[wi] |= idx[j] << sh;
+    if (sh + BITS > 32) w[wi + 1] |= idx[j] >> (32 - sh);
+  }
+  return s;
+}
+
+template <int BITS>
+__device__ __forceinline__ void store_packed(uint8_t *__restrict__ packed, long long blk,
+                                             const uint32_t (&w)[Packed<BITS>::kWords]) {
+  uint32_t *p = reinterpret_cast<uint32_t *>(packed + blk * Packed<BITS>::kBytes);
+  if constexpr (BITS == 4) {
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else if constexpr (BITS == 2) {
+    *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+  } else {
+    p[0] = w[0];
+    p[1] = w[1];
+    p[2] = w[2];
+  }
+}
+
+// ROTATE: input is raw activations (fused forward rotation, butterfly order).
+// Otherwise input is already rotated f32 (the reference kernel's contract).
+template <int BITS, int IN_DT, bool ROTATE>
+__global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__ x,
+                                                        uint8_t *__restrict__ packed,
+                                                        uint16_t *__restrict__ scales,
+                                                        long long nblocks, QuantConsts k) {
+  const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= nblocks) return;
+  float r[32];
+  load_block<IN_DT>(x, blk, r);
+  if constexpr (ROTATE) {
+    butterfly<32>(r);
+#pragma unroll
+    for (int j = 0; j < 32; j++) r[j] = r[j] * (pqo_neg(j) ? -kInvSqrt32 : kInvSqrt32);
+  }
+  uint32_t w[Packed<BITS>::kWords];
+  float s = quantize_block<BITS>(r, k, w);
+  store_packed<BITS>(packed, blk, w);
+  scales[blk] = f32_to_f16(s * k.scale_sign);
+}
+
+// Reference-ABI variant: boundaries and outer centroid come from the caller
+// (device boundaries), constants derived in-kernel per lane.
+template <int BITS>
+__global__ __launch_bounds__(256) void pqo_quant_rotated_dev_kernel(
+    const float *__restrict__ rotated, const float *__restrict__ boundaries,
+    uint8_t *__restrict__ packed, uint16_t *__restrict__ scales, long long nblocks, float outer,
+    float scale_sign) {
+  const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= nblocks) return;
+  constexpr int NB = (1 << BITS) - 1;
+  QuantConsts k;
+#pragma unroll
+  for (int t = 0; t < NB; t++) {
+    float b = boundaries[t];
+    float up = next_up(b);
+    k.b[t] = b;
+    k.mu[t] = ((double)b + (double)up) * 0.5;
+  }
+  k.strict_mask = 0;
+#pragma unroll
+  for (int t = 0; t < NB; t++) k.strict_mask |= ((f2u(k.b[t]) & 1u) == 0 ? 1u : 0u) << t;
+  k.mul = (float)(1.0 / (double)outer);
+  k.scale_sign = scale_sign;
+  float r[32];
+  load_block<kF32>(rotated, blk, r);
+  uint32_t w[Packed<BITS>::kWords];
+  float s = quantize_block<BITS>(r, k, w);
+  store_packed<BITS>(packed, blk, w);
+  scales[blk] = f32_to_f16(s * scale_sign);
+}
+
+struct DequantConsts {
+  float cb[16];  // codebook values (f32)
+  float sg[32];  // sign factor per element (the reference passes fl(R_fwd[0][j] * sqrt(32)))
+};
+
+// out_j = fl(fl(W_j * fl(1/sqrt(32))) * |scale|), W = butterfly(cb[idx] * sign):
+// butterfly_wht_inverse_cpu (wht_tensor.rs:38-64) then the broadcast_mul by
+// |scale| (quantize_tensor.rs:203, 217-218).
+template <int BITS, int OUT_DT, bool DEV_CONSTS>
+__global__ __launch_bounds__(256) void pqo_dequant_kernel(const uint8_t *__restrict__ packed,
+                                                          const uint16_t *__restrict__ scales,
+                                                          void *__restrict__ out, long long nblocks,
+                                                          DequantConsts dc,
+                                                          const float *__restrict__ dev_cb,
+                                                          const float *__restrict__ dev_sg) {
+  __shared__ float lut[16];
+  constexpr int NC = 1 << BITS;
+  if (threadIdx.x < NC) lut[threadIdx.x] = DEV_CONSTS ? dev_cb[threadIdx.x] : dc.cb[threadIdx.x];
+  __syncthreads();
+  const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= nblocks) return;
+  uint32_t w[Packed<BITS>::kWords];
+  const uint32_t *p = reinterpret_cast<const uint32_t *>(packed + blk * Packed<BITS>::kBytes);
+  if constexpr (BITS == 4) {
+    uint4 v = *reinterpret_cast<const uint4 *>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if constexpr (BITS == 2) {
+    uint2 v = *reinterpret_cast<const uint2 *>(p);
+    w[0] = v.x; w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 3; q++) w[q] = p[q];
+  }
+  const float s = fabsf(f16_to_f32(scales[blk]));
+  float z[32];
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    const float sgn = DEV_CONSTS ? dev_sg[j] : dc.sg[j];
+    z[j] = lut[field<BITS>(w, j)] * sgn;
+  }
+  butterfly<32>(z);
+#pragma unroll
+  for (int j = 0; j < 32; j++) z[j] = (z[j] * kInvSqrt32) * s;
+  if constexpr (OUT_DT == kF32) {
+    float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + blk * 32);
+#pragma unroll
+    for (int q = 0; q < 8; q++) o[q] = make_float4(z[4 * q], z[4 * q + 1], z[4 * q + 2], z[4 * q + 3]);
+  } else {
+    uint4 *o = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + blk * 32);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint32_t v[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float a = z[8 * q + 2 * k], b = z[8 * q + 2 * k + 1];
+        uint32_t ha = OUT_DT == kBF16 ? f32_to_bf16(a) : f32_to_f16(a);
+        uint32_t hb = OUT_DT == kBF16 ? f32_to_bf16(b) : f32_to_f16(b);
+        v[k] = ha | (hb << 16);
+      }
+      o[q] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  }
+}
+
+// One thread per output byte: gathers the codes overlapping bits [8i, 8i+8).
+__global__ __launch_bounds__(256) void pack_indices_kernel(const uint8_t *__restrict__ idx,
+                                                           uint8_t *__restrict__ out,
+                                                           long long nvec, int block_size, int bits,
+                                                           int bytes_per_block) {
+  const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= nvec * bytes_per_block) return;
+  const long long v = g / bytes_per_block;
+  const int byte = (int)(g % bytes_per_block);
+  const uint8_t *src = idx + v * block_size;
+  uint32_t acc = 0;
+  const int lo = byte * 8, hi = lo + 8;
+  const int mask = (1 << bits) - 1;
+  for (int i = lo / bits; i * bits < hi && i < block_size; i++) {
+    const int pos = i * bits - lo;  // may be negative for a code straddling in
+    uint32_t c = (uint32_t)(src[i] & mask);
+    acc |= pos >= 0 ? (c << pos) : (c >> -pos);
+  }
+  out[g] = (uint8_t)(acc & 0xffu);
+}
+
+int launch_quant(const void *x, int dt, bool rotate, uint8_t *packed, uint16_t *scales, long long nblocks,
+                 int bits, const QuantConsts &k, hipStream_t st) {
+  const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
+#define QL(B, D, R) hipLaunchKernelGGL((pqo_quant_kernel<B, D, R>), grid, block, 0, st, x, packed, scales, nblocks, k)
+  if (!rotate) {
+    if (bits == 2) QL(2, kF32, false);
+    else if (bits == 3) QL(3, kF32, false);
+    else QL(4, kF32, false);
+  } else if (bits == 3) {
+    if (dt == kF32) QL(3, kF32, true);
+    else if (dt == kBF16) QL(3, kBF16, true);
+    else QL(3, kF16, true);
+  } else {
+    if (dt == kF32) QL(4, kF32, true);
+    else if (dt == kBF16) QL(4, kBF16, true);
+    else QL(4, kF16, true);
+  }
+#undef QL
+  return tqh::check_launch("pqo_quant_kernel");
+}
+
+QuantConsts make_quant_consts(const tqh::PqoCodebook &cb, float scale_sign) {
+  tqh::DivThresholds t = tqh::div_thresholds(cb.b, cb.nc - 1, cb.outer);
+  QuantConsts k{};
+  for (int i = 0; i < t.nb; i++) {
+    k.mu[i] = t.mu[i];
+    k.b[i] = cb.b[i];
+  }
+  k.strict_mask = t.strict_mask;
+  k.mul = t.mul;
+  k.scale_sign = scale_sign;
+  return k;
+}
+
+DequantConsts make_dequant_consts(const tqh::PqoCodebook &cb) {
+  DequantConsts dc{};
+  for (int i = 0; i < cb.nc; i++) dc.cb[i] = cb.c[i];
+  // fl(R_fwd[0][j] * sqrt(32)) = fl(+-fl(1/sqrt(32)) * fl(sqrt(32))) (wht_tensor.rs:28-41)
+  volatile float thirty_two = 32.0f;
+  volatile float sq = sqrtf(thirty_two);  // fl(sqrt(32)), IEEE sqrt
+  volatile float inv = 1.0f / sq;
+  for (int j = 0; j < 32; j++) {
+    volatile float rf = pqo_neg(j) ? -inv : inv;
+    dc.sg[j] = rf * sq;
+  }
+  return dc;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+extern "C" int tq_pqo_quantize(const void *x, int x_dtype, uint8_t *packed_out, uint16_t *scales_out,
+                               size_t num_vectors, int head_dim, int bits, hipStream_t stream) {
+  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+  if (head_dim <= 0 || head_dim % 32 != 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "head_dim (%d) must be divisible by QUANT_BLOCK_SIZE (32)", head_dim);
+  if (!tqh::valid_dtype(x_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", x_dtype);
+  if (num_vectors == 0) return TQ_OK;
+  if (!x || !packed_out || !scales_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long nblocks = (long long)num_vectors * (head_dim / 32);
+  QuantConsts k = make_quant_consts(tqh::pqo_codebook(bits), -1.0f);
+  return launch_quant(x, x_dtype, true, packed_out, scales_out, nblocks, bits, k, stream);
+}
+
+extern "C" int tq_pqo_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
+                                 size_t num_vectors, int head_dim, int bits, hipStream_t stream) {
+  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+  if (head_dim <= 0 || head_dim % 32 != 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "head_dim (%d) must be divisible by QUANT_BLOCK_SIZE (32)", head_dim);
+  if (!tqh::valid_dtype(out_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", out_dtype);
+  if (num_vectors == 0) return TQ_OK;
+  if (!packed || !scales || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long nblocks = (long long)num_vectors * (head_dim / 32);
+  DequantConsts dc = make_dequant_consts(tqh::pqo_codebook(bits));
+  const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
+#define DL(B, D) hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false>), grid, block, 0, stream, packed, scales, out, nblocks, dc, nullptr, nullptr)
+  if (bits == 3) {
+    if (out_dtype == kF32) DL(3, kF32);
+    else if (out_dtype == kBF16) DL(3, kBF16);
+    else DL(3, kF16);
+  } else {
+    if (out_dtype == kF32) DL(4, kF32);
+    else if (out_dtype == kBF16) DL(4, kBF16);
+    else DL(4, kF16);
+  }
+#undef DL
+  return tqh::check_launch("pqo_dequant_kernel");
+}
+
+extern "C" int tq_quant_maxnorm_batch(const float *rotated_input, const float *boundaries, uint8_t *packed_out,
+                                      uint16_t *scales_out, int num_blocks, int block_size, int bits,
+                                      int num_boundaries, int bytes_per_block, float outer_centroid,
+                                      float scale_sign, hipStream_t stream) {
+  if (num_blocks == 0) return TQ_OK;  // tq_quant_kernel.cu:430
+  if (num_blocks < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_blocks < 0");
+  if (block_size != 32) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "block_size must be QUANT_BLOCK_SIZE (32), got %d", block_size);
+  if (bits < 2 || bits > 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bit width %d", bits);
+  if (num_boundaries != (1 << bits) - 1)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_boundaries %d != 2^bits - 1", num_boundaries);
+  if (bytes_per_block != 32 * bits / 8)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "bytes_per_block %d != 32*bits/8", bytes_per_block);
+  if (!rotated_input || !boundaries || !packed_out || !scales_out)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long nb = num_blocks;
+  const dim3 grid((unsigned)((nb + 255) / 256)), block(256);
+  if (bits == 2)
+    hipLaunchKernelGGL((pqo_quant_rotated_dev_kernel<2>), grid, block, 0, stream, rotated_input, boundaries,
+                       packed_out, scales_out, nb, outer_centroid, scale_sign);
+  else if (bits == 3)
+    hipLaunchKernelGGL((pqo_quant_rotated_dev_kernel<3>), grid, block, 0, stream, rotated_input, boundaries,
+                       packed_out, scales_out, nb, outer_centroid, scale_sign);
+  else
+    hipLaunchKernelGGL((pqo_quant_rotated_dev_kernel<4>), grid, block, 0, stream, rotated_input, boundaries,
+                       packed_out, scales_out, nb, outer_centroid, scale_sign);
+  return tqh::check_launch("pqo_quant_rotated_dev_kernel");
+}
+
+extern "C" int tq_dequant_batch(const uint8_t *packed_indices, const uint16_t *scales, const float *codebook,
+                                const float *sign_pattern, float *output, int num_blocks, int block_size, int bits,
+                                int bytes_per_block, hipStream_t stream) {
+  if (num_blocks == 0) return TQ_OK;  // tq_dequant_kernel.cu:116
+  if (num_blocks < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_blocks < 0");
+  if (block_size != 32) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "block_size must be QUANT_BLOCK_SIZE (32), got %d", block_size);
+  if (bits < 2 || bits > 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bit width %d", bits);
+  if (bytes_per_block != 32 * bits / 8)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "bytes_per_block %d != 32*bits/8", bytes_per_block);
+  if (!packed_indices || !scales || !codebook || !sign_pattern || !output)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long nb = num_blocks;
+  const dim3 grid((unsigned)((nb + 255) / 256)), block(256);
+  DequantConsts dc{};
+  if (bits == 2)
+    hipLaunchKernelGGL((pqo_dequant_kernel<2, kF32, true>), grid, block, 0, stream, packed_indices, scales, output,
+                       nb, dc, codebook, sign_pattern);
+  else if (bits == 3)
+    hipLaunchKernelGGL((pqo_dequant_kernel<3, kF32, true>), grid, block, 0, stream, packed_indices, scales, output,
+                       nb, dc, codebook, sign_pattern);
+  else
+    hipLaunchKernelGGL((pqo_dequant_kernel<4, kF32, true>), grid, block, 0, stream, packed_indices, scales, output,
+                       nb, dc, codebook, sign_pattern);
+  return tqh::check_launch("pqo_dequant_kernel");
+}
+
+extern "C" int tq_pack_indices(const uint8_t *indices, uint8_t *packed_out, int num_vectors, int block_size,
+                               int bits, int bytes_per_block, hipStream_t stream) {
+  if (num_vectors == 0) return TQ_OK;
+  if (num_vectors < 0 || block_size <= 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "negative size");
+  if (bits < 2 || bits > 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bit width %d", bits);
+  if (bytes_per_block * 8 < block_size * bits)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "bytes_per_block %d too small", bytes_per_block);
+  if (!indices || !packed_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long total = (long long)num_vectors * bytes_per_block;
+  hipLaunchKernelGGL(pack_indices_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, indices,
+                     packed_out, (long long)num_vectors, block_size, bits, bytes_per_block);
+  return tqh::check_launch("pack_indices_kernel");
+}
