@@ -78,9 +78,15 @@ def test_pqo_rotation_is_matrix_product():
     r = orc.pqo_rotate(x)
     R = hadamard(32) / np.sqrt(32) * orc.pqo_sign32()[None, :]
     assert np.allclose(r, x.astype(np.float64) @ R, atol=2e-6)
-    # integer inputs: butterfly and dot-product orders are both exact
+    # integer inputs: every butterfly sum is exact, so the oracle's order gives
+    # exactly fl((H x)_j * fl(1/sqrt 32)) * s_j
     xi = rng.integers(-20, 20, size=(16, 32)).astype(np.float32)
-    assert np.array_equal(orc.pqo_rotate(xi), orc.pqo_rotate(xi, gemm=True))
+    inv = np.float32(np.float32(1.0) / np.sqrt(np.float32(32)))
+    assert inv.view(np.uint32) == 0x3E3504F3
+    ref = ((xi.astype(np.float64) @ hadamard(32)).astype(np.float32) * inv) * orc.pqo_sign32()[None, :]
+    assert np.array_equal(orc.pqo_rotate(xi), ref.astype(np.float32))
+    # the dot-product order (each x_i * R_ij rounded, then summed) agrees to rounding
+    assert np.allclose(orc.pqo_rotate(xi, gemm=True), ref, rtol=0, atol=1e-5)
 
 
 def test_device_sign_mask_matches_pattern():

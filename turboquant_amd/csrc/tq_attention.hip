@@ -191,44 +191,38 @@ template <int BITS, int NR, int QT, bool INLINE_MERGE>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   using G = Geo<BITS>;
   constexpr int NQB = 4, HD = 128, CH = kChunk;
-  constexpr int QW = BITS;                      // 32-bit words per qblock
-  constexpr int PACKED = NQB * QW * 4;          // bytes per token record
-  constexpr int SUB = kThreads / NQB;           // tokens per sub-chunk: one (token, qblock) per lane
-  constexpr int NSUB = CH / SUB;                // sub-chunks per tile
-  constexpr bool LIGHT = (BITS == 3 && NR <= 2);  // register budget allows the deeper pipeline
-  constexpr int EPL = LIGHT ? 16 : 8;           // V-pass elements per lane
-  constexpr int NSET = LIGHT ? 3 : 2;           // register sets of loads in flight
-  constexpr int GPQ = 32 / EPL;                 // V lanes per qblock of a token
-  constexpr int VLPT = NQB * GPQ;               // V lanes per token
-  constexpr int VSL = kThreads / VLPT;          // V token slices
-  constexpr int VTS = SUB / VSL;                // tokens per V lane per sub-chunk
-  constexpr int VCODES = 1 << (2 * BITS);       // pair-codebook entries
-  constexpr int KTAB = NQB * G::KPOS * G::KENT * NR;
-  constexpr int VRED = kWaves * HD * NR;
-  constexpr int TABSZ = KTAB > VRED ? KTAB : VRED;
-  // LDS carve, in 32-bit words.  The key table sits at offset 0 so every
-  // lookup's table position folds into the ds_read immediate offset.
-  constexpr int OFF_CB2 = TABSZ;                        // float2[VCODES]
-  constexpr int OFF_V = OFF_CB2 + 2 * VCODES;           // u32 [2][SUB * NQB * QW]  V records
-  constexpr int VBUF = SUB * NQB * QW;
-  constexpr int OFF_VS = OFF_V + 2 * VBUF;              // u16 [2][SUB * NQB]       V scales
-  constexpr int VSBUF = SUB * NQB / 2;
-  constexpr int OFF_P = OFF_VS + 2 * VSBUF;             // f32 [2][NR][SUB]         scores
-  constexpr int OFF_Q = OFF_P + 2 * NR * SUB;           // f32 [NR * HD]            rotated queries
-  constexpr int OFF_RED = OFF_Q + NR * HD;              // f32 [3][NR][kWaves]: 2 max buffers + l sums
-  constexpr int OFF_MISC = OFF_V;                       // merge scratch aliases the staging buffers
-  constexpr int TOTAL0 = OFF_RED + 3 * NR * kWaves + 8;
+  constexpr int QW = BITS;                       // 32-bit words per qblock
+  constexpr int RW = NQB * QW;                   // words per token record (12 / 16)
+  constexpr int PACKED = RW * 4;                 // bytes per token record
+  constexpr int WT = 64;                         // tokens per wave: lane = token
+  constexpr int EPL = NR <= 2 ? 16 : 8;          // V-pass elements per lane
+  constexpr int GPQ = 32 / EPL;                  // V lanes per qblock of a token
+  constexpr int VLPT = NQB * GPQ;                // V lanes per token
+  constexpr int VSL = 64 / VLPT;                 // token slices per wave in the V pass
+  constexpr int VTS = WT / VSL;                  // tokens per lane in the V pass
+  constexpr int VCODES = 1 << (2 * BITS);        // pair-codebook entries
+  constexpr int KROW = G::KPOS * G::KENT;        // key-table entries per (head, qblock)
+  constexpr int KTAB = NR * NQB * KROW;          // one 4-byte entry per (head, qblock, position, code)
+  constexpr int SPITCH = WT + 8;                 // V-scale rows: 4 qblock rows of 8 tokens on distinct banks
+  constexpr int WSTAGE = WT * RW + NR * WT + NQB * SPITCH;  // per-wave staging: V records, p, |V scale|
+  static_assert(kWaves * WT == CH, "one token per lane");
+  static_assert(WSTAGE >= NR * HD + 2 * NR, "combine record fits the staging area");
+  static_assert(KTAB * 4 <= 65536, "key-table offsets fit the ds_read immediate");
+  // LDS carve (32-bit words).  Tables use 4-byte entries in rows of 64 (or 16):
+  // a wave's 64 lookups into one row hit 64 distinct banks or share an address.
+  constexpr int OFF_CBL = KTAB;                         // pair codebook: value of the low element
+  constexpr int OFF_CBH = OFF_CBL + VCODES;             //                value of the high element
+  constexpr int OFF_Q = OFF_CBH + VCODES;
+  constexpr int OFF_W = OFF_Q + NR * HD;
+  constexpr int OFF_MISC = OFF_W;                       // merge scratch aliases the staging areas
+  constexpr int TOTAL0 = OFF_W + kWaves * WSTAGE;
   constexpr int TOTAL = TOTAL0 > OFF_MISC + kMiscFloats ? TOTAL0 : OFF_MISC + kMiscFloats;
-  static_assert(NSUB * SUB == CH, "tile shape");
   __shared__ float lds[TOTAL];
   __shared__ int s_flag;
-  float *s_tab = lds;
-  float2 *s_cb2 = reinterpret_cast<float2 *>(lds + OFF_CB2);
-  uint32_t *s_v = reinterpret_cast<uint32_t *>(lds + OFF_V);
-  uint16_t *s_vs = reinterpret_cast<uint16_t *>(lds + OFF_VS);
-  float *s_p = lds + OFF_P;
+  float *s_ktab = lds;
+  float *s_cbl = lds + OFF_CBL;
+  float *s_cbh = lds + OFF_CBH;
   float *s_q = lds + OFF_Q;
-  float *s_red = lds + OFF_RED;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -238,38 +232,35 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   if (t0 >= len) return;  // empty tile: not counted by the merge
   const int nchunks = (len + CH - 1) / CH;
   const long long rec0 = (long long)b * a.seq_stride + (long long)g * a.kv_head_stride;
+  uint32_t *stage = reinterpret_cast<uint32_t *>(lds + OFF_W + wave * WSTAGE);
+  uint32_t *st_v = stage;                                     // [WT][RW]
+  float *st_p = reinterpret_cast<float *>(stage + WT * RW);   // [NR][WT]: softmax numerators
+  float *st_s = st_p + NR * WT;                               // [NQB][SPITCH]: |V scale|
 
-  // ---- loads: lane = (token kt, qblock kq) of a sub-chunk; three register sets ----
-  const int kq = tid & (NQB - 1), kt = tid / NQB;
-  uint32_t kw[NSET][QW], vw[NSET][QW], ksc[NSET], vsc[NSET];
-  auto issue = [&](int s, int set) {
-    const int t = min(t0 + s * SUB + kt, len - 1);
-    const long long rec = rec0 + t;
-    const uint32_t *kp = reinterpret_cast<const uint32_t *>(a.k_idx + rec * PACKED) + kq * QW;
-    const uint32_t *vp = reinterpret_cast<const uint32_t *>(a.v_idx + rec * PACKED) + kq * QW;
-    if constexpr (QW == 4) {
-      const uint4 k4 = *reinterpret_cast<const uint4 *>(kp);
-      kw[set][0] = k4.x; kw[set][1] = k4.y; kw[set][2] = k4.z; kw[set][3] = k4.w;
-    } else {
-#pragma unroll
-      for (int w = 0; w < QW; w++) kw[set][w] = kp[w];
-    }
-    ksc[set] = a.k_sc[rec * NQB + kq];
-    if constexpr (QW == 4) {
-      const uint4 v4 = *reinterpret_cast<const uint4 *>(vp);
-      vw[set][0] = v4.x; vw[set][1] = v4.y; vw[set][2] = v4.z; vw[set][3] = v4.w;
-    } else {
-#pragma unroll
-      for (int w = 0; w < QW; w++) vw[set][w] = vp[w];
-    }
-    vsc[set] = a.v_sc[rec * NQB + kq];
-  };
-  const int nsub = min(NSUB, (len - t0 + SUB - 1) / SUB);  // sub-chunks holding tokens (uniform)
-  // the query load goes first so the table build below overlaps the K/V loads
+  // ---- loads: query first (it feeds the table build), then this lane's token ----
   float qv = 0.f;
   if (tid < NR * HD) qv = load_q<QT>(a.q, ((long long)b * a.num_heads + g * NR) * HD + tid);
-  issue(0, 0);
-  if (NSET > 2 && nsub > 1) issue(1, 1);
+  const int tok = t0 + wave * WT + lane;
+  const bool valid = tok < len;
+  const long long rec = rec0 + min(tok, len - 1);
+  uint32_t kr[RW], vr[RW];
+  uint2 ksr, vsr;
+  {
+    const uint4 *kp = reinterpret_cast<const uint4 *>(a.k_idx + rec * PACKED);
+    const uint4 *vp = reinterpret_cast<const uint4 *>(a.v_idx + rec * PACKED);
+#pragma unroll
+    for (int q = 0; q < RW / 4; q++) {
+      const uint4 v = kp[q];
+      kr[4 * q] = v.x; kr[4 * q + 1] = v.y; kr[4 * q + 2] = v.z; kr[4 * q + 3] = v.w;
+    }
+    ksr = *reinterpret_cast<const uint2 *>(a.k_sc + rec * NQB);
+#pragma unroll
+    for (int q = 0; q < RW / 4; q++) {
+      const uint4 v = vp[q];
+      vr[4 * q] = v.x; vr[4 * q + 1] = v.y; vr[4 * q + 2] = v.z; vr[4 * q + 3] = v.w;
+    }
+    vsr = *reinterpret_cast<const uint2 *>(a.v_sc + rec * NQB);
+  }
 
   // ---- rotated, scaled queries (32-lane butterflies) and the LDS tables ----
   const float qscale = a.softmax_scale * kLog2e * kInvSqrt32;
@@ -286,29 +277,83 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   }
   if (tid < VCODES) {
     constexpr int NCm = G::NC - 1;
-    s_cb2[tid] = make_float2(a.cb[tid & NCm], a.cb[(tid >> BITS) & NCm]);
+    s_cbl[tid] = a.cb[tid & NCm];
+    s_cbh[tid] = a.cb[(tid >> BITS) & NCm];
   }
   __syncthreads();
-  for (int e = tid; e < NQB * G::KPOS * G::KENT; e += kThreads) {
-    // e = (qb * KPOS + pos) * KENT + code
-    const int code = e % G::KENT, qp = e / G::KENT;
-    const int qb = qp / G::KPOS, pos = qp % G::KPOS;
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-      float v;
-      if constexpr (G::KPAIR) {
-        const float *qt = s_q + r * HD + qb * 32 + 2 * pos;
-        v = qt[0] * a.cb[code & 7] + qt[1] * a.cb[code >> 3];
-      } else {
-        v = s_q[r * HD + qb * 32 + pos] * a.cb[code];
-      }
-      s_tab[e * NR + r] = v;
+  for (int e = tid; e < NR * NQB * KROW; e += kThreads) {
+    // e = ((r * NQB + qb) * KPOS + pos) * KENT + code
+    const int code = e % G::KENT, rqp = e / G::KENT;
+    const int pos = rqp % G::KPOS, rq = rqp / G::KPOS;
+    const int qb = rq % NQB, r = rq / NQB;
+    float v;
+    if constexpr (G::KPAIR) {
+      const float *qt = s_q + r * HD + qb * 32 + 2 * pos;
+      v = qt[0] * a.cb[code & 7] + qt[1] * a.cb[code >> 3];
+    } else {
+      v = s_q[r * HD + qb * 32 + pos] * a.cb[code];
     }
+    s_ktab[e] = v;
   }
   __syncthreads();
 
-  // ---- V-pass lane geometry: (token slice, qblock, element group of EPL) ----
-  const int vgrp = tid % GPQ, vqb = (tid / GPQ) % NQB, vsl = tid / VLPT;
+  // ---- stage this wave's V records and scales (wave-private LDS; frees their VGPRs) ----
+#pragma unroll
+  for (int q = 0; q < RW / 4; q++)
+    *reinterpret_cast<uint4 *>(st_v + lane * RW + 4 * q) = make_uint4(vr[4 * q], vr[4 * q + 1], vr[4 * q + 2], vr[4 * q + 3]);
+#pragma unroll
+  for (int qb = 0; qb < NQB; qb++) {
+    const uint32_t sbits = (qb < 2 ? vsr.x : vsr.y) >> ((qb & 1) ? 16 : 0);
+    st_s[qb * SPITCH + lane] = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+  }
+
+  // ---- K pass: lane = token, all qblocks in-lane ----
+  float score[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) score[r] = 0.f;
+  constexpr int QBU = BITS == 3 ? (NR <= 2 ? NQB : 2) : 1;  // bound the LDS reads in flight
+#pragma unroll QBU
+  for (int qb = 0; qb < NQB; qb++) {
+    uint32_t w[QW];  // words of qblock qb, selected without dynamic register indexing
+#pragma unroll
+    for (int k = 0; k < QW; k++) {
+      uint32_t x = kr[k];
+#pragma unroll
+      for (int qq = 1; qq < NQB; qq++) x = (qb == qq) ? kr[qq * QW + k] : x;
+      w[k] = x;
+    }
+    float part[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) part[r] = 0.f;
+#pragma unroll
+    for (int pos = 0; pos < G::KPOS; pos++) {
+      const uint32_t code = bits_at<BITS * G::KG>(w, pos * BITS * G::KG);
+      const float *row = s_ktab + (qb * G::KPOS + pos) * G::KENT + code;
+#pragma unroll
+      for (int r = 0; r < NR; r++) part[r] += row[r * NQB * KROW];
+    }
+    const uint32_t sbits = (qb < 2 ? ksr.x : ksr.y) >> ((qb & 1) ? 16 : 0);
+    const float ks = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+#pragma unroll
+    for (int r = 0; r < NR; r++) score[r] = __builtin_fmaf(part[r], ks, score[r]);
+  }
+
+  // ---- wave-local softmax (base 2): m = max over the wave's tokens ----
+  float m_w[NR], p[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const float sc = valid ? score[r] : -INFINITY;
+    m_w[r] = wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
+    p[r] = valid ? __builtin_amdgcn_exp2f(sc - m_w[r]) : 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++) st_p[r * WT + lane] = p[r];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- V pass: lane = (token slice, qblock, group of EPL elements) ----
+  const int vgrp = lane % GPQ, vqb = (lane / GPQ) % NQB, vsl = lane / VLPT;
   int vlo, vhi, vsh;
   if constexpr (BITS == 3 && EPL == 16) {
     vlo = (48 * vgrp) >> 5; vhi = vlo + 1; vsh = (48 * vgrp) & 31;
@@ -324,174 +369,88 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int e = 0; e < EPL; e++) acc[r][e] = 0.f;
-  float m_run[NR], l_part[NR];
+#pragma unroll 4
+  for (int tk = 0; tk < VTS; tk++) {
+    const int tl = vsl + tk * VSL;
+    const uint32_t *rw = st_v + tl * RW + vqb * QW;
+    uint64_t bits64;
+    if constexpr (BITS == 3 && EPL == 16) {
+      bits64 = (((uint64_t)rw[vhi] << 32) | rw[vlo]) >> vsh;
+    } else if constexpr (BITS == 3) {
+      bits64 = __builtin_amdgcn_alignbit(rw[vhi], rw[vlo], vsh);
+    } else if constexpr (EPL == 16) {
+      bits64 = ((uint64_t)rw[vhi] << 32) | rw[vlo];
+    } else {
+      bits64 = rw[vlo];
+    }
+    const float vs = st_s[vqb * SPITCH + tl];
+    float wgt[NR];
 #pragma unroll
-  for (int r = 0; r < NR; r++) {
-    m_run[r] = -INFINITY;
-    l_part[r] = 0.f;
-  }
-  const float *ktab = s_tab + kq * G::KPOS * G::KENT * NR;
-
+    for (int r = 0; r < NR; r++) wgt[r] = st_p[r * WT + tl] * vs;
 #pragma unroll
-  for (int s = 0; s < NSUB; s++) {
-    if (s >= nsub) break;  // uniform: the tile ends here
-    const int set = s % NSET, buf = s & 1;
-    if (s + NSET - 1 < nsub) issue(s + NSET - 1, (s + NSET - 1) % NSET);
-
-    // ---- K pass on this sub-chunk: lane = (token, qblock) ----
-    {
-      float part[NR];
-#pragma unroll
-      for (int r = 0; r < NR; r++) part[r] = 0.f;
-#pragma unroll
-      for (int pos = 0; pos < G::KPOS; pos++) {
-        const uint32_t code = bits_at<BITS * G::KG>(kw[set], pos * BITS * G::KG);
-        const float *e = ktab + (pos * G::KENT + code) * NR;
-        if constexpr (NR == 2) {
-          const float2 v = *reinterpret_cast<const float2 *>(e);
-          part[0] += v.x;
-          part[1] += v.y;
-        } else if constexpr (NR == 4) {
-          const float4 v = *reinterpret_cast<const float4 *>(e);
-          part[0] += v.x;
-          part[1] += v.y;
-          part[2] += v.z;
-          part[3] += v.w;
-        } else {
-#pragma unroll
-          for (int r = 0; r < NR; r++) part[r] += e[r];
-        }
-      }
-      const float ks = fabsf(f16_to_f32((uint16_t)ksc[set]));
-      const bool valid = t0 + s * SUB + kt < len;
+    for (int pr = 0; pr < EPL / 2; pr++) {
+      const uint32_t code = (uint32_t)(bits64 >> (pr * 2 * BITS)) & (VCODES - 1);
+      const float cl = s_cbl[code], ch = s_cbh[code];
 #pragma unroll
       for (int r = 0; r < NR; r++) {
-        float sc = part[r] * ks;
-        sc += dpp_quad_xor1(sc);
-        sc += dpp_quad_xor2(sc);
-        if (kq == (r & (NQB - 1))) s_p[(buf * NR + r) * SUB + kt] = valid ? sc : -INFINITY;
-      }
-      // stage this sub-chunk's V qblock for the transposed V pass
-      uint32_t *dst = s_v + buf * VBUF + (kt * NQB + kq) * QW;
-      if constexpr (QW == 4) {
-        *reinterpret_cast<uint4 *>(dst) = make_uint4(vw[set][0], vw[set][1], vw[set][2], vw[set][3]);
-      } else {
-#pragma unroll
-        for (int w = 0; w < QW; w++) dst[w] = vw[set][w];
-      }
-      s_vs[buf * 2 * VSBUF + kt * NQB + kq] = (uint16_t)vsc[set];
-    }
-    __syncthreads();
-
-    // ---- running max over the sub-chunk (base-2 logits) ----
-    if (tid < NR * SUB) {
-      const float v = s_p[buf * NR * SUB + tid];
-      const float mx = wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
-      if (lane == 0) s_red[buf * NR * kWaves + wave] = mx;  // wave w covers head w / (SUB/64)
-    }
-    __syncthreads();
-    float alpha[NR];
-    bool grow = false;
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-      float mx = m_run[r];
-#pragma unroll
-      for (int w = 0; w < SUB / 64; w++) mx = fmaxf(mx, s_red[buf * NR * kWaves + r * (SUB / 64) + w]);
-      alpha[r] = (mx > m_run[r]) ? exp2f(m_run[r] - mx) : 1.f;  // 2^-inf = 0 on the first growth
-      grow |= mx > m_run[r];
-      m_run[r] = mx;
-    }
-    if (__builtin_amdgcn_readfirstlane((int)grow)) {  // uniform across the workgroup: scalar branch
-#pragma unroll
-      for (int r = 0; r < NR; r++) {
-        l_part[r] *= alpha[r];
-#pragma unroll
-        for (int e = 0; e < EPL; e++) acc[r][e] *= alpha[r];
-      }
-    }
-
-    // ---- V pass on this sub-chunk (pair codebook, rotated domain) ----
-#pragma unroll
-    for (int tk = 0; tk < VTS; tk++) {
-      const int tl = vsl + tk * VSL;
-      const uint32_t *rw = s_v + buf * VBUF + (tl * NQB + vqb) * QW;
-      uint64_t bits64;
-      if constexpr (BITS == 3 && EPL == 16) {
-        bits64 = (((uint64_t)rw[vhi] << 32) | rw[vlo]) >> vsh;
-      } else if constexpr (BITS == 3) {
-        bits64 = __builtin_amdgcn_alignbit(rw[vhi], rw[vlo], vsh);
-      } else if constexpr (EPL == 16) {
-        bits64 = ((uint64_t)rw[vhi] << 32) | rw[vlo];
-      } else {
-        bits64 = rw[vlo];
-      }
-      const float vs = fabsf(f16_to_f32(s_vs[buf * 2 * VSBUF + tl * NQB + vqb]));
-      const bool tv = t0 + s * SUB + tl < len;
-      float wgt[NR];
-#pragma unroll
-      for (int r = 0; r < NR; r++) {
-        const float p = tv ? exp2f(s_p[(buf * NR + r) * SUB + tl] - m_run[r]) : 0.f;
-        if (vqb == 0 && vgrp == 0) l_part[r] += p;
-        wgt[r] = p * vs;
-      }
-#pragma unroll
-      for (int pr = 0; pr < EPL / 2; pr++) {
-        const float2 cv = s_cb2[(uint32_t)(bits64 >> (pr * 2 * BITS)) & (VCODES - 1)];
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-          acc[r][2 * pr] = __builtin_fmaf(wgt[r], cv.x, acc[r][2 * pr]);
-          acc[r][2 * pr + 1] = __builtin_fmaf(wgt[r], cv.y, acc[r][2 * pr + 1]);
-        }
+        acc[r][2 * pr] = __builtin_fmaf(wgt[r], cl, acc[r][2 * pr]);
+        acc[r][2 * pr + 1] = __builtin_fmaf(wgt[r], ch, acc[r][2 * pr + 1]);
       }
     }
   }
+  // reduce over the wave's token slices (lane bits above the V lane id)
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) {
+      float v = acc[r][e];
+#pragma unroll
+      for (int o = VLPT; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+      acc[r][e] = v;
+    }
+  float l_w[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) l_w[r] = wave_reduce(p[r], [](float x, float y) { return x + y; });
 
-  // ---- reduce: V accumulators over the token slices, l over all lanes ----
-  float l_r[NR];
+  // ---- this wave's (m, l, acc) into its own staging area, then combine 16 waves ----
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
   {
-    float *s_lr = s_red + 2 * NR * kWaves;  // [NR][kWaves], distinct from the max buffers
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-      const float sm = wave_reduce(l_part[r], [](float x, float y) { return x + y; });
-      if (lane == 0) s_lr[r * kWaves + wave] = sm;
-    }
-#pragma unroll
-    for (int r = 0; r < NR; r++)
-#pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        float v = acc[r][e];
-#pragma unroll
-        for (int o = VLPT; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-        acc[r][e] = v;
-      }
-    __syncthreads();  // key table and scores no longer needed
+    float *comb = reinterpret_cast<float *>(stage);  // [HD][NR] acc, then m[NR], l[NR]
     if (lane < VLPT) {
 #pragma unroll
       for (int r = 0; r < NR; r++)
 #pragma unroll
-        for (int e = 0; e < EPL; e++) s_tab[(wave * HD + vqb * 32 + vgrp * EPL + e) * NR + r] = acc[r][e];
+        for (int e = 0; e < EPL; e++) comb[(vqb * 32 + vgrp * EPL + e) * NR + r] = acc[r][e];
     }
-    __syncthreads();
+    if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < NR; r++) {
-      float sm = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; w++) sm += s_lr[r * kWaves + w];
-      l_r[r] = sm;
+      for (int r = 0; r < NR; r++) {
+        comb[HD * NR + r] = m_w[r];
+        comb[HD * NR + NR + r] = l_w[r];
+      }
     }
   }
-
-  // ---- tile partials ----
+  __syncthreads();
   if (tid < NR * HD) {
     const int r = tid / HD, d = tid % HD;
-    float sum = 0.f;
+    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) sum += s_tab[(w * HD + d) * NR + r];
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds[OFF_W + w * WSTAGE + HD * NR + r]);
+    float A = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const float *cw = lds + OFF_W + w * WSTAGE;
+      const float mw = cw[HD * NR + r];
+      const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+      A = __builtin_fmaf(cw[d * NR + r], f, A);
+      L = __builtin_fmaf(cw[HD * NR + NR + r], f, L);
+    }
     const long long bh = (long long)b * a.num_heads + g * NR + r;
-    a.po[(bh * a.P + c) * HD + d] = sum;
+    a.po[(bh * a.P + c) * HD + d] = A;
     if (d == 0) {
-      a.pm[bh * a.P + c] = m_run[r];
-      a.ps[bh * a.P + c] = l_r[r];
+      a.pm[bh * a.P + c] = M;
+      a.ps[bh * a.P + c] = L;
     }
   }
 
