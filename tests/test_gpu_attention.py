@@ -95,6 +95,43 @@ def test_decode_repeated_calls_rearm_counters(tq):
         assert np.array_equal(o, outs[0])
 
 
+def test_decode_graph_replays_match_eager(tq):
+    """The decode captured in a HIP graph (as bench.py times it): every replay,
+    with eager work and synchronizations between replays, equals the eager
+    result bit for bit and the oracle to TOL."""
+    rng = np.random.default_rng(6)
+    t, hkv, h, bits = 4100, 8, 16, 3
+    cache = _make_cache(rng, hkv, t, bits)
+    kidx, ksc, vidx, vsc, kd, vd = cache
+    qn = bf16_round(rng.standard_normal((h, 128)).astype(np.float32) / np.float32(math.sqrt(128)))
+    ref = orc.attention_dense(qn, kd, vd, 1.0 / math.sqrt(128))
+    q = _dev(bf16_bits(qn)).view(torch.bfloat16).reshape(1, h, 128)
+    lens = torch.tensor([t], dtype=torch.int32, device="cuda")
+    ws = tq.AttentionWorkspace(1, h, hkv, 128, t)
+    out = torch.empty((1, h, 128), dtype=torch.float32, device="cuda")
+
+    def step():
+        tq.pqo_decode_attention(q, kidx, ksc, vidx, vsc, lens, hkv, bits, t, t, 0, 1.0 / math.sqrt(128), ws, out=out)
+
+    step()
+    torch.cuda.synchronize()
+    eager = out.cpu().numpy().reshape(h, 128).copy()
+    assert np.abs(eager - ref).max() <= TOL
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+        step()
+    for rep in range(4):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(h, 128)
+        assert np.array_equal(got, eager), rep
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().reshape(h, 128), eager), rep
+
+
 def test_decode_c3_full_size(tq):
     """BASELINE config 3 at full size: 16 q-heads / 8 KV heads, ctx 32,768, PQO3."""
     rng = np.random.default_rng(3)

@@ -32,6 +32,13 @@ using namespace tqd;
 
 constexpr float kInvSqrt32 = 0x1.6a09e6p-3f;
 constexpr float kLog2e = 1.44269504088896340736f;
+// fl(fl(1/fl(sqrt 32)) * fl(sqrt 32)): the magnitude of every decode sign
+// factor R_fwd[0][j] * sqrt(32) (wht_tensor.rs:28-41)
+constexpr float kDecodeFactor = 0x1.fffffep-1f;
+
+__device__ __forceinline__ float decode_sign(int j) {
+  return ((kPqoSignMask >> j) & 1u) ? -kDecodeFactor : kDecodeFactor;
+}
 constexpr int kThreads = 1024;
 constexpr int kChunk = 1024;
 constexpr int kWaves = kThreads / 64;
@@ -58,7 +65,6 @@ struct AttnArgs {
   void *out;
   int out_dtype;
   float cb[16];              // codebook
-  float sg[32];              // decode sign factor per element
 };
 
 template <int QT>
@@ -80,6 +86,69 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
   return v;
+}
+
+// DPP move: lanes whose source is outside the row (or whose row is masked
+// off) take `id`.  Controls: row_shr:n = 0x110 + n, row_ror:n = 0x120 + n,
+// row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp(float v, float id) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, id), __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xf, false));
+}
+
+// Whole-wave reduction on the VALU (no LDS traffic): a row scan with
+// row_shr 1/2/4/8 leaves each row's total in its lane 15, two row
+// broadcasts fold the rows into lane 63, which is read back as a uniform.
+template <typename Op>
+__device__ __forceinline__ float wave_allreduce(float v, float id, Op op) {
+  v = op(v, dpp<0x111>(v, id));
+  v = op(v, dpp<0x112>(v, id));
+  v = op(v, dpp<0x114>(v, id));
+  v = op(v, dpp<0x118>(v, id));
+  v = op(v, dpp<0x142, 0xa>(v, id));
+  v = op(v, dpp<0x143, 0xc>(v, id));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  return wave_allreduce(v, -INFINITY, [](float x, float y) { return fmaxf(x, y); });
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_allreduce(v, 0.f, [](float x, float y) { return x + y; });
+}
+
+// Sum of v over the lanes that differ only in lane bits 3..5 (the 8 lanes
+// l ^ {0, 8, ..., 56}); every lane receives its group's total.  xor 8 is a
+// DPP row rotate, xor 16 a swizzle inside each half-wave, xor 32 a permute.
+__device__ __forceinline__ float xor16(float v) {
+  // ds_swizzle bit mode: lane' = ((lane & 0x1f) | 0) ^ 0x10 within 32 lanes
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
+}
+__device__ __forceinline__ float sum_lane_bits_4_5(float v) {
+  v += xor16(v);
+  return v + __shfl_xor(v, 32, 64);
+}
+__device__ __forceinline__ float sum_lane_bits_3_5(float v) {
+  v += dpp<0x128>(v, 0.f);  // row_ror:8 == lane ^ 8 inside a row of 16
+  return sum_lane_bits_4_5(v);
+}
+
+// Device-coherent accesses to the split-K partials: relaxed atomics at agent
+// scope bypass the non-coherent per-XCD caches.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reads `W` bits starting at bit `pos` of little-endian words (pos and the
+// word indices must fold to constants after unrolling).
+template <int W>
+__device__ __forceinline__ uint32_t bits_at_p(const uint32_t *w, int pos) {
+  const int wi = pos >> 5, sh = pos & 31;
+  if (sh + W <= 32) return (w[wi] >> sh) & ((1u << W) - 1u);
+  return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & ((1u << W) - 1u);
 }
 
 // Reads `W` bits starting at bit `pos` of a little-endian word array.
@@ -132,13 +201,13 @@ __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, fl
 #pragma unroll
   for (int k = 0; k < MAXC; k++) {
     const int cc = part + k * PARTS;
-    pv[k] = cc < nchunks ? a.po[(bh * a.P + cc) * HD + d] : 0.f;
+    pv[k] = cc < nchunks ? ld_agent(&a.po[(bh * a.P + cc) * HD + d]) : 0.f;
   }
   for (int e = tid; e < NR * nchunks; e += kThreads) {
     const int rr = e / nchunks, cc = e % nchunks;
     const long long bh2 = (long long)b * a.num_heads + g * NR + rr;
-    s_w[e] = a.pm[bh2 * a.P + cc];
-    s_ls[e] = a.ps[bh2 * a.P + cc];
+    s_w[e] = ld_agent(&a.pm[bh2 * a.P + cc]);
+    s_ls[e] = ld_agent(&a.ps[bh2 * a.P + cc]);
   }
   __syncthreads();
   if (wave < NR) {  // wave rr reduces head rr
@@ -163,7 +232,7 @@ __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, fl
     if (cc < nchunks) acc = __builtin_fmaf(pv[k], s_w[r * nchunks + cc], acc);
   }
   for (int cc = part + MAXC * PARTS; cc < nchunks; cc += PARTS)  // long contexts only
-    acc = __builtin_fmaf(a.po[(bh * a.P + cc) * HD + d], s_w[r * nchunks + cc], acc);
+    acc = __builtin_fmaf(ld_agent(&a.po[(bh * a.P + cc) * HD + d]), s_w[r * nchunks + cc], acc);
   s_part[tid] = acc;
   __syncthreads();
   if (tid < OUTS) {
@@ -172,7 +241,7 @@ __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, fl
     for (int p = 0; p < PARTS; p++) A += s_part[p * OUTS + tid];
     // inverse rotation over the 32 lanes of this block (lane bits 0..4 = i)
     const int i = d & 31;
-    float v = A * a.sg[i];
+    float v = A * decode_sign(i);
 #pragma unroll
     for (int hh = 1; hh < 32; hh <<= 1) {
       float ov = __shfl_xor(v, hh, 64);
@@ -201,28 +270,31 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   constexpr int VSL = 64 / VLPT;                 // token slices per wave in the V pass
   constexpr int VTS = WT / VSL;                  // tokens per lane in the V pass
   constexpr int VCODES = 1 << (2 * BITS);        // pair-codebook entries
-  constexpr int KROW = G::KPOS * G::KENT;        // key-table entries per (head, qblock)
-  constexpr int KTAB = NR * NQB * KROW;          // one 4-byte entry per (head, qblock, position, code)
+  constexpr int KV = NR == 1 ? 1 : 2;            // heads per key-table entry (one 4- or 8-byte read)
+  constexpr int KNT = NR / KV;                   // key tables (entry reads per lookup)
+  constexpr int KROW = G::KPOS * G::KENT;        // key-table entries per qblock
+  constexpr int KTAB = NR * NQB * KROW;          // floats in all key tables
   constexpr int SPITCH = WT + 8;                 // V-scale rows: 4 qblock rows of 8 tokens on distinct banks
   constexpr int WSTAGE = WT * RW + NR * WT + NQB * SPITCH;  // per-wave staging: V records, p, |V scale|
   static_assert(kWaves * WT == CH, "one token per lane");
   static_assert(WSTAGE >= NR * HD + 2 * NR, "combine record fits the staging area");
   static_assert(KTAB * 4 <= 65536, "key-table offsets fit the ds_read immediate");
-  // LDS carve (32-bit words).  Tables use 4-byte entries in rows of 64 (or 16):
-  // a wave's 64 lookups into one row hit 64 distinct banks or share an address.
-  constexpr int OFF_CBL = KTAB;                         // pair codebook: value of the low element
-  constexpr int OFF_CBH = OFF_CBL + VCODES;             //                value of the high element
-  constexpr int OFF_Q = OFF_CBH + VCODES;
+  // LDS carve (32-bit words).  Key tables [KNT][qblock][position][code] hold
+  // KV heads per entry, so one lookup serves KV heads; the pair codebook holds
+  // (cb[lo], cb[hi]) per 2*BITS-bit code.
+  constexpr int OFF_CB2 = KTAB;
+  constexpr int OFF_CB1 = OFF_CB2 + 2 * VCODES;
+  constexpr int OFF_Q = OFF_CB1 + 16;
   constexpr int OFF_W = OFF_Q + NR * HD;
   constexpr int OFF_MISC = OFF_W;                       // merge scratch aliases the staging areas
   constexpr int TOTAL0 = OFF_W + kWaves * WSTAGE;
   constexpr int TOTAL = TOTAL0 > OFF_MISC + kMiscFloats ? TOTAL0 : OFF_MISC + kMiscFloats;
-  __shared__ float lds[TOTAL];
+  __shared__ __attribute__((aligned(16))) float lds[TOTAL];
   __shared__ int s_flag;
   float *s_ktab = lds;
-  float *s_cbl = lds + OFF_CBL;
-  float *s_cbh = lds + OFF_CBH;
+  float2 *s_cb2 = reinterpret_cast<float2 *>(lds + OFF_CB2);
   float *s_q = lds + OFF_Q;
+  float *s_cb1 = lds + OFF_CB1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -234,12 +306,20 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const long long rec0 = (long long)b * a.seq_stride + (long long)g * a.kv_head_stride;
   uint32_t *stage = reinterpret_cast<uint32_t *>(lds + OFF_W + wave * WSTAGE);
   uint32_t *st_v = stage;                                     // [WT][RW]
-  float *st_p = reinterpret_cast<float *>(stage + WT * RW);   // [NR][WT]: softmax numerators
+  float *st_p = reinterpret_cast<float *>(stage + WT * RW);   // [WT][NR]: softmax numerators
   float *st_s = st_p + NR * WT;                               // [NQB][SPITCH]: |V scale|
 
-  // ---- loads: query first (it feeds the table build), then this lane's token ----
-  float qv = 0.f;
-  if (tid < NR * HD) qv = load_q<QT>(a.q, ((long long)b * a.num_heads + g * NR) * HD + tid);
+  // ---- loads.  The query goes out alone, ahead of the code stream, so the
+  // table build is not queued behind it.  K records follow; V records are
+  // issued only after the tables are built, so device-wide the K bytes arrive
+  // first and the V transfer overlaps the K pass. ----
+  // (every lane loads, clamped, so the wait for q lands at its first use)
+  const float qv = load_q<QT>(a.q, ((long long)b * a.num_heads + g * NR) * HD + min(tid, NR * HD - 1));
+  if (tid == 0) {  // codebook into LDS straight from the scalar kernel arguments
+#pragma unroll
+    for (int k = 0; k < 16; k++) s_cb1[k] = a.cb[k];
+  }
+  __syncthreads();
   const int tok = t0 + wave * WT + lane;
   const bool valid = tok < len;
   const long long rec = rec0 + min(tok, len - 1);
@@ -247,19 +327,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   uint2 ksr, vsr;
   {
     const uint4 *kp = reinterpret_cast<const uint4 *>(a.k_idx + rec * PACKED);
-    const uint4 *vp = reinterpret_cast<const uint4 *>(a.v_idx + rec * PACKED);
 #pragma unroll
     for (int q = 0; q < RW / 4; q++) {
       const uint4 v = kp[q];
       kr[4 * q] = v.x; kr[4 * q + 1] = v.y; kr[4 * q + 2] = v.z; kr[4 * q + 3] = v.w;
     }
     ksr = *reinterpret_cast<const uint2 *>(a.k_sc + rec * NQB);
-#pragma unroll
-    for (int q = 0; q < RW / 4; q++) {
-      const uint4 v = vp[q];
-      vr[4 * q] = v.x; vr[4 * q + 1] = v.y; vr[4 * q + 2] = v.z; vr[4 * q + 3] = v.w;
-    }
-    vsr = *reinterpret_cast<const uint2 *>(a.v_sc + rec * NQB);
   }
 
   // ---- rotated, scaled queries (32-lane butterflies) and the LDS tables ----
@@ -273,31 +346,100 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
       float ov = __shfl_xor(v, hh, 64);
       v = (i & hh) ? (ov - v) : (v + ov);
     }
-    s_q[tid] = v * (a.sg[i] * qscale);
+    s_q[tid] = v * (decode_sign(i) * qscale);
   }
   if (tid < VCODES) {
     constexpr int NCm = G::NC - 1;
-    s_cbl[tid] = a.cb[tid & NCm];
-    s_cbh[tid] = a.cb[(tid >> BITS) & NCm];
+    s_cb2[tid] = make_float2(s_cb1[tid & NCm], s_cb1[(tid >> BITS) & NCm]);
   }
   __syncthreads();
-  for (int e = tid; e < NR * NQB * KROW; e += kThreads) {
-    // e = ((r * NQB + qb) * KPOS + pos) * KENT + code
-    const int code = e % G::KENT, rqp = e / G::KENT;
-    const int pos = rqp % G::KPOS, rq = rqp / G::KPOS;
-    const int qb = rq % NQB, r = rq / NQB;
-    float v;
-    if constexpr (G::KPAIR) {
-      const float *qt = s_q + r * HD + qb * 32 + 2 * pos;
-      v = qt[0] * a.cb[code & 7] + qt[1] * a.cb[code >> 3];
-    } else {
-      v = s_q[r * HD + qb * 32 + pos] * a.cb[code];
+  // Table entry (((t * NQB + qb) * KPOS + pos) * KENT + code) * KV + j holds,
+  // for head r = t * KV + j, qt[2 pos] * cb[code & 7] + qt[2 pos + 1] * cb[code >> 3]
+  // (3-bit pairs) or qt[pos] * cb[code] (4-bit).  Each work item fills four
+  // consecutive codes of one row for its KV heads (one contiguous run).
+  constexpr int ITEMS = KNT * NQB * G::KPOS * (G::KENT / 4);
+  for (int it = tid; it < ITEMS; it += kThreads) {
+    const int c4 = it % (G::KENT / 4), row = it / (G::KENT / 4);
+    const int pos = row % G::KPOS, rq = row / G::KPOS;
+    const int qb = rq % NQB, t = rq / NQB;
+    float ov[4 * KV];
+#pragma unroll
+    for (int j = 0; j < KV; j++) {
+      const int r = t * KV + j;
+      if constexpr (G::KPAIR) {
+        const float2 qt = *reinterpret_cast<const float2 *>(s_q + r * HD + qb * 32 + 2 * pos);
+        const float hi = qt.y * s_cb1[(4 * c4) >> 3];
+#pragma unroll
+        for (int k = 0; k < 4; k++) ov[k * KV + j] = qt.x * s_cb1[(4 * c4 + k) & 7] + hi;
+      } else {
+        const float qt = s_q[r * HD + qb * 32 + pos];
+#pragma unroll
+        for (int k = 0; k < 4; k++) ov[k * KV + j] = qt * s_cb1[4 * c4 + k];
+      }
     }
-    s_ktab[e] = v;
+    float *dst = s_ktab + (row * G::KENT + 4 * c4) * KV;
+#pragma unroll
+    for (int k = 0; k < KV; k++)
+      *reinterpret_cast<float4 *>(dst + 4 * k) = make_float4(ov[4 * k], ov[4 * k + 1], ov[4 * k + 2], ov[4 * k + 3]);
+  }
+  {
+    const uint4 *vp = reinterpret_cast<const uint4 *>(a.v_idx + rec * PACKED);
+#pragma unroll
+    for (int q = 0; q < RW / 4; q++) {
+      const uint4 v = vp[q];
+      vr[4 * q] = v.x; vr[4 * q + 1] = v.y; vr[4 * q + 2] = v.z; vr[4 * q + 3] = v.w;
+    }
+    vsr = *reinterpret_cast<const uint2 *>(a.v_sc + rec * NQB);
   }
   __syncthreads();
 
-  // ---- stage this wave's V records and scales (wave-private LDS; frees their VGPRs) ----
+  // ---- K pass: lane = token, all qblocks in-lane (fully unrolled; the
+  // scheduling barriers bound the LDS reads in flight to 16 positions) ----
+  float score[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) score[r] = 0.f;
+#pragma unroll
+  for (int qb = 0; qb < NQB; qb++) {
+    float part[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) part[r] = 0.f;
+    // groups of 16 positions: all table reads of a group are issued before
+    // any is consumed, then summed as a tree (short dependency chains)
+#pragma unroll
+    for (int p0 = 0; p0 < G::KPOS; p0 += 16) {
+      float ev[NR][16];
+#pragma unroll
+      for (int pos = p0; pos < p0 + 16; pos++) {
+        const uint32_t code = bits_at_p<BITS * G::KG>(kr + qb * QW, pos * BITS * G::KG);
+        const float *ent = s_ktab + ((qb * G::KPOS + pos) * G::KENT + code) * KV;
+        if constexpr (KV == 1) {
+          ev[0][pos - p0] = ent[0];
+        } else {
+#pragma unroll
+          for (int t = 0; t < KNT; t++) {
+            const float2 v = *reinterpret_cast<const float2 *>(ent + t * NQB * KROW * KV);
+            ev[2 * t][pos - p0] = v.x;
+            ev[2 * t + 1][pos - p0] = v.y;
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+#pragma unroll
+        for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+          for (int i = 0; i < w; i++) ev[r][i] += ev[r][i + w];
+        part[r] += ev[r][0];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint32_t sbits = (qb < 2 ? ksr.x : ksr.y) >> ((qb & 1) ? 16 : 0);
+    const float ks = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+#pragma unroll
+    for (int r = 0; r < NR; r++) score[r] = __builtin_fmaf(part[r], ks, score[r]);
+  }
+
+  // ---- stage this wave's V records and scales (wave-private LDS) ----
 #pragma unroll
   for (int q = 0; q < RW / 4; q++)
     *reinterpret_cast<uint4 *>(st_v + lane * RW + 4 * q) = make_uint4(vr[4 * q], vr[4 * q + 1], vr[4 * q + 2], vr[4 * q + 3]);
@@ -307,47 +449,21 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     st_s[qb * SPITCH + lane] = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
   }
 
-  // ---- K pass: lane = token, all qblocks in-lane ----
-  float score[NR];
-#pragma unroll
-  for (int r = 0; r < NR; r++) score[r] = 0.f;
-  constexpr int QBU = BITS == 3 ? (NR <= 2 ? NQB : 2) : 1;  // bound the LDS reads in flight
-#pragma unroll QBU
-  for (int qb = 0; qb < NQB; qb++) {
-    uint32_t w[QW];  // words of qblock qb, selected without dynamic register indexing
-#pragma unroll
-    for (int k = 0; k < QW; k++) {
-      uint32_t x = kr[k];
-#pragma unroll
-      for (int qq = 1; qq < NQB; qq++) x = (qb == qq) ? kr[qq * QW + k] : x;
-      w[k] = x;
-    }
-    float part[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) part[r] = 0.f;
-#pragma unroll
-    for (int pos = 0; pos < G::KPOS; pos++) {
-      const uint32_t code = bits_at<BITS * G::KG>(w, pos * BITS * G::KG);
-      const float *row = s_ktab + (qb * G::KPOS + pos) * G::KENT + code;
-#pragma unroll
-      for (int r = 0; r < NR; r++) part[r] += row[r * NQB * KROW];
-    }
-    const uint32_t sbits = (qb < 2 ? ksr.x : ksr.y) >> ((qb & 1) ? 16 : 0);
-    const float ks = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
-#pragma unroll
-    for (int r = 0; r < NR; r++) score[r] = __builtin_fmaf(part[r], ks, score[r]);
-  }
-
   // ---- wave-local softmax (base 2): m = max over the wave's tokens ----
   float m_w[NR], p[NR];
 #pragma unroll
   for (int r = 0; r < NR; r++) {
     const float sc = valid ? score[r] : -INFINITY;
-    m_w[r] = wave_reduce(sc, [](float x, float y) { return fmaxf(x, y); });
+    m_w[r] = wave_max(sc);
     p[r] = valid ? __builtin_amdgcn_exp2f(sc - m_w[r]) : 0.f;
   }
-#pragma unroll
-  for (int r = 0; r < NR; r++) st_p[r * WT + lane] = p[r];
+  if constexpr (NR == 1) {
+    st_p[lane] = p[0];
+  } else if constexpr (NR == 2) {
+    *reinterpret_cast<float2 *>(st_p + 2 * lane) = make_float2(p[0], p[1]);
+  } else {
+    *reinterpret_cast<float4 *>(st_p + 4 * lane) = make_float4(p[0], p[1], p[2], p[3]);
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -364,12 +480,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   } else {
     vlo = vgrp; vhi = vgrp; vsh = 0;
   }
+  constexpr int VU = 4;  // V-pass unroll
   float acc[NR][EPL];
 #pragma unroll
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int e = 0; e < EPL; e++) acc[r][e] = 0.f;
-#pragma unroll 4
+#pragma unroll VU
   for (int tk = 0; tk < VTS; tk++) {
     const int tl = vsl + tk * VSL;
     const uint32_t *rw = st_v + tl * RW + vqb * QW;
@@ -385,32 +502,36 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     }
     const float vs = st_s[vqb * SPITCH + tl];
     float wgt[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) wgt[r] = st_p[r * WT + tl] * vs;
+    if constexpr (NR == 1) {
+      wgt[0] = st_p[tl] * vs;
+    } else if constexpr (NR == 2) {
+      const float2 pp = *reinterpret_cast<const float2 *>(st_p + 2 * tl);
+      wgt[0] = pp.x * vs; wgt[1] = pp.y * vs;
+    } else {
+      const float4 pp = *reinterpret_cast<const float4 *>(st_p + 4 * tl);
+      wgt[0] = pp.x * vs; wgt[1] = pp.y * vs; wgt[2] = pp.z * vs; wgt[3] = pp.w * vs;
+    }
 #pragma unroll
     for (int pr = 0; pr < EPL / 2; pr++) {
       const uint32_t code = (uint32_t)(bits64 >> (pr * 2 * BITS)) & (VCODES - 1);
-      const float cl = s_cbl[code], ch = s_cbh[code];
+      const float2 cv = s_cb2[code];
 #pragma unroll
       for (int r = 0; r < NR; r++) {
-        acc[r][2 * pr] = __builtin_fmaf(wgt[r], cl, acc[r][2 * pr]);
-        acc[r][2 * pr + 1] = __builtin_fmaf(wgt[r], ch, acc[r][2 * pr + 1]);
+        acc[r][2 * pr] = __builtin_fmaf(wgt[r], cv.x, acc[r][2 * pr]);
+        acc[r][2 * pr + 1] = __builtin_fmaf(wgt[r], cv.y, acc[r][2 * pr + 1]);
       }
     }
   }
   // reduce over the wave's token slices (lane bits above the V lane id)
+  static_assert(VLPT == 8 || VLPT == 16, "token slices sit in lane bits 3..5 or 4..5");
 #pragma unroll
   for (int r = 0; r < NR; r++)
 #pragma unroll
-    for (int e = 0; e < EPL; e++) {
-      float v = acc[r][e];
-#pragma unroll
-      for (int o = VLPT; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-      acc[r][e] = v;
-    }
+    for (int e = 0; e < EPL; e++)
+      acc[r][e] = VLPT == 8 ? sum_lane_bits_3_5(acc[r][e]) : sum_lane_bits_4_5(acc[r][e]);
   float l_w[NR];
 #pragma unroll
-  for (int r = 0; r < NR; r++) l_w[r] = wave_reduce(p[r], [](float x, float y) { return x + y; });
+  for (int r = 0; r < NR; r++) l_w[r] = wave_sum(p[r]);
 
   // ---- this wave's (m, l, acc) into its own staging area, then combine 16 waves ----
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -447,26 +568,26 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
       L = __builtin_fmaf(cw[HD * NR + NR + r], f, L);
     }
     const long long bh = (long long)b * a.num_heads + g * NR + r;
-    a.po[(bh * a.P + c) * HD + d] = A;
+    st_agent(&a.po[(bh * a.P + c) * HD + d], A);
     if (d == 0) {
-      a.pm[bh * a.P + c] = M;
-      a.ps[bh * a.P + c] = L;
+      st_agent(&a.pm[bh * a.P + c], M);
+      st_agent(&a.ps[bh * a.P + c], L);
     }
   }
 
   if constexpr (INLINE_MERGE) {
-    // Every writing wave waits for its stores, then one wave publishes them
-    // device-wide with a single release fence before the arrival counter.
+    // The partials went out as agent-scope atomic stores, which are coherent
+    // at device scope by themselves (no L2 writeback/invalidate needed).
+    // Each wave waits until its stores have completed; after the barrier one
+    // lane counts the tile in.  The last tile's merge reads the partials with
+    // agent-scope atomic loads.
     __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
-    if (wave == 0) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      if (lane == 0) {
-        const int prev = __hip_atomic_fetch_add(&a.counters[b * a.num_kv_heads + g], 1, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-        s_flag = (prev == nchunks - 1);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (tid == 0) {
+      const int prev = __hip_atomic_fetch_add(&a.counters[b * a.num_kv_heads + g], 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      s_flag = (prev == nchunks - 1);
     }
     __syncthreads();
     if (s_flag) {
@@ -516,13 +637,6 @@ AttnArgs base_args(int bits) {
   AttnArgs a{};
   tqh::PqoCodebook cb = tqh::pqo_codebook(bits);
   for (int i = 0; i < cb.nc; i++) a.cb[i] = cb.c[i];
-  volatile float thirty_two = 32.0f;
-  volatile float sq = sqrtf(thirty_two);
-  volatile float inv = 1.0f / sq;
-  for (int j = 0; j < 32; j++) {
-    volatile float rf = pqo_neg(j) ? -inv : inv;
-    a.sg[j] = rf * sq;
-  }
   a.out_dtype = kF32;
   return a;
 }
