@@ -92,6 +92,18 @@ def time_steps(torch, fn, steps: int, warmup: int, graph: bool = False):
     return ev0.elapsed_time(ev1) / steps, wall
 
 
+def traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading
+    for a plain copy of known size); None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f).get("kernels", {}).get(kernel)
+    return None if rec is None else rec.get("hbm_bytes_per_launch")
+
+
 def cpu_baseline_c3():
     """Oracle (C restatement of the reference CPU path: polar_dequantize then
     dense softmax attention, single thread) on a bounded sample: one KV head
@@ -143,6 +155,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run one plain device copy of this many MiB (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -151,6 +166,15 @@ def main():
 
     import torch
     import turboquant_amd as tq
+
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 18  # float32 elements
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---- config 3: fused decode attention ----
     copies = max(1, math.ceil((1 << 30) / c3_bytes()) + 1)
@@ -217,13 +241,14 @@ def main():
                    "launch": "K steps captured in one HIP graph, timed replay",
                    "eager_ms_per_step": round(ms_eager, 6)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic("attn_decode_kernel")},
         "cpu_baseline": cpu,
         "quantize": {"metric": "PQO3 quantize Mvec/s at d=128 (C2, bf16 in, fused rotation)",
                      "value": round(mvec, 2), "unit": "Mvec/s", "ms_per_step": round(qms, 6),
                      "vectors_per_step": n_vec, "algorithmic_bytes_per_step": q_bytes,
                      "roofline": {"bound": "hbm", "achieved": round(q_gbs, 2), "peak": HBM_PEAK_GBS,
-                                  "unit": "GB/s", "frac": round(q_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                                  "unit": "GB/s", "frac": round(q_gbs / HBM_PEAK_GBS, 4),
+                                  "traffic": traffic("pqo_quant_kernel")},
                      "cpu_baseline": qcpu},
         "wall_s_timed": round(wall, 4),
     }

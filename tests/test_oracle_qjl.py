@@ -1,0 +1,153 @@
+"""Pins of the oracle's QJL estimator (reference src/qjl.rs).
+
+Independent checks:
+  * the sign hash is the SplitMix64 finalizer (Steele, Lea, Flood 2014): a
+    from-scratch Python SplitMix64 is itself pinned by the generator's
+    published first outputs for seed 0, then decides the parity of every
+    oracle Rademacher sign on a grid (qjl.rs:157-171);
+  * rows are +-fl(1/sqrt d) (qjl.rs:735-745), deterministic, rows differ,
+    and the matrix-free product equals the explicit row (qjl.rs:765-776);
+  * sign bits are (R r)_j >= 0, LSB-first (qjl.rs:233-256, 305-319);
+  * c = |r| sqrt(pi/2) / sqrt(d) (qjl.rs:863-879) and Algorithm 2's
+    estimate <y, x_mse> + c sum_j (S y)_j sign_j to 1e-5
+    (paper_verification_tests.rs:413-470);
+  * statistics: Theorem 2 unbiasedness over varying QJL seeds (bias < 0.03,
+    paper_verification_tests.rs:142-175), the d=64 pair bias (< 0.02,
+    inner_product_tests.rs:78-111) and the residual-norm identity.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+M64 = (1 << 64) - 1
+GOLDEN = 0x9E3779B97F4A7C15
+
+
+def splitmix64_finalize(z):
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+    return z ^ (z >> 31)
+
+
+def test_python_splitmix64_matches_published_outputs():
+    # splitmix64 seeded with 0: state advances by the golden gamma, then mixes
+    outs = [splitmix64_finalize((k * GOLDEN) & M64) for k in range(1, 5)]
+    assert outs == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+
+
+def test_rademacher_sign_is_splitmix_parity():
+    rng = np.random.default_rng(0)
+    for _ in range(400):
+        rs = int(rng.integers(0, 1 << 63)) * 2 + int(rng.integers(0, 2))
+        row, col = int(rng.integers(0, 512)), int(rng.integers(0, 512))
+        z = (rs + row * GOLDEN + col) & M64
+        want = 1.0 if splitmix64_finalize(z) % 2 == 0 else -1.0
+        assert orc.lib.tqo_rademacher_sign(rs, row, col) == want
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_rows_magnitude_determinism_and_product(dim):
+    mag = np.float32(1.0) / np.sqrt(np.float32(dim))
+    rows = np.stack([orc.rademacher_row(dim, 77, j) for j in range(dim)])
+    assert np.all(np.abs(rows) == mag)
+    assert np.array_equal(rows[5], orc.rademacher_row(dim, 77, 5))
+    assert not np.array_equal(rows[0], rows[1])
+    # a Rademacher matrix is close to orthogonal: R R^T ~ I
+    g = rows.astype(np.float64) @ rows.T.astype(np.float64)
+    assert np.abs(np.diag(g) - 1).max() < 1e-6 and np.abs(g - np.diag(np.diag(g))).max() < 0.5
+    x = orc.pseudo_random_vec(dim, 3)
+    for j in (0, 7, dim - 1):
+        p = orc.lib.tqo_rademacher_vector_product(x, dim, 77, j)
+        assert abs(p - float(rows[j].astype(np.float64) @ x)) < 1e-5
+
+
+def test_sign_bits_are_nonnegative_projection_lsb_first():
+    dim = 128
+    r = orc.pseudo_random_vec(dim, 9)
+    rows = np.stack([orc.rademacher_row(dim, 1234, j) for j in range(dim)]).astype(np.float64)
+    bits = (rows @ r >= 0).astype(np.uint8)
+    want = np.packbits(bits, bitorder="little")
+    assert np.array_equal(orc.compute_qjl_signs(r, 1234), want)
+    assert np.array_equal(orc.query_projections(r, 1234), np.array(
+        [orc.lib.tqo_rademacher_vector_product(r, dim, 1234, j) for j in range(dim)], np.float32))
+
+
+def test_scaling_constant():
+    for norm, dim in ((0.7, 64), (2.5, 128), (0.0, 128)):
+        want = np.float32(norm) * np.float32(math.sqrt(math.pi / 2)) / np.sqrt(np.float32(dim))
+        assert abs(orc.lib.tqo_qjl_scaling_constant(norm, dim) - want) < 1e-7
+
+
+def _unit(dim, seed):
+    v = orc.lcg_normal_vecs(seed, dim, 1)[0].astype(np.float64)
+    return (v / np.linalg.norm(v)).astype(np.float32)
+
+
+def test_algorithm2_formula():
+    dim, rot, qs = 128, 42, 42424
+    x, y = _unit(dim, 11111), _unit(dim, 22222)
+    packed, scales, signs, norms = orc.qjl_quantize_batch(3, dim, rot, qs, x.reshape(1, dim))
+    ry = orc.query_projections(y, qs)
+    est = orc.estimate_inner_product(2, dim, rot, y, ry, packed[0], scales[0], signs[0], norms[0])
+    x_mse = orc.dequantize_vec_batch(2, dim, rot, packed, scales)[0]
+    gamma = np.float16(norms.view(np.float16)[0]).astype(np.float32)
+    c = gamma * np.float32(math.sqrt(math.pi / 2)) / np.float32(math.sqrt(dim))
+    sg = np.unpackbits(signs[0], bitorder="little")[:dim].astype(np.float64) * 2 - 1
+    manual = float(y.astype(np.float64) @ x_mse) + float(c) * float(ry.astype(np.float64) @ sg)
+    assert abs(est - manual) < 1e-5
+
+
+def test_residual_norm_is_polar_error_norm():
+    dim = 128
+    x = orc.lcg_normal_vecs(5, dim, 50)
+    packed, scales, signs, norms = orc.qjl_quantize_batch(3, dim, 42, 7, x)
+    x_mse = orc.dequantize_vec_batch(2, dim, 42, packed, scales)
+    r = np.linalg.norm(x.astype(np.float64) - x_mse, axis=1)
+    assert np.allclose(norms.view(np.float16).astype(np.float64), r, rtol=2e-3)
+
+
+def test_theorem2_unbiased_over_projection_seeds():
+    dim, n = 128, 2000
+    bias = 0.0
+    for i in range(n):
+        x, y = _unit(dim, i * 31 + 1000), _unit(dim, i * 37 + 2000)
+        qs = 12345 + i
+        packed, scales, signs, norms = orc.qjl_quantize_batch(3, dim, 42, qs, x.reshape(1, dim))
+        ry = orc.query_projections(y, qs)
+        est = orc.estimate_inner_product(2, dim, 42, y, ry, packed[0], scales[0], signs[0], norms[0])
+        bias += est - float(x.astype(np.float64) @ y)
+    assert abs(bias / n) < 0.03
+
+
+def test_pair_bias_d64():
+    dim, n = 64, 3000
+    bias = 0.0
+    for i in range(n):
+        key = orc.pseudo_random_vec(dim, (i * 6364136223846793005 + 1000) & M64)
+        qry = orc.pseudo_random_vec(dim, (i * 6364136223846793005 + 2000) & M64)
+        qs = 777 + i
+        packed, scales, signs, norms = orc.qjl_quantize_batch(3, dim, 42, qs, key.reshape(1, dim))
+        est = orc.estimate_inner_product(2, dim, 42, qry, orc.query_projections(qry, qs), packed[0], scales[0],
+                                         signs[0], norms[0])
+        bias += est - float(key.astype(np.float64) @ qry)
+    assert abs(bias / n) < 0.02
+
+
+def test_scores_batch_and_weighted_values_match_single_calls():
+    dim, nk = 128, 40
+    keys = orc.lcg_normal_vecs(3, dim, nk)
+    qs = orc.lcg_normal_vecs(4, dim, 3)
+    packed, scales, signs, norms = orc.qjl_quantize_batch(3, dim, 42, 99, keys)
+    sc = orc.qjl_scores(2, dim, 42, 99, qs, packed, scales, signs, norms)
+    for a in range(3):
+        ry = orc.query_projections(qs[a], 99)
+        for b in (0, 17, nk - 1):
+            assert sc[a, b] == orc.estimate_inner_product(2, dim, 42, qs[a], ry, packed[b], scales[b], signs[b],
+                                                          norms[b])
+    w = np.linspace(0.1, 1.0, nk).astype(np.float32)
+    out = orc.weighted_values(2, dim, 42, packed, scales, w)
+    ref = (w.astype(np.float64)[:, None] * orc.dequantize_vec_batch(2, dim, 42, packed, scales)).sum(0)
+    assert np.abs(out - ref).max() < 1e-4
