@@ -38,4 +38,4 @@ def test_host_only_entry_points():
     # 1 x 16 heads x 32K: partials for 32 chunks of 1024 plus counters
     n = lib.tq_attention_workspace_size(1, 16, 8, 128, 32768)
     assert n >= 16 * 32 * 130 * 4
-    assert lib.tq_attention_workspace_size(1, 16, 8, 64, 32768) == 0  # head_dim 128 only
+    assert lib.tq_attention_workspace_size(0, 16, 8, 128, 32768) == 0  # invalid shape -> 0
