@@ -138,6 +138,32 @@ int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices
                             float softmax_scale, void *out, int out_dtype, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* =========================================================================
+ * Core full-vector codec (TurboQuantConfig{bits, dim, rotation_seed}),
+ * batched over vectors.  A PackedBlock maps to one row of packed_out
+ * (packed/mod.rs:149-233: LSB-first bits-wide indices, dim*bits/8 bytes) plus
+ * its f16 scale (the vector's L2 norm).  dim: 32, 64, 128 or 256 (the
+ * dimensions with codebook tables, codebook/tables.rs:89-105); bits 2..4.
+ * ========================================================================= */
+
+/* Replaces quantize_vec (quantize.rs:142-157) applied to each row of
+ * data[num_vectors][dim] f32.  packed_out [num_vectors][dim*bits/8],
+ * scales_out [num_vectors] f16 bits. */
+int tq_quantize_vec_batch(const float *data, uint8_t *packed_out, uint16_t *scales_out,
+                          size_t num_vectors, int bits, int dim, uint64_t rotation_seed,
+                          hipStream_t stream);
+
+/* Replaces dequantize_vec (quantize.rs:207-240) per row: centroid lookup,
+ * inverse rotation, times the f16 scale.  out [num_vectors][dim] f32. */
+int tq_dequantize_vec_batch(const uint8_t *packed, const uint16_t *scales, float *out,
+                            size_t num_vectors, int bits, int dim, uint64_t rotation_seed,
+                            hipStream_t stream);
+
+/* Replaces dequantize_rotated (quantize.rs:306-316): centroids times scale,
+ * left in the rotated domain. */
+int tq_dequantize_rotated_batch(const uint8_t *packed, const uint16_t *scales, float *out,
+                                size_t num_vectors, int bits, int dim, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

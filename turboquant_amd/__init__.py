@@ -17,6 +17,7 @@ from ._lib import (TQ_DTYPE_BF16, TQ_DTYPE_F16, TQ_DTYPE_F32, TurboQuantError, c
 __all__ = [
     "TurboQuantError", "lib", "pqo_quantize", "pqo_dequantize", "quant_maxnorm_batch", "dequant_batch",
     "pack_indices", "fused_attention", "AttentionWorkspace", "pqo_decode_attention", "pqo_codebook_values",
+    "quantize_vec_batch", "dequantize_vec_batch", "dequantize_rotated_batch",
 ]
 
 _DT = {torch.float32: TQ_DTYPE_F32, torch.bfloat16: TQ_DTYPE_BF16, torch.float16: TQ_DTYPE_F16}
@@ -154,6 +155,33 @@ def pqo_codebook_values(bits: int):
     else:
         raise ValueError("bits must be 3 or 4")
     return c, b, np.float32(c.max())
+
+
+def quantize_vec_batch(x: torch.Tensor, bits: int, rotation_seed: int = 0):
+    """Core codec quantize_vec over the rows of x [N, dim] f32 (dim 32..256).
+    Returns (packed u8 [N, dim*bits/8], scales int16 [N] holding f16 bits)."""
+    if x.dim() != 2 or x.dtype != torch.float32:
+        raise ValueError("x must be f32 [N, dim]")
+    n, d = x.shape
+    packed = torch.empty((n, d * bits // 8), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((n,), dtype=torch.int16, device=x.device)
+    check(lib.tq_quantize_vec_batch(_ptr(x), _ptr(packed), _ptr(scales), n, bits, d, rotation_seed, _stream()))
+    return packed, scales
+
+
+def dequantize_vec_batch(packed: torch.Tensor, scales: torch.Tensor, bits: int, dim: int, rotation_seed: int = 0):
+    n = scales.numel()
+    out = torch.empty((n, dim), dtype=torch.float32, device=packed.device)
+    check(lib.tq_dequantize_vec_batch(_ptr(packed), _ptr(scales), _ptr(out), n, bits, dim, rotation_seed,
+                                      _stream()))
+    return out
+
+
+def dequantize_rotated_batch(packed: torch.Tensor, scales: torch.Tensor, bits: int, dim: int):
+    n = scales.numel()
+    out = torch.empty((n, dim), dtype=torch.float32, device=packed.device)
+    check(lib.tq_dequantize_rotated_batch(_ptr(packed), _ptr(scales), _ptr(out), n, bits, dim, _stream()))
+    return out
 
 
 def default_softmax_scale(head_dim: int) -> float:
