@@ -164,6 +164,53 @@ int tq_dequantize_vec_batch(const uint8_t *packed, const uint16_t *scales, float
 int tq_dequantize_rotated_batch(const uint8_t *packed, const uint16_t *scales, float *out,
                                 size_t num_vectors, int bits, int dim, hipStream_t stream);
 
+/* =========================================================================
+ * QJL estimator (TurboQuant_prod): (total_bits-1)-bit polar codec plus a
+ * 1-bit sign sketch of the residual under the implicit hash-Rademacher
+ * matrix R (qjl.rs:143-208).  dim: 32, 64 or 128; total_bits 3 or 4.
+ * A QjlBlock maps to one row of polar_packed [dim*(total_bits-1)/8] u8, its
+ * polar f16 scale, one row of signs [dim/8] u8 (bit j of byte j/8 =
+ * (R r)_j >= 0) and the f16 residual norm (qjl.rs:111-134).
+ * ========================================================================= */
+
+/* Replaces quantize_with_qjl (qjl.rs:355-377) over the rows of
+ * data[num_vectors][dim] f32 (QuantizedKVCache::push_batch, attention.rs:274-301,
+ * uses one qjl_seed for the whole cache). */
+int tq_qjl_quantize_batch(const float *data, uint8_t *polar_packed, uint16_t *polar_scales,
+                          uint8_t *signs, uint16_t *residual_norms, size_t num_vectors,
+                          int total_bits, int dim, uint64_t rotation_seed, uint64_t qjl_seed,
+                          hipStream_t stream);
+
+/* EstimationContext for a batch of queries (qjl.rs:488-492, 561-572):
+ * ctx_out[q] = { qt[dim] = forward rotation of query q, rq[dim] =
+ * precompute_query_projections(q) }, f32 [num_queries][2*dim]. */
+int tq_qjl_query_context(const float *queries, float *ctx_out, size_t num_queries, int dim,
+                         uint64_t rotation_seed, uint64_t qjl_seed, hipStream_t stream);
+
+/* Replaces estimate_inner_product_with_codebook over all (query, key) pairs
+ * (qjl.rs:585-606; attention_scores, attention.rs:319-353):
+ * scores[q][k] = <q, x_mse_k> + |r_k| sqrt(pi/2)/sqrt(d) * sum_j rq_j (2 b_kj - 1). */
+int tq_qjl_scores(const float *ctx, size_t num_queries, const uint8_t *polar_packed,
+                  const uint16_t *polar_scales, const uint8_t *signs,
+                  const uint16_t *residual_norms, size_t num_keys, int polar_bits, int dim,
+                  uint64_t rotation_seed, float *scores, hipStream_t stream);
+
+/* Row softmax probs = exp(scale (s - max)) / sum over cols; no reference
+ * counterpart (attention_scores returns raw scores, attention.rs:344-352). */
+int tq_softmax_rows(const float *scores, float *probs, size_t rows, size_t cols, float scale,
+                    hipStream_t stream);
+
+/* Workspace bytes for tq_qjl_weighted_values. */
+size_t tq_qjl_weighted_values_workspace_size(size_t num_queries, size_t num_values, int dim);
+
+/* Replaces QuantizedKVCache::weighted_values (attention.rs:371-408) for a
+ * batch of weight rows: out[q] = sum_t weights[q][t] * dequantize(value_t),
+ * weights f32 [num_queries][num_values], out f32 [num_queries][dim]. */
+int tq_qjl_weighted_values(const uint8_t *polar_packed, const uint16_t *polar_scales,
+                           size_t num_values, const float *weights, size_t num_queries,
+                           int polar_bits, int dim, uint64_t rotation_seed, float *out,
+                           void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

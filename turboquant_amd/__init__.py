@@ -17,7 +17,8 @@ from ._lib import (TQ_DTYPE_BF16, TQ_DTYPE_F16, TQ_DTYPE_F32, TurboQuantError, c
 __all__ = [
     "TurboQuantError", "lib", "pqo_quantize", "pqo_dequantize", "quant_maxnorm_batch", "dequant_batch",
     "pack_indices", "fused_attention", "AttentionWorkspace", "pqo_decode_attention", "pqo_codebook_values",
-    "quantize_vec_batch", "dequantize_vec_batch", "dequantize_rotated_batch",
+    "quantize_vec_batch", "dequantize_vec_batch", "dequantize_rotated_batch", "qjl_quantize_batch",
+    "qjl_query_context", "qjl_scores", "softmax_rows", "qjl_weighted_values",
 ]
 
 _DT = {torch.float32: TQ_DTYPE_F32, torch.bfloat16: TQ_DTYPE_BF16, torch.float16: TQ_DTYPE_F16}
@@ -181,6 +182,57 @@ def dequantize_rotated_batch(packed: torch.Tensor, scales: torch.Tensor, bits: i
     n = scales.numel()
     out = torch.empty((n, dim), dtype=torch.float32, device=packed.device)
     check(lib.tq_dequantize_rotated_batch(_ptr(packed), _ptr(scales), _ptr(out), n, bits, dim, _stream()))
+    return out
+
+
+def qjl_quantize_batch(x: torch.Tensor, total_bits: int, rotation_seed: int, qjl_seed: int):
+    """quantize_with_qjl over the rows of x [N, dim] f32.  Returns (polar packed
+    u8 [N, dim*(total_bits-1)/8], polar scales int16 [N], signs u8 [N, dim/8],
+    residual norms int16 [N]); f16 values as raw bits."""
+    if x.dim() != 2 or x.dtype != torch.float32:
+        raise ValueError("x must be f32 [N, dim]")
+    n, d = x.shape
+    dev = x.device
+    polar = torch.empty((n, d * (total_bits - 1) // 8), dtype=torch.uint8, device=dev)
+    scales = torch.empty((n,), dtype=torch.int16, device=dev)
+    signs = torch.empty((n, d // 8), dtype=torch.uint8, device=dev)
+    norms = torch.empty((n,), dtype=torch.int16, device=dev)
+    check(lib.tq_qjl_quantize_batch(_ptr(x), _ptr(polar), _ptr(scales), _ptr(signs), _ptr(norms), n, total_bits, d,
+                                    rotation_seed, qjl_seed, _stream()))
+    return polar, scales, signs, norms
+
+
+def qjl_query_context(queries: torch.Tensor, rotation_seed: int, qjl_seed: int) -> torch.Tensor:
+    """[nq, 2*dim] f32: forward-rotated query, then its Rademacher projections."""
+    nq, d = queries.shape
+    ctx = torch.empty((nq, 2 * d), dtype=torch.float32, device=queries.device)
+    check(lib.tq_qjl_query_context(_ptr(queries), _ptr(ctx), nq, d, rotation_seed, qjl_seed, _stream()))
+    return ctx
+
+
+def qjl_scores(ctx: torch.Tensor, polar, scales, signs, norms, polar_bits: int, rotation_seed: int) -> torch.Tensor:
+    nq, d2 = ctx.shape
+    nk = scales.numel()
+    out = torch.empty((nq, nk), dtype=torch.float32, device=ctx.device)
+    check(lib.tq_qjl_scores(_ptr(ctx), nq, _ptr(polar), _ptr(scales), _ptr(signs), _ptr(norms), nk, polar_bits,
+                            d2 // 2, rotation_seed, _ptr(out), _stream()))
+    return out
+
+
+def softmax_rows(scores: torch.Tensor, scale: float) -> torch.Tensor:
+    rows, cols = scores.shape
+    out = torch.empty_like(scores)
+    check(lib.tq_softmax_rows(_ptr(scores), _ptr(out), rows, cols, float(scale), _stream()))
+    return out
+
+
+def qjl_weighted_values(polar, scales, weights: torch.Tensor, polar_bits: int, dim: int, rotation_seed: int):
+    nq, nv = weights.shape
+    out = torch.empty((nq, dim), dtype=torch.float32, device=weights.device)
+    nbytes = lib.tq_qjl_weighted_values_workspace_size(nq, nv, dim)
+    ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=weights.device)
+    check(lib.tq_qjl_weighted_values(_ptr(polar), _ptr(scales), nv, _ptr(weights), nq, polar_bits, dim, rotation_seed,
+                                     _ptr(out), _ptr(ws), nbytes, _stream()))
     return out
 
 

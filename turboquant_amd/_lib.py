@@ -47,6 +47,12 @@ SIGNATURES = {
     "tq_quantize_vec_batch": (_i, [_p, _p, _p, _sz, _i, _i, _u64, _p]),
     "tq_dequantize_vec_batch": (_i, [_p, _p, _p, _sz, _i, _i, _u64, _p]),
     "tq_dequantize_rotated_batch": (_i, [_p, _p, _p, _sz, _i, _i, _p]),
+    "tq_qjl_quantize_batch": (_i, [_p, _p, _p, _p, _p, _sz, _i, _i, _u64, _u64, _p]),
+    "tq_qjl_query_context": (_i, [_p, _p, _sz, _i, _u64, _u64, _p]),
+    "tq_qjl_scores": (_i, [_p, _sz, _p, _p, _p, _p, _sz, _i, _i, _u64, _p, _p]),
+    "tq_softmax_rows": (_i, [_p, _p, _sz, _sz, _f, _p]),
+    "tq_qjl_weighted_values_workspace_size": (_sz, [_sz, _sz, _i]),
+    "tq_qjl_weighted_values": (_i, [_p, _p, _sz, _p, _sz, _i, _i, _u64, _p, _p, _sz, _p]),
 }
 
 
