@@ -149,6 +149,91 @@ def cpu_baseline_quantize():
             "sample": "200,000 vectors d=128, oracle/tq_oracle.c pqo_quantize (rotation + MaxNorm + pack)"}
 
 
+def bench_c4(torch, tq, args):
+    """Config 4: PQO4 batched decode, 32 q-heads / 8 KV heads, d=128, batch 16,
+    contexts ~ U[4096, 16384] (seeded), bf16 queries, split-K; rotating >= 1 GiB
+    of cache copies.  Bytes per step = sum_b ctx_b * 8 * (64+8)*2."""
+    import numpy as np
+    rng = np.random.default_rng(4)
+    b, h, hkv, hd, bits, cap = 16, 32, 8, 128, 4, 16384
+    lens_np = rng.integers(4096, 16385, size=b).astype(np.int32)
+    step_bytes = int(lens_np.sum()) * hkv * 2 * (hd * bits // 8 + 8)
+    n = b * hkv * cap
+    gen = torch.Generator(device="cuda").manual_seed(44)
+    kv = []
+    for _ in range(2):
+        x = torch.randn((n, hd), generator=gen, device="cuda", dtype=torch.float32)
+        x[:, torch.tensor([3, 40, 77, 101], device="cuda")] *= 8.0
+        kv.extend(tq.pqo_quantize(x.to(torch.bfloat16), bits))
+        del x
+    cache_bytes = sum(t.numel() * t.element_size() for t in kv)
+    copies = max(1, math.ceil((1 << 30) / cache_bytes) + 1)
+    caches = [kv] + [[t.clone() for t in kv] for _ in range(copies - 1)]
+    q = (torch.randn((b, h, hd), generator=gen, device="cuda") / math.sqrt(hd)).to(torch.bfloat16)
+    lens = torch.from_numpy(lens_np).cuda()
+    ws = tq.AttentionWorkspace(b, h, hkv, hd, cap)
+    out = torch.empty((b, h, hd), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        kp, ks, vp, vs = caches[i % copies]
+        tq.pqo_decode_attention(q, kp, ks, vp, vs, lens, hkv, bits, cap, cap, hkv * cap, 1 / math.sqrt(hd), ws,
+                                out=out)
+
+    ms, _ = time_steps(torch, step, max(10, args.steps // 2), max(2, args.warmup // 2), graph=True)
+    del caches, kv
+    return {"metric": "PQO4 batched decode (C4) tokens/s per layer and GB/s",
+            "tokens_per_s_per_layer": round(b / (ms * 1e-3), 1), "ms_per_step": round(ms, 6),
+            "gbs": round(step_bytes / (ms * 1e-3) / 1e9, 2), "algorithmic_bytes_per_step": step_bytes,
+            "contexts": lens_np.tolist(), "copies": copies}
+
+
+def bench_c1(torch, tq, args):
+    """Config 1 on the GPU: 10,000 N(0,1) vectors (seed 42), d=128, TQ3 with
+    rotation seed 42: quantize_vec + dequantize_vec per step; nMSE of the
+    round trip (reference window [0.030, 0.038], mse_validation.rs:125-132)."""
+    gen = torch.Generator(device="cuda").manual_seed(42)
+    x = torch.randn((10_000, 128), generator=gen, device="cuda", dtype=torch.float32)
+    holder = {}
+
+    def step(i):
+        p, s = tq.quantize_vec_batch(x, 3, 42)
+        holder["y"] = tq.dequantize_vec_batch(p, s, 3, 128, 42)
+
+    ms, _ = time_steps(torch, step, max(10, args.steps // 2), max(2, args.warmup // 2))
+    y = holder["y"].double()
+    xd = x.double()
+    nmse = float((((xd - y) ** 2).sum(1) / (xd ** 2).sum(1)).mean())
+    return {"metric": "TQ3 codec round trip (C1), 10,000 x d=128", "ms_per_step": round(ms, 6),
+            "us_per_vector_roundtrip": round(ms * 1e3 / 10_000, 5), "nmse": round(nmse, 5),
+            "nmse_window": [0.030, 0.038]}
+
+
+def bench_c5(torch, tq, args):
+    """Config 5: TQ3 QJL (2-bit polar + 1-bit sketch, hash-Rademacher m = d =
+    128) on 8192 N(0,1) keys and 64 queries: sketch, query context, 524,288
+    estimates, softmax (scale 1/sqrt(128)) and weighted values."""
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    keys = torch.randn((8192, 128), generator=gen, device="cuda")
+    vals = torch.randn((8192, 128), generator=gen, device="cuda")
+    qs = torch.randn((64, 128), generator=gen, device="cuda")
+    times = {}
+    steps = max(5, args.steps // 10)
+    kb = tq.qjl_quantize_batch(keys, 3, 42, 4242)
+    vb = tq.qjl_quantize_batch(vals, 3, 42, 4242)
+    times["sketch_8192_keys_ms"], _ = time_steps(torch, lambda i: tq.qjl_quantize_batch(keys, 3, 42, 4242), steps, 1)
+    ctx = tq.qjl_query_context(qs, 42, 4242)
+    times["query_context_64_ms"], _ = time_steps(torch, lambda i: tq.qjl_query_context(qs, 42, 4242), steps, 1)
+    sc = tq.qjl_scores(ctx, *kb, 2, 42)
+    times["scores_64x8192_ms"], _ = time_steps(torch, lambda i: tq.qjl_scores(ctx, *kb, 2, 42), steps, 1)
+    pr = tq.softmax_rows(sc, 1 / math.sqrt(128))
+    times["softmax_ms"], _ = time_steps(torch, lambda i: tq.softmax_rows(sc, 1 / math.sqrt(128)), steps, 1)
+    times["weighted_values_ms"], _ = time_steps(
+        torch, lambda i: tq.qjl_weighted_values(vb[0], vb[1], pr, 2, 128, 42), steps, 1)
+    return {"metric": "TQ3 QJL estimator (C5) absolute times",
+            **{k: round(v, 6) for k, v in times.items()},
+            "estimates_per_s": round(64 * 8192 / (times["scores_64x8192_ms"] * 1e-3), 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,6 +301,11 @@ def main():
     q_gbs = q_bytes / (qms * 1e-3) / 1e9
     mvec = n_vec / (qms * 1e-3) / 1e6
 
+    del x, packed, scales
+    c4 = bench_c4(torch, tq, args)
+    c1 = bench_c1(torch, tq, args)
+    c5 = bench_c5(torch, tq, args)
+
     cpu = None
     qcpu = None
     if not args.no_cpu_baseline:
@@ -250,6 +340,9 @@ def main():
                                   "unit": "GB/s", "frac": round(q_gbs / HBM_PEAK_GBS, 4),
                                   "traffic": traffic("pqo_quant_kernel")},
                      "cpu_baseline": qcpu},
+        "c4_batched_decode": c4,
+        "c1_codec": c1,
+        "c5_qjl": c5,
         "wall_s_timed": round(wall, 4),
     }
     print(json.dumps(rec))
