@@ -112,6 +112,23 @@ int tq_pqo_quantize(const void *x, int x_dtype, uint8_t *packed_out, uint16_t *s
 int tq_pqo_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
                       size_t num_vectors, int head_dim, int bits, hipStream_t stream);
 
+/* PQO quantize of contiguous x [num_heads][tokens][head_dim] straight into
+ * cache records: vector (h, t) goes to record h * cache_head_stride +
+ * cache_offset + t of packed_cache / scales_cache.  Replaces
+ * quantize_kv_pair + CompressedStorage::append's slice_set
+ * (pqo.rs:64-100, storage.rs:145-172). */
+int tq_pqo_quantize_to_cache(const void *x, int x_dtype, int num_heads, int tokens,
+                             uint8_t *packed_cache, uint16_t *scales_cache,
+                             long long cache_head_stride, long long cache_offset, int head_dim,
+                             int bits, hipStream_t stream);
+
+/* Dequantize records [0, tokens) of every head of a cache into contiguous
+ * out [num_heads][tokens][head_dim].  Replaces dequantize_full_impl
+ * (common.rs:16-62). */
+int tq_pqo_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *scales_cache,
+                                 long long cache_head_stride, int num_heads, int tokens, void *out,
+                                 int out_dtype, int head_dim, int bits, hipStream_t stream);
+
 /* Workspace for tq_pqo_decode_attention (partials + merge counters). */
 size_t tq_attention_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
                                    int max_kv_len);
@@ -210,6 +227,44 @@ int tq_qjl_weighted_values(const uint8_t *polar_packed, const uint16_t *polar_sc
                            size_t num_values, const float *weights, size_t num_queries,
                            int polar_bits, int dim, uint64_t rotation_seed, float *out,
                            void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* =========================================================================
+ * Device-resident PQO KV cache: PqoCache with the CompressedKVCache contract
+ * (pqo.rs:21-236) over a CompressedStorage (storage.rs:24-203).  The handle
+ * owns its device buffers.  K/V inputs are one sequence's
+ * [num_kv_heads][tokens][head_dim] (the reference's [1, H, T, D]).
+ * ========================================================================= */
+
+/* PqoCache::new(CacheConfig{bits, head_dim, num_kv_heads, num_layers, PQO}). */
+int tq_pqo_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, void **cache);
+void tq_pqo_cache_destroy(void *cache);
+
+/* CompressedKVCache::prefill (pqo.rs:184-200): stores k, v; on the layer's
+ * first call sets *returned_originals = 1 (the caller's k, v are the result),
+ * otherwise writes the whole dequantized layer [num_kv_heads][seq_len][head_dim]
+ * into k_out, v_out in `dtype`. */
+int tq_pqo_cache_prefill(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,
+                         void *k_out, void *v_out, int *returned_originals, hipStream_t stream);
+
+/* CompressedKVCache::decode (pqo.rs:202-222) on the fused path: stores k, v,
+ * then out [num_q_heads][head_dim] = attention of q over the whole layer. */
+int tq_pqo_cache_decode(void *cache, int layer, const void *k, const void *v, int kv_dtype, int tokens,
+                        const void *q, int q_dtype, int num_q_heads, float softmax_scale, void *out,
+                        int out_dtype, hipStream_t stream);
+
+/* seq_len / reset / memory_usage (pqo.rs:224-236, storage.rs:175-202). */
+size_t tq_pqo_cache_seq_len(void *cache, int layer);
+int tq_pqo_cache_reset(void *cache);
+size_t tq_pqo_cache_memory_usage(void *cache);
+/* Records per head allocated for a layer (grows to needed + max(needed/4, 128)). */
+size_t tq_pqo_cache_capacity(void *cache, int layer);
+/* Copies a layer's stored records [num_kv_heads][seq_len] (codes and scales)
+ * into contiguous caller buffers. */
+int tq_pqo_cache_read_layer(void *cache, int layer, uint8_t *k_indices, uint16_t *k_scales,
+                            uint8_t *v_indices, uint16_t *v_scales, hipStream_t stream);
+/* Device views of a layer's buffers (CompressedStorage::k_indices etc.). */
+int tq_pqo_cache_buffers(void *cache, int layer, uint8_t **k_indices, uint16_t **k_scales,
+                         uint8_t **v_indices, uint16_t **v_scales);
 
 #ifdef __cplusplus
 }

@@ -13,12 +13,14 @@ import math
 import torch
 
 from ._lib import (TQ_DTYPE_BF16, TQ_DTYPE_F16, TQ_DTYPE_F32, TurboQuantError, check, lib)
+from .cache import AttendConfig, DequantResult, PqoCache
 
 __all__ = [
     "TurboQuantError", "lib", "pqo_quantize", "pqo_dequantize", "quant_maxnorm_batch", "dequant_batch",
     "pack_indices", "fused_attention", "AttentionWorkspace", "pqo_decode_attention", "pqo_codebook_values",
     "quantize_vec_batch", "dequantize_vec_batch", "dequantize_rotated_batch", "qjl_quantize_batch",
-    "qjl_query_context", "qjl_scores", "softmax_rows", "qjl_weighted_values",
+    "qjl_query_context", "qjl_scores", "softmax_rows", "qjl_weighted_values", "PqoCache", "AttendConfig",
+    "DequantResult",
 ]
 
 _DT = {torch.float32: TQ_DTYPE_F32, torch.bfloat16: TQ_DTYPE_BF16, torch.float16: TQ_DTYPE_F16}

@@ -53,6 +53,19 @@ SIGNATURES = {
     "tq_softmax_rows": (_i, [_p, _p, _sz, _sz, _f, _p]),
     "tq_qjl_weighted_values_workspace_size": (_sz, [_sz, _sz, _i]),
     "tq_qjl_weighted_values": (_i, [_p, _p, _sz, _p, _sz, _i, _i, _u64, _p, _p, _sz, _p]),
+    "tq_pqo_quantize_to_cache": (_i, [_p, _i, _i, _i, _p, _p, _ll, _ll, _i, _i, _p]),
+    "tq_pqo_dequantize_from_cache": (_i, [_p, _p, _ll, _i, _i, _p, _i, _i, _i, _p]),
+    "tq_pqo_cache_create": (_i, [_i, _i, _i, _i, C.POINTER(C.c_void_p)]),
+    "tq_pqo_cache_destroy": (None, [_p]),
+    "tq_pqo_cache_prefill": (_i, [_p, _i, _p, _p, _i, _i, _p, _p, C.POINTER(C.c_int), _p]),
+    "tq_pqo_cache_decode": (_i, [_p, _i, _p, _p, _i, _i, _p, _i, _i, _f, _p, _i, _p]),
+    "tq_pqo_cache_seq_len": (_sz, [_p, _i]),
+    "tq_pqo_cache_reset": (_i, [_p]),
+    "tq_pqo_cache_memory_usage": (_sz, [_p]),
+    "tq_pqo_cache_capacity": (_sz, [_p, _i]),
+    "tq_pqo_cache_read_layer": (_i, [_p, _i, _p, _p, _p, _p, _p]),
+    "tq_pqo_cache_buffers": (_i, [_p, _i, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
+                                  C.POINTER(C.c_void_p)]),
 }
 
 

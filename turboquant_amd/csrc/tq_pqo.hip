@@ -128,15 +128,33 @@ __device__ __forceinline__ void store_packed(uint8_t *__restrict__ packed, long 
   }
 }
 
+// Placement of contiguous [heads][tokens] vectors in a cache laid out
+// [heads][head_stride] records (CompressedStorage, storage.rs:24-139):
+// vector (h, t) <-> record h * head_stride + offset + t.
+struct CacheMap {
+  uint32_t qb_per_vec;  // head_dim / 32
+  uint32_t tokens;
+  long long head_stride;
+  long long offset;
+};
+
+__device__ __forceinline__ long long cache_block(uint32_t blk, const CacheMap &m) {
+  const uint32_t v = blk / m.qb_per_vec, j = blk - v * m.qb_per_vec;
+  const uint32_t h = v / m.tokens, t = v - h * m.tokens;
+  return ((long long)h * m.head_stride + m.offset + t) * m.qb_per_vec + j;
+}
+
 // ROTATE: input is raw activations (fused forward rotation, butterfly order).
 // Otherwise input is already rotated f32 (the reference kernel's contract).
-template <int BITS, int IN_DT, bool ROTATE>
+// MAP: outputs go to cache records (CacheMap) instead of block order.
+template <int BITS, int IN_DT, bool ROTATE, bool MAP = false>
 __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__ x,
                                                         uint8_t *__restrict__ packed,
                                                         uint16_t *__restrict__ scales,
-                                                        long long nblocks, QuantConsts k) {
+                                                        long long nblocks, QuantConsts k, CacheMap map = {}) {
   const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
   if (blk >= nblocks) return;
+  const long long ob = MAP ? cache_block((uint32_t)blk, map) : blk;
   float r[32];
   load_block<IN_DT>(x, blk, r);
   if constexpr (ROTATE) {
@@ -146,8 +164,8 @@ __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__
   }
   uint32_t w[Packed<BITS>::kWords];
   float s = quantize_block<BITS>(r, k, w);
-  store_packed<BITS>(packed, blk, w);
-  scales[blk] = f32_to_f16(s * k.scale_sign);
+  store_packed<BITS>(packed, ob, w);
+  scales[ob] = f32_to_f16(s * k.scale_sign);
 }
 
 // Reference-ABI variant: boundaries and outer centroid come from the caller
@@ -189,21 +207,23 @@ struct DequantConsts {
 // out_j = fl(fl(W_j * fl(1/sqrt(32))) * |scale|), W = butterfly(cb[idx] * sign):
 // butterfly_wht_inverse_cpu (wht_tensor.rs:38-64) then the broadcast_mul by
 // |scale| (quantize_tensor.rs:203, 217-218).
-template <int BITS, int OUT_DT, bool DEV_CONSTS>
+// MAP: inputs come from cache records (CacheMap); outputs in block order.
+template <int BITS, int OUT_DT, bool DEV_CONSTS, bool MAP = false>
 __global__ __launch_bounds__(256) void pqo_dequant_kernel(const uint8_t *__restrict__ packed,
                                                           const uint16_t *__restrict__ scales,
                                                           void *__restrict__ out, long long nblocks,
                                                           DequantConsts dc,
                                                           const float *__restrict__ dev_cb,
-                                                          const float *__restrict__ dev_sg) {
+                                                          const float *__restrict__ dev_sg, CacheMap map = {}) {
   __shared__ float lut[16];
   constexpr int NC = 1 << BITS;
   if (threadIdx.x < NC) lut[threadIdx.x] = DEV_CONSTS ? dev_cb[threadIdx.x] : dc.cb[threadIdx.x];
   __syncthreads();
   const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
   if (blk >= nblocks) return;
+  const long long ib = MAP ? cache_block((uint32_t)blk, map) : blk;
   uint32_t w[Packed<BITS>::kWords];
-  const uint32_t *p = reinterpret_cast<const uint32_t *>(packed + blk * Packed<BITS>::kBytes);
+  const uint32_t *p = reinterpret_cast<const uint32_t *>(packed + ib * Packed<BITS>::kBytes);
   if constexpr (BITS == 4) {
     uint4 v = *reinterpret_cast<const uint4 *>(p);
     w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
@@ -214,7 +234,7 @@ __global__ __launch_bounds__(256) void pqo_dequant_kernel(const uint8_t *__restr
 #pragma unroll
     for (int q = 0; q < 3; q++) w[q] = p[q];
   }
-  const float s = fabsf(f16_to_f32(scales[blk]));
+  const float s = fabsf(f16_to_f32(scales[ib]));
   float z[32];
 #pragma unroll
   for (int j = 0; j < 32; j++) {
@@ -424,4 +444,82 @@ extern "C" int tq_pack_indices(const uint8_t *indices, uint8_t *packed_out, int 
   hipLaunchKernelGGL(pack_indices_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, indices,
                      packed_out, (long long)num_vectors, block_size, bits, bytes_per_block);
   return tqh::check_launch("pack_indices_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Cache placement (CompressedStorage append / full dequantize)
+// ---------------------------------------------------------------------------
+
+namespace {
+int cache_map(int num_heads, int tokens, int head_dim, long long head_stride, long long offset, CacheMap &m) {
+  if (num_heads < 0 || tokens < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "negative shape");
+  if (head_dim <= 0 || head_dim % 32 != 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "head_dim (%d) must be divisible by QUANT_BLOCK_SIZE (32)", head_dim);
+  if (offset < 0 || head_stride < offset + tokens)
+    return tqh::fail(TQ_ERR_RANGE_OUT_OF_BOUNDS, "cache rows [%lld, %lld) exceed head stride %lld", offset,
+                     offset + tokens, head_stride);
+  if ((long long)num_heads * tokens * (head_dim / 32) >= (1ll << 31))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "too many blocks in one call");
+  m.qb_per_vec = (uint32_t)(head_dim / 32);
+  m.tokens = (uint32_t)(tokens > 0 ? tokens : 1);
+  m.head_stride = head_stride;
+  m.offset = offset;
+  return TQ_OK;
+}
+}  // namespace
+
+extern "C" int tq_pqo_quantize_to_cache(const void *x, int x_dtype, int num_heads, int tokens, uint8_t *packed_cache,
+                                        uint16_t *scales_cache, long long cache_head_stride, long long cache_offset,
+                                        int head_dim, int bits, hipStream_t stream) {
+  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+  if (!tqh::valid_dtype(x_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", x_dtype);
+  CacheMap m;
+  int rc = cache_map(num_heads, tokens, head_dim, cache_head_stride, cache_offset, m);
+  if (rc) return rc;
+  const long long nblocks = (long long)num_heads * tokens * (head_dim / 32);
+  if (nblocks == 0) return TQ_OK;
+  if (!x || !packed_cache || !scales_cache) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const QuantConsts k = make_quant_consts(tqh::pqo_codebook(bits), -1.0f);
+  const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
+#define QM(B, D) hipLaunchKernelGGL((pqo_quant_kernel<B, D, true, true>), grid, block, 0, stream, x, packed_cache, \
+                                    scales_cache, nblocks, k, m)
+  if (bits == 3) {
+    if (x_dtype == kF32) QM(3, kF32);
+    else if (x_dtype == kBF16) QM(3, kBF16);
+    else QM(3, kF16);
+  } else {
+    if (x_dtype == kF32) QM(4, kF32);
+    else if (x_dtype == kBF16) QM(4, kBF16);
+    else QM(4, kF16);
+  }
+#undef QM
+  return tqh::check_launch("pqo_quant_kernel (cache)");
+}
+
+extern "C" int tq_pqo_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *scales_cache,
+                                            long long cache_head_stride, int num_heads, int tokens, void *out,
+                                            int out_dtype, int head_dim, int bits, hipStream_t stream) {
+  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+  if (!tqh::valid_dtype(out_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", out_dtype);
+  CacheMap m;
+  int rc = cache_map(num_heads, tokens, head_dim, cache_head_stride, 0, m);
+  if (rc) return rc;
+  const long long nblocks = (long long)num_heads * tokens * (head_dim / 32);
+  if (nblocks == 0) return TQ_OK;
+  if (!packed_cache || !scales_cache || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const DequantConsts dc = make_dequant_consts(tqh::pqo_codebook(bits));
+  const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
+#define DM(B, D) hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false, true>), grid, block, 0, stream, packed_cache, \
+                                    scales_cache, out, nblocks, dc, nullptr, nullptr, m)
+  if (bits == 3) {
+    if (out_dtype == kF32) DM(3, kF32);
+    else if (out_dtype == kBF16) DM(3, kBF16);
+    else DM(3, kF16);
+  } else {
+    if (out_dtype == kF32) DM(4, kF32);
+    else if (out_dtype == kBF16) DM(4, kBF16);
+    else DM(4, kF16);
+  }
+#undef DM
+  return tqh::check_launch("pqo_dequant_kernel (cache)");
 }
