@@ -68,6 +68,34 @@ __device__ __forceinline__ void load_block(const void *__restrict__ x, long long
   }
 }
 
+// #{t : U[t] <= x} for the 2^BITS - 1 ascending thresholds U: a binary search
+// whose probe at each level is picked from the candidates by the decisions
+// already made (a select tree), BITS compares per element instead of
+// 2^BITS - 1.
+template <int BITS>
+__device__ __forceinline__ uint32_t bucket_sorted(float x, const float (&U)[(1 << BITS) - 1]) {
+  if constexpr (BITS == 2) {
+    const bool b1 = x >= U[1];
+    const bool b0 = x >= (b1 ? U[2] : U[0]);
+    return (b1 ? 2u : 0u) | (b0 ? 1u : 0u);
+  } else if constexpr (BITS == 3) {
+    const bool b2 = x >= U[3];
+    const bool b1 = x >= (b2 ? U[5] : U[1]);
+    const float lo = b1 ? U[2] : U[0], hi = b1 ? U[6] : U[4];
+    const bool b0 = x >= (b2 ? hi : lo);
+    return (b2 ? 4u : 0u) | (b1 ? 2u : 0u) | (b0 ? 1u : 0u);
+  } else {
+    const bool b3 = x >= U[7];
+    const bool b2 = x >= (b3 ? U[11] : U[3]);
+    const float l1 = b2 ? U[5] : U[1], h1 = b2 ? U[13] : U[9];
+    const bool b1 = x >= (b3 ? h1 : l1);
+    const float a0 = b1 ? U[2] : U[0], a1 = b1 ? U[6] : U[4], a2 = b1 ? U[10] : U[8], a3 = b1 ? U[14] : U[12];
+    const float l0 = b2 ? a1 : a0, h0 = b2 ? a3 : a2;
+    const bool b0 = x >= (b3 ? h0 : l0);
+    return (b3 ? 8u : 0u) | (b2 ? 4u : 0u) | (b1 ? 2u : 0u) | (b0 ? 1u : 0u);
+  }
+}
+
 // MaxNorm scale, exact bucketize and pack of one rotated block.
 template <int BITS>
 __device__ __forceinline__ float quantize_block(const float (&r)[32], const QuantConsts &k,
@@ -85,12 +113,7 @@ __device__ __forceinline__ float quantize_block(const float (&r)[32], const Quan
 #pragma unroll
     for (int t = 0; t < NB; t++) U[t] = div_threshold(k.mu[t], (k.strict_mask >> t) & 1u, s);
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-      uint32_t c = 0;
-#pragma unroll
-      for (int t = 0; t < NB; t++) c += (r[j] >= U[t]) ? 1u : 0u;
-      idx[j] = c;
-    }
+    for (int j = 0; j < 32; j++) idx[j] = bucket_sorted<BITS>(r[j], U);
   } else {
     // Infinite scale (an infinite input): follow the reference's division.
 #pragma unroll
