@@ -42,6 +42,14 @@ __device__ __forceinline__ float decode_sign(int j) {
 constexpr int kThreads = 1024;
 constexpr int kChunk = 1024;
 constexpr int kWaves = kThreads / 64;
+// One split-K counter per (sequence, KV head), each on its own 256-byte line
+// so the tiles' arrivals at different counters do not queue on one line.
+constexpr int kCounterStride = 64;  // ints
+#ifndef TQ_ATTN_LOAD_GROUPS
+#define TQ_ATTN_LOAD_GROUPS 4
+#endif
+constexpr int kLoadGroups = TQ_ATTN_LOAD_GROUPS;  // staggered K/V fetch groups per tile
+static_assert(kWaves % kLoadGroups == 0, "load groups split the waves evenly");
 
 struct AttnArgs {
   const void *q;
@@ -60,7 +68,7 @@ struct AttnArgs {
   float *po;                 // partial acc  [(b*H + h) * P + c][head_dim]
   float *pm;                 // partial max  [(b*H + h) * P + c]   (base-2 logits)
   float *ps;                 // partial sum  [(b*H + h) * P + c]
-  int *counters;             // [b * Hkv + g], zero between launches
+  int *counters;             // [(b * Hkv + g) * kCounterStride], zero between launches
   int P;                     // chunk stride per (b, h) in the partial arrays
   void *out;
   int out_dtype;
@@ -291,6 +299,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   constexpr int TOTAL = TOTAL0 > OFF_MISC + kMiscFloats ? TOTAL0 : OFF_MISC + kMiscFloats;
   __shared__ __attribute__((aligned(16))) float lds[TOTAL];
   __shared__ int s_flag;
+  __shared__ int s_ready;  // waves whose K/V records have arrived (staggered loads)
   float *s_ktab = lds;
   float2 *s_cb2 = reinterpret_cast<float2 *>(lds + OFF_CB2);
   float *s_q = lds + OFF_Q;
@@ -310,14 +319,20 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   float *st_s = st_p + NR * WT;                               // [NQB][SPITCH]: |V scale|
 
   // ---- loads.  The query goes out alone, ahead of the code stream, so the
-  // table build is not queued behind it.  K records follow; V records are
-  // issued only after the tables are built, so device-wide the K bytes arrive
-  // first and the V transfer overlaps the K pass. ----
+  // table build is not queued behind it.  The tile's waves then fetch their
+  // K/V records in NGRP staggered groups: group g issues only once the
+  // records of group g - 1 have arrived, so device-wide the early groups'
+  // bytes come back first and their K/V passes overlap the later transfers
+  // (all groups issuing at once would make every wave wait for the whole
+  // tile). ----
+  constexpr int GW = kWaves / kLoadGroups;  // waves per load group
+  const int grp = wave / GW;
   // (every lane loads, clamped, so the wait for q lands at its first use)
   const float qv = load_q<QT>(a.q, ((long long)b * a.num_heads + g * NR) * HD + min(tid, NR * HD - 1));
   if (tid == 0) {  // codebook into LDS straight from the scalar kernel arguments
 #pragma unroll
     for (int k = 0; k < 16; k++) s_cb1[k] = a.cb[k];
+    s_ready = 0;
   }
   __syncthreads();
   const int tok = t0 + wave * WT + lane;
@@ -325,15 +340,27 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const long long rec = rec0 + min(tok, len - 1);
   uint32_t kr[RW], vr[RW];
   uint2 ksr, vsr;
-  {
-    const uint4 *kp = reinterpret_cast<const uint4 *>(a.k_idx + rec * PACKED);
+  auto issue_loads = [&](long long r) {
+    const uint4 *kp = reinterpret_cast<const uint4 *>(a.k_idx + r * PACKED);
+    const uint4 *vp = reinterpret_cast<const uint4 *>(a.v_idx + r * PACKED);
 #pragma unroll
     for (int q = 0; q < RW / 4; q++) {
       const uint4 v = kp[q];
       kr[4 * q] = v.x; kr[4 * q + 1] = v.y; kr[4 * q + 2] = v.z; kr[4 * q + 3] = v.w;
     }
-    ksr = *reinterpret_cast<const uint2 *>(a.k_sc + rec * NQB);
-  }
+    ksr = *reinterpret_cast<const uint2 *>(a.k_sc + r * NQB);
+#pragma unroll
+    for (int q = 0; q < RW / 4; q++) {
+      const uint4 v = vp[q];
+      vr[4 * q] = v.x; vr[4 * q + 1] = v.y; vr[4 * q + 2] = v.z; vr[4 * q + 3] = v.w;
+    }
+    vsr = *reinterpret_cast<const uint2 *>(a.v_sc + r * NQB);
+  };
+  // Every wave issues the same load sequence here (later groups fetch the
+  // tile's first record, one cache line per instruction, as a placeholder),
+  // so the number of loads in flight does not depend on the group and the
+  // wait for the query below counts only the query.
+  issue_loads(grp == 0 ? rec : rec0 + t0);
 
   // ---- rotated, scaled queries (32-lane butterflies) and the LDS tables ----
   const float qscale = a.softmax_scale * kLog2e * kInvSqrt32;
@@ -382,16 +409,22 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     for (int k = 0; k < KV; k++)
       *reinterpret_cast<float4 *>(dst + 4 * k) = make_float4(ov[4 * k], ov[4 * k + 1], ov[4 * k + 2], ov[4 * k + 3]);
   }
-  {
-    const uint4 *vp = reinterpret_cast<const uint4 *>(a.v_idx + rec * PACKED);
-#pragma unroll
-    for (int q = 0; q < RW / 4; q++) {
-      const uint4 v = vp[q];
-      vr[4 * q] = v.x; vr[4 * q + 1] = v.y; vr[4 * q + 2] = v.z; vr[4 * q + 3] = v.w;
-    }
-    vsr = *reinterpret_cast<const uint2 *>(a.v_sc + rec * NQB);
-  }
   __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);  // keep the record-dependent code below the table build
+  if (grp > 0) {
+    // wait (acquire: the loads below cannot move above it) until every wave
+    // of the previous group has its records, then fetch ours
+    if (lane == 0)
+      while (__hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < grp * GW)
+        __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    issue_loads(rec);
+  }
+  if constexpr (kLoadGroups > 1) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's records are in registers
+    if (lane == 0) __hip_atomic_fetch_add(&s_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
 
   // ---- K pass: lane = token, all qblocks in-lane (fully unrolled; the
   // scheduling barriers bound the LDS reads in flight to 16 positions) ----
@@ -585,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     if (tid == 0) {
-      const int prev = __hip_atomic_fetch_add(&a.counters[b * a.num_kv_heads + g], 1, __ATOMIC_RELAXED,
+      const int prev = __hip_atomic_fetch_add(&a.counters[(b * a.num_kv_heads + g) * kCounterStride], 1, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
       s_flag = (prev == nchunks - 1);
     }
@@ -593,7 +626,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     if (s_flag) {
       merge_and_store<NR>(a, b, g, nchunks, lds + OFF_MISC);
       if (tid == 0)
-        __hip_atomic_store(&a.counters[b * a.num_kv_heads + g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&a.counters[(b * a.num_kv_heads + g) * kCounterStride], 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -629,7 +663,7 @@ WsLayout ws_layout(int batch, int num_heads, int num_kv_heads, int head_dim, int
   w.pm = al(w.po + bhp * head_dim * sizeof(float));
   w.ps = al(w.pm + bhp * sizeof(float));
   w.cnt = al(w.ps + bhp * sizeof(float));
-  w.total = al(w.cnt + (size_t)batch * num_kv_heads * sizeof(int));
+  w.total = al(w.cnt + (size_t)batch * num_kv_heads * kCounterStride * sizeof(int));
   return w;
 }
 
@@ -689,7 +723,7 @@ extern "C" int tq_attention_workspace_init(void *workspace, size_t workspace_byt
   const WsLayout w = ws_layout(batch, num_heads, num_kv_heads, head_dim, max_kv_len);
   if (!workspace || workspace_bytes < w.total)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
-  const long long n = (long long)batch * num_kv_heads;
+  const long long n = (long long)batch * num_kv_heads * kCounterStride;
   hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                      reinterpret_cast<int *>(static_cast<char *>(workspace) + w.cnt), n);
   return tqh::check_launch("fill_zero_kernel");
