@@ -3,26 +3,33 @@
 // One workgroup (1024 lanes, 16 waves) owns a tile (sequence b, KV head g,
 // chunk of CH = 1024 tokens) and serves all NR = num_heads / num_kv_heads
 // query heads of that KV head, so every compressed byte is read from HBM
-// exactly once (GQA sharing).  All of the tile's global loads (K and V codes
-// and scales) are issued before any arithmetic and sit in VGPRs while the
-// query tables are built, so each lane has ~25 loads in flight.
+// exactly once (GQA sharing).  Each wave owns 64 tokens, fetched as four
+// 16-token tiles in which lane (t, q) loads qblock q of token t, so one load
+// instruction reads one contiguous run of 16 records.
 //
 // Keys are never inverse-rotated.  With the block dequantization
 //   k_j = |s| * inv * (H (cb[idx] * sg))_j               (wht_tensor.rs:38-64)
 // the dot product is q.k = |s| * sum_i cb[idx_i] * qt_i, qt = inv * sg * (H q)
-// (the rotated query), built once per tile.  The tile builds an LDS table of
-// qt_i * cb[code] (times softmax scale * log2 e) for every code PAIR of
-// adjacent elements (3-bit: 64 pair codes), so one 6-bit field extract and
-// one LDS read cover two key elements for all NR heads at once.  Values are
-// accumulated in the rotated domain, sum_t w_t |s_t| cb[idx_t], with a pair
-// codebook (one LDS read per two elements), and inverse-rotated once per
-// head after the split-K merge.
+// (the rotated query), built once per tile.  Both contractions run on the
+// matrix cores (v_mfma_f32_16x16x32_f16) with every f32 operand split into
+// two f16 parts (hi = the value cut to 11 significant bits, lo = the exact
+// remainder), so the products carry 22 significant bits and accumulate in f32:
+//   scores  D[(qblock, head, part)][token] = sum_k Q[..][k] K[k][token], the
+//           query operand block-diagonal over qblocks so that the
+//           per-(token, qblock) key scale applies after the contraction;
+//   values  D[element][(qblock, head, part)] = sum_t V[element][t] W[t][..],
+//           W = p * |s_V|, with the codes transposed to token-major order in
+//           LDS.
+// A pair of codes is decoded by one 8-byte LDS read from a 2^(2 BITS)-entry
+// table of (hi(cb[c0]), hi(cb[c1]), lo(cb[c0]), lo(cb[c1])).  Values are
+// accumulated in the rotated domain and inverse-rotated once per head after
+// the split-K merge.
 //
-// Softmax is two-pass inside a tile (all CH scores staged in LDS, one max,
-// one exp2 per score).  Split-K partials (m, l, acc) go to a workspace; with
-// INLINE_MERGE the last tile of a (b, g) to finish (device-scope atomic
-// counter) merges them and writes the output, then re-arms the counter, so
-// one launch does the whole decode.
+// Softmax is two-pass inside a wave (all 64 scores, one max, one exp2 per
+// score); the 16 waves' (m, l, acc) are combined in LDS.  Split-K partials go
+// to a workspace; with INLINE_MERGE the last tile of a (b, g) to finish
+// (device-scope atomic counter) merges them and writes the output, then
+// re-arms the counter, so one launch does the whole decode.
 #include "tq_common.h"
 #include "tq_device.h"
 
@@ -72,21 +79,25 @@ struct AttnArgs {
   int P;                     // chunk stride per (b, h) in the partial arrays
   void *out;
   int out_dtype;
-  float cb[16];              // codebook
 };
 
+// Query element i as stored (f32 bits or a 16-bit pattern), converted
+// separately so that the wait for the load lands at the first use.
 template <int QT>
-__device__ __forceinline__ float load_q(const void *q, long long i) {
-  if constexpr (QT == kF32) return static_cast<const float *>(q)[i];
-  else if constexpr (QT == kBF16) return bf16_to_f32(static_cast<const uint16_t *>(q)[i]);
-  else return f16_to_f32(static_cast<const uint16_t *>(q)[i]);
+__device__ __forceinline__ uint32_t load_q_bits(const uint8_t *p) {
+  if constexpr (QT == kF32) return *reinterpret_cast<const uint32_t *>(p);
+  else return *reinterpret_cast<const uint16_t *>(p);
+}
+template <int QT>
+__device__ __forceinline__ float q_value(uint32_t bits) {
+  if constexpr (QT == kF32) return u2f(bits);
+  else if constexpr (QT == kBF16) return bf16_to_f32((uint16_t)bits);
+  else return f16_to_f32((uint16_t)bits);
 }
 
+// Value of lane l ^ 1 (DPP quad permute [1, 0, 3, 2]).
 __device__ __forceinline__ float dpp_quad_xor1(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float dpp_quad_xor2(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
 }
 
 template <typename Op>
@@ -97,8 +108,8 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
 }
 
 // DPP move: lanes whose source is outside the row (or whose row is masked
-// off) take `id`.  Controls: row_shr:n = 0x110 + n, row_ror:n = 0x120 + n,
-// row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+// off) take `id`.  Controls: row_shr:n = 0x110 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143.
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ float dpp(float v, float id) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, id), __builtin_bit_cast(int, v),
@@ -125,22 +136,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return wave_allreduce(v, 0.f, [](float x, float y) { return x + y; });
 }
 
-// Sum of v over the lanes that differ only in lane bits 3..5 (the 8 lanes
-// l ^ {0, 8, ..., 56}); every lane receives its group's total.  xor 8 is a
-// DPP row rotate, xor 16 a swizzle inside each half-wave, xor 32 a permute.
-__device__ __forceinline__ float xor16(float v) {
-  // ds_swizzle bit mode: lane' = ((lane & 0x1f) | 0) ^ 0x10 within 32 lanes
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
-}
-__device__ __forceinline__ float sum_lane_bits_4_5(float v) {
-  v += xor16(v);
-  return v + __shfl_xor(v, 32, 64);
-}
-__device__ __forceinline__ float sum_lane_bits_3_5(float v) {
-  v += dpp<0x128>(v, 0.f);  // row_ror:8 == lane ^ 8 inside a row of 16
-  return sum_lane_bits_4_5(v);
-}
-
 // Device-coherent accesses to the split-K partials: relaxed atomics at agent
 // scope bypass the non-coherent per-XCD caches.
 __device__ __forceinline__ void st_agent(float *p, float v) {
@@ -150,34 +145,59 @@ __device__ __forceinline__ float ld_agent(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Reads `W` bits starting at bit `pos` of little-endian words (pos and the
-// word indices must fold to constants after unrolling).
-template <int W>
-__device__ __forceinline__ uint32_t bits_at_p(const uint32_t *w, int pos) {
-  const int wi = pos >> 5, sh = pos & 31;
-  if (sh + W <= 32) return (w[wi] >> sh) & ((1u << W) - 1u);
-  return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & ((1u << W) - 1u);
+// ---- matrix-core operands ----
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// D + A B over 16 x 16 x 32 (f16 in, f32 accumulate).  Lane l holds A row
+// l % 16 and B column l % 16, each at k = 8 (l / 16) .. 8 (l / 16) + 7 (two
+// f16 per word, lower k in the low half), and D column l % 16 at rows
+// 4 (l / 16) .. 4 (l / 16) + 3.
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 d) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), d, 0, 0,
+                                                0);
 }
 
-// Reads `W` bits starting at bit `pos` of a little-endian word array.
-template <int W, int NW>
-__device__ __forceinline__ uint32_t bits_at(const uint32_t (&w)[NW], int pos) {
-  const int wi = pos >> 5, sh = pos & 31;
-  if (sh + W <= 32) return (w[wi] >> sh) & ((1u << W) - 1u);
-  return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & ((1u << W) - 1u);
+// Upper part of the two-part f16 split: x with its significand cut to 11
+// bits (exact in f16 while |x| is in f16's normal range); x - hi is exact in
+// f32 and is the lower part.
+__device__ __forceinline__ float split_hi(float x) { return u2f(f2u(x) & 0xffffe000u); }
+__device__ __forceinline__ uint32_t pack_f16(float lo_half, float hi_half) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo_half, hi_half));
 }
+// E with m * 2^-E in [0.5, 1) for finite m > 0 (0 for m == 0), clamped so
+// that 2^E and 2^-E are normal f32.
+__device__ __forceinline__ int pow2_exponent(float m) {
+  const int e = (int)((f2u(m) >> 23) & 0xffu);
+  return e == 0 ? 0 : min(max(e - 126, -100), 100);
+}
+__device__ __forceinline__ float exp2i(int e) { return u2f((uint32_t)(127 + e) << 23); }
 
+// Codes 8j .. 8j+7 of a qblock (BITS words, LSB-first codes) in the low
+// 8 * BITS bits of the result; for 3-bit codes bits 24..31 are left over
+// from the next group and are never read.
 template <int BITS>
-struct Geo {
-  static constexpr int NC = 1 << BITS;
-  static constexpr int QB_BYTES = 4 * BITS;  // bytes per 32-element qblock
-  // key table: 3-bit uses code pairs (64 entries per pair position),
-  // 4-bit single codes (16 entries per element) to keep the table in LDS
-  static constexpr bool KPAIR = (BITS == 3);
-  static constexpr int KG = KPAIR ? 2 : 1;            // elements per key lookup
-  static constexpr int KENT = KPAIR ? 64 : 16;        // entries per position
-  static constexpr int KPOS = 32 / KG;                // positions per qblock
-};
+__device__ __forceinline__ uint32_t code_group(const uint32_t (&w)[BITS], int j) {
+  if constexpr (BITS == 3) {
+    if (j == 0) return w[0];
+    if (j == 1) return __builtin_amdgcn_alignbit(w[1], w[0], 24);
+    if (j == 2) return __builtin_amdgcn_alignbit(w[2], w[1], 16);
+    return w[2] >> 8;
+  } else {
+    return w[j];
+  }
+}
+
+// Code pair p (codes 2p, 2p+1) of a qblock's BITS words, LSB-first: the
+// 2 BITS-bit pair-table index (p must fold to a constant after unrolling).
+template <int BITS>
+__device__ __forceinline__ uint32_t pair_code(const uint32_t (&w)[BITS], int p) {
+  constexpr int W = 2 * BITS;
+  const int pos = W * p, wi = pos >> 5, sh = pos & 31;
+  if (sh + W <= 32) return __builtin_amdgcn_ubfe(w[wi], sh, W);
+  return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & ((1u << W) - 1u);
+}
 
 // ---------------------------------------------------------------------------
 // Split-K merge and final inverse rotation for NR heads of one (b, g):
@@ -266,151 +286,159 @@ __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, fl
 
 template <int BITS, int NR, int QT, bool INLINE_MERGE>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
-  using G = Geo<BITS>;
   constexpr int NQB = 4, HD = 128, CH = kChunk;
   constexpr int QW = BITS;                       // 32-bit words per qblock
-  constexpr int RW = NQB * QW;                   // words per token record (12 / 16)
-  constexpr int PACKED = RW * 4;                 // bytes per token record
-  constexpr int WT = 64;                         // tokens per wave: lane = token
-  constexpr int EPL = NR <= 2 ? 16 : 8;          // V-pass elements per lane
-  constexpr int GPQ = 32 / EPL;                  // V lanes per qblock of a token
-  constexpr int VLPT = NQB * GPQ;                // V lanes per token
-  constexpr int VSL = 64 / VLPT;                 // token slices per wave in the V pass
-  constexpr int VTS = WT / VSL;                  // tokens per lane in the V pass
-  constexpr int VCODES = 1 << (2 * BITS);        // pair-codebook entries
-  constexpr int KV = NR == 1 ? 1 : 2;            // heads per key-table entry (one 4- or 8-byte read)
-  constexpr int KNT = NR / KV;                   // key tables (entry reads per lookup)
-  constexpr int KROW = G::KPOS * G::KENT;        // key-table entries per qblock
-  constexpr int KTAB = NR * NQB * KROW;          // floats in all key tables
-  constexpr int SPITCH = WT + 8;                 // V-scale rows: 4 qblock rows of 8 tokens on distinct banks
-  constexpr int WSTAGE = WT * RW + NR * WT + NQB * SPITCH;  // per-wave staging: V records, p, |V scale|
-  static_assert(kWaves * WT == CH, "one token per lane");
-  static_assert(WSTAGE >= NR * HD + 2 * NR, "combine record fits the staging area");
-  static_assert(KTAB * 4 <= 65536, "key-table offsets fit the ds_read immediate");
-  // LDS carve (32-bit words).  Key tables [KNT][qblock][position][code] hold
-  // KV heads per entry, so one lookup serves KV heads; the pair codebook holds
-  // (cb[lo], cb[hi]) per 2*BITS-bit code.
-  constexpr int OFF_CB2 = KTAB;
-  constexpr int OFF_CB1 = OFF_CB2 + 2 * VCODES;
-  constexpr int OFF_Q = OFF_CB1 + 16;
-  constexpr int OFF_W = OFF_Q + NR * HD;
-  constexpr int OFF_MISC = OFF_W;                       // merge scratch aliases the staging areas
+  constexpr int PACKED = NQB * QW * 4;           // bytes per token record
+  constexpr int NC = 1 << BITS;
+  constexpr int NPAIR = 1 << (2 * BITS);         // pair-table entries
+  constexpr int WT = 64;                         // tokens per wave
+  constexpr int NT = WT / 16;                    // 16-token tiles per wave
+  constexpr int NG = NR > 2 ? NR / 2 : 1;        // MFMA head groups: 16 rows = 4 qblocks x 2 heads x 2 parts
+  constexpr int VROW = 68;                       // code-group row pitch: a half-wave's 32 writes on 32 banks
+  // per-wave staging (32-bit words)
+  constexpr int XW = NQB * WT * NR;              // K partial scores [qblock][token][head]
+  constexpr int VW = 16 * VROW;                  // V code groups [group][token]
+  constexpr int RA = XW > VW ? XW : VW;          // the V groups reuse the K partials' space
+  constexpr int PW = NR * WT;                    // softmax numerators [head][token]
+  constexpr int SW = NQB * WT;                   // |V scale| * 2^-Ev [qblock][token]
+  constexpr int CW = (NR * HD + 2 * NR + 1 + 3) & ~3;  // combine record: acc [head][d], m, l, 2^Ev
+  constexpr int WSTAGE = RA + PW + SW + CW;
+  // LDS carve (32-bit words)
+  constexpr int OFF_PAIR = 0;                    // uint2 [NPAIR]
+  constexpr int OFF_QA = OFF_PAIR + 2 * NPAIR;   // u32x4 [NG][8][64]: key-pass query operands
+  constexpr int OFF_Q = OFF_QA + NG * 8 * 64 * 4;
+  constexpr int OFF_QMAX = OFF_Q + NR * HD;      // [2 NR] max |qt| per half head
+  constexpr int OFF_W = OFF_QMAX + 8;
+  constexpr int OFF_MISC = OFF_W;                // merge scratch aliases the staging areas
   constexpr int TOTAL0 = OFF_W + kWaves * WSTAGE;
   constexpr int TOTAL = TOTAL0 > OFF_MISC + kMiscFloats ? TOTAL0 : OFF_MISC + kMiscFloats;
+  static_assert(kWaves * WT == CH, "64 tokens per wave");
+  static_assert(TOTAL * 4 <= 160 * 1024, "fits the LDS of one CU");
+  static_assert(NR * HD % 64 == 0, "whole waves rotate the query");
   __shared__ __attribute__((aligned(16))) float lds[TOTAL];
   __shared__ int s_flag;
   __shared__ int s_ready;  // waves whose K/V records have arrived (staggered loads)
-  float *s_ktab = lds;
-  float2 *s_cb2 = reinterpret_cast<float2 *>(lds + OFF_CB2);
+  uint2 *s_pair = reinterpret_cast<uint2 *>(lds + OFF_PAIR);
+  u32x4 *s_qa = reinterpret_cast<u32x4 *>(lds + OFF_QA);
   float *s_q = lds + OFF_Q;
-  float *s_cb1 = lds + OFF_CB1;
+  float *s_qmax = lds + OFF_QMAX;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;  // matrix-core column / row group of this lane
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
   const int t0 = c * CH;
-  if (t0 >= len) return;  // empty tile: not counted by the merge
-  const int nchunks = (len + CH - 1) / CH;
   const long long rec0 = (long long)b * a.seq_stride + (long long)g * a.kv_head_stride;
-  uint32_t *stage = reinterpret_cast<uint32_t *>(lds + OFF_W + wave * WSTAGE);
-  uint32_t *st_v = stage;                                     // [WT][RW]
-  float *st_p = reinterpret_cast<float *>(stage + WT * RW);   // [WT][NR]: softmax numerators
-  float *st_s = st_p + NR * WT;                               // [NQB][SPITCH]: |V scale|
+  const uint8_t *kbase = a.k_idx + rec0 * PACKED, *vbase = a.v_idx + rec0 * PACKED;
 
-  // ---- loads.  The query goes out alone, ahead of the code stream, so the
-  // table build is not queued behind it.  The tile's waves then fetch their
-  // K/V records in NGRP staggered groups: group g issues only once the
-  // records of group g - 1 have arrived, so device-wide the early groups'
-  // bytes come back first and their K/V passes overlap the later transfers
-  // (all groups issuing at once would make every wave wait for the whole
-  // tile). ----
-  constexpr int GW = kWaves / kLoadGroups;  // waves per load group
-  const int grp = wave / GW;
-  // (every lane loads, clamped, so the wait for q lands at its first use)
-  const float qv = load_q<QT>(a.q, ((long long)b * a.num_heads + g * NR) * HD + min(tid, NR * HD - 1));
-  if (tid == 0) {  // codebook into LDS straight from the scalar kernel arguments
-#pragma unroll
-    for (int k = 0; k < 16; k++) s_cb1[k] = a.cb[k];
-    s_ready = 0;
+  // ---- the query goes out first (it does not depend on the sequence
+  // length), loaded by the waves that rotate it, one element per lane (whole
+  // waves: NR * HD % 64 == 0).  These waves rotate it before they queue any
+  // record load, so the wait for it counts nothing else. ----
+  constexpr int QBYTES = QT == kF32 ? 4 : 2;
+  uint32_t qbits = 0;
+  if (tid < NR * HD)
+    qbits = load_q_bits<QT>(static_cast<const uint8_t *>(a.q) +
+                            (((long long)b * a.num_heads + g * NR) * HD + tid) * QBYTES);
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
+  if (t0 >= len) {  // empty tile: not counted by the merge
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
   }
-  __syncthreads();
-  const int tok = t0 + wave * WT + lane;
-  const bool valid = tok < len;
-  const long long rec = rec0 + min(tok, len - 1);
-  uint32_t kr[RW], vr[RW];
-  uint2 ksr, vsr;
-  auto issue_loads = [&](long long r) {
-    const uint4 *kp = reinterpret_cast<const uint4 *>(a.k_idx + r * PACKED);
-    const uint4 *vp = reinterpret_cast<const uint4 *>(a.v_idx + r * PACKED);
-#pragma unroll
-    for (int q = 0; q < RW / 4; q++) {
-      const uint4 v = kp[q];
-      kr[4 * q] = v.x; kr[4 * q + 1] = v.y; kr[4 * q + 2] = v.z; kr[4 * q + 3] = v.w;
-    }
-    ksr = *reinterpret_cast<const uint2 *>(a.k_sc + r * NQB);
-#pragma unroll
-    for (int q = 0; q < RW / 4; q++) {
-      const uint4 v = vp[q];
-      vr[4 * q] = v.x; vr[4 * q + 1] = v.y; vr[4 * q + 2] = v.z; vr[4 * q + 3] = v.w;
-    }
-    vsr = *reinterpret_cast<const uint2 *>(a.v_sc + r * NQB);
-  };
-  // Every wave issues the same load sequence here (later groups fetch the
-  // tile's first record, one cache line per instruction, as a placeholder),
-  // so the number of loads in flight does not depend on the group and the
-  // wait for the query below counts only the query.
-  issue_loads(grp == 0 ? rec : rec0 + t0);
+  const int nchunks = (len + CH - 1) / CH;
+  float *stage = lds + OFF_W + wave * WSTAGE;
+  uint32_t *st_x = reinterpret_cast<uint32_t *>(stage);  // [NQB][WT][NR] K partial scores (f32 bits)
+  uint32_t *st_vt = st_x;                                 // [16][VROW] V code groups, after the K pass
+  float *st_p = stage + RA;                               // [NR][WT]
+  float *st_s = st_p + PW;                                // [NQB][WT]
+  float *comb = st_s + SW;                                // [NR][HD], m[NR], l[NR], 2^Ev
 
-  // ---- rotated, scaled queries (32-lane butterflies) and the LDS tables ----
+  // ---- pair table from the constant codebook ----
+  if (tid < NPAIR) {
+    const float c0 = pqo_centroid<BITS>(tid & (NC - 1)), c1 = pqo_centroid<BITS>(tid >> BITS);
+    const float h0 = split_hi(c0), h1 = split_hi(c1);
+    s_pair[tid] = make_uint2(pack_f16(h0, h1), pack_f16(c0 - h0, c1 - h1));
+  }
+  if (tid == 0) s_ready = 0;
+
+  // ---- rotated, scaled queries (32-lane butterflies), before these waves
+  // queue their record loads behind the query ----
   const float qscale = a.softmax_scale * kLog2e * kInvSqrt32;
   if (tid < NR * HD) {
     const int d = tid % HD;
-    float v = qv;
+    float v = q_value<QT>(qbits);
     const int i = d & 31;
 #pragma unroll
     for (int hh = 1; hh < 32; hh <<= 1) {
       float ov = __shfl_xor(v, hh, 64);
       v = (i & hh) ? (ov - v) : (v + ov);
     }
-    s_q[tid] = v * (decode_sign(i) * qscale);
+    const float qt = v * (decode_sign(i) * qscale);
+    s_q[tid] = qt;
+    const float am = wave_max(fabsf(qt));
+    if (lane == 0) s_qmax[wave] = am;
   }
-  if (tid < VCODES) {
-    constexpr int NCm = G::NC - 1;
-    s_cb2[tid] = make_float2(s_cb1[tid & NCm], s_cb1[(tid >> BITS) & NCm]);
-  }
+
+  // ---- K/V records.  The tile's waves fetch them in kLoadGroups staggered
+  // groups: group k issues only once the records of group k - 1 have
+  // arrived, so device-wide the early groups' bytes come back first and their
+  // passes overlap the later transfers.  Group 0 is the highest waves (the
+  // query waves above fetch last).  Codes: tile tt of this wave, lane
+  // (l16, lg) holds qblock lg of token 16 tt + l16; scales: lane = token, all
+  // four qblock scales in one load.  Addresses are a per-(b, g) base plus a
+  // 32-bit offset inside the head. ----
+  constexpr int GW = kWaves / kLoadGroups;  // waves per load group
+  const int grp = (kWaves - 1 - wave) / GW;
+  const uint8_t *ksbase = reinterpret_cast<const uint8_t *>(a.k_sc + rec0 * NQB);
+  const uint8_t *vsbase = reinterpret_cast<const uint8_t *>(a.v_sc + rec0 * NQB);
+  uint32_t kq[NT][QW], vq[NT][QW];
+  uint2 ksc, vsc;
+  auto issue_loads = [&](bool real) {
+    const int tw = t0 + wave * WT;
+    const uint32_t soff = (uint32_t)(real ? min(tw + lane, len - 1) : t0) * (NQB * 2);
+    uint32_t off[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+      off[tt] = (uint32_t)(real ? min(tw + 16 * tt + l16, len - 1) : t0) * PACKED + lg * (QW * 4);
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+      for (int w = 0; w < QW; w++) kq[tt][w] = *reinterpret_cast<const uint32_t *>(kbase + off[tt] + 4 * w);
+    ksc = *reinterpret_cast<const uint2 *>(ksbase + soff);
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+      for (int w = 0; w < QW; w++) vq[tt][w] = *reinterpret_cast<const uint32_t *>(vbase + off[tt] + 4 * w);
+    vsc = *reinterpret_cast<const uint2 *>(vsbase + soff);
+  };
+  // Every wave issues the same load sequence here (later groups fetch the
+  // tile's first record as a placeholder), so the number of loads in flight
+  // does not depend on the group.
+  issue_loads(grp == 0);
   __syncthreads();
-  // Table entry (((t * NQB + qb) * KPOS + pos) * KENT + code) * KV + j holds,
-  // for head r = t * KV + j, qt[2 pos] * cb[code & 7] + qt[2 pos + 1] * cb[code >> 3]
-  // (3-bit pairs) or qt[pos] * cb[code] (4-bit).  Each work item fills four
-  // consecutive codes of one row for its KV heads (one contiguous run).
-  constexpr int ITEMS = KNT * NQB * G::KPOS * (G::KENT / 4);
-  for (int it = tid; it < ITEMS; it += kThreads) {
-    const int c4 = it % (G::KENT / 4), row = it / (G::KENT / 4);
-    const int pos = row % G::KPOS, rq = row / G::KPOS;
-    const int qb = rq % NQB, t = rq / NQB;
-    float ov[4 * KV];
-#pragma unroll
-    for (int j = 0; j < KV; j++) {
-      const int r = t * KV + j;
-      if constexpr (G::KPAIR) {
-        const float2 qt = *reinterpret_cast<const float2 *>(s_q + r * HD + qb * 32 + 2 * pos);
-        const float hi = qt.y * s_cb1[(4 * c4) >> 3];
-#pragma unroll
-        for (int k = 0; k < 4; k++) ov[k * KV + j] = qt.x * s_cb1[(4 * c4 + k) & 7] + hi;
-      } else {
-        const float qt = s_q[r * HD + qb * 32 + pos];
-#pragma unroll
-        for (int k = 0; k < 4; k++) ov[k * KV + j] = qt * s_cb1[4 * c4 + k];
-      }
+  // Key-pass query operands.  MFMA j covers elements 4 j .. 4 j + 3 of every
+  // qblock, each twice along k (against the hi and the lo part of the key
+  // value), so lane (m, kg) supplies k = 8 kg + (x0, x1, x0, x1, x2, x3, x2,
+  // x3), x_i = part(Q[32 kg + 4 j + i]) for row m = (qblock qb, head
+  // 2 gi + rl, part) when kg == qb, zero otherwise; Q = qt * 2^-Eq, scaled
+  // per head into f16's range.
+  if (tid < NG * 512) {
+    const int gi = tid >> 9, j = (tid >> 6) & 7, m = lane & 15, kg = lane >> 4;
+    const int qb = m >> 2, rl = (m >> 1) & 1, part = m & 1, r = 2 * gi + rl;
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (kg == qb && r < NR) {
+      const float sc = exp2i(-pow2_exponent(fmaxf(s_qmax[2 * r], s_qmax[2 * r + 1])));
+      const float4 q4 = *reinterpret_cast<const float4 *>(s_q + r * HD + 32 * kg + 4 * j);
+      const float x0 = q4.x * sc, x1 = q4.y * sc, x2 = q4.z * sc, x3 = q4.w * sc;
+      const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
+      const uint32_t w01 = part ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
+      const uint32_t w23 = part ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
+      val = u32x4{w01, w01, w23, w23};
     }
-    float *dst = s_ktab + (row * G::KENT + 4 * c4) * KV;
-#pragma unroll
-    for (int k = 0; k < KV; k++)
-      *reinterpret_cast<float4 *>(dst + 4 * k) = make_float4(ov[4 * k], ov[4 * k + 1], ov[4 * k + 2], ov[4 * k + 3]);
+    s_qa[(gi * 8 + j) * 64 + lane] = val;
   }
   __syncthreads();
-  __builtin_amdgcn_sched_barrier(0);  // keep the record-dependent code below the table build
+  __builtin_amdgcn_sched_barrier(0);  // keep the record-dependent code below the setup
   if (grp > 0) {
     // wait (acquire: the loads below cannot move above it) until every wave
     // of the previous group has its records, then fetch ours
@@ -419,186 +447,214 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         __builtin_amdgcn_s_sleep(2);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    issue_loads(rec);
+    issue_loads(true);
   }
   if constexpr (kLoadGroups > 1) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's records are in registers
     if (lane == 0) __hip_atomic_fetch_add(&s_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 
-  // ---- K pass: lane = token, all qblocks in-lane (fully unrolled; the
-  // scheduling barriers bound the LDS reads in flight to 16 positions) ----
+  float escale[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) escale[r] = exp2i(pow2_exponent(fmaxf(s_qmax[2 * r], s_qmax[2 * r + 1])));
+
+  // ---- K pass: D[tile][(qblock, head, part)][token] over the eight
+  // 4-element slices j of every qblock.  The key operand of lane (t, q) for
+  // slice j is (hi pair, lo pair) of codes 4j, 4j+1 and of codes 4j+2, 4j+3
+  // of qblock q of token t: two pair-table reads.  Lane (t, q) ends with
+  // token t's (unscaled) qblock-q partial of each head. ----
+  f32x4 dk[NT][NG];
+#pragma unroll
+  for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) dk[tt][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    u32x4 qa[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) qa[gi] = s_qa[(gi * 8 + j) * 64 + lane];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+      const uint2 e0 = s_pair[pair_code<BITS>(kq[tt], 2 * j)];
+      const uint2 e1 = s_pair[pair_code<BITS>(kq[tt], 2 * j + 1)];
+      const u32x4 kb = {e0.x, e0.y, e1.x, e1.y};
+#pragma unroll
+      for (int gi = 0; gi < NG; gi++) dk[tt][gi] = mfma(qa[gi], kb, dk[tt][gi]);
+    }
+  }
+#pragma unroll
+  for (int tt = 0; tt < NT; tt++) {
+    uint32_t *dst = st_x + (lg * WT + 16 * tt + l16) * NR;
+    uint32_t xv[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) xv[r] = f2u(dk[tt][r >> 1][2 * (r & 1)] + dk[tt][r >> 1][2 * (r & 1) + 1]);
+    if constexpr (NR == 1) {
+      dst[0] = xv[0];
+    } else if constexpr (NR == 2) {
+      *reinterpret_cast<uint2 *>(dst) = make_uint2(xv[0], xv[1]);
+    } else {
+      *reinterpret_cast<uint4 *>(dst) = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // lane = token: the four qblock partials times the token's key scales
   float score[NR];
 #pragma unroll
   for (int r = 0; r < NR; r++) score[r] = 0.f;
 #pragma unroll
   for (int qb = 0; qb < NQB; qb++) {
-    float part[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) part[r] = 0.f;
-    // groups of 16 positions: all table reads of a group are issued before
-    // any is consumed, then summed as a tree (short dependency chains)
-#pragma unroll
-    for (int p0 = 0; p0 < G::KPOS; p0 += 16) {
-      float ev[NR][16];
-#pragma unroll
-      for (int pos = p0; pos < p0 + 16; pos++) {
-        const uint32_t code = bits_at_p<BITS * G::KG>(kr + qb * QW, pos * BITS * G::KG);
-        const float *ent = s_ktab + ((qb * G::KPOS + pos) * G::KENT + code) * KV;
-        if constexpr (KV == 1) {
-          ev[0][pos - p0] = ent[0];
-        } else {
-#pragma unroll
-          for (int t = 0; t < KNT; t++) {
-            const float2 v = *reinterpret_cast<const float2 *>(ent + t * NQB * KROW * KV);
-            ev[2 * t][pos - p0] = v.x;
-            ev[2 * t + 1][pos - p0] = v.y;
-          }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < NR; r++) {
-#pragma unroll
-        for (int w = 8; w > 0; w >>= 1)
-#pragma unroll
-          for (int i = 0; i < w; i++) ev[r][i] += ev[r][i + w];
-        part[r] += ev[r][0];
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    const uint32_t sbits = (qb < 2 ? ksc.x : ksc.y) >> ((qb & 1) ? 16 : 0);
+    const float sk = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+    const uint32_t *src = st_x + (qb * WT + lane) * NR;
+    uint32_t xv[NR];
+    if constexpr (NR == 1) {
+      xv[0] = src[0];
+    } else if constexpr (NR == 2) {
+      const uint2 t = *reinterpret_cast<const uint2 *>(src);
+      xv[0] = t.x; xv[1] = t.y;
+    } else {
+      const uint4 t = *reinterpret_cast<const uint4 *>(src);
+      xv[0] = t.x; xv[1] = t.y; xv[2] = t.z; xv[3] = t.w;
     }
-    const uint32_t sbits = (qb < 2 ? ksr.x : ksr.y) >> ((qb & 1) ? 16 : 0);
-    const float ks = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
 #pragma unroll
-    for (int r = 0; r < NR; r++) score[r] = __builtin_fmaf(part[r], ks, score[r]);
-  }
-
-  // ---- stage this wave's V records and scales (wave-private LDS) ----
-#pragma unroll
-  for (int q = 0; q < RW / 4; q++)
-    *reinterpret_cast<uint4 *>(st_v + lane * RW + 4 * q) = make_uint4(vr[4 * q], vr[4 * q + 1], vr[4 * q + 2], vr[4 * q + 3]);
-#pragma unroll
-  for (int qb = 0; qb < NQB; qb++) {
-    const uint32_t sbits = (qb < 2 ? vsr.x : vsr.y) >> ((qb & 1) ? 16 : 0);
-    st_s[qb * SPITCH + lane] = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+    for (int r = 0; r < NR; r++) score[r] = __builtin_fmaf(u2f(xv[r]), sk, score[r]);
   }
 
   // ---- wave-local softmax (base 2): m = max over the wave's tokens ----
-  float m_w[NR], p[NR];
+  const int tok = t0 + wave * WT + lane;
+  const bool valid = tok < len;
+  float m_w[NR], p[NR], l_w[NR];
 #pragma unroll
   for (int r = 0; r < NR; r++) {
-    const float sc = valid ? score[r] : -INFINITY;
+    const float sc = valid ? score[r] * escale[r] : -INFINITY;
     m_w[r] = wave_max(sc);
     p[r] = valid ? __builtin_amdgcn_exp2f(sc - m_w[r]) : 0.f;
+    st_p[r * WT + lane] = p[r];
   }
-  if constexpr (NR == 1) {
-    st_p[lane] = p[0];
-  } else if constexpr (NR == 2) {
-    *reinterpret_cast<float2 *>(st_p + 2 * lane) = make_float2(p[0], p[1]);
-  } else {
-    *reinterpret_cast<float4 *>(st_p + 4 * lane) = make_float4(p[0], p[1], p[2], p[3]);
+#pragma unroll
+  for (int r = 0; r < NR; r++) l_w[r] = wave_sum(p[r]);
+
+  // ---- V codes to LDS in [code group][token] order, scales * 2^-Ev ----
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();  // every lane has read its K partials
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) st_vt[(4 * lg + j) * VROW + 16 * tt + l16] = code_group<BITS>(vq[tt], j);
+  float sv[NQB];
+  float smax = 0.f;
+#pragma unroll
+  for (int qb = 0; qb < NQB; qb++) {
+    const uint32_t sbits = (qb < 2 ? vsc.x : vsc.y) >> ((qb & 1) ? 16 : 0);
+    sv[qb] = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+    smax = fmaxf(smax, sv[qb]);
   }
+  const int ev = pow2_exponent(wave_max(smax));
+  const float vinv = exp2i(-ev);
+#pragma unroll
+  for (int qb = 0; qb < NQB; qb++) st_s[qb * WT + lane] = sv[qb] * vinv;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- V pass: lane = (token slice, qblock, group of EPL elements) ----
-  const int vgrp = lane % GPQ, vqb = (lane / GPQ) % NQB, vsl = lane / VLPT;
-  int vlo, vhi, vsh;
-  if constexpr (BITS == 3 && EPL == 16) {
-    vlo = (48 * vgrp) >> 5; vhi = vlo + 1; vsh = (48 * vgrp) & 31;
-  } else if constexpr (BITS == 3) {
-    vlo = (24 * vgrp) >> 5; vhi = min(vlo + 1, 2); vsh = (24 * vgrp) & 31;
-  } else if constexpr (EPL == 16) {
-    vlo = 2 * vgrp; vhi = vlo + 1; vsh = 0;
-  } else {
-    vlo = vgrp; vhi = vgrp; vsh = 0;
+  // ---- V pass.  Four 16-token steps; the value operand of lane (m, lg) at
+  // step ks is (hi pair, lo pair) of tokens (t0, t1) and of (t2, t3),
+  // t_i = 16 ks + 4 lg + i, for element 16 et + m, so the weight operand
+  // holds each token's weight twice: (w0, w1, w0, w1, w2, w3, w2, w3) for
+  // column n = (qblock bq, head 2 gi + brl, part) ----
+  const int bq = l16 >> 2, brl = (l16 >> 1) & 1, bpart = l16 & 1;
+  u32x4 bw[4][NG];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) {
+      const int r = min(2 * gi + brl, NR - 1);  // NR == 1: the second head's columns are never read
+      const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * ks + 4 * lg);
+      const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * ks + 4 * lg);
+      const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
+      const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
+      const uint32_t w01 = bpart ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
+      const uint32_t w23 = bpart ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
+      bw[ks][gi] = u32x4{w01, w01, w23, w23};
+    }
   }
-  constexpr int VU = 4;  // V-pass unroll
-  float acc[NR][EPL];
+  // Element tiles: A row m = element 16 et + m.
+  // Two tiles (one qblock) per round: all eight code-word reads go out first,
+  // then all sixteen pair-table reads, then the MFMAs, so each wave keeps
+  // several LDS round trips in flight.
+  const int aoff = BITS * (l16 & 7), arow = l16 >> 3;
 #pragma unroll
-  for (int r = 0; r < NR; r++)
+  for (int e2 = 0; e2 < 8; e2 += 2) {
+    u32x4 u[2][4];
 #pragma unroll
-    for (int e = 0; e < EPL; e++) acc[r][e] = 0.f;
-#pragma unroll VU
-  for (int tk = 0; tk < VTS; tk++) {
-    const int tl = vsl + tk * VSL;
-    const uint32_t *rw = st_v + tl * RW + vqb * QW;
-    uint64_t bits64;
-    if constexpr (BITS == 3 && EPL == 16) {
-      bits64 = (((uint64_t)rw[vhi] << 32) | rw[vlo]) >> vsh;
-    } else if constexpr (BITS == 3) {
-      bits64 = __builtin_amdgcn_alignbit(rw[vhi], rw[vlo], vsh);
-    } else if constexpr (EPL == 16) {
-      bits64 = ((uint64_t)rw[vhi] << 32) | rw[vlo];
-    } else {
-      bits64 = rw[vlo];
-    }
-    const float vs = st_s[vqb * SPITCH + tl];
-    float wgt[NR];
-    if constexpr (NR == 1) {
-      wgt[0] = st_p[tl] * vs;
-    } else if constexpr (NR == 2) {
-      const float2 pp = *reinterpret_cast<const float2 *>(st_p + 2 * tl);
-      wgt[0] = pp.x * vs; wgt[1] = pp.y * vs;
-    } else {
-      const float4 pp = *reinterpret_cast<const float4 *>(st_p + 4 * tl);
-      wgt[0] = pp.x * vs; wgt[1] = pp.y * vs; wgt[2] = pp.z * vs; wgt[3] = pp.w * vs;
-    }
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-    for (int pr = 0; pr < EPL / 2; pr++) {
-      const uint32_t code = (uint32_t)(bits64 >> (pr * 2 * BITS)) & (VCODES - 1);
-      const float2 cv = s_cb2[code];
+      for (int ks = 0; ks < 4; ks++)
+        u[h][ks] = *reinterpret_cast<const u32x4 *>(st_vt + (2 * (e2 + h) + arow) * VROW + 16 * ks + 4 * lg);
+    u32x4 va[2][4];
 #pragma unroll
-      for (int r = 0; r < NR; r++) {
-        acc[r][2 * pr] = __builtin_fmaf(wgt[r], cv.x, acc[r][2 * pr]);
-        acc[r][2 * pr + 1] = __builtin_fmaf(wgt[r], cv.y, acc[r][2 * pr + 1]);
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) {
+        const u32x4 w = u[h][ks];
+        const uint32_t c0 = __builtin_amdgcn_ubfe(w.x, aoff, BITS), c1 = __builtin_amdgcn_ubfe(w.y, aoff, BITS);
+        const uint32_t c2 = __builtin_amdgcn_ubfe(w.z, aoff, BITS), c3 = __builtin_amdgcn_ubfe(w.w, aoff, BITS);
+        const uint2 e01 = s_pair[c0 | (c1 << BITS)];
+        const uint2 e23 = s_pair[c2 | (c3 << BITS)];
+        va[h][ks] = u32x4{e01.x, e01.y, e23.x, e23.y};
+      }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int et = e2 + h;
+      f32x4 dv[NG];
+#pragma unroll
+      for (int gi = 0; gi < NG; gi++) dv[gi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) dv[gi] = mfma(va[h][ks], bw[ks][gi], dv[gi]);
+      // lane (n, lg) holds column n at elements 16 et + 4 lg + i; the parts
+      // of one head sit in lanes n and n ^ 1, and only this tile's qblock counts
+#pragma unroll
+      for (int gi = 0; gi < NG; gi++) {
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = dpp_quad_xor1(dv[gi][i]) + dv[gi][i];
+        __builtin_amdgcn_sched_barrier(0);  // the sums stay outside the store's branch (DPP adds)
+        const int r = 2 * gi + brl;
+        if (bpart == 0 && bq == (et >> 1) && r < NR)
+          *reinterpret_cast<f32x4 *>(comb + r * HD + 16 * et + 4 * lg) = o;
       }
     }
   }
-  // reduce over the wave's token slices (lane bits above the V lane id)
-  static_assert(VLPT == 8 || VLPT == 16, "token slices sit in lane bits 3..5 or 4..5");
+  if (lane == 0) {
 #pragma unroll
-  for (int r = 0; r < NR; r++)
-#pragma unroll
-    for (int e = 0; e < EPL; e++)
-      acc[r][e] = VLPT == 8 ? sum_lane_bits_3_5(acc[r][e]) : sum_lane_bits_4_5(acc[r][e]);
-  float l_w[NR];
-#pragma unroll
-  for (int r = 0; r < NR; r++) l_w[r] = wave_sum(p[r]);
+    for (int r = 0; r < NR; r++) {
+      comb[NR * HD + r] = m_w[r];
+      comb[NR * HD + NR + r] = l_w[r];
+    }
+    comb[NR * HD + 2 * NR] = exp2i(ev);
+  }
 
-  // ---- this wave's (m, l, acc) into its own staging area, then combine 16 waves ----
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  {
-    float *comb = reinterpret_cast<float *>(stage);  // [HD][NR] acc, then m[NR], l[NR]
-    if (lane < VLPT) {
-#pragma unroll
-      for (int r = 0; r < NR; r++)
-#pragma unroll
-        for (int e = 0; e < EPL; e++) comb[(vqb * 32 + vgrp * EPL + e) * NR + r] = acc[r][e];
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < NR; r++) {
-        comb[HD * NR + r] = m_w[r];
-        comb[HD * NR + NR + r] = l_w[r];
-      }
-    }
-  }
+  // ---- combine the 16 waves' records ----
   __syncthreads();
   if (tid < NR * HD) {
     const int r = tid / HD, d = tid % HD;
+    constexpr int COMB = RA + PW + SW;  // offset of the record inside a wave's staging
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds[OFF_W + w * WSTAGE + HD * NR + r]);
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds[OFF_W + w * WSTAGE + COMB + NR * HD + r]);
     float A = 0.f, L = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; w++) {
-      const float *cw = lds + OFF_W + w * WSTAGE;
-      const float mw = cw[HD * NR + r];
+      const float *cw = lds + OFF_W + w * WSTAGE + COMB;
+      const float mw = cw[NR * HD + r];
       const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-      A = __builtin_fmaf(cw[d * NR + r], f, A);
-      L = __builtin_fmaf(cw[HD * NR + NR + r], f, L);
+      A = __builtin_fmaf(cw[r * HD + d], f * cw[NR * HD + 2 * NR], A);
+      L = __builtin_fmaf(cw[NR * HD + NR + r], f, L);
     }
     const long long bh = (long long)b * a.num_heads + g * NR + r;
     st_agent(&a.po[(bh * a.P + c) * HD + d], A);
@@ -667,10 +723,8 @@ WsLayout ws_layout(int batch, int num_heads, int num_kv_heads, int head_dim, int
   return w;
 }
 
-AttnArgs base_args(int bits) {
+AttnArgs base_args() {
   AttnArgs a{};
-  tqh::PqoCodebook cb = tqh::pqo_codebook(bits);
-  for (int i = 0; i < cb.nc; i++) a.cb[i] = cb.c[i];
   a.out_dtype = kF32;
   return a;
 }
@@ -751,7 +805,7 @@ extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
   if ((long long)(num_heads / num_kv_heads) * w.P > kMergeCap)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "max_kv_len %d too long for one merge", max_kv_len);
-  AttnArgs a = base_args(bits);
+  AttnArgs a = base_args();
   char *ws = static_cast<char *>(workspace);
   a.q = q;
   a.k_idx = k_indices;
@@ -805,7 +859,7 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
   // partitions) hold this entry's 1024-token partials.
   (void)codebook;
   (void)sign_pattern;
-  AttnArgs a = base_args(bits);
+  AttnArgs a = base_args();
   a.q = q;
   a.k_idx = k_indices;
   a.k_sc = k_scales;

@@ -1,5 +1,6 @@
 // tq_common.cpp -- error reporting and host-side constant tables.
 #include "tq_common.h"
+#include "tq_device.h"
 
 #include <cmath>
 #include <cstring>
@@ -30,25 +31,22 @@ int check_launch(const char *what) {
 PqoCodebook pqo_codebook(int bits) {
   // src/cache/precomputed/codebooks.rs:8-88.  3-bit: the llama.cpp table;
   // 4-bit: c4[i] = -R + i * (2R/15), b4[i] = -R + (i + 0.5) * (2R/15), f32.
-  static const float c3[8] = {-2.1573f, -1.3336f, -0.7434f, -0.2428f, 0.2428f, 0.7434f, 1.3336f, 2.1573f};
+  // The centroids come from tqd::pqo_centroid, which the decode kernels
+  // evaluate on the device, so both sides hold the same values.
   static const float b3[7] = {-1.7455f, -1.0385f, -0.4931f, 0.0f, 0.4931f, 1.0385f, 1.7455f};
-  static const float c2[4] = {-2.1573f, -0.7434f, 0.7434f, 2.1573f};
   static const float b2[3] = {-1.0385f, 0.0f, 1.0385f};
   PqoCodebook cb;
   cb.bits = bits;
   const float range = 2.1573f;
   if (bits == 3) {
     cb.nc = 8;
-    std::memcpy(cb.c, c3, sizeof c3);
+    for (int i = 0; i < 8; i++) cb.c[i] = tqd::pqo_centroid<3>(i);
     std::memcpy(cb.b, b3, sizeof b3);
   } else if (bits == 4) {
     cb.nc = 16;
+    for (int i = 0; i < 16; i++) cb.c[i] = tqd::pqo_centroid<4>(i);
     volatile float full = 2.0f * range;  // volatile: keep every f32 rounding step
     volatile float step = full / 15.0f;
-    for (int i = 0; i < 16; i++) {
-      volatile float t = (float)i * step;
-      cb.c[i] = -range + t;
-    }
     for (int i = 0; i < 15; i++) {
       volatile float k = (float)i + 0.5f;
       volatile float t = k * step;
@@ -56,7 +54,7 @@ PqoCodebook pqo_codebook(int bits) {
     }
   } else if (bits == 2) {
     cb.nc = 4;
-    std::memcpy(cb.c, c2, sizeof c2);
+    for (int i = 0; i < 4; i++) cb.c[i] = tqd::pqo_centroid<2>(i);
     std::memcpy(cb.b, b2, sizeof b2);
   } else {
     return cb;

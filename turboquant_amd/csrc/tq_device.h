@@ -86,6 +86,30 @@ constexpr uint32_t kPqoSignMask =
 
 __host__ __device__ constexpr bool pqo_neg(int j) { return (kPqoSignMask >> j) & 1u; }
 
+// PQO centroid i in f32 exactly as src/cache/precomputed/codebooks.rs:51-88
+// evaluates it: 3-bit the fixed table, 4-bit -R + i * fl(2R / 15) with every
+// step rounded to f32 (the library is built without contraction).  Written
+// as a select chain so that device code indexes it by a lane-varying i
+// without a memory table.
+template <int BITS>
+__host__ __device__ inline float pqo_centroid(int i) {
+  static_assert(BITS == 2 || BITS == 3 || BITS == 4, "PQO codebooks are 2-, 3- or 4-bit");
+  if constexpr (BITS == 4) {
+    const float range = 2.1573f;
+    const float step = (2.0f * range) / 15.0f;
+    const float t = (float)i * step;
+    return -range + t;
+  } else {
+    constexpr int NC = 1 << BITS;
+    constexpr float c3[8] = {-2.1573f, -1.3336f, -0.7434f, -0.2428f, 0.2428f, 0.7434f, 1.3336f, 2.1573f};
+    constexpr float c2[4] = {-2.1573f, -0.7434f, 0.7434f, 2.1573f};
+    float v = BITS == 3 ? c3[0] : c2[0];
+#pragma unroll
+    for (int k = 1; k < NC; k++) v = (i == k) ? (BITS == 3 ? c3[k] : c2[k]) : v;
+    return v;
+  }
+}
+
 // Extracts the BITS-wide field i from a little-endian bitstream held in
 // 32-bit words (fields may straddle a word boundary for BITS = 3).
 template <int BITS, int NW>
