@@ -95,9 +95,13 @@ __device__ __forceinline__ float q_value(uint32_t bits) {
   else return f16_to_f32((uint16_t)bits);
 }
 
-// Value of lane l ^ 1 (DPP quad permute [1, 0, 3, 2]).
+// Value of lane l ^ 1 (DPP quad permute [1, 0, 3, 2]) and of lane l ^ 2
+// ([2, 3, 0, 1]).
 __device__ __forceinline__ float dpp_quad_xor1(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_quad_xor2(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
 }
 
 template <typename Op>
@@ -129,8 +133,24 @@ __device__ __forceinline__ float wave_allreduce(float v, float id, Op op) {
   v = op(v, dpp<0x143, 0xc>(v, id));
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+// Whole-wave max of non-NaN floats on order-preserving integer keys (the
+// magnitude bits of negative values flipped), so every step is one integer
+// max with a DPP operand and no float canonicalization.
+__device__ __forceinline__ int order_key(int bits) { return bits ^ (int)((uint32_t)(bits >> 31) >> 1); }
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int v, int id) {
+  return __builtin_amdgcn_update_dpp(id, v, CTRL, ROW_MASK, 0xf, false);
+}
 __device__ __forceinline__ float wave_max(float v) {
-  return wave_allreduce(v, -INFINITY, [](float x, float y) { return fmaxf(x, y); });
+  constexpr int kMin = -2147483647 - 1;
+  int k = order_key(__builtin_bit_cast(int, v));
+  k = max(k, dpp_i<0x111>(k, kMin));
+  k = max(k, dpp_i<0x112>(k, kMin));
+  k = max(k, dpp_i<0x114>(k, kMin));
+  k = max(k, dpp_i<0x118>(k, kMin));
+  k = max(k, dpp_i<0x142, 0xa>(k, kMin));
+  k = max(k, dpp_i<0x143, 0xc>(k, kMin));
+  return __builtin_bit_cast(float, order_key(__builtin_amdgcn_readlane(k, 63)));
 }
 __device__ __forceinline__ float wave_sum(float v) {
   return wave_allreduce(v, 0.f, [](float x, float y) { return x + y; });
@@ -149,6 +169,8 @@ __device__ __forceinline__ float ld_agent(const float *p) {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // D + A B over 16 x 16 x 32 (f16 in, f32 accumulate).  Lane l holds A row
 // l % 16 and B column l % 16, each at k = 8 (l / 16) .. 8 (l / 16) + 7 (two
@@ -157,6 +179,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 d) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), d, 0, 0,
                                                 0);
+}
+
+// A B over 16 x 16 x 16 (f16 in, f32 out): lane l holds A row l % 16 and B
+// column l % 16 at k = 4 (l / 16) .. 4 (l / 16) + 3, and D column l % 16 at
+// rows 4 (l / 16) .. 4 (l / 16) + 3.  With B = I it is an exact transpose.
+__device__ __forceinline__ f32x4 mfma_t(u32x2 a, u32x2 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, a), __builtin_bit_cast(half4, b),
+                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 }
 
 // Upper part of the two-part f16 split: x with its significand cut to 11
@@ -173,21 +203,6 @@ __device__ __forceinline__ int pow2_exponent(float m) {
   return e == 0 ? 0 : min(max(e - 126, -100), 100);
 }
 __device__ __forceinline__ float exp2i(int e) { return u2f((uint32_t)(127 + e) << 23); }
-
-// Codes 8j .. 8j+7 of a qblock (BITS words, LSB-first codes) in the low
-// 8 * BITS bits of the result; for 3-bit codes bits 24..31 are left over
-// from the next group and are never read.
-template <int BITS>
-__device__ __forceinline__ uint32_t code_group(const uint32_t (&w)[BITS], int j) {
-  if constexpr (BITS == 3) {
-    if (j == 0) return w[0];
-    if (j == 1) return __builtin_amdgcn_alignbit(w[1], w[0], 24);
-    if (j == 2) return __builtin_amdgcn_alignbit(w[2], w[1], 16);
-    return w[2] >> 8;
-  } else {
-    return w[j];
-  }
-}
 
 // Code pair p (codes 2p, 2p+1) of a qblock's BITS words, LSB-first: the
 // 2 BITS-bit pair-table index (p must fold to a constant after unrolling).
@@ -291,21 +306,22 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   constexpr int PACKED = NQB * QW * 4;           // bytes per token record
   constexpr int NC = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);         // pair-table entries
+  // Pair-table copies: with 16, entry e of copy s sits at word 32 e + 2 s, so
+  // the 16 lanes of a row, each reading copy l % 16, always hit 16 distinct
+  // bank pairs whatever codes they look up (PQO3: 8 KB; PQO4 keeps one copy).
+  constexpr int PREP = BITS == 3 ? 16 : 1;
   constexpr int WT = 64;                         // tokens per wave
   constexpr int NT = WT / 16;                    // 16-token tiles per wave
   constexpr int NG = NR > 2 ? NR / 2 : 1;        // MFMA head groups: 16 rows = 4 qblocks x 2 heads x 2 parts
-  constexpr int VROW = 68;                       // code-group row pitch: a half-wave's 32 writes on 32 banks
   // per-wave staging (32-bit words)
-  constexpr int XW = NQB * WT * NR;              // K partial scores [qblock][token][head]
-  constexpr int VW = 16 * VROW;                  // V code groups [group][token]
-  constexpr int RA = XW > VW ? XW : VW;          // the V groups reuse the K partials' space
+  constexpr int RA = NQB * WT * NR;              // K partial scores [qblock][token][head]
   constexpr int PW = NR * WT;                    // softmax numerators [head][token]
   constexpr int SW = NQB * WT;                   // |V scale| * 2^-Ev [qblock][token]
   constexpr int CW = (NR * HD + 2 * NR + 1 + 3) & ~3;  // combine record: acc [head][d], m, l, 2^Ev
   constexpr int WSTAGE = RA + PW + SW + CW;
   // LDS carve (32-bit words)
-  constexpr int OFF_PAIR = 0;                    // uint2 [NPAIR]
-  constexpr int OFF_QA = OFF_PAIR + 2 * NPAIR;   // u32x4 [NG][8][64]: key-pass query operands
+  constexpr int OFF_PAIR = 0;                    // uint2 [NPAIR][PREP]
+  constexpr int OFF_QA = OFF_PAIR + 2 * NPAIR * PREP;  // u32x4 [NG][8][64]: key-pass query operands
   constexpr int OFF_Q = OFF_QA + NG * 8 * 64 * 4;
   constexpr int OFF_QMAX = OFF_Q + NR * HD;      // [2 NR] max |qt| per half head
   constexpr int OFF_W = OFF_QMAX + 8;
@@ -326,6 +342,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;  // matrix-core column / row group of this lane
+  const uint2 *s_pair_l = s_pair + (l16 % PREP);  // this lane's copy: entry e at s_pair_l[e * PREP]
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int t0 = c * CH;
   const long long rec0 = (long long)b * a.seq_stride + (long long)g * a.kv_head_stride;
@@ -348,16 +365,16 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int nchunks = (len + CH - 1) / CH;
   float *stage = lds + OFF_W + wave * WSTAGE;
   uint32_t *st_x = reinterpret_cast<uint32_t *>(stage);  // [NQB][WT][NR] K partial scores (f32 bits)
-  uint32_t *st_vt = st_x;                                 // [16][VROW] V code groups, after the K pass
   float *st_p = stage + RA;                               // [NR][WT]
   float *st_s = st_p + PW;                                // [NQB][WT]
   float *comb = st_s + SW;                                // [NR][HD], m[NR], l[NR], 2^Ev
 
   // ---- pair table from the constant codebook ----
-  if (tid < NPAIR) {
-    const float c0 = pqo_centroid<BITS>(tid & (NC - 1)), c1 = pqo_centroid<BITS>(tid >> BITS);
+  for (int it = tid; it < NPAIR * PREP; it += kThreads) {
+    const int e = it / PREP;
+    const float c0 = pqo_centroid<BITS>(e & (NC - 1)), c1 = pqo_centroid<BITS>(e >> BITS);
     const float h0 = split_hi(c0), h1 = split_hi(c1);
-    s_pair[tid] = make_uint2(pack_f16(h0, h1), pack_f16(c0 - h0, c1 - h1));
+    s_pair[it] = make_uint2(pack_f16(h0, h1), pack_f16(c0 - h0, c1 - h1));
   }
   if (tid == 0) s_ready = 0;
 
@@ -475,8 +492,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     for (int gi = 0; gi < NG; gi++) qa[gi] = s_qa[(gi * 8 + j) * 64 + lane];
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
-      const uint2 e0 = s_pair[pair_code<BITS>(kq[tt], 2 * j)];
-      const uint2 e1 = s_pair[pair_code<BITS>(kq[tt], 2 * j + 1)];
+      const uint2 e0 = s_pair_l[pair_code<BITS>(kq[tt], 2 * j) * PREP];
+      const uint2 e1 = s_pair_l[pair_code<BITS>(kq[tt], 2 * j + 1) * PREP];
       const u32x4 kb = {e0.x, e0.y, e1.x, e1.y};
 #pragma unroll
       for (int gi = 0; gi < NG; gi++) dk[tt][gi] = mfma(qa[gi], kb, dk[tt][gi]);
@@ -536,14 +553,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < NR; r++) l_w[r] = wave_sum(p[r]);
 
-  // ---- V codes to LDS in [code group][token] order, scales * 2^-Ev ----
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();  // every lane has read its K partials
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-  for (int tt = 0; tt < NT; tt++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) st_vt[(4 * lg + j) * VROW + 16 * tt + l16] = code_group<BITS>(vq[tt], j);
+  // ---- V scales * 2^-Ev to LDS (lane = token) ----
   float sv[NQB];
   float smax = 0.f;
 #pragma unroll
@@ -560,74 +570,62 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- V pass.  Four 16-token steps; the value operand of lane (m, lg) at
-  // step ks is (hi pair, lo pair) of tokens (t0, t1) and of (t2, t3),
-  // t_i = 16 ks + 4 lg + i, for element 16 et + m, so the weight operand
-  // holds each token's weight twice: (w0, w1, w0, w1, w2, w3, w2, w3) for
-  // column n = (qblock bq, head 2 gi + brl, part) ----
+  // ---- V pass.  Weight operands, one per 16-token tile: lane (n, kg) holds
+  // for column n = (qblock bq, head 2 gi + brl, part) the weights of tokens
+  // 4 kg + (0, 1, 0, 1, 2, 3, 2, 3) of the tile (each twice: against the hi
+  // and the lo part of the value) ----
   const int bq = l16 >> 2, brl = (l16 >> 1) & 1, bpart = l16 & 1;
-  u32x4 bw[4][NG];
+  u32x4 bw[NT][NG];
 #pragma unroll
-  for (int ks = 0; ks < 4; ks++) {
+  for (int tt = 0; tt < NT; tt++) {
 #pragma unroll
     for (int gi = 0; gi < NG; gi++) {
       const int r = min(2 * gi + brl, NR - 1);  // NR == 1: the second head's columns are never read
-      const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * ks + 4 * lg);
-      const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * ks + 4 * lg);
+      const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * tt + 4 * lg);
+      const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * tt + 4 * lg);
       const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
       const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
       const uint32_t w01 = bpart ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
       const uint32_t w23 = bpart ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
-      bw[ks][gi] = u32x4{w01, w01, w23, w23};
+      bw[tt][gi] = u32x4{w01, w01, w23, w23};
     }
   }
-  // Element tiles: A row m = element 16 et + m.
-  // Two tiles (one qblock) per round: all eight code-word reads go out first,
-  // then all sixteen pair-table reads, then the MFMAs, so each wave keeps
-  // several LDS round trips in flight.
-  const int aoff = BITS * (l16 & 7), arow = l16 >> 3;
+  // The value codes are decoded where they were loaded (lane (t, q): qblock
+  // q of token t), two pair-table reads per 4-element slice j as for the
+  // keys, and turned to element-major order on the matrix core: V_hi x I
+  // and V_lo x I (16 x 16 x 16, exact) leave lane (n, g) with element
+  // (qblock n / 4, 4 j + n % 4) of tokens 4 g .. 4 g + 3, which is the value
+  // operand's row n.  D then holds rows = those elements, columns (qblock,
+  // head, part); a lane's rows count only under its own qblock's columns.
+  const int idk = l16 - 4 * lg;  // the identity's single 1 in this lane, if 0 <= idk < 4
+  const uint32_t one = 0x3C00u << (16 * (idk & 1));
+  const u32x2 ident = {(idk == 0 || idk == 1) ? one : 0u, (idk == 2 || idk == 3) ? one : 0u};
 #pragma unroll
-  for (int e2 = 0; e2 < 8; e2 += 2) {
-    u32x4 u[2][4];
+  for (int j = 0; j < 8; j++) {
+    f32x4 dv[NG];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int gi = 0; gi < NG; gi++) dv[gi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ks++)
-        u[h][ks] = *reinterpret_cast<const u32x4 *>(st_vt + (2 * (e2 + h) + arow) * VROW + 16 * ks + 4 * lg);
-    u32x4 va[2][4];
+    for (int tt = 0; tt < NT; tt++) {
+      const uint2 e0 = s_pair_l[pair_code<BITS>(vq[tt], 2 * j) * PREP];
+      const uint2 e1 = s_pair_l[pair_code<BITS>(vq[tt], 2 * j + 1) * PREP];
+      const f32x4 th = mfma_t(u32x2{e0.x, e1.x}, ident);
+      const f32x4 tl = mfma_t(u32x2{e0.y, e1.y}, ident);
+      const u32x4 va = {pack_f16(th[0], th[1]), pack_f16(tl[0], tl[1]), pack_f16(th[2], th[3]),
+                        pack_f16(tl[2], tl[3])};
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+      for (int gi = 0; gi < NG; gi++) dv[gi] = mfma(va, bw[tt][gi], dv[gi]);
+    }
+    // lane (n, lg) holds column n at elements (qblock lg, 4 j + i); the parts
+    // of one head sit in lanes n and n ^ 1
 #pragma unroll
-      for (int ks = 0; ks < 4; ks++) {
-        const u32x4 w = u[h][ks];
-        const uint32_t c0 = __builtin_amdgcn_ubfe(w.x, aoff, BITS), c1 = __builtin_amdgcn_ubfe(w.y, aoff, BITS);
-        const uint32_t c2 = __builtin_amdgcn_ubfe(w.z, aoff, BITS), c3 = __builtin_amdgcn_ubfe(w.w, aoff, BITS);
-        const uint2 e01 = s_pair[c0 | (c1 << BITS)];
-        const uint2 e23 = s_pair[c2 | (c3 << BITS)];
-        va[h][ks] = u32x4{e01.x, e01.y, e23.x, e23.y};
-      }
+    for (int gi = 0; gi < NG; gi++) {
+      f32x4 o;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int et = e2 + h;
-      f32x4 dv[NG];
-#pragma unroll
-      for (int gi = 0; gi < NG; gi++) dv[gi] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) dv[gi] = mfma(va[h][ks], bw[ks][gi], dv[gi]);
-      // lane (n, lg) holds column n at elements 16 et + 4 lg + i; the parts
-      // of one head sit in lanes n and n ^ 1, and only this tile's qblock counts
-#pragma unroll
-      for (int gi = 0; gi < NG; gi++) {
-        f32x4 o;
-#pragma unroll
-        for (int i = 0; i < 4; i++) o[i] = dpp_quad_xor1(dv[gi][i]) + dv[gi][i];
-        __builtin_amdgcn_sched_barrier(0);  // the sums stay outside the store's branch (DPP adds)
-        const int r = 2 * gi + brl;
-        if (bpart == 0 && bq == (et >> 1) && r < NR)
-          *reinterpret_cast<f32x4 *>(comb + r * HD + 16 * et + 4 * lg) = o;
-      }
+      for (int i = 0; i < 4; i++) o[i] = dpp_quad_xor1(dv[gi][i]) + dv[gi][i];
+      __builtin_amdgcn_sched_barrier(0);  // the sums stay outside the store's branch (DPP adds)
+      const int r = 2 * gi + brl;
+      if (bpart == 0 && bq == lg && r < NR) *reinterpret_cast<f32x4 *>(comb + r * HD + 32 * lg + 4 * j) = o;
     }
   }
   if (lane == 0) {
@@ -639,28 +637,53 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     comb[NR * HD + 2 * NR] = exp2i(ev);
   }
 
-  // ---- combine the 16 waves' records ----
+  // ---- combine the 16 waves' records: CP consecutive lanes share one output
+  // (head r, element d), each folding kWaves / CP waves, then a DPP reduction
+  // over the CP lanes ----
   __syncthreads();
-  if (tid < NR * HD) {
-    const int r = tid / HD, d = tid % HD;
-    constexpr int COMB = RA + PW + SW;  // offset of the record inside a wave's staging
+  {
+    constexpr int OUTS = NR * HD;
+    constexpr int CP = kThreads / OUTS;  // 8, 4 or 2 lanes per output
+    constexpr int WPP = kWaves / CP;
+    constexpr int COMB = RA + PW + SW;   // offset of the record inside a wave's staging
+    static_assert(CP == 2 || CP == 4 || CP == 8, "lanes per output");
+    const int o = tid / CP, part = tid % CP;
+    const int r = o / HD, d = o % HD;
+    float mw[WPP];
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds[OFF_W + w * WSTAGE + COMB + NR * HD + r]);
+    for (int i = 0; i < WPP; i++) {
+      mw[i] = lds[OFF_W + (part + i * CP) * WSTAGE + COMB + NR * HD + r];
+      M = fmaxf(M, mw[i]);
+    }
+    M = fmaxf(M, dpp_quad_xor1(M));
+    if constexpr (CP >= 4) M = fmaxf(M, dpp_quad_xor2(M));
+    if constexpr (CP == 8) M = fmaxf(M, __shfl_xor(M, 4, 64));
     float A = 0.f, L = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-      const float *cw = lds + OFF_W + w * WSTAGE + COMB;
-      const float mw = cw[NR * HD + r];
-      const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+    for (int i = 0; i < WPP; i++) {
+      const float *cw = lds + OFF_W + (part + i * CP) * WSTAGE + COMB;
+      const float f = (mw[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw[i] - M);
       A = __builtin_fmaf(cw[r * HD + d], f * cw[NR * HD + 2 * NR], A);
       L = __builtin_fmaf(cw[NR * HD + NR + r], f, L);
     }
-    const long long bh = (long long)b * a.num_heads + g * NR + r;
-    st_agent(&a.po[(bh * a.P + c) * HD + d], A);
-    if (d == 0) {
-      st_agent(&a.pm[bh * a.P + c], M);
-      st_agent(&a.ps[bh * a.P + c], L);
+    A += dpp_quad_xor1(A);
+    L += dpp_quad_xor1(L);
+    if constexpr (CP >= 4) {
+      A += dpp_quad_xor2(A);
+      L += dpp_quad_xor2(L);
+    }
+    if constexpr (CP == 8) {
+      A += __shfl_xor(A, 4, 64);
+      L += __shfl_xor(L, 4, 64);
+    }
+    if (part == 0) {
+      const long long bh = (long long)b * a.num_heads + g * NR + r;
+      st_agent(&a.po[(bh * a.P + c) * HD + d], A);
+      if (d == 0) {
+        st_agent(&a.pm[bh * a.P + c], M);
+        st_agent(&a.ps[bh * a.P + c], L);
+      }
     }
   }
 
