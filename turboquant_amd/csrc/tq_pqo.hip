@@ -96,7 +96,48 @@ __device__ __forceinline__ uint32_t bucket_sorted(float x, const float (&U)[(1 <
   }
 }
 
-// MaxNorm scale, exact bucketize and pack of one rotated block.
+// The code bits of x, most significant first, by the same binary search as
+// bucket_sorted.
+template <int BITS>
+__device__ __forceinline__ void bucket_bits(float x, const float (&U)[(1 << BITS) - 1], bool (&bit)[BITS]) {
+  if constexpr (BITS == 2) {
+    bit[0] = x >= U[1];
+    bit[1] = x >= (bit[0] ? U[2] : U[0]);
+  } else if constexpr (BITS == 3) {
+    bit[0] = x >= U[3];
+    bit[1] = x >= (bit[0] ? U[5] : U[1]);
+    const float lo = bit[1] ? U[2] : U[0], hi = bit[1] ? U[6] : U[4];
+    bit[2] = x >= (bit[0] ? hi : lo);
+  } else {
+    bit[0] = x >= U[7];
+    bit[1] = x >= (bit[0] ? U[11] : U[3]);
+    const float l1 = bit[1] ? U[5] : U[1], h1 = bit[1] ? U[13] : U[9];
+    bit[2] = x >= (bit[0] ? h1 : l1);
+    const float a0 = bit[2] ? U[2] : U[0], a1 = bit[2] ? U[6] : U[4], a2 = bit[2] ? U[10] : U[8],
+                a3 = bit[2] ? U[14] : U[12];
+    const float l0 = bit[1] ? a1 : a0, h0 = bit[1] ? a3 : a2;
+    bit[3] = x >= (bit[0] ? h0 : l0);
+  }
+}
+
+// acc = 2 acc + bit, with the bit taken straight from the comparison's lane
+// mask as the carry-in of one v_addc (LLVM would rebuild it as a select, a
+// shift and an or).  The s_nop covers the wait after a VALU write of the
+// mask's SGPRs.
+__device__ __forceinline__ uint32_t push_bit(uint32_t acc, bool bit) {
+  uint32_t r;
+  uint64_t carry_out;
+  asm("s_nop 1\n\tv_addc_co_u32_e64 %0, %1, %2, %2, %3"
+      : "=v"(r), "=s"(carry_out)
+      : "v"(acc), "s"(__builtin_amdgcn_ballot_w64(bit)));
+  return r;
+}
+
+// MaxNorm scale, exact bucketize and pack of one rotated block.  The packed
+// LSB-first bitstream is built from its most significant bit down: code j's
+// bits go to stream bits 3j+2 .. 3j (for 3-bit codes) and each 32-bit word
+// is the last 32 bits pushed into it, so codes that straddle words need no
+// special case.
 template <int BITS>
 __device__ __forceinline__ float quantize_block(const float (&r)[32], const QuantConsts &k,
                                                 uint32_t (&w)[Packed<BITS>::kWords]) {
@@ -112,8 +153,22 @@ __device__ __forceinline__ float quantize_block(const float (&r)[32], const Quan
     float U[NB];
 #pragma unroll
     for (int t = 0; t < NB; t++) U[t] = div_threshold(k.mu[t], (k.strict_mask >> t) & 1u, s);
+    uint32_t acc[Packed<BITS>::kWords];
 #pragma unroll
-    for (int j = 0; j < 32; j++) idx[j] = bucket_sorted<BITS>(r[j], U);
+    for (int q = 0; q < Packed<BITS>::kWords; q++) acc[q] = 0;
+#pragma unroll
+    for (int j = 31; j >= 0; j--) {
+      bool bit[BITS];
+      bucket_bits<BITS>(r[j], U, bit);
+#pragma unroll
+      for (int t = 0; t < BITS; t++) {
+        const int pos = j * BITS + (BITS - 1 - t);
+        acc[pos >> 5] = push_bit(acc[pos >> 5], bit[t]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < Packed<BITS>::kWords; q++) w[q] = acc[q];
+    return s;
   } else {
     // Infinite scale (an infinite input): follow the reference's division.
 #pragma unroll
