@@ -47,6 +47,12 @@ enum {
 /* Element types of activations crossing the boundary. */
 enum { TQ_DTYPE_F32 = 0, TQ_DTYPE_BF16 = 1, TQ_DTYPE_F16 = 2 };
 
+/* QuantNormMode (src/cache/config.rs:20-31).  MaxNorm is the default. */
+enum { TQ_NORM_MAXNORM = 0, TQ_NORM_L2NORM = 1 };
+/* CacheConfig::outlier_blocks = usize::MAX: PQO, every block on the outlier
+ * codebook.  0 selects the standard codebook (PQ, and TQ with QJL). */
+#define TQ_OUTLIER_ALL ((size_t)-1)
+
 /* Message of the calling thread's last failed call ("" if none). */
 const char *tq_last_error(void);
 /* Library version string. */
@@ -81,9 +87,13 @@ int tq_pack_indices(const uint8_t *indices, uint8_t *packed_out, int num_vectors
  * q [num_attention_heads][head_dim] f32, out the same shape.  partial_out
  * [num_attention_heads * num_partitions][head_dim], partial_max/sum
  * [num_attention_heads * num_partitions] are caller scratch, with
- * num_partitions = ceil(kv_len / 512) as in cuda/attention.rs:13,70.  The QJL
- * arguments must be null / 0: the reference never enables them
- * (cuda/attention.rs:153-157). */
+ * num_partitions = ceil(kv_len / 512) as in cuda/attention.rs:13,70.  The
+ * codebook and sign pattern arguments are validated non-null and the PQO
+ * constants applied.  qjl_enabled = 1 attends TQ records (standard
+ * (bits-1)-bit codebook) with the QJL correction of the kernel's dormant
+ * branch (tq_attention_kernel.cu:192-231): qjl_signs [num_kv_heads]
+ * [kv_stride][head_dim/8], qjl_residual_norms [num_kv_heads][kv_stride] f16,
+ * rq [num_attention_heads][head_dim] = R q. */
 int tq_fused_attention(const float *q, const uint8_t *k_indices, const uint16_t *k_scales,
                        const uint8_t *v_indices, const uint16_t *v_scales,
                        const float *codebook, const float *sign_pattern, float *output,
@@ -129,6 +139,27 @@ int tq_pqo_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *sc
                                  long long cache_head_stride, int num_heads, int tokens, void *out,
                                  int out_dtype, int head_dim, int bits, hipStream_t stream);
 
+/* The cache codec of any supported CacheConfig mode: polar_quantize /
+ * polar_dequantize (quantize_tensor.rs:40-76, 179-220) with
+ * outlier_blocks = TQ_OUTLIER_ALL (PQO: bits-bit outlier codebook, negative
+ * scales) or 0 (PQ and TQ: the standard (bits-1)-bit codebook in bits-wide
+ * slots, positive scales), norm_mode TQ_NORM_MAXNORM.  The tq_pqo_* entries
+ * above are these with TQ_OUTLIER_ALL. */
+int tq_polar_quantize(const void *x, int x_dtype, uint8_t *packed_out, uint16_t *scales_out,
+                      size_t num_vectors, int head_dim, int bits, size_t outlier_blocks,
+                      int norm_mode, hipStream_t stream);
+int tq_polar_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
+                        size_t num_vectors, int head_dim, int bits, size_t outlier_blocks,
+                        int norm_mode, hipStream_t stream);
+int tq_polar_quantize_to_cache(const void *x, int x_dtype, int num_heads, int tokens,
+                               uint8_t *packed_cache, uint16_t *scales_cache,
+                               long long cache_head_stride, long long cache_offset, int head_dim,
+                               int bits, size_t outlier_blocks, int norm_mode, hipStream_t stream);
+int tq_polar_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *scales_cache,
+                                   long long cache_head_stride, int num_heads, int tokens,
+                                   void *out, int out_dtype, int head_dim, int bits,
+                                   size_t outlier_blocks, int norm_mode, hipStream_t stream);
+
 /* Workspace for tq_pqo_decode_attention (partials + merge counters). */
 size_t tq_attention_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
                                    int max_kv_len);
@@ -154,6 +185,25 @@ int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices
                             int max_kv_len, long long kv_head_stride, long long seq_stride,
                             float softmax_scale, void *out, int out_dtype, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
+
+/* Fused decode attention over any cache mode: outlier_blocks TQ_OUTLIER_ALL
+ * (PQO) or 0 (PQ), norm_mode TQ_NORM_MAXNORM; arguments as
+ * tq_pqo_decode_attention.  qjl_signs non-null selects TQ: the logits get
+ * the QJL correction softmax_scale * |r_t| sqrt(pi/2)/sqrt(d) *
+ * sum_j rq_j (2 b_tj - 1) (tq_attention_kernel.cu:192-231; tq.rs:185-253),
+ * with rq [batch][num_heads][head_dim] f32 = R q (tq_qjl_project),
+ * qjl_signs [..records..][head_dim/8] and qjl_norms [..records..] f16 laid
+ * out by record like the codes.  Replaces TqCache::decode's dequantize +
+ * logit bias + SDPA (tq.rs:275-297). */
+int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
+                              const uint16_t *k_scales, const uint8_t *v_indices,
+                              const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                              const uint16_t *qjl_norms, const int *kv_lens, int batch,
+                              int num_heads, int num_kv_heads, int head_dim, int bits,
+                              size_t outlier_blocks, int norm_mode, int max_kv_len,
+                              long long kv_head_stride, long long seq_stride, float softmax_scale,
+                              void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+                              hipStream_t stream);
 
 /* =========================================================================
  * Core full-vector codec (TurboQuantConfig{bits, dim, rotation_seed}),
@@ -228,41 +278,122 @@ int tq_qjl_weighted_values(const uint8_t *polar_packed, const uint16_t *polar_sc
                            int polar_bits, int dim, uint64_t rotation_seed, float *out,
                            void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---- TqCache building blocks (reference src/cache/tq.rs) ----
+ * head_dim 64, 128 or 256 (32 also for the sign matrix). */
+
+/* The d x d sign bits of the Rademacher matrix R (qjl.rs:143-189) for
+ * qjl_seed: bits_out[j * dim/32 + w] bit b set <=> R[j][32 w + b] < 0
+ * (build_rademacher_matrix, precomputed/mod.rs:116-125). */
+int tq_qjl_sign_matrix(uint32_t *bits_out, int dim, uint64_t qjl_seed, hipStream_t stream);
+
+/* compute_qjl_signs_and_norms for keys just stored in a TQ cache
+ * (tq.rs:154-182, 373-412): k [num_heads][tokens][head_dim] as appended;
+ * its records h * cache_head_stride + cache_offset + t are dequantized, the
+ * residual r = k - k_hat gives norms_cache[record] = f16(|r|) and
+ * signs_cache[record][head_dim/8] = bits (R r)_j >= 0 (LSB first). */
+int tq_qjl_cache_sketch(const void *k, int k_dtype, int num_heads, int tokens,
+                        const uint8_t *packed_cache, const uint16_t *scales_cache,
+                        const uint32_t *sign_matrix, uint8_t *signs_cache, uint16_t *norms_cache,
+                        long long cache_head_stride, long long cache_offset, int head_dim, int bits,
+                        size_t outlier_blocks, int norm_mode, hipStream_t stream);
+
+/* rq[row] = R q[row] (precompute_query_projections, qjl.rs:488-492; r_q of
+ * tq.rs:233-234), q [num_rows][dim] in q_dtype, rq f32. */
+int tq_qjl_project(const void *q, int q_dtype, const uint32_t *sign_matrix, float *rq,
+                   size_t num_rows, int dim, hipStream_t stream);
+
+/* f32(sqrt(pi/2)) / sqrt(head_dim), the per-norm factor of tq.rs:213-214. */
+float tq_qjl_bias_scale(int head_dim);
+
+/* compute_logit_bias (tq.rs:185-253): out [num_q_heads][q_len][kv_len] in
+ * out_dtype = (sum_j rq[h][i][j] (2 b_tj - 1)) * (|r_t| * tq_qjl_bias_scale),
+ * query head h reading KV head h / (num_q_heads / num_kv_heads);
+ * rq [num_q_heads][q_len][head_dim] f32 from tq_qjl_project. */
+int tq_qjl_logit_bias(const float *rq, int num_q_heads, int q_len, const uint8_t *signs_cache,
+                      const uint16_t *norms_cache, int num_kv_heads, int kv_len,
+                      long long cache_head_stride, int head_dim, void *out, int out_dtype,
+                      hipStream_t stream);
+
 /* =========================================================================
- * Device-resident PQO KV cache: PqoCache with the CompressedKVCache contract
- * (pqo.rs:21-236) over a CompressedStorage (storage.rs:24-203).  The handle
- * owns its device buffers.  K/V inputs are one sequence's
- * [num_kv_heads][tokens][head_dim] (the reference's [1, H, T, D]).
+ * Device-resident KV caches with the CompressedKVCache contract (trait of
+ * mistralrs-kv-cache, methods as used in pqo.rs:183-236 and tq.rs:256-324):
+ * PqoCache (pqo.rs:21-236; outlier_blocks TQ_OUTLIER_ALL = PQO, 0 = PQ) and
+ * TqCache (tq.rs: PQ codes plus the QJL sketch of every key's residual,
+ * qjl = 1), over a CompressedStorage (storage.rs:24-203).  The handle owns
+ * its device buffers.  K/V inputs are one sequence's
+ * [num_kv_heads][tokens][head_dim] (the reference's [1, H, T, D]); queries
+ * [num_q_heads][q_len][head_dim] ([1, Hq, q_len, D]).
  * ========================================================================= */
 
-/* PqoCache::new(CacheConfig{bits, head_dim, num_kv_heads, num_layers, PQO}). */
-int tq_pqo_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, void **cache);
-void tq_pqo_cache_destroy(void *cache);
+/* PqoCache::new / TqCache::new (CacheConfig{bits, head_dim, num_kv_heads,
+ * num_layers, norm_mode, outlier_blocks}). */
+int tq_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, int norm_mode,
+                    size_t outlier_blocks, int qjl, void **cache);
+void tq_cache_destroy(void *cache);
+/* 1 for a TqCache handle. */
+int tq_cache_is_tq(void *cache);
 
-/* CompressedKVCache::prefill (pqo.rs:184-200): stores k, v; on the layer's
- * first call sets *returned_originals = 1 (the caller's k, v are the result),
- * otherwise writes the whole dequantized layer [num_kv_heads][seq_len][head_dim]
- * into k_out, v_out in `dtype`. */
+/* CompressedKVCache::prefill (pqo.rs:184-200, tq.rs:258-273): stores k, v;
+ * on the layer's first call sets *returned_originals = 1 (the caller's k, v
+ * are the result), otherwise writes the whole dequantized layer
+ * [num_kv_heads][seq_len][head_dim] into k_out, v_out in `dtype`.  A TqCache
+ * also writes logit_bias_out [num_q_heads][q_len][seq_len] in q_dtype
+ * (compute_logit_bias, tq.rs:185-253); q is unused by a PqoCache. */
+int tq_cache_prefill(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,
+                     const void *q, int q_dtype, int num_q_heads, int q_len, void *k_out,
+                     void *v_out, int *returned_originals, void *logit_bias_out,
+                     hipStream_t stream);
+
+/* CompressedKVCache::decode on the fused path (DecodeOutput::Fused): stores
+ * k, v, then out [num_q_heads][head_dim] = attention of q [num_q_heads]
+ * [head_dim] over the whole layer; a TqCache adds the QJL correction to the
+ * logits inline (replacing tq.rs:275-297's dequantize + logit bias). */
+int tq_cache_decode(void *cache, int layer, const void *k, const void *v, int kv_dtype, int tokens,
+                    const void *q, int q_dtype, int num_q_heads, float softmax_scale, void *out,
+                    int out_dtype, hipStream_t stream);
+
+/* CompressedKVCache::decode on the dequantized path (DecodeOutput::
+ * Dequantized, pqo.rs:218-221, tq.rs:275-297): stores k, v, writes the whole
+ * layer into k_out, v_out and, for a TqCache, logit_bias_out [num_q_heads]
+ * [q_len][seq_len] in q_dtype. */
+int tq_cache_decode_dequantized(void *cache, int layer, const void *k, const void *v, int dtype,
+                                int tokens, const void *q, int q_dtype, int num_q_heads, int q_len,
+                                void *k_out, void *v_out, void *logit_bias_out, hipStream_t stream);
+
+/* seq_len / reset / memory_usage (pqo.rs:224-236, tq.rs:299-323,
+ * storage.rs:175-202). */
+size_t tq_cache_seq_len(void *cache, int layer);
+int tq_cache_reset(void *cache);
+size_t tq_cache_memory_usage(void *cache);
+/* Records per head allocated for a layer (grows to needed + max(needed/4, 128)). */
+size_t tq_cache_capacity(void *cache, int layer);
+/* Copies a layer's stored records [num_kv_heads][seq_len] (codes, scales and,
+ * for a TqCache, signs and norms when non-null) into contiguous buffers. */
+int tq_cache_read_layer(void *cache, int layer, uint8_t *k_indices, uint16_t *k_scales,
+                        uint8_t *v_indices, uint16_t *v_scales, uint8_t *qjl_signs,
+                        uint16_t *qjl_norms, hipStream_t stream);
+/* Device views of a layer's buffers (CompressedStorage::k_indices etc.; the
+ * QJL ones null for a PqoCache). */
+int tq_cache_buffers(void *cache, int layer, uint8_t **k_indices, uint16_t **k_scales,
+                     uint8_t **v_indices, uint16_t **v_scales, uint8_t **qjl_signs,
+                     uint16_t **qjl_norms);
+
+/* PqoCache with the PQO config / TqCache with the TQ config (MaxNorm). */
+int tq_pqo_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, void **cache);
+int tq_tq_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, void **cache);
+/* The tq_cache_* calls above for PqoCache handles, without the query. */
+void tq_pqo_cache_destroy(void *cache);
 int tq_pqo_cache_prefill(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,
                          void *k_out, void *v_out, int *returned_originals, hipStream_t stream);
-
-/* CompressedKVCache::decode (pqo.rs:202-222) on the fused path: stores k, v,
- * then out [num_q_heads][head_dim] = attention of q over the whole layer. */
 int tq_pqo_cache_decode(void *cache, int layer, const void *k, const void *v, int kv_dtype, int tokens,
                         const void *q, int q_dtype, int num_q_heads, float softmax_scale, void *out,
                         int out_dtype, hipStream_t stream);
-
-/* seq_len / reset / memory_usage (pqo.rs:224-236, storage.rs:175-202). */
 size_t tq_pqo_cache_seq_len(void *cache, int layer);
 int tq_pqo_cache_reset(void *cache);
 size_t tq_pqo_cache_memory_usage(void *cache);
-/* Records per head allocated for a layer (grows to needed + max(needed/4, 128)). */
 size_t tq_pqo_cache_capacity(void *cache, int layer);
-/* Copies a layer's stored records [num_kv_heads][seq_len] (codes and scales)
- * into contiguous caller buffers. */
 int tq_pqo_cache_read_layer(void *cache, int layer, uint8_t *k_indices, uint16_t *k_scales,
                             uint8_t *v_indices, uint16_t *v_scales, hipStream_t stream);
-/* Device views of a layer's buffers (CompressedStorage::k_indices etc.). */
 int tq_pqo_cache_buffers(void *cache, int layer, uint8_t **k_indices, uint16_t **k_scales,
                          uint8_t **v_indices, uint16_t **v_scales);
 

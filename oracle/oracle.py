@@ -53,6 +53,12 @@ def _load():
         "tqo_pqo_quantize": (C.c_int, [C.c_int, _sz, _sz, _f32p, _u8p, _u16p]),
         "tqo_pqo_dequantize": (C.c_int, [C.c_int, _sz, _sz, _u8p, _u16p, _f32p]),
         "tqo_attention_dense": (C.c_int, [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_float, _f32p]),
+        "tqo_polar_quantize": (C.c_int, [C.c_int, _sz, _sz, _sz, _f32p, _u8p, _u16p]),
+        "tqo_polar_dequantize": (C.c_int, [C.c_int, _sz, _sz, _sz, _u8p, _u16p, _f32p]),
+        "tqo_tq_signs_norms": (C.c_int, [_sz, _sz, _f32p, _f32p, _u8p, _u16p]),
+        "tqo_tq_logit_bias": (C.c_int, [_sz, _sz, _sz, _sz, _sz, _f32p, _u8p, _u16p, _f32p]),
+        "tqo_attention_dense_bias": (C.c_int, [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, C.c_float,
+                                               _f32p]),
         "tqo_qjl_mix_seed": (_u64, [_u64, _sz]),
         "tqo_rademacher_sign": (C.c_float, [_u64, _sz, _sz]),
         "tqo_generate_rademacher_row": (None, [_sz, _u64, _sz, _f32p]),
@@ -252,6 +258,60 @@ def pqo_dequantize(bits: int, packed: np.ndarray, scales: np.ndarray, head_dim: 
     n = packed.size // (head_dim * bits // 8)
     out = np.zeros((n, head_dim), np.float32)
     _check(lib.tqo_pqo_dequantize(bits, n, head_dim, packed, scales, out))
+    return out
+
+
+OUTLIER_ALL = (1 << 64) - 1
+
+
+def polar_quantize(bits: int, outlier_blocks: int, x: np.ndarray, head_dim: int):
+    x = _c(x, np.float32).reshape(-1, head_dim)
+    n = x.shape[0]
+    packed = np.zeros((n, head_dim * bits // 8), np.uint8)
+    scales = np.zeros((n, head_dim // 32), np.uint16)
+    _check(lib.tqo_polar_quantize(bits, outlier_blocks, n, head_dim, x, packed, scales))
+    return packed, scales
+
+
+def polar_dequantize(bits: int, outlier_blocks: int, packed: np.ndarray, scales: np.ndarray, head_dim: int):
+    packed = _c(packed, np.uint8)
+    scales = _c(scales, np.uint16)
+    n = packed.size // (head_dim * bits // 8)
+    out = np.zeros((n, head_dim), np.float32)
+    _check(lib.tqo_polar_dequantize(bits, outlier_blocks, n, head_dim, packed, scales, out))
+    return out
+
+
+def tq_signs_norms(x: np.ndarray, xhat: np.ndarray):
+    """(signs [N, D/8] u8, norms [N] f16 bits) of the residuals x - xhat (tq.rs:373-412)."""
+    x = _c(x, np.float32)
+    xhat = _c(xhat, np.float32)
+    n, d = x.shape
+    signs = np.zeros((n, d // 8), np.uint8)
+    norms = np.zeros(n, np.uint16)
+    _check(lib.tqo_tq_signs_norms(n, d, x, xhat, signs, norms))
+    return signs, norms
+
+
+def tq_logit_bias(q: np.ndarray, signs: np.ndarray, norms: np.ndarray) -> np.ndarray:
+    """q [Hq, q_len, D]; signs [Hkv, T, D/8]; norms [Hkv, T] f16 bits -> [Hq, q_len, T] f32."""
+    q = _c(q, np.float32)
+    signs = _c(signs, np.uint8)
+    norms = _c(norms, np.uint16)
+    hq, ql, d = q.shape
+    hkv, t = norms.shape
+    out = np.zeros((hq, ql, t), np.float32)
+    _check(lib.tqo_tq_logit_bias(hq, hkv, d, ql, t, q, signs, norms, out))
+    return out
+
+
+def attention_dense_bias(q, k, v, bias, softmax_scale: float) -> np.ndarray:
+    """softmax(scale * (q K^T + bias)) V; q [H, D]; k, v [Hkv, T, D]; bias [H, T]."""
+    q, k, v, bias = (_c(a, np.float32) for a in (q, k, v, bias))
+    h, d = q.shape
+    hkv, t, _ = k.shape
+    out = np.zeros((h, d), np.float32)
+    _check(lib.tqo_attention_dense_bias(h, hkv, d, t, q, k, v, bias, softmax_scale, out))
     return out
 
 

@@ -637,6 +637,200 @@ int tqo_pqo_dequantize(int bits, size_t n, size_t head_dim, const uint8_t *packe
     return TQO_OK;
 }
 
+/* polar_quantize for the cache modes (quantize_tensor.rs:40-76): the
+   MaxNorm scale divides by the outlier codebook's largest centroid
+   (precomputed/mod.rs:78); bucketize_blocks (:118-150) sends the first
+   n * min(outlier_blocks, nb) rows of the [n * nb, 32] block matrix to the
+   outlier boundaries and the rest to the standard (bits - 1)-bit ones; the
+   scale sign is -1 for the first min(outlier_blocks, nb) blocks of every
+   vector (build_scale_sign_tensor, precomputed/mod.rs:102-114); codes are
+   packed bits-wide (:73).  For outlier_blocks 0 or >= nb the two
+   orderings agree. */
+int tqo_polar_quantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim, const float *x,
+                       uint8_t *packed_out, uint16_t *scales_out)
+{
+    if (head_dim % QBLOCK != 0 || head_dim == 0) return TQO_ERR_INVALID_ARGUMENT;
+    if (bits != 3 && bits != 4) return TQO_ERR_UNSUPPORTED_BITS;
+    float oc[16], ob[15], nc_[16], nb_[15], outer, outer_n;
+    int onc, nnc;
+    tqo_pqo_codebook(bits, oc, ob, &onc, &outer);
+    tqo_pqo_codebook(bits - 1, nc_, nb_, &nnc, &outer_n);
+    (void)oc;
+    (void)nc_;
+    const size_t nblk_v = head_dim / QBLOCK;
+    const size_t eo = outlier_blocks < nblk_v ? outlier_blocks : nblk_v;
+    const size_t rows = n * nblk_v, outlier_rows = n * eo;
+    const float mul = (float)(1.0 / (double)outer);
+    const size_t bpb = (size_t)QBLOCK * (size_t)bits / 8;
+    float r[QBLOCK];
+    uint8_t idx[QBLOCK];
+    for (size_t row = 0; row < rows; row++) {
+        tqo_pqo_rotate_block(x + row * QBLOCK, r);
+        float amax = 0.0f;
+        for (int j = 0; j < QBLOCK; j++) {
+            float a = fabsf(r[j]);
+            amax = a > amax ? a : amax;
+        }
+        float s = amax * mul;
+        if (s < MIN_NORM) s = MIN_NORM;
+        const int outlier_row = row < outlier_rows;
+        const float *bnd = outlier_row ? ob : nb_;
+        const int nbnd = outlier_row ? onc - 1 : nnc - 1;
+        for (int j = 0; j < QBLOCK; j++) {
+            float v = r[j] / s;
+            int k = 0;
+            for (int t = 0; t < nbnd; t++) k += v > bnd[t];
+            idx[j] = (uint8_t)k;
+        }
+        const float sign = (row % nblk_v) < eo ? -1.0f : 1.0f;
+        scales_out[row] = tqo_f32_to_f16(s * sign);
+        tqo_pack_indices(bits, idx, QBLOCK, packed_out + row * bpb);
+    }
+    return TQO_OK;
+}
+
+/* polar_dequantize CPU branch (quantize_tensor.rs:197-261): codebook_lookup
+   picks the outlier centroids for all-outlier configs, the standard ones
+   for outlier_blocks 0, and per block by the scale's sign otherwise (with
+   the index clamped into the standard codebook, :242-260). */
+int tqo_polar_dequantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim, const uint8_t *packed,
+                         const uint16_t *scales, float *out)
+{
+    if (head_dim % QBLOCK != 0 || head_dim == 0) return TQO_ERR_INVALID_ARGUMENT;
+    if (bits != 3 && bits != 4) return TQO_ERR_UNSUPPORTED_BITS;
+    float oc[16], ob[15], ncb[16], nbb[15], outer, outer_n;
+    int onc, nnc;
+    tqo_pqo_codebook(bits, oc, ob, &onc, &outer);
+    tqo_pqo_codebook(bits - 1, ncb, nbb, &nnc, &outer_n);
+    const size_t nblk_v = head_dim / QBLOCK;
+    float sg[32];
+    tqo_pqo_decode_signs(sg);
+    const float inv = 1.0f / sqrtf(32.0f);
+    const size_t bpb = (size_t)QBLOCK * (size_t)bits / 8;
+    const size_t nblk = n * nblk_v;
+    uint8_t idx[QBLOCK];
+    for (size_t blk = 0; blk < nblk; blk++) {
+        tqo_unpack_indices(bits, packed + blk * bpb, bpb, QBLOCK, idx);
+        const float sc = tqo_f16_to_f32(scales[blk]);
+        float *o = out + blk * QBLOCK;
+        for (int j = 0; j < QBLOCK; j++) {
+            float c;
+            if (outlier_blocks >= nblk_v) c = oc[idx[j]];
+            else if (outlier_blocks == 0) c = ncb[idx[j]];
+            else c = sc < 0.0f ? oc[idx[j]] : ncb[idx[j] < nnc ? idx[j] : nnc - 1];
+            o[j] = c * sg[j];
+        }
+        butterfly(o, QBLOCK);
+        float s = fabsf(sc);
+        for (int j = 0; j < QBLOCK; j++) o[j] = (o[j] * inv) * s;
+    }
+    return TQO_OK;
+}
+
+/* compute_qjl_signs_and_norms (tq.rs:373-412): residual r = x - x_hat,
+   norm = f16(sqrt(sum r^2)) (candle sqr, sum_keepdim, sqrt: the sum in
+   element order from +0), signs = compute_qjl_signs(r, d, DEFAULT_QJL_SEED
+   = 12345). */
+int tqo_tq_signs_norms(size_t n, size_t head_dim, const float *x, const float *xhat, uint8_t *signs,
+                       uint16_t *norms)
+{
+    float *r = malloc(head_dim * sizeof(float));
+    for (size_t v = 0; v < n; v++) {
+        float ss = 0.0f;
+        for (size_t e = 0; e < head_dim; e++) {
+            r[e] = x[v * head_dim + e] - xhat[v * head_dim + e];
+            ss = ss + r[e] * r[e];
+        }
+        norms[v] = tqo_f32_to_f16(sqrtf(ss));
+        int rc = tqo_compute_qjl_signs(r, head_dim, 12345u, signs + v * (head_dim / 8));
+        if (rc) {
+            free(r);
+            return rc;
+        }
+    }
+    free(r);
+    return TQO_OK;
+}
+
+/* compute_logit_bias (tq.rs:185-253) for one layer: q [num_q_heads][q_len]
+   [d]; signs [num_kv_heads][kv_len][d/8], norms [num_kv_heads][kv_len];
+   out [num_q_heads][q_len][kv_len] f32.  r_q = q R^T with R[j][c] =
+   sign(j, c) * fl(1/sqrt d) (generate_rademacher_row, qjl.rs:179-189),
+   raw = r_q s^T, bias = raw * fl(norm * sf), sf = f32(sqrt(pi/2)) / sqrt(d).
+   The two products' summation order is candle's matmul order, which is not
+   visible in the reference sources: element order here (parity unpinned at
+   the last-ulp level). */
+int tqo_tq_logit_bias(size_t num_q_heads, size_t num_kv_heads, size_t d, size_t q_len, size_t kv_len,
+                      const float *q, const uint8_t *signs, const uint16_t *norms, float *out)
+{
+    if (num_kv_heads == 0 || num_q_heads % num_kv_heads != 0) return TQO_ERR_INVALID_ARGUMENT;
+    const size_t rep = num_q_heads / num_kv_heads;
+    float *R = malloc(d * d * sizeof(float));
+    for (size_t j = 0; j < d; j++) tqo_generate_rademacher_row(d, 12345u, j, R + j * d);
+    const float sp = (float)sqrt(3.14159265358979323846 / 2.0);
+    const float sf = sp / sqrtf((float)d);
+    float *rq = malloc(d * sizeof(float));
+    for (size_t h = 0; h < num_q_heads; h++) {
+        const size_t g = h / rep;
+        for (size_t i = 0; i < q_len; i++) {
+            const float *qv = q + (h * q_len + i) * d;
+            for (size_t j = 0; j < d; j++) {
+                float acc = 0.0f;
+                for (size_t c = 0; c < d; c++) acc += qv[c] * R[j * d + c];
+                rq[j] = acc;
+            }
+            for (size_t t = 0; t < kv_len; t++) {
+                const uint8_t *sb = signs + (g * kv_len + t) * (d / 8);
+                float raw = 0.0f;
+                for (size_t j = 0; j < d; j++) raw += rq[j] * (((sb[j / 8] >> (j % 8)) & 1) ? 1.0f : -1.0f);
+                const float c = tqo_f16_to_f32(norms[g * kv_len + t]) * sf;
+                out[(h * q_len + i) * kv_len + t] = raw * c;
+            }
+        }
+    }
+    free(R);
+    free(rq);
+    return TQO_OK;
+}
+
+/* Decode attention with an additive logit term: o_h = softmax(scale *
+   (q_h K^T + bias_h)) V, bias [num_heads][kv_len] -- the TQ logits of the
+   QJL branch of tq_attention_kernel.cu:192-231 (score += correction *
+   softmax_scale).  Accumulated in double. */
+int tqo_attention_dense_bias(size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t kv_len, const float *q,
+                             const float *k, const float *v, const float *bias, float softmax_scale, float *out)
+{
+    if (num_kv_heads == 0 || num_heads % num_kv_heads != 0) return TQO_ERR_INVALID_ARGUMENT;
+    size_t rep = num_heads / num_kv_heads;
+    double *sc = malloc((kv_len ? kv_len : 1) * sizeof(double));
+    double *acc = malloc(head_dim * sizeof(double));
+    for (size_t h = 0; h < num_heads; h++) {
+        size_t g = h / rep;
+        const float *qh = q + h * head_dim;
+        const float *kg = k + g * kv_len * head_dim;
+        const float *vg = v + g * kv_len * head_dim;
+        double mx = -INFINITY;
+        for (size_t t = 0; t < kv_len; t++) {
+            double s = 0.0;
+            for (size_t dd = 0; dd < head_dim; dd++) s += (double)qh[dd] * (double)kg[t * head_dim + dd];
+            s = (s + (double)bias[h * kv_len + t]) * (double)softmax_scale;
+            sc[t] = s;
+            mx = s > mx ? s : mx;
+        }
+        double l = 0.0;
+        for (size_t dd = 0; dd < head_dim; dd++) acc[dd] = 0.0;
+        for (size_t t = 0; t < kv_len; t++) {
+            double p = exp(sc[t] - mx);
+            l += p;
+            for (size_t dd = 0; dd < head_dim; dd++) acc[dd] += p * (double)vg[t * head_dim + dd];
+        }
+        for (size_t dd = 0; dd < head_dim; dd++) out[h * head_dim + dd] = kv_len ? (float)(acc[dd] / l) : 0.0f;
+    }
+    free(sc);
+    free(acc);
+    return TQO_OK;
+}
+
 /* ------------------------------------------------------------------------
  * Dense decode attention over dequantized K/V: o_h = softmax(scale q_h K^T) V
  * with GQA group g(h) = h / (num_heads / num_kv_heads) (the mapping of

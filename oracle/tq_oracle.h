@@ -87,6 +87,22 @@ int tqo_pqo_quantize(int bits, size_t n, size_t head_dim, const float *x,
 int tqo_pqo_dequantize(int bits, size_t n, size_t head_dim, const uint8_t *packed,
                        const uint16_t *scales, float *out);
 
+/* polar_quantize / polar_dequantize for the cache modes (outlier_blocks:
+ * >= num_blocks PQO, 0 PQ/TQ), MaxNorm. */
+int tqo_polar_quantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim, const float *x,
+                       uint8_t *packed_out, uint16_t *scales_out);
+int tqo_polar_dequantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim,
+                         const uint8_t *packed, const uint16_t *scales, float *out);
+
+/* ---- TqCache (src/cache/tq.rs) ---- */
+int tqo_tq_signs_norms(size_t n, size_t head_dim, const float *x, const float *xhat, uint8_t *signs,
+                       uint16_t *norms);
+int tqo_tq_logit_bias(size_t num_q_heads, size_t num_kv_heads, size_t d, size_t q_len, size_t kv_len,
+                      const float *q, const uint8_t *signs, const uint16_t *norms, float *out);
+int tqo_attention_dense_bias(size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t kv_len,
+                             const float *q, const float *k, const float *v, const float *bias,
+                             float softmax_scale, float *out);
+
 /* ---- dense attention oracle over dequantized K/V ---- */
 int tqo_attention_dense(size_t num_heads, size_t num_kv_heads, size_t head_dim,
                         size_t kv_len, const float *q, const float *k, const float *v,

@@ -12,15 +12,19 @@ import math
 
 import torch
 
-from ._lib import (TQ_DTYPE_BF16, TQ_DTYPE_F16, TQ_DTYPE_F32, TurboQuantError, check, lib)
-from .cache import AttendConfig, DequantResult, PqoCache
+from ._lib import (TQ_DTYPE_BF16, TQ_DTYPE_F16, TQ_DTYPE_F32, TQ_NORM_MAXNORM, TQ_OUTLIER_ALL, TurboQuantError,
+                   check, lib)
+from .cache import (AttendConfig, CacheConfig, DecodeOutput, Dequantized, DequantResult, Fused, PqoCache,
+                    QuantNormMode, TqCache)
 
 __all__ = [
     "TurboQuantError", "lib", "pqo_quantize", "pqo_dequantize", "quant_maxnorm_batch", "dequant_batch",
     "pack_indices", "fused_attention", "AttentionWorkspace", "pqo_decode_attention", "pqo_codebook_values",
     "quantize_vec_batch", "dequantize_vec_batch", "dequantize_rotated_batch", "qjl_quantize_batch",
     "qjl_query_context", "qjl_scores", "softmax_rows", "qjl_weighted_values", "PqoCache", "AttendConfig",
-    "DequantResult",
+    "DequantResult", "TqCache", "CacheConfig", "QuantNormMode", "DecodeOutput", "Fused", "Dequantized",
+    "polar_quantize", "polar_dequantize", "cache_decode_attention", "qjl_sign_matrix", "qjl_project",
+    "qjl_cache_sketch", "qjl_logit_bias",
 ]
 
 _DT = {torch.float32: TQ_DTYPE_F32, torch.bfloat16: TQ_DTYPE_BF16, torch.float16: TQ_DTYPE_F16}
@@ -52,6 +56,31 @@ def pqo_quantize(x: torch.Tensor, bits: int):
     scales = torch.empty((n, max(hd // 32, 1)), dtype=torch.int16, device=x.device)
     check(lib.tq_pqo_quantize(_ptr(x), _DT[x.dtype], _ptr(packed), _ptr(scales), n, hd, bits, _stream()))
     return packed, scales
+
+
+def polar_quantize(x: torch.Tensor, bits: int, outlier_blocks: int = TQ_OUTLIER_ALL,
+                   norm_mode: int = TQ_NORM_MAXNORM):
+    """polar_quantize (quantize_tensor.rs:40-76) of [N, head_dim] for a cache mode:
+    outlier_blocks TQ_OUTLIER_ALL (PQO) or 0 (PQ / TQ: (bits-1)-bit codes in
+    bits-wide slots, positive scales)."""
+    if x.dim() != 2:
+        raise ValueError("x must be [N, head_dim]")
+    n, hd = x.shape
+    packed = torch.empty((n, hd * bits // 8), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((n, max(hd // 32, 1)), dtype=torch.int16, device=x.device)
+    check(lib.tq_polar_quantize(_ptr(x), _DT[x.dtype], _ptr(packed), _ptr(scales), n, hd, bits, int(outlier_blocks),
+                                int(norm_mode), _stream()))
+    return packed, scales
+
+
+def polar_dequantize(packed: torch.Tensor, scales: torch.Tensor, bits: int, head_dim: int,
+                     outlier_blocks: int = TQ_OUTLIER_ALL, norm_mode: int = TQ_NORM_MAXNORM,
+                     out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    n = packed.shape[0]
+    out = torch.empty((n, head_dim), dtype=out_dtype, device=packed.device)
+    check(lib.tq_polar_dequantize(_ptr(packed), _ptr(scales), _ptr(out), _DT[out_dtype], n, head_dim, bits,
+                                  int(outlier_blocks), int(norm_mode), _stream()))
+    return out
 
 
 def pqo_dequantize(packed: torch.Tensor, scales: torch.Tensor, bits: int, head_dim: int,
@@ -140,6 +169,56 @@ def pqo_decode_attention(q, k_idx, k_sc, v_idx, v_sc, kv_lens, num_kv_heads, bit
                                       _ptr(kv_lens), b, h, num_kv_heads, hd, bits, max_kv_len, kv_head_stride,
                                       seq_stride, float(softmax_scale), _ptr(out), _DT[out.dtype],
                                       _ptr(workspace.buf), workspace.nbytes, _stream()))
+    return out
+
+
+def cache_decode_attention(q, k_idx, k_sc, v_idx, v_sc, kv_lens, num_kv_heads, bits, max_kv_len, kv_head_stride,
+                           seq_stride, softmax_scale, workspace: AttentionWorkspace, outlier_blocks: int,
+                           rq: torch.Tensor | None = None, qjl_signs: torch.Tensor | None = None,
+                           qjl_norms: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32):
+    """Fused decode attention over PQO / PQ records, or TQ records with the QJL
+    correction when qjl_signs is given (rq [B, H, D] f32 = R q)."""
+    b, h, hd = q.shape
+    out = torch.empty((b, h, hd), dtype=out_dtype, device=q.device)
+    check(lib.tq_cache_decode_attention(_ptr(q), _DT[q.dtype], _ptr(k_idx), _ptr(k_sc), _ptr(v_idx), _ptr(v_sc),
+                                        _ptr(rq), _ptr(qjl_signs), _ptr(qjl_norms), _ptr(kv_lens), b, h,
+                                        num_kv_heads, hd, bits, int(outlier_blocks), TQ_NORM_MAXNORM, max_kv_len,
+                                        kv_head_stride, seq_stride, float(softmax_scale), _ptr(out), _DT[out.dtype],
+                                        _ptr(workspace.buf), workspace.nbytes, _stream()))
+    return out
+
+
+def qjl_sign_matrix(dim: int, qjl_seed: int, device="cuda") -> torch.Tensor:
+    """Sign bits of R: int32 [dim * dim / 32], bit b of word j*dim/32 + w set <=> R[j][32w+b] < 0."""
+    out = torch.empty((dim * dim // 32,), dtype=torch.int32, device=device)
+    check(lib.tq_qjl_sign_matrix(_ptr(out), dim, qjl_seed, _stream()))
+    return out
+
+
+def qjl_project(q: torch.Tensor, sign_matrix: torch.Tensor) -> torch.Tensor:
+    """rq = R q per row of q [N, dim] (f32 out)."""
+    n, d = q.shape
+    rq = torch.empty((n, d), dtype=torch.float32, device=q.device)
+    check(lib.tq_qjl_project(_ptr(q), _DT[q.dtype], _ptr(sign_matrix), _ptr(rq), n, d, _stream()))
+    return rq
+
+
+def qjl_cache_sketch(k: torch.Tensor, packed_cache, scales_cache, sign_matrix, signs_cache, norms_cache,
+                     head_stride: int, offset: int, bits: int, outlier_blocks: int = 0):
+    """Signs and residual norms of keys k [H, T, D] already stored at records h*head_stride + offset + t."""
+    h, t, d = k.shape
+    check(lib.tq_qjl_cache_sketch(_ptr(k), _DT[k.dtype], h, t, _ptr(packed_cache), _ptr(scales_cache),
+                                  _ptr(sign_matrix), _ptr(signs_cache), _ptr(norms_cache), head_stride, offset, d,
+                                  bits, int(outlier_blocks), TQ_NORM_MAXNORM, _stream()))
+
+
+def qjl_logit_bias(rq: torch.Tensor, signs_cache, norms_cache, num_kv_heads: int, kv_len: int, head_stride: int,
+                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """compute_logit_bias: rq [Hq, q_len, D] f32 -> bias [Hq, q_len, kv_len]."""
+    hq, ql, d = rq.shape
+    out = torch.empty((hq, ql, kv_len), dtype=out_dtype, device=rq.device)
+    check(lib.tq_qjl_logit_bias(_ptr(rq), hq, ql, _ptr(signs_cache), _ptr(norms_cache), num_kv_heads, kv_len,
+                                head_stride, d, _ptr(out), _DT[out_dtype], _stream()))
     return out
 
 

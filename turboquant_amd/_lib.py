@@ -11,6 +11,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libturboquant_amd.so")
 
 TQ_DTYPE_F32, TQ_DTYPE_BF16, TQ_DTYPE_F16 = 0, 1, 2
+TQ_NORM_MAXNORM, TQ_NORM_L2NORM = 0, 1
+TQ_OUTLIER_ALL = (1 << 64) - 1  # CacheConfig::outlier_blocks = usize::MAX (PQO)
 
 ERRORS = {
     1: "InvalidDimension",
@@ -55,6 +57,30 @@ SIGNATURES = {
     "tq_qjl_weighted_values": (_i, [_p, _p, _sz, _p, _sz, _i, _i, _u64, _p, _p, _sz, _p]),
     "tq_pqo_quantize_to_cache": (_i, [_p, _i, _i, _i, _p, _p, _ll, _ll, _i, _i, _p]),
     "tq_pqo_dequantize_from_cache": (_i, [_p, _p, _ll, _i, _i, _p, _i, _i, _i, _p]),
+    "tq_polar_quantize": (_i, [_p, _i, _p, _p, _sz, _i, _i, _sz, _i, _p]),
+    "tq_polar_dequantize": (_i, [_p, _p, _p, _i, _sz, _i, _i, _sz, _i, _p]),
+    "tq_polar_quantize_to_cache": (_i, [_p, _i, _i, _i, _p, _p, _ll, _ll, _i, _i, _sz, _i, _p]),
+    "tq_polar_dequantize_from_cache": (_i, [_p, _p, _ll, _i, _i, _p, _i, _i, _i, _sz, _i, _p]),
+    "tq_cache_decode_attention": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _sz, _i, _i,
+                                       _ll, _ll, _f, _p, _i, _p, _sz, _p]),
+    "tq_qjl_sign_matrix": (_i, [_p, _i, _u64, _p]),
+    "tq_qjl_cache_sketch": (_i, [_p, _i, _i, _i, _p, _p, _p, _p, _p, _ll, _ll, _i, _i, _sz, _i, _p]),
+    "tq_qjl_project": (_i, [_p, _i, _p, _p, _sz, _i, _p]),
+    "tq_qjl_bias_scale": (_f, [_i]),
+    "tq_qjl_logit_bias": (_i, [_p, _i, _i, _p, _p, _i, _i, _ll, _i, _p, _i, _p]),
+    "tq_cache_create": (_i, [_i, _i, _i, _i, _i, _sz, _i, C.POINTER(C.c_void_p)]),
+    "tq_cache_destroy": (None, [_p]),
+    "tq_cache_is_tq": (_i, [_p]),
+    "tq_cache_prefill": (_i, [_p, _i, _p, _p, _i, _i, _p, _i, _i, _i, _p, _p, C.POINTER(C.c_int), _p, _p]),
+    "tq_cache_decode": (_i, [_p, _i, _p, _p, _i, _i, _p, _i, _i, _f, _p, _i, _p]),
+    "tq_cache_decode_dequantized": (_i, [_p, _i, _p, _p, _i, _i, _p, _i, _i, _i, _p, _p, _p, _p]),
+    "tq_cache_seq_len": (_sz, [_p, _i]),
+    "tq_cache_reset": (_i, [_p]),
+    "tq_cache_memory_usage": (_sz, [_p]),
+    "tq_cache_capacity": (_sz, [_p, _i]),
+    "tq_cache_read_layer": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p]),
+    "tq_cache_buffers": (_i, [_p, _i] + [C.POINTER(C.c_void_p)] * 6),
+    "tq_tq_cache_create": (_i, [_i, _i, _i, _i, C.POINTER(C.c_void_p)]),
     "tq_pqo_cache_create": (_i, [_i, _i, _i, _i, C.POINTER(C.c_void_p)]),
     "tq_pqo_cache_destroy": (None, [_p]),
     "tq_pqo_cache_prefill": (_i, [_p, _i, _p, _p, _i, _i, _p, _p, C.POINTER(C.c_int), _p]),

@@ -58,8 +58,15 @@ constexpr int kCounterStride = 64;  // ints
 constexpr int kLoadGroups = TQ_ATTN_LOAD_GROUPS;  // staggered K/V fetch groups per tile
 static_assert(kWaves % kLoadGroups == 0, "load groups split the waves evenly");
 
+// Cache codec of the attended records: PQO (outlier codebook, CB = BITS),
+// PQ (standard (BITS - 1)-bit codebook in BITS-wide slots) and TQ (PQ plus
+// the QJL correction of the keys' residuals, tq.rs:185-253 and the QJL
+// branch of tq_attention_kernel.cu:192-231).
+enum Mode : int { kModePqo = 0, kModePq = 1, kModeTq = 2 };
+
 struct AttnArgs {
   const void *q;
+  int q_dtype;
   const uint8_t *k_idx;
   const uint16_t *k_sc;
   const uint8_t *v_idx;
@@ -79,20 +86,21 @@ struct AttnArgs {
   int P;                     // chunk stride per (b, h) in the partial arrays
   void *out;
   int out_dtype;
+  // TQ: rq [b][h][head_dim] f32 = R q (precompute_query_projections); per
+  // record, signs [16] u8 of R r and the f16 residual norm |r|; qjl_c =
+  // f32(sqrt(pi/2)) / sqrt(head_dim)
+  const float *rq;
+  const uint32_t *qjl_signs;
+  const uint16_t *qjl_norms;
+  float qjl_c;
 };
 
-// Query element i as stored (f32 bits or a 16-bit pattern), converted
+// Query element as stored (f32 bits or a 16-bit pattern), converted
 // separately so that the wait for the load lands at the first use.
-template <int QT>
-__device__ __forceinline__ uint32_t load_q_bits(const uint8_t *p) {
-  if constexpr (QT == kF32) return *reinterpret_cast<const uint32_t *>(p);
-  else return *reinterpret_cast<const uint16_t *>(p);
-}
-template <int QT>
-__device__ __forceinline__ float q_value(uint32_t bits) {
-  if constexpr (QT == kF32) return u2f(bits);
-  else if constexpr (QT == kBF16) return bf16_to_f32((uint16_t)bits);
-  else return f16_to_f32((uint16_t)bits);
+__device__ __forceinline__ float q_value(uint32_t bits, int qt) {
+  if (qt == kF32) return u2f(bits);
+  if (qt == kBF16) return bf16_to_f32((uint16_t)bits);
+  return f16_to_f32((uint16_t)bits);
 }
 
 // Value of lane l ^ 1 (DPP quad permute [1, 0, 3, 2]) and of lane l ^ 2
@@ -299,8 +307,10 @@ __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, fl
   }
 }
 
-template <int BITS, int NR, int QT, bool INLINE_MERGE>
+template <int BITS, int MODE, int NR, bool INLINE_MERGE>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
+  constexpr int CB = MODE == kModePqo ? BITS : BITS - 1;  // codebook bits
+  constexpr bool QJL = MODE == kModeTq;
   constexpr int NQB = 4, HD = 128, CH = kChunk;
   constexpr int QW = BITS;                       // 32-bit words per qblock
   constexpr int PACKED = NQB * QW * 4;           // bytes per token record
@@ -324,7 +334,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   constexpr int OFF_QA = OFF_PAIR + 2 * NPAIR * PREP;  // u32x4 [NG][8][64]: key-pass query operands
   constexpr int OFF_Q = OFF_QA + NG * 8 * 64 * 4;
   constexpr int OFF_QMAX = OFF_Q + NR * HD;      // [2 NR] max |qt| per half head
-  constexpr int OFF_W = OFF_QMAX + 8;
+  // QJL: u32x4 [4][64] correction operands, uint2 [16] +-1 f16 nibble table,
+  // [2 NR] max |rq| per half head
+  constexpr int OFF_RA = OFF_QMAX + 8;
+  constexpr int OFF_NIB = OFF_RA + (QJL ? 4 * 64 * 4 : 0);
+  constexpr int OFF_RQMAX = OFF_NIB + (QJL ? 32 : 0);
+  constexpr int OFF_W = OFF_RQMAX + (QJL ? 8 : 0);
   constexpr int OFF_MISC = OFF_W;                // merge scratch aliases the staging areas
   constexpr int TOTAL0 = OFF_W + kWaves * WSTAGE;
   constexpr int TOTAL = TOTAL0 > OFF_MISC + kMiscFloats ? TOTAL0 : OFF_MISC + kMiscFloats;
@@ -338,6 +353,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   u32x4 *s_qa = reinterpret_cast<u32x4 *>(lds + OFF_QA);
   float *s_q = lds + OFF_Q;
   float *s_qmax = lds + OFF_QMAX;
+  u32x4 *s_ra = reinterpret_cast<u32x4 *>(lds + OFF_RA);
+  uint2 *s_nib = reinterpret_cast<uint2 *>(lds + OFF_NIB);
+  float *s_rqmax = lds + OFF_RQMAX;
+  float *s_rq = lds + OFF_W;  // scaled rq [NR][HD]: read before any wave stages its records here
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -352,11 +371,14 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   // length), loaded by the waves that rotate it, one element per lane (whole
   // waves: NR * HD % 64 == 0).  These waves rotate it before they queue any
   // record load, so the wait for it counts nothing else. ----
-  constexpr int QBYTES = QT == kF32 ? 4 : 2;
+  const long long qidx = ((long long)b * a.num_heads + g * NR) * HD + tid;
   uint32_t qbits = 0;
-  if (tid < NR * HD)
-    qbits = load_q_bits<QT>(static_cast<const uint8_t *>(a.q) +
-                            (((long long)b * a.num_heads + g * NR) * HD + tid) * QBYTES);
+  float rqv = 0.f;
+  if (tid < NR * HD) {
+    if (a.q_dtype == kF32) qbits = static_cast<const uint32_t *>(a.q)[qidx];
+    else qbits = static_cast<const uint16_t *>(a.q)[qidx];
+    if constexpr (QJL) rqv = a.rq[qidx];
+  }
   const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
   if (t0 >= len) {  // empty tile: not counted by the merge
     __builtin_amdgcn_s_waitcnt(0);
@@ -372,18 +394,26 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   // ---- pair table from the constant codebook ----
   for (int it = tid; it < NPAIR * PREP; it += kThreads) {
     const int e = it / PREP;
-    const float c0 = pqo_centroid<BITS>(e & (NC - 1)), c1 = pqo_centroid<BITS>(e >> BITS);
+    constexpr int CM = (1 << CB) - 1;  // slot codes >= 2^CB never occur
+    const float c0 = pqo_centroid<CB>(e & (NC - 1) & CM), c1 = pqo_centroid<CB>((e >> BITS) & CM);
     const float h0 = split_hi(c0), h1 = split_hi(c1);
     s_pair[it] = make_uint2(pack_f16(h0, h1), pack_f16(c0 - h0, c1 - h1));
   }
   if (tid == 0) s_ready = 0;
+  if constexpr (QJL) {
+    // +-1 in f16 for the four sign bits of a nibble, LSB first
+    if (tid < 16) {
+      auto pm1 = [&](int bit) { return ((tid >> bit) & 1) ? 0x3C00u : 0xBC00u; };
+      s_nib[tid] = make_uint2(pm1(0) | (pm1(1) << 16), pm1(2) | (pm1(3) << 16));
+    }
+  }
 
   // ---- rotated, scaled queries (32-lane butterflies), before these waves
   // queue their record loads behind the query ----
   const float qscale = a.softmax_scale * kLog2e * kInvSqrt32;
   if (tid < NR * HD) {
     const int d = tid % HD;
-    float v = q_value<QT>(qbits);
+    float v = q_value(qbits, a.q_dtype);
     const int i = d & 31;
 #pragma unroll
     for (int hh = 1; hh < 32; hh <<= 1) {
@@ -394,6 +424,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     s_q[tid] = qt;
     const float am = wave_max(fabsf(qt));
     if (lane == 0) s_qmax[wave] = am;
+    if constexpr (QJL) {
+      const float rs = rqv * (a.softmax_scale * kLog2e);
+      s_rq[tid] = rs;
+      const float rm = wave_max(fabsf(rs));
+      if (lane == 0) s_rqmax[wave] = rm;
+    }
   }
 
   // ---- K/V records.  The tile's waves fetch them in kLoadGroups staggered
@@ -410,6 +446,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const uint8_t *vsbase = reinterpret_cast<const uint8_t *>(a.v_sc + rec0 * NQB);
   uint32_t kq[NT][QW], vq[NT][QW];
   uint2 ksc, vsc;
+  uint32_t sq[NT];   // QJL: sign word lg of token 16 tt + l16
+  uint32_t nrm = 0;  // QJL: residual norm of token lane
+  const uint8_t *sgbase = reinterpret_cast<const uint8_t *>(a.qjl_signs) + rec0 * 16;
+  const uint16_t *nmbase = a.qjl_norms + rec0;
   auto issue_loads = [&](bool real) {
     const int tw = t0 + wave * WT;
     const uint32_t soff = (uint32_t)(real ? min(tw + lane, len - 1) : t0) * (NQB * 2);
@@ -422,6 +462,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
       for (int w = 0; w < QW; w++) kq[tt][w] = *reinterpret_cast<const uint32_t *>(kbase + off[tt] + 4 * w);
     ksc = *reinterpret_cast<const uint2 *>(ksbase + soff);
+    if constexpr (QJL) {
+#pragma unroll
+      for (int tt = 0; tt < NT; tt++)
+        sq[tt] = *reinterpret_cast<const uint32_t *>(
+            sgbase + (uint32_t)(real ? min(tw + 16 * tt + l16, len - 1) : t0) * 16 + lg * 4);
+      nrm = nmbase[real ? min(tw + lane, len - 1) : t0];
+    }
 #pragma unroll
     for (int tt = 0; tt < NT; tt++)
 #pragma unroll
@@ -454,6 +501,29 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     }
     s_qa[(gi * 8 + j) * 64 + lane] = val;
   }
+  if constexpr (QJL) {
+    // Correction operands: MFMA s covers sign bits 32 kg + 8 s .. + 7 of a
+    // token (k = 8 kg + i); row m = (head m / 2, part m % 2) holds part(rq)
+    // of those projections, rq scaled per head by 2^-Er into f16's range.
+    if (tid >= kThreads - 256) {
+      const int e = tid - (kThreads - 256), sl = e >> 6, ln = e & 63, m = ln & 15, kg = ln >> 4;
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if (m < 2 * NR) {
+        const int r = m >> 1, part = m & 1;
+        const float sc = exp2i(-pow2_exponent(fmaxf(s_rqmax[2 * r], s_rqmax[2 * r + 1])));
+        const float *src = s_rq + r * HD + 32 * kg + 8 * sl;
+        uint32_t wv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float x0 = src[2 * i] * sc, x1 = src[2 * i + 1] * sc;
+          const float h0 = split_hi(x0), h1 = split_hi(x1);
+          wv[i] = part ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
+        }
+        val = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      }
+      s_ra[sl * 64 + ln] = val;
+    }
+  }
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);  // keep the record-dependent code below the setup
   if (grp > 0) {
@@ -471,9 +541,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     if (lane == 0) __hip_atomic_fetch_add(&s_ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 
-  float escale[NR];
+  float escale[NR], erscale[NR];
 #pragma unroll
-  for (int r = 0; r < NR; r++) escale[r] = exp2i(pow2_exponent(fmaxf(s_qmax[2 * r], s_qmax[2 * r + 1])));
+  for (int r = 0; r < NR; r++) {
+    escale[r] = exp2i(pow2_exponent(fmaxf(s_qmax[2 * r], s_qmax[2 * r + 1])));
+    if constexpr (QJL) erscale[r] = exp2i(pow2_exponent(fmaxf(s_rqmax[2 * r], s_rqmax[2 * r + 1])));
+  }
 
   // ---- K pass: D[tile][(qblock, head, part)][token] over the eight
   // 4-element slices j of every qblock.  The key operand of lane (t, q) for
@@ -498,6 +571,32 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
       for (int gi = 0; gi < NG; gi++) dk[tt][gi] = mfma(qa[gi], kb, dk[tt][gi]);
     }
+  }
+  if constexpr (QJL) {
+    // sum_j rq_j (2 b_j - 1) per (head, token) on the matrix core: the sign
+    // operand of lane (t, kg) for MFMA s is the +-1 pairs of byte s of its
+    // sign word; the (unscaled) sums go to st_p, which the softmax
+    // overwrites only after they are read
+    f32x4 dq[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) dq[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sl = 0; sl < 4; sl++) {
+      const u32x4 ra = s_ra[sl * 64 + lane];
+#pragma unroll
+      for (int tt = 0; tt < NT; tt++) {
+        const uint32_t byte = (sq[tt] >> (8 * sl)) & 0xffu;
+        const uint2 n0 = s_nib[byte & 15u], n1 = s_nib[byte >> 4];
+        dq[tt] = mfma(ra, u32x4{n0.x, n0.y, n1.x, n1.y}, dq[tt]);
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int r = 2 * lg + u;
+        if (r < NR) st_p[r * WT + 16 * tt + l16] = dq[tt][2 * u] + dq[tt][2 * u + 1];
+      }
   }
 #pragma unroll
   for (int tt = 0; tt < NT; tt++) {
@@ -543,9 +642,17 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int tok = t0 + wave * WT + lane;
   const bool valid = tok < len;
   float m_w[NR], p[NR], l_w[NR];
+  float corr[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) corr[r] = 0.f;
+  if constexpr (QJL) {
+    const float cn = f16_to_f32((uint16_t)nrm) * a.qjl_c;
+#pragma unroll
+    for (int r = 0; r < NR; r++) corr[r] = st_p[r * WT + lane] * (cn * erscale[r]);
+  }
 #pragma unroll
   for (int r = 0; r < NR; r++) {
-    const float sc = valid ? score[r] * escale[r] : -INFINITY;
+    const float sc = valid ? (QJL ? __builtin_fmaf(score[r], escale[r], corr[r]) : score[r] * escale[r]) : -INFINITY;
     m_w[r] = wave_max(sc);
     p[r] = valid ? __builtin_amdgcn_exp2f(sc - m_w[r]) : 0.f;
     st_p[r * WT + lane] = p[r];
@@ -752,24 +859,24 @@ AttnArgs base_args() {
   return a;
 }
 
-template <int BITS, int NR, bool INLINE>
-int launch_decode_q(const AttnArgs &a, int qt, dim3 grid, hipStream_t st) {
-  if (qt == kF32) hipLaunchKernelGGL((attn_decode_kernel<BITS, NR, kF32, INLINE>), grid, dim3(kThreads), 0, st, a);
-  else if (qt == kBF16) hipLaunchKernelGGL((attn_decode_kernel<BITS, NR, kBF16, INLINE>), grid, dim3(kThreads), 0, st, a);
-  else hipLaunchKernelGGL((attn_decode_kernel<BITS, NR, kF16, INLINE>), grid, dim3(kThreads), 0, st, a);
+template <int BITS, int MODE, bool INLINE>
+int launch_decode_m(const AttnArgs &a, int nr, dim3 grid, hipStream_t st) {
+  if (nr == 1) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 1, INLINE>), grid, dim3(kThreads), 0, st, a);
+  else if (nr == 2) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 2, INLINE>), grid, dim3(kThreads), 0, st, a);
+  else hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 4, INLINE>), grid, dim3(kThreads), 0, st, a);
   return tqh::check_launch("attn_decode_kernel");
 }
 
 template <bool INLINE>
-int launch_decode(const AttnArgs &a, int bits, int nr, int qt, dim3 grid, hipStream_t st) {
+int launch_decode(const AttnArgs &a, int bits, int mode, int nr, dim3 grid, hipStream_t st) {
   if (bits == 3) {
-    if (nr == 1) return launch_decode_q<3, 1, INLINE>(a, qt, grid, st);
-    if (nr == 2) return launch_decode_q<3, 2, INLINE>(a, qt, grid, st);
-    return launch_decode_q<3, 4, INLINE>(a, qt, grid, st);
+    if (mode == kModePqo) return launch_decode_m<3, kModePqo, INLINE>(a, nr, grid, st);
+    if (mode == kModePq) return launch_decode_m<3, kModePq, INLINE>(a, nr, grid, st);
+    return launch_decode_m<3, kModeTq, INLINE>(a, nr, grid, st);
   }
-  if (nr == 1) return launch_decode_q<4, 1, INLINE>(a, qt, grid, st);
-  if (nr == 2) return launch_decode_q<4, 2, INLINE>(a, qt, grid, st);
-  return launch_decode_q<4, 4, INLINE>(a, qt, grid, st);
+  if (mode == kModePqo) return launch_decode_m<4, kModePqo, INLINE>(a, nr, grid, st);
+  if (mode == kModePq) return launch_decode_m<4, kModePq, INLINE>(a, nr, grid, st);
+  return launch_decode_m<4, kModeTq, INLINE>(a, nr, grid, st);
 }
 
 int check_common(int num_heads, int num_kv_heads, int head_dim, int bits) {
@@ -806,19 +913,28 @@ extern "C" int tq_attention_workspace_init(void *workspace, size_t workspace_byt
   return tqh::check_launch("fill_zero_kernel");
 }
 
-extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
-                                       const uint8_t *v_indices, const uint16_t *v_scales, const int *kv_lens,
-                                       int batch, int num_heads, int num_kv_heads, int head_dim, int bits,
-                                       int max_kv_len, long long kv_head_stride, long long seq_stride,
-                                       float softmax_scale, void *out, int out_dtype, void *workspace,
-                                       size_t workspace_bytes, hipStream_t stream) {
+extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
+                                         const uint16_t *k_scales, const uint8_t *v_indices,
+                                         const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                                         const uint16_t *qjl_norms, const int *kv_lens, int batch, int num_heads,
+                                         int num_kv_heads, int head_dim, int bits, size_t outlier_blocks,
+                                         int norm_mode, int max_kv_len, long long kv_head_stride,
+                                         long long seq_stride, float softmax_scale, void *out, int out_dtype,
+                                         void *workspace, size_t workspace_bytes, hipStream_t stream) {
   int rc = check_common(num_heads, num_kv_heads, head_dim, bits);
   if (rc) return rc;
+  tqh::PolarCodec codec;
+  rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
+  const bool qjl = qjl_signs != nullptr;
+  if (qjl && codec.outlier)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL correction applies to the standard codebook (outlier_blocks 0)");
   if (!tqh::valid_dtype(q_dtype) || !tqh::valid_dtype(out_dtype))
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype");
   if (batch <= 0 || max_kv_len <= 0) return TQ_OK;
   if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !kv_lens || !out)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  if (qjl && (!rq || !qjl_norms)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL needs rq, signs and norms");
   if (kv_head_stride < max_kv_len)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_head_stride %lld < max_kv_len %d", kv_head_stride, max_kv_len);
   if (batch > 1 && seq_stride < (long long)num_kv_heads * kv_head_stride)
@@ -831,6 +947,7 @@ extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t
   AttnArgs a = base_args();
   char *ws = static_cast<char *>(workspace);
   a.q = q;
+  a.q_dtype = q_dtype;
   a.k_idx = k_indices;
   a.k_sc = k_scales;
   a.v_idx = v_indices;
@@ -850,8 +967,25 @@ extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t
   a.P = w.P;
   a.out = out;
   a.out_dtype = out_dtype;
+  a.rq = rq;
+  a.qjl_signs = reinterpret_cast<const uint32_t *>(qjl_signs);
+  a.qjl_norms = qjl_norms;
+  a.qjl_c = tq_qjl_bias_scale(head_dim);
+  const int mode = codec.outlier ? kModePqo : (qjl ? kModeTq : kModePq);
   const dim3 grid((unsigned)w.P, (unsigned)num_kv_heads, (unsigned)batch);
-  return launch_decode<true>(a, bits, num_heads / num_kv_heads, q_dtype, grid, stream);
+  return launch_decode<true>(a, bits, mode, num_heads / num_kv_heads, grid, stream);
+}
+
+extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
+                                       const uint8_t *v_indices, const uint16_t *v_scales, const int *kv_lens,
+                                       int batch, int num_heads, int num_kv_heads, int head_dim, int bits,
+                                       int max_kv_len, long long kv_head_stride, long long seq_stride,
+                                       float softmax_scale, void *out, int out_dtype, void *workspace,
+                                       size_t workspace_bytes, hipStream_t stream) {
+  return tq_cache_decode_attention(q, q_dtype, k_indices, k_scales, v_indices, v_scales, nullptr, nullptr, nullptr,
+                                   kv_lens, batch, num_heads, num_kv_heads, head_dim, bits, TQ_OUTLIER_ALL,
+                                   TQ_NORM_MAXNORM, max_kv_len, kv_head_stride, seq_stride, softmax_scale, out,
+                                   out_dtype, workspace, workspace_bytes, stream);
 }
 
 extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, const uint16_t *k_scales,
@@ -861,11 +995,9 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
                                   const float *rq, int qjl_enabled, int num_attention_heads, int num_kv_heads,
                                   int head_dim, int kv_len, int kv_stride, int packed_dim, int num_qblocks, int bits,
                                   float softmax_scale, int num_partitions, hipStream_t stream) {
-  (void)qjl_signs;
-  (void)qjl_residual_norms;
-  (void)rq;
   if (kv_len == 0 || num_kv_heads == 0) return TQ_OK;  // tq_attention_kernel.cu:366
-  if (qjl_enabled) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL correction in fused attention is not enabled");
+  if (qjl_enabled && (!qjl_signs || !qjl_residual_norms || !rq))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "qjl_enabled needs signs, residual norms and rq");
   int rc = check_common(num_attention_heads, num_kv_heads, head_dim, bits);
   if (rc) return rc;
   if (num_qblocks != head_dim / 32 || packed_dim != head_dim * bits / 8)
@@ -878,12 +1010,15 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   // The codebook and sign pattern are device tensors in the reference
   // (pqo.rs:134-160) holding the PQO constants, which this entry applies from
-  // its own copy.  The caller's partial buffers (sized for 512-token
-  // partitions) hold this entry's 1024-token partials.
+  // its own copy; with qjl_enabled the records are TQ records (standard
+  // (bits-1)-bit codebook, the QJL branch of tq_attention_kernel.cu:192-231).
+  // The caller's partial buffers (sized for 512-token partitions) hold this
+  // entry's 1024-token partials.
   (void)codebook;
   (void)sign_pattern;
   AttnArgs a = base_args();
   a.q = q;
+  a.q_dtype = kF32;
   a.k_idx = k_indices;
   a.k_sc = k_scales;
   a.v_idx = v_indices;
@@ -903,10 +1038,15 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
   a.P = num_partitions;
   a.out = output;
   a.out_dtype = kF32;
+  a.rq = rq;
+  a.qjl_signs = reinterpret_cast<const uint32_t *>(qjl_signs);
+  a.qjl_norms = qjl_residual_norms;
+  a.qjl_c = tq_qjl_bias_scale(head_dim);
   const int nr = num_attention_heads / num_kv_heads;
   const int P = (kv_len + kChunk - 1) / kChunk;
   if ((long long)nr * P > kMergeCap) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_len %d too long for one merge", kv_len);
-  rc = launch_decode<false>(a, bits, nr, kF32, dim3((unsigned)P, (unsigned)num_kv_heads, 1u), stream);
+  rc = launch_decode<false>(a, bits, qjl_enabled ? kModeTq : kModePqo, nr, dim3((unsigned)P, (unsigned)num_kv_heads, 1u),
+                            stream);
   if (rc) return rc;
   const dim3 mgrid((unsigned)num_kv_heads, 1u);
   if (nr == 1) hipLaunchKernelGGL((attn_merge_kernel<1>), mgrid, dim3(kThreads), 0, stream, a);

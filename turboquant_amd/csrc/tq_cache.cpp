@@ -1,14 +1,19 @@
-// tq_cache.cpp -- device-resident PQO KV cache: CompressedStorage
-// (reference src/cache/storage.rs:24-203) and PqoCache with the
-// CompressedKVCache contract (src/cache/pqo.rs:21-236), behind a C ABI.
+// tq_cache.cpp -- device-resident compressed KV caches behind a C ABI:
+// CompressedStorage (reference src/cache/storage.rs:24-203), PqoCache
+// (src/cache/pqo.rs:21-236; PQO, and PQ with outlier_blocks = 0) and TqCache
+// (src/cache/tq.rs: PQ codes plus the QJL sketch of the keys' residuals),
+// each with the CompressedKVCache contract.
 //
 // Layout per layer: K/V codes [num_kv_heads][capacity][head_dim*bits/8] u8
 // and scales [num_kv_heads][capacity][head_dim/32] f16, token t of head h at
 // record h * capacity + t, exactly what the fused kernels read with
-// kv_head_stride = capacity.  Appends quantize straight into their records
-// (one launch per tensor, all heads at once); growth reallocates to
-// needed + max(needed / 4, 128) and copies the old rows (storage.rs:108-139).
-// Decode runs the single-launch fused attention over the stored records.
+// kv_head_stride = capacity; a TqCache adds signs [num_kv_heads][capacity]
+// [head_dim/8] u8 and residual norms [num_kv_heads][capacity] f16 at the
+// same records.  Appends quantize straight into their records (one launch
+// per tensor, all heads at once; a TqCache then sketches the new keys);
+// growth reallocates to needed + max(needed / 4, 128) and copies the old rows
+// (storage.rs:108-139, tq.rs:64-94).  Decode runs the single-launch fused
+// attention over the stored records.
 #include "tq_common.h"
 
 #include <cstring>
@@ -24,56 +29,71 @@ __global__ void set_len_kernel(int *p, int v) {
 struct LayerBuffers {
   uint8_t *k_idx = nullptr, *v_idx = nullptr;
   uint16_t *k_sc = nullptr, *v_sc = nullptr;
+  uint8_t *signs = nullptr;     // QJL only
+  uint16_t *norms = nullptr;    // QJL only
   size_t cap = 0;   // records per head
   size_t seq = 0;   // stored tokens per head
   bool active = false;
 };
 
+struct CacheMode {
+  int bits = 3;
+  int norm_mode = TQ_NORM_MAXNORM;
+  size_t outlier_blocks = TQ_OUTLIER_ALL;
+  bool qjl = false;
+};
+
 class CompressedStorage {
  public:
-  CompressedStorage(int num_kv_heads, int head_dim, int bits, int num_layers)
-      : heads_(num_kv_heads), head_dim_(head_dim), bits_(bits), layers_(num_layers) {}
+  CompressedStorage(int num_kv_heads, int head_dim, int bits, int num_layers, bool qjl)
+      : heads_(num_kv_heads), head_dim_(head_dim), bits_(bits), qjl_(qjl), layers_(num_layers) {}
   ~CompressedStorage() { release_all(); }
 
   int packed_dim() const { return head_dim_ * bits_ / 8; }
   int num_blocks() const { return head_dim_ / 32; }
+  int sign_bytes() const { return head_dim_ / 8; }
   size_t seq_len(int l) const { return layers_[l].seq; }
   size_t capacity(int l) const { return layers_[l].cap; }
   bool is_active(int l) const { return layers_[l].active && layers_[l].seq > 0; }
   const LayerBuffers &layer(int l) const { return layers_[l]; }
 
-  // storage.rs:108-139
+  // storage.rs:108-139 (and ensure_qjl_capacity, tq.rs:64-94, same rule)
   int ensure_capacity(int l, size_t needed, hipStream_t stream) {
     LayerBuffers &L = layers_[l];
     if (L.cap >= needed) return TQ_OK;
     const size_t grow = needed / 4 > 128 ? needed / 4 : 128;
     const size_t cap = needed + grow;
     const size_t ib = (size_t)heads_ * cap * packed_dim(), sb = (size_t)heads_ * cap * num_blocks() * 2;
+    const size_t gb = (size_t)heads_ * cap * sign_bytes(), nb = (size_t)heads_ * cap * 2;
     LayerBuffers N;
     N.cap = cap;
     N.seq = L.seq;
     N.active = L.active;
-    if (hipMalloc(&N.k_idx, ib) != hipSuccess || hipMalloc(&N.v_idx, ib) != hipSuccess ||
-        hipMalloc(&N.k_sc, sb) != hipSuccess || hipMalloc(&N.v_sc, sb) != hipSuccess) {
+    bool ok = hipMalloc(&N.k_idx, ib) == hipSuccess && hipMalloc(&N.v_idx, ib) == hipSuccess &&
+              hipMalloc(&N.k_sc, sb) == hipSuccess && hipMalloc(&N.v_sc, sb) == hipSuccess;
+    if (ok && qjl_) ok = hipMalloc(&N.signs, gb) == hipSuccess && hipMalloc(&N.norms, nb) == hipSuccess;
+    if (!ok) {
       free_layer(N);
       return tqh::fail(TQ_ERR_DEVICE, "cache allocation of %zu records per head failed", cap);
     }
     // new capacity starts zeroed, as Tensor::zeros
-    if (hipMemsetAsync(N.k_idx, 0, ib, stream) != hipSuccess || hipMemsetAsync(N.v_idx, 0, ib, stream) != hipSuccess ||
-        hipMemsetAsync(N.k_sc, 0, sb, stream) != hipSuccess || hipMemsetAsync(N.v_sc, 0, sb, stream) != hipSuccess) {
+    ok = hipMemsetAsync(N.k_idx, 0, ib, stream) == hipSuccess && hipMemsetAsync(N.v_idx, 0, ib, stream) == hipSuccess &&
+         hipMemsetAsync(N.k_sc, 0, sb, stream) == hipSuccess && hipMemsetAsync(N.v_sc, 0, sb, stream) == hipSuccess;
+    if (ok && qjl_)
+      ok = hipMemsetAsync(N.signs, 0, gb, stream) == hipSuccess && hipMemsetAsync(N.norms, 0, nb, stream) == hipSuccess;
+    if (!ok) {
       free_layer(N);
       return tqh::fail(TQ_ERR_DEVICE, "cache clear failed");
     }
     if (L.seq > 0) {
+      auto copy = [&](void *dst, const void *src, size_t rec_bytes) {
+        return hipMemcpy2DAsync(dst, cap * rec_bytes, src, L.cap * rec_bytes, L.seq * rec_bytes, heads_,
+                                hipMemcpyDeviceToDevice, stream) == hipSuccess;
+      };
       const size_t pi = packed_dim(), ps = (size_t)num_blocks() * 2;
-      bool ok = hipMemcpy2DAsync(N.k_idx, cap * pi, L.k_idx, L.cap * pi, L.seq * pi, heads_, hipMemcpyDeviceToDevice,
-                                 stream) == hipSuccess;
-      ok = ok && hipMemcpy2DAsync(N.v_idx, cap * pi, L.v_idx, L.cap * pi, L.seq * pi, heads_,
-                                  hipMemcpyDeviceToDevice, stream) == hipSuccess;
-      ok = ok && hipMemcpy2DAsync(N.k_sc, cap * ps, L.k_sc, L.cap * ps, L.seq * ps, heads_, hipMemcpyDeviceToDevice,
-                                  stream) == hipSuccess;
-      ok = ok && hipMemcpy2DAsync(N.v_sc, cap * ps, L.v_sc, L.cap * ps, L.seq * ps, heads_, hipMemcpyDeviceToDevice,
-                                  stream) == hipSuccess;
+      ok = copy(N.k_idx, L.k_idx, pi) && copy(N.v_idx, L.v_idx, pi) && copy(N.k_sc, L.k_sc, ps) &&
+           copy(N.v_sc, L.v_sc, ps);
+      if (ok && qjl_) ok = copy(N.signs, L.signs, sign_bytes()) && copy(N.norms, L.norms, 2);
       if (!ok) {
         free_layer(N);
         return tqh::fail(TQ_ERR_DEVICE, "cache growth copy failed");
@@ -91,26 +111,26 @@ class CompressedStorage {
     layers_[l].active = true;
   }
 
-  // storage.rs:175-186
+  // storage.rs:175-186 (and the QJL buffers, tq.rs:303-312)
   void reset() { release_all(); }
 
-  // storage.rs:188-202
+  // storage.rs:188-202, plus the whole QJL tensors as tq.rs:314-323 counts them
   size_t memory_usage() const {
     size_t total = 0;
     for (const LayerBuffers &L : layers_) {
-      if (L.seq == 0) continue;
-      total += 2 * (size_t)heads_ * L.seq * packed_dim();
-      total += 2 * (size_t)heads_ * L.seq * num_blocks() * 2;
+      if (L.seq > 0) {
+        total += 2 * (size_t)heads_ * L.seq * packed_dim();
+        total += 2 * (size_t)heads_ * L.seq * num_blocks() * 2;
+      }
+      if (qjl_ && L.signs) total += (size_t)heads_ * L.cap * (sign_bytes() + 2);
     }
     return total;
   }
 
  private:
   static void free_layer(LayerBuffers &L) {
-    if (L.k_idx) (void)hipFree(L.k_idx);
-    if (L.v_idx) (void)hipFree(L.v_idx);
-    if (L.k_sc) (void)hipFree(L.k_sc);
-    if (L.v_sc) (void)hipFree(L.v_sc);
+    for (void *p : {(void *)L.k_idx, (void *)L.v_idx, (void *)L.k_sc, (void *)L.v_sc, (void *)L.signs, (void *)L.norms})
+      if (p) (void)hipFree(p);
     L = LayerBuffers{};
   }
   void release_all() {
@@ -118,25 +138,30 @@ class CompressedStorage {
   }
 
   int heads_, head_dim_, bits_;
+  bool qjl_;
   std::vector<LayerBuffers> layers_;
 };
 
-class PqoCache {
+// A PqoCache (mode.qjl false) or TqCache (mode.qjl true).
+class KvCache {
  public:
-  PqoCache(int num_layers, int num_kv_heads, int head_dim, int bits)
-      : layers_(num_layers), heads_(num_kv_heads), head_dim_(head_dim), bits_(bits),
-        storage_(num_kv_heads, head_dim, bits, num_layers), lens_(num_layers, nullptr) {}
-  ~PqoCache() {
+  KvCache(int num_layers, int num_kv_heads, int head_dim, const CacheMode &mode)
+      : layers_(num_layers), heads_(num_kv_heads), head_dim_(head_dim), mode_(mode),
+        storage_(num_kv_heads, head_dim, mode.bits, num_layers, mode.qjl), lens_(num_layers, nullptr) {}
+  ~KvCache() {
     for (int *p : lens_)
       if (p) (void)hipFree(p);
-    if (ws_) (void)hipFree(ws_);
+    for (void *p : {ws_, rmat_, rq_})
+      if (p) (void)hipFree(p);
   }
 
   int layers() const { return layers_; }
   int num_kv_heads() const { return heads_; }
+  int head_dim() const { return head_dim_; }
+  const CacheMode &mode() const { return mode_; }
   CompressedStorage &storage() { return storage_; }
 
-  // quantize_and_store (pqo.rs:64-100): k, v [num_kv_heads][tokens][head_dim]
+  // quantize_and_store (pqo.rs:64-100, tq.rs:97-145): k, v [num_kv_heads][tokens][head_dim]
   int append(int l, const void *k, const void *v, int dtype, int tokens, size_t *old_seq, hipStream_t stream) {
     const size_t old = storage_.seq_len(l);
     *old_seq = old;
@@ -144,27 +169,63 @@ class PqoCache {
     int rc = storage_.ensure_capacity(l, old + tokens, stream);
     if (rc) return rc;
     const LayerBuffers &L = storage_.layer(l);
-    rc = tq_pqo_quantize_to_cache(k, dtype, heads_, tokens, L.k_idx, L.k_sc, (long long)L.cap, (long long)old,
-                                  head_dim_, bits_, stream);
+    rc = tq_polar_quantize_to_cache(k, dtype, heads_, tokens, L.k_idx, L.k_sc, (long long)L.cap, (long long)old,
+                                    head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode, stream);
     if (rc) return rc;
-    rc = tq_pqo_quantize_to_cache(v, dtype, heads_, tokens, L.v_idx, L.v_sc, (long long)L.cap, (long long)old,
-                                  head_dim_, bits_, stream);
+    rc = tq_polar_quantize_to_cache(v, dtype, heads_, tokens, L.v_idx, L.v_sc, (long long)L.cap, (long long)old,
+                                    head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode, stream);
     if (rc) return rc;
+    if (mode_.qjl) {
+      rc = sign_matrix(stream);
+      if (rc) return rc;
+      rc = tq_qjl_cache_sketch(k, dtype, heads_, tokens, L.k_idx, L.k_sc, static_cast<const uint32_t *>(rmat_),
+                               L.signs, L.norms, (long long)L.cap, (long long)old, head_dim_, mode_.bits,
+                               mode_.outlier_blocks, mode_.norm_mode, stream);
+      if (rc) return rc;
+    }
     storage_.set_seq(l, old + tokens);
     return TQ_OK;
   }
 
-  // dequantize_full (pqo.rs:176-180, common.rs:16-62): [num_kv_heads][seq][head_dim]
+  // dequantize_full (common.rs:16-62): [num_kv_heads][seq][head_dim]
   int dequantize_full(int l, void *k_out, void *v_out, int dtype, hipStream_t stream) {
     const LayerBuffers &L = storage_.layer(l);
-    int rc = tq_pqo_dequantize_from_cache(L.k_idx, L.k_sc, (long long)L.cap, heads_, (int)L.seq, k_out, dtype,
-                                          head_dim_, bits_, stream);
+    int rc = tq_polar_dequantize_from_cache(L.k_idx, L.k_sc, (long long)L.cap, heads_, (int)L.seq, k_out, dtype,
+                                            head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode, stream);
     if (rc) return rc;
-    return tq_pqo_dequantize_from_cache(L.v_idx, L.v_sc, (long long)L.cap, heads_, (int)L.seq, v_out, dtype,
-                                        head_dim_, bits_, stream);
+    return tq_polar_dequantize_from_cache(L.v_idx, L.v_sc, (long long)L.cap, heads_, (int)L.seq, v_out, dtype,
+                                          head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode, stream);
   }
 
-  // decode_cuda (pqo.rs:106-174) as one fused launch over the stored records
+  // rq = R q for num_rows query rows, in the cache's scratch
+  int project(const void *q, int q_dtype, size_t num_rows, hipStream_t stream) {
+    int rc = sign_matrix(stream);
+    if (rc) return rc;
+    const size_t need = num_rows * (size_t)head_dim_ * sizeof(float);
+    if (need > rq_bytes_) {
+      if (hipStreamSynchronize(stream) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "stream synchronize failed");
+      if (rq_) (void)hipFree(rq_);
+      rq_ = nullptr;
+      rq_bytes_ = 0;
+      if (hipMalloc(&rq_, need) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "rq allocation failed");
+      rq_bytes_ = need;
+    }
+    return tq_qjl_project(q, q_dtype, static_cast<const uint32_t *>(rmat_), static_cast<float *>(rq_), num_rows,
+                          head_dim_, stream);
+  }
+
+  // compute_logit_bias (tq.rs:185-253): q [num_q_heads][q_len][head_dim],
+  // bias [num_q_heads][q_len][seq_len] in q's dtype
+  int logit_bias(int l, const void *q, int q_dtype, int num_q_heads, int q_len, void *bias, hipStream_t stream) {
+    int rc = project(q, q_dtype, (size_t)num_q_heads * q_len, stream);
+    if (rc) return rc;
+    const LayerBuffers &L = storage_.layer(l);
+    return tq_qjl_logit_bias(static_cast<const float *>(rq_), num_q_heads, q_len, L.signs, L.norms, heads_,
+                             (int)L.seq, (long long)L.cap, head_dim_, bias, q_dtype, stream);
+  }
+
+  // decode_cuda (pqo.rs:106-174) as one fused launch over the stored records;
+  // a TqCache adds the QJL correction inline
   int attend(int l, const void *q, int q_dtype, int num_q_heads, float scale, void *out, int out_dtype,
              hipStream_t stream) {
     const LayerBuffers &L = storage_.layer(l);
@@ -185,73 +246,137 @@ class PqoCache {
       rc = tq_attention_workspace_init(ws_, ws_bytes_, 1, num_q_heads, heads_, head_dim_, (int)L.cap, stream);
       if (rc) return rc;
     }
-    return tq_pqo_decode_attention(q, q_dtype, L.k_idx, L.k_sc, L.v_idx, L.v_sc, lens_[l], 1, num_q_heads, heads_,
-                                   head_dim_, bits_, (int)L.cap, (long long)L.cap, 0, scale, out, out_dtype, ws_,
-                                   ws_bytes_, stream);
+    if (mode_.qjl) {
+      rc = project(q, q_dtype, (size_t)num_q_heads, stream);
+      if (rc) return rc;
+    }
+    return tq_cache_decode_attention(q, q_dtype, L.k_idx, L.k_sc, L.v_idx, L.v_sc,
+                                     mode_.qjl ? static_cast<const float *>(rq_) : nullptr,
+                                     mode_.qjl ? L.signs : nullptr, mode_.qjl ? L.norms : nullptr, lens_[l], 1,
+                                     num_q_heads, heads_, head_dim_, mode_.bits, mode_.outlier_blocks,
+                                     mode_.norm_mode, (int)L.cap, (long long)L.cap, 0, scale, out, out_dtype, ws_,
+                                     ws_bytes_, stream);
   }
 
  private:
-  int layers_, heads_, head_dim_, bits_;
+  // build_rademacher_matrix (precomputed/mod.rs:116-125) as sign bits, once
+  int sign_matrix(hipStream_t stream) {
+    if (rmat_) return TQ_OK;
+    const size_t bytes = (size_t)head_dim_ * head_dim_ / 8;
+    if (hipMalloc(&rmat_, bytes) != hipSuccess) {
+      rmat_ = nullptr;
+      return tqh::fail(TQ_ERR_DEVICE, "sign matrix allocation failed");
+    }
+    return tq_qjl_sign_matrix(static_cast<uint32_t *>(rmat_), head_dim_, kDefaultQjlSeed, stream);
+  }
+
+  static constexpr uint64_t kDefaultQjlSeed = 12345;  // DEFAULT_QJL_SEED (config.rs:17)
+
+  int layers_, heads_, head_dim_;
+  CacheMode mode_;
   CompressedStorage storage_;
   std::vector<int *> lens_;
   void *ws_ = nullptr;
   size_t ws_bytes_ = 0;
+  void *rmat_ = nullptr;
+  void *rq_ = nullptr;
+  size_t rq_bytes_ = 0;
 };
 
-PqoCache *as_cache(void *h) { return static_cast<PqoCache *>(h); }
+KvCache *as_cache(void *h) { return static_cast<KvCache *>(h); }
 
-int check_layer(PqoCache *c, int layer) {
+int check_layer(KvCache *c, int layer) {
   if (!c) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null cache");
   if (layer < 0 || layer >= c->layers())
     return tqh::fail(TQ_ERR_LAYER_OUT_OF_RANGE, "layer %d out of range (num_layers %d)", layer, c->layers());
   return TQ_OK;
 }
 
+int check_q(KvCache *c, const void *q, int q_dtype, int num_q_heads) {
+  if (!q) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null query");
+  if (!tqh::valid_dtype(q_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", q_dtype);
+  if (num_q_heads <= 0 || num_q_heads % c->num_kv_heads() != 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_q_heads (%d) must be a multiple of num_kv_heads (%d)", num_q_heads,
+                     c->num_kv_heads());
+  return TQ_OK;
+}
+
 }  // namespace
 
-extern "C" int tq_pqo_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, void **cache) {
+extern "C" int tq_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, int norm_mode,
+                               size_t outlier_blocks, int qjl, void **cache) {
   if (!cache) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null handle pointer");
   *cache = nullptr;
-  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
-  if (head_dim <= 0 || head_dim % 32 != 0)  // PqoCache::new, pqo.rs:30-39
+  if (head_dim <= 0 || head_dim % 32 != 0)  // PqoCache::new / TqCache::new (pqo.rs:30-39, tq.rs:33-40)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT,
                      "head_dim (%d) must be divisible by QUANT_BLOCK_SIZE (32). Models with head_dim=%d are not "
                      "supported by TurboQuant compression.", head_dim, head_dim);
   if (num_layers <= 0 || num_kv_heads <= 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "empty cache shape");
-  PqoCache *c = new (std::nothrow) PqoCache(num_layers, num_kv_heads, head_dim, bits);
+  tqh::PolarCodec codec;
+  int rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
+  if (qjl && codec.outlier)  // only outlier_blocks = 0 builds the Rademacher matrix (precomputed/mod.rs:84-88)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL Rademacher matrix not precomputed: TqCache needs outlier_blocks 0");
+  if (qjl && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return tqh::fail(TQ_ERR_INVALID_DIMENSION, "TqCache takes head_dim 64, 128 or 256 (got %d)", head_dim);
+  CacheMode mode;
+  mode.bits = bits;
+  mode.norm_mode = norm_mode;
+  mode.outlier_blocks = outlier_blocks;
+  mode.qjl = qjl != 0;
+  KvCache *c = new (std::nothrow) KvCache(num_layers, num_kv_heads, head_dim, mode);
   if (!c) return tqh::fail(TQ_ERR_DEVICE, "out of host memory");
   *cache = c;
   return TQ_OK;
 }
 
-extern "C" void tq_pqo_cache_destroy(void *cache) { delete as_cache(cache); }
+extern "C" void tq_cache_destroy(void *cache) { delete as_cache(cache); }
 
-extern "C" int tq_pqo_cache_prefill(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,
-                                    void *k_out, void *v_out, int *returned_originals, hipStream_t stream) {
-  PqoCache *c = as_cache(cache);
+extern "C" int tq_cache_is_tq(void *cache) {
+  KvCache *c = as_cache(cache);
+  return c && c->mode().qjl ? 1 : 0;
+}
+
+extern "C" int tq_cache_prefill(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,
+                                const void *q, int q_dtype, int num_q_heads, int q_len, void *k_out, void *v_out,
+                                int *returned_originals, void *logit_bias_out, hipStream_t stream) {
+  KvCache *c = as_cache(cache);
   int rc = check_layer(c, layer);
   if (rc) return rc;
   if (!tqh::valid_dtype(dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
   if (tokens < 0 || !returned_originals) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid arguments");
+  const bool tq = c->mode().qjl;
+  if (tq) {
+    rc = check_q(c, q, q_dtype, num_q_heads);
+    if (rc) return rc;
+    if (q_len < 0 || (q_len > 0 && !logit_bias_out))
+      return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "TqCache prefill needs q_len >= 0 and a logit bias output");
+  }
   size_t old = 0;
   rc = c->append(layer, k, v, dtype, tokens, &old, stream);
   if (rc) return rc;
-  // pqo.rs:184-200: the first prefill returns the caller's own K/V
+  // pqo.rs:184-200, tq.rs:258-273: the first prefill returns the caller's own K/V
   *returned_originals = old == 0 ? 1 : 0;
-  if (old == 0) return TQ_OK;
-  if (!k_out || !v_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null output for the dequantized cache");
-  return c->dequantize_full(layer, k_out, v_out, dtype, stream);
+  if (old != 0) {
+    if (!k_out || !v_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null output for the dequantized cache");
+    rc = c->dequantize_full(layer, k_out, v_out, dtype, stream);
+    if (rc) return rc;
+  }
+  if (tq && q_len > 0) return c->logit_bias(layer, q, q_dtype, num_q_heads, q_len, logit_bias_out, stream);
+  return TQ_OK;
 }
 
-extern "C" int tq_pqo_cache_decode(void *cache, int layer, const void *k, const void *v, int kv_dtype, int tokens,
-                                   const void *q, int q_dtype, int num_q_heads, float softmax_scale, void *out,
-                                   int out_dtype, hipStream_t stream) {
-  PqoCache *c = as_cache(cache);
+extern "C" int tq_cache_decode(void *cache, int layer, const void *k, const void *v, int kv_dtype, int tokens,
+                               const void *q, int q_dtype, int num_q_heads, float softmax_scale, void *out,
+                               int out_dtype, hipStream_t stream) {
+  KvCache *c = as_cache(cache);
   int rc = check_layer(c, layer);
   if (rc) return rc;
-  if (!tqh::valid_dtype(kv_dtype) || !tqh::valid_dtype(q_dtype) || !tqh::valid_dtype(out_dtype))
+  if (!tqh::valid_dtype(kv_dtype) || !tqh::valid_dtype(out_dtype))
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype");
-  if (tokens < 0 || !q || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid arguments");
+  rc = check_q(c, q, q_dtype, num_q_heads);
+  if (rc) return rc;
+  if (tokens < 0 || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid arguments");
   size_t old = 0;
   rc = c->append(layer, k, v, kv_dtype, tokens, &old, stream);
   if (rc) return rc;
@@ -259,32 +384,55 @@ extern "C" int tq_pqo_cache_decode(void *cache, int layer, const void *k, const 
   return c->attend(layer, q, q_dtype, num_q_heads, softmax_scale, out, out_dtype, stream);
 }
 
-extern "C" size_t tq_pqo_cache_seq_len(void *cache, int layer) {
-  PqoCache *c = as_cache(cache);
+extern "C" int tq_cache_decode_dequantized(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,
+                                           const void *q, int q_dtype, int num_q_heads, int q_len, void *k_out,
+                                           void *v_out, void *logit_bias_out, hipStream_t stream) {
+  KvCache *c = as_cache(cache);
+  int rc = check_layer(c, layer);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (tokens < 0 || !k_out || !v_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid arguments");
+  const bool tq = c->mode().qjl;
+  if (tq) {
+    rc = check_q(c, q, q_dtype, num_q_heads);
+    if (rc) return rc;
+    if (q_len <= 0 || !logit_bias_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "TqCache decode needs a logit bias output");
+  }
+  size_t old = 0;
+  rc = c->append(layer, k, v, dtype, tokens, &old, stream);
+  if (rc) return rc;
+  rc = c->dequantize_full(layer, k_out, v_out, dtype, stream);  // pqo.rs:219-221, tq.rs:284-289
+  if (rc) return rc;
+  if (tq) return c->logit_bias(layer, q, q_dtype, num_q_heads, q_len, logit_bias_out, stream);
+  return TQ_OK;
+}
+
+extern "C" size_t tq_cache_seq_len(void *cache, int layer) {
+  KvCache *c = as_cache(cache);
   return check_layer(c, layer) ? 0 : c->storage().seq_len(layer);
 }
 
-extern "C" size_t tq_pqo_cache_capacity(void *cache, int layer) {
-  PqoCache *c = as_cache(cache);
+extern "C" size_t tq_cache_capacity(void *cache, int layer) {
+  KvCache *c = as_cache(cache);
   return check_layer(c, layer) ? 0 : c->storage().capacity(layer);
 }
 
-extern "C" int tq_pqo_cache_reset(void *cache) {
-  PqoCache *c = as_cache(cache);
+extern "C" int tq_cache_reset(void *cache) {
+  KvCache *c = as_cache(cache);
   if (!c) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null cache");
   if (hipDeviceSynchronize() != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "device synchronize failed");
   c->storage().reset();
   return TQ_OK;
 }
 
-extern "C" size_t tq_pqo_cache_memory_usage(void *cache) {
-  PqoCache *c = as_cache(cache);
+extern "C" size_t tq_cache_memory_usage(void *cache) {
+  KvCache *c = as_cache(cache);
   return c ? c->storage().memory_usage() : 0;
 }
 
-extern "C" int tq_pqo_cache_buffers(void *cache, int layer, uint8_t **k_indices, uint16_t **k_scales,
-                                    uint8_t **v_indices, uint16_t **v_scales) {
-  PqoCache *c = as_cache(cache);
+extern "C" int tq_cache_buffers(void *cache, int layer, uint8_t **k_indices, uint16_t **k_scales, uint8_t **v_indices,
+                                uint16_t **v_scales, uint8_t **qjl_signs, uint16_t **qjl_norms) {
+  KvCache *c = as_cache(cache);
   int rc = check_layer(c, layer);
   if (rc) return rc;
   const LayerBuffers &L = c->storage().layer(layer);
@@ -292,26 +440,71 @@ extern "C" int tq_pqo_cache_buffers(void *cache, int layer, uint8_t **k_indices,
   if (k_scales) *k_scales = L.k_sc;
   if (v_indices) *v_indices = L.v_idx;
   if (v_scales) *v_scales = L.v_sc;
+  if (qjl_signs) *qjl_signs = L.signs;
+  if (qjl_norms) *qjl_norms = L.norms;
   return TQ_OK;
 }
 
-extern "C" int tq_pqo_cache_read_layer(void *cache, int layer, uint8_t *k_indices, uint16_t *k_scales,
-                                       uint8_t *v_indices, uint16_t *v_scales, hipStream_t stream) {
-  PqoCache *c = as_cache(cache);
+extern "C" int tq_cache_read_layer(void *cache, int layer, uint8_t *k_indices, uint16_t *k_scales, uint8_t *v_indices,
+                                   uint16_t *v_scales, uint8_t *qjl_signs, uint16_t *qjl_norms, hipStream_t stream) {
+  KvCache *c = as_cache(cache);
   int rc = check_layer(c, layer);
   if (rc) return rc;
   const LayerBuffers &L = c->storage().layer(layer);
   if (L.seq == 0) return TQ_OK;
   if (!k_indices || !k_scales || !v_indices || !v_scales) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  const size_t pi = (size_t)c->storage().packed_dim(), ps = (size_t)c->storage().num_blocks() * 2;
   const size_t h = (size_t)c->num_kv_heads();
-  bool ok = hipMemcpy2DAsync(k_indices, L.seq * pi, L.k_idx, L.cap * pi, L.seq * pi, h, hipMemcpyDeviceToDevice,
-                             stream) == hipSuccess;
-  ok = ok && hipMemcpy2DAsync(v_indices, L.seq * pi, L.v_idx, L.cap * pi, L.seq * pi, h, hipMemcpyDeviceToDevice,
-                              stream) == hipSuccess;
-  ok = ok && hipMemcpy2DAsync(k_scales, L.seq * ps, L.k_sc, L.cap * ps, L.seq * ps, h, hipMemcpyDeviceToDevice,
-                              stream) == hipSuccess;
-  ok = ok && hipMemcpy2DAsync(v_scales, L.seq * ps, L.v_sc, L.cap * ps, L.seq * ps, h, hipMemcpyDeviceToDevice,
-                              stream) == hipSuccess;
+  auto copy = [&](void *dst, const void *src, size_t rec_bytes) {
+    return hipMemcpy2DAsync(dst, L.seq * rec_bytes, src, L.cap * rec_bytes, L.seq * rec_bytes, h,
+                            hipMemcpyDeviceToDevice, stream) == hipSuccess;
+  };
+  const size_t pi = (size_t)c->storage().packed_dim(), ps = (size_t)c->storage().num_blocks() * 2;
+  bool ok = copy(k_indices, L.k_idx, pi) && copy(v_indices, L.v_idx, pi) && copy(k_scales, L.k_sc, ps) &&
+            copy(v_scales, L.v_sc, ps);
+  if (ok && c->mode().qjl) {
+    if (qjl_signs) ok = copy(qjl_signs, L.signs, (size_t)c->storage().sign_bytes());
+    if (ok && qjl_norms) ok = copy(qjl_norms, L.norms, 2);
+  }
   return ok ? TQ_OK : tqh::fail(TQ_ERR_DEVICE, "layer copy failed");
+}
+
+// ---- PqoCache / TqCache entry points of the earlier interface ----
+
+extern "C" int tq_pqo_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, void **cache) {
+  return tq_cache_create(num_layers, num_kv_heads, head_dim, bits, TQ_NORM_MAXNORM, TQ_OUTLIER_ALL, 0, cache);
+}
+
+extern "C" int tq_tq_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, void **cache) {
+  return tq_cache_create(num_layers, num_kv_heads, head_dim, bits, TQ_NORM_MAXNORM, 0, 1, cache);
+}
+
+extern "C" void tq_pqo_cache_destroy(void *cache) { tq_cache_destroy(cache); }
+
+extern "C" int tq_pqo_cache_prefill(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,
+                                    void *k_out, void *v_out, int *returned_originals, hipStream_t stream) {
+  if (tq_cache_is_tq(cache)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "TqCache prefill takes q (tq_cache_prefill)");
+  return tq_cache_prefill(cache, layer, k, v, dtype, tokens, nullptr, 0, 0, 0, k_out, v_out, returned_originals,
+                          nullptr, stream);
+}
+
+extern "C" int tq_pqo_cache_decode(void *cache, int layer, const void *k, const void *v, int kv_dtype, int tokens,
+                                   const void *q, int q_dtype, int num_q_heads, float softmax_scale, void *out,
+                                   int out_dtype, hipStream_t stream) {
+  return tq_cache_decode(cache, layer, k, v, kv_dtype, tokens, q, q_dtype, num_q_heads, softmax_scale, out, out_dtype,
+                         stream);
+}
+
+extern "C" size_t tq_pqo_cache_seq_len(void *cache, int layer) { return tq_cache_seq_len(cache, layer); }
+extern "C" size_t tq_pqo_cache_capacity(void *cache, int layer) { return tq_cache_capacity(cache, layer); }
+extern "C" int tq_pqo_cache_reset(void *cache) { return tq_cache_reset(cache); }
+extern "C" size_t tq_pqo_cache_memory_usage(void *cache) { return tq_cache_memory_usage(cache); }
+
+extern "C" int tq_pqo_cache_buffers(void *cache, int layer, uint8_t **k_indices, uint16_t **k_scales,
+                                    uint8_t **v_indices, uint16_t **v_scales) {
+  return tq_cache_buffers(cache, layer, k_indices, k_scales, v_indices, v_scales, nullptr, nullptr);
+}
+
+extern "C" int tq_pqo_cache_read_layer(void *cache, int layer, uint8_t *k_indices, uint16_t *k_scales,
+                                       uint8_t *v_indices, uint16_t *v_scales, hipStream_t stream) {
+  return tq_cache_read_layer(cache, layer, k_indices, k_scales, v_indices, v_scales, nullptr, nullptr, stream);
 }

@@ -65,6 +65,24 @@ PqoCodebook pqo_codebook(int bits) {
   return cb;
 }
 
+int polar_codec(int bits, int norm_mode, size_t outlier_blocks, int num_blocks, PolarCodec &codec) {
+  if (bits != 3 && bits != 4) return fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+  if (norm_mode != TQ_NORM_MAXNORM)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "norm mode %d is not implemented by this library (MaxNorm only)", norm_mode);
+  const bool all = outlier_blocks >= (size_t)num_blocks;
+  if (!all && outlier_blocks != 0)
+    return fail(TQ_ERR_INVALID_ARGUMENT,
+                "mixed outlier blocks (%zu of %d) are not implemented by this library (0 or all)", outlier_blocks,
+                num_blocks);
+  codec.bits = bits;
+  codec.cb_bits = all ? bits : bits - 1;
+  codec.outlier = all;
+  codec.cb = pqo_codebook(codec.cb_bits);
+  codec.outer = pqo_codebook(bits).outer;  // outlier codebook = polar_bits + 1 = bits (codebooks.rs:84-88)
+  codec.scale_sign = all ? -1.f : 1.f;     // build_scale_sign_tensor (precomputed/mod.rs:102-114)
+  return TQ_OK;
+}
+
 static float next_up_host(float f) {
   uint32_t u;
   std::memcpy(&u, &f, 4);

@@ -29,6 +29,25 @@ struct PqoCodebook {
 };
 PqoCodebook pqo_codebook(int bits);
 
+// Codec of one cache mode (CacheConfig, src/cache/config.rs:50-85;
+// GpuPrecomputed, precomputed/mod.rs:45-98).  outlier_blocks >= num_blocks
+// (PQO): every block on the bits-bit outlier codebook, negative scales.
+// outlier_blocks == 0 (PQ / TQ): the standard (bits - 1)-bit codebook, its
+// codes in bits-wide slots (packed_dim = head_dim * bits / 8), positive
+// scales.  MaxNorm divides by the outlier codebook's largest centroid in both
+// (quantize_tensor.rs:103-108).
+struct PolarCodec {
+  int bits = 0;     // slot width
+  int cb_bits = 0;  // codebook width (bits or bits - 1)
+  bool outlier = false;
+  PqoCodebook cb;   // centroids / boundaries of the blocks' codebook
+  float outer = 0.f;
+  float scale_sign = 1.f;
+};
+// Fills `codec` for (bits, norm_mode, outlier_blocks) or returns an error
+// status for a mode this library does not implement.
+int polar_codec(int bits, int norm_mode, size_t outlier_blocks, int num_blocks, PolarCodec &codec);
+
 // Per-boundary constants of the exact division threshold (see
 // tqd::div_threshold): mu = midpoint of b and nextup(b), strict = b even.
 struct DivThresholds {

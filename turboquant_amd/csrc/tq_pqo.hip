@@ -137,11 +137,13 @@ __device__ __forceinline__ uint32_t push_bit(uint32_t acc, bool bit) {
 // LSB-first bitstream is built from its most significant bit down: code j's
 // bits go to stream bits 3j+2 .. 3j (for 3-bit codes) and each 32-bit word
 // is the last 32 bits pushed into it, so codes that straddle words need no
-// special case.
-template <int BITS>
+// special case.  CB < BITS: CB-bit codes (the standard codebook) in BITS-wide
+// slots, whose top bits stay zero (quantize_tensor.rs:73, config.rs:82-84).
+template <int BITS, int CB = BITS>
 __device__ __forceinline__ float quantize_block(const float (&r)[32], const QuantConsts &k,
                                                 uint32_t (&w)[Packed<BITS>::kWords]) {
-  constexpr int NB = (1 << BITS) - 1;
+  static_assert(CB <= BITS, "codes fit their slots");
+  constexpr int NB = (1 << CB) - 1;
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(r[j]));
@@ -158,12 +160,13 @@ __device__ __forceinline__ float quantize_block(const float (&r)[32], const Quan
     for (int q = 0; q < Packed<BITS>::kWords; q++) acc[q] = 0;
 #pragma unroll
     for (int j = 31; j >= 0; j--) {
-      bool bit[BITS];
-      bucket_bits<BITS>(r[j], U, bit);
+      bool bit[CB];
+      bucket_bits<CB>(r[j], U, bit);
 #pragma unroll
       for (int t = 0; t < BITS; t++) {
         const int pos = j * BITS + (BITS - 1 - t);
-        acc[pos >> 5] = push_bit(acc[pos >> 5], bit[t]);
+        if (t < BITS - CB) acc[pos >> 5] <<= 1;
+        else acc[pos >> 5] = push_bit(acc[pos >> 5], bit[t - (BITS - CB)]);
       }
     }
 #pragma unroll
@@ -225,7 +228,7 @@ __device__ __forceinline__ long long cache_block(uint32_t blk, const CacheMap &m
 // ROTATE: input is raw activations (fused forward rotation, butterfly order).
 // Otherwise input is already rotated f32 (the reference kernel's contract).
 // MAP: outputs go to cache records (CacheMap) instead of block order.
-template <int BITS, int IN_DT, bool ROTATE, bool MAP = false>
+template <int BITS, int CB, int IN_DT, bool ROTATE, bool MAP = false>
 __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__ x,
                                                         uint8_t *__restrict__ packed,
                                                         uint16_t *__restrict__ scales,
@@ -241,7 +244,7 @@ __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__
     for (int j = 0; j < 32; j++) r[j] = r[j] * (pqo_neg(j) ? -kInvSqrt32 : kInvSqrt32);
   }
   uint32_t w[Packed<BITS>::kWords];
-  float s = quantize_block<BITS>(r, k, w);
+  float s = quantize_block<BITS, CB>(r, k, w);
   store_packed<BITS>(packed, ob, w);
   scales[ob] = f32_to_f16(s * k.scale_sign);
 }
@@ -364,29 +367,32 @@ __global__ __launch_bounds__(256) void pack_indices_kernel(const uint8_t *__rest
   out[g] = (uint8_t)(acc & 0xffu);
 }
 
-int launch_quant(const void *x, int dt, bool rotate, uint8_t *packed, uint16_t *scales, long long nblocks,
-                 int bits, const QuantConsts &k, hipStream_t st) {
+// One launch of pqo_quant_kernel for (slot bits, codebook bits, input type):
+// ROTATE for activations, MAP for cache placement.
+template <bool ROTATE, bool MAP>
+int launch_quant(const void *x, int dt, uint8_t *packed, uint16_t *scales, long long nblocks, int bits, int cb_bits,
+                 const QuantConsts &k, const CacheMap &m, hipStream_t st) {
   const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
-#define QL(B, D, R) hipLaunchKernelGGL((pqo_quant_kernel<B, D, R>), grid, block, 0, st, x, packed, scales, nblocks, k)
-  if (!rotate) {
-    if (bits == 2) QL(2, kF32, false);
-    else if (bits == 3) QL(3, kF32, false);
-    else QL(4, kF32, false);
-  } else if (bits == 3) {
-    if (dt == kF32) QL(3, kF32, true);
-    else if (dt == kBF16) QL(3, kBF16, true);
-    else QL(3, kF16, true);
-  } else {
-    if (dt == kF32) QL(4, kF32, true);
-    else if (dt == kBF16) QL(4, kBF16, true);
-    else QL(4, kF16, true);
-  }
+#define QL(B, C, D) hipLaunchKernelGGL((pqo_quant_kernel<B, C, D, ROTATE, MAP>), grid, block, 0, st, x, packed, \
+                                       scales, nblocks, k, m)
+#define QD(B, C) \
+  do {                                      \
+    if (!ROTATE || dt == kF32) QL(B, C, kF32); \
+    else if (dt == kBF16) QL(B, C, kBF16);  \
+    else QL(B, C, kF16);                    \
+  } while (0)
+  if (bits == 2) QD(2, 2);
+  else if (bits == 3 && cb_bits == 3) QD(3, 3);
+  else if (bits == 3) QD(3, 2);
+  else if (cb_bits == 4) QD(4, 4);
+  else QD(4, 3);
+#undef QD
 #undef QL
   return tqh::check_launch("pqo_quant_kernel");
 }
 
-QuantConsts make_quant_consts(const tqh::PqoCodebook &cb, float scale_sign) {
-  tqh::DivThresholds t = tqh::div_thresholds(cb.b, cb.nc - 1, cb.outer);
+QuantConsts make_quant_consts(const tqh::PqoCodebook &cb, float outer, float scale_sign) {
+  tqh::DivThresholds t = tqh::div_thresholds(cb.b, cb.nc - 1, outer);
   QuantConsts k{};
   for (int i = 0; i < t.nb; i++) {
     k.mu[i] = t.mu[i];
@@ -418,31 +424,19 @@ DequantConsts make_dequant_consts(const tqh::PqoCodebook &cb) {
 // C ABI
 // ---------------------------------------------------------------------------
 
-extern "C" int tq_pqo_quantize(const void *x, int x_dtype, uint8_t *packed_out, uint16_t *scales_out,
-                               size_t num_vectors, int head_dim, int bits, hipStream_t stream) {
-  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+namespace {
+int check_shape(int head_dim) {
   if (head_dim <= 0 || head_dim % 32 != 0)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "head_dim (%d) must be divisible by QUANT_BLOCK_SIZE (32)", head_dim);
-  if (!tqh::valid_dtype(x_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", x_dtype);
-  if (num_vectors == 0) return TQ_OK;
-  if (!x || !packed_out || !scales_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  const long long nblocks = (long long)num_vectors * (head_dim / 32);
-  QuantConsts k = make_quant_consts(tqh::pqo_codebook(bits), -1.0f);
-  return launch_quant(x, x_dtype, true, packed_out, scales_out, nblocks, bits, k, stream);
+  return TQ_OK;
 }
 
-extern "C" int tq_pqo_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
-                                 size_t num_vectors, int head_dim, int bits, hipStream_t stream) {
-  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
-  if (head_dim <= 0 || head_dim % 32 != 0)
-    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "head_dim (%d) must be divisible by QUANT_BLOCK_SIZE (32)", head_dim);
-  if (!tqh::valid_dtype(out_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", out_dtype);
-  if (num_vectors == 0) return TQ_OK;
-  if (!packed || !scales || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  const long long nblocks = (long long)num_vectors * (head_dim / 32);
-  DequantConsts dc = make_dequant_consts(tqh::pqo_codebook(bits));
+template <bool MAP>
+int launch_dequant(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype, long long nblocks,
+                   int bits, const DequantConsts &dc, const CacheMap &m, hipStream_t stream) {
   const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
-#define DL(B, D) hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false>), grid, block, 0, stream, packed, scales, out, nblocks, dc, nullptr, nullptr)
+#define DL(B, D) hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false, MAP>), grid, block, 0, stream, packed, scales, \
+                                    out, nblocks, dc, nullptr, nullptr, m)
   if (bits == 3) {
     if (out_dtype == kF32) DL(3, kF32);
     else if (out_dtype == kBF16) DL(3, kBF16);
@@ -454,6 +448,52 @@ extern "C" int tq_pqo_dequantize(const uint8_t *packed, const uint16_t *scales, 
   }
 #undef DL
   return tqh::check_launch("pqo_dequant_kernel");
+}
+}  // namespace
+
+extern "C" int tq_polar_quantize(const void *x, int x_dtype, uint8_t *packed_out, uint16_t *scales_out,
+                                 size_t num_vectors, int head_dim, int bits, size_t outlier_blocks, int norm_mode,
+                                 hipStream_t stream) {
+  int rc = check_shape(head_dim);
+  if (rc) return rc;
+  tqh::PolarCodec codec;
+  rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(x_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", x_dtype);
+  if (num_vectors == 0) return TQ_OK;
+  if (!x || !packed_out || !scales_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long nblocks = (long long)num_vectors * (head_dim / 32);
+  const QuantConsts k = make_quant_consts(codec.cb, codec.outer, codec.scale_sign);
+  return launch_quant<true, false>(x, x_dtype, packed_out, scales_out, nblocks, bits, codec.cb_bits, k, CacheMap{},
+                                   stream);
+}
+
+extern "C" int tq_polar_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
+                                   size_t num_vectors, int head_dim, int bits, size_t outlier_blocks, int norm_mode,
+                                   hipStream_t stream) {
+  int rc = check_shape(head_dim);
+  if (rc) return rc;
+  tqh::PolarCodec codec;
+  rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(out_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", out_dtype);
+  if (num_vectors == 0) return TQ_OK;
+  if (!packed || !scales || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long nblocks = (long long)num_vectors * (head_dim / 32);
+  return launch_dequant<false>(packed, scales, out, out_dtype, nblocks, bits, make_dequant_consts(codec.cb),
+                               CacheMap{}, stream);
+}
+
+extern "C" int tq_pqo_quantize(const void *x, int x_dtype, uint8_t *packed_out, uint16_t *scales_out,
+                               size_t num_vectors, int head_dim, int bits, hipStream_t stream) {
+  return tq_polar_quantize(x, x_dtype, packed_out, scales_out, num_vectors, head_dim, bits, TQ_OUTLIER_ALL,
+                           TQ_NORM_MAXNORM, stream);
+}
+
+extern "C" int tq_pqo_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
+                                 size_t num_vectors, int head_dim, int bits, hipStream_t stream) {
+  return tq_polar_dequantize(packed, scales, out, out_dtype, num_vectors, head_dim, bits, TQ_OUTLIER_ALL,
+                             TQ_NORM_MAXNORM, stream);
 }
 
 extern "C" int tq_quant_maxnorm_batch(const float *rotated_input, const float *boundaries, uint8_t *packed_out,
@@ -546,58 +586,56 @@ int cache_map(int num_heads, int tokens, int head_dim, long long head_stride, lo
 }
 }  // namespace
 
-extern "C" int tq_pqo_quantize_to_cache(const void *x, int x_dtype, int num_heads, int tokens, uint8_t *packed_cache,
-                                        uint16_t *scales_cache, long long cache_head_stride, long long cache_offset,
-                                        int head_dim, int bits, hipStream_t stream) {
-  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
+extern "C" int tq_polar_quantize_to_cache(const void *x, int x_dtype, int num_heads, int tokens,
+                                          uint8_t *packed_cache, uint16_t *scales_cache, long long cache_head_stride,
+                                          long long cache_offset, int head_dim, int bits, size_t outlier_blocks,
+                                          int norm_mode, hipStream_t stream) {
+  int rc = check_shape(head_dim);
+  if (rc) return rc;
+  tqh::PolarCodec codec;
+  rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
   if (!tqh::valid_dtype(x_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", x_dtype);
   CacheMap m;
-  int rc = cache_map(num_heads, tokens, head_dim, cache_head_stride, cache_offset, m);
+  rc = cache_map(num_heads, tokens, head_dim, cache_head_stride, cache_offset, m);
   if (rc) return rc;
   const long long nblocks = (long long)num_heads * tokens * (head_dim / 32);
   if (nblocks == 0) return TQ_OK;
   if (!x || !packed_cache || !scales_cache) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  const QuantConsts k = make_quant_consts(tqh::pqo_codebook(bits), -1.0f);
-  const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
-#define QM(B, D) hipLaunchKernelGGL((pqo_quant_kernel<B, D, true, true>), grid, block, 0, stream, x, packed_cache, \
-                                    scales_cache, nblocks, k, m)
-  if (bits == 3) {
-    if (x_dtype == kF32) QM(3, kF32);
-    else if (x_dtype == kBF16) QM(3, kBF16);
-    else QM(3, kF16);
-  } else {
-    if (x_dtype == kF32) QM(4, kF32);
-    else if (x_dtype == kBF16) QM(4, kBF16);
-    else QM(4, kF16);
-  }
-#undef QM
-  return tqh::check_launch("pqo_quant_kernel (cache)");
+  const QuantConsts k = make_quant_consts(codec.cb, codec.outer, codec.scale_sign);
+  return launch_quant<true, true>(x, x_dtype, packed_cache, scales_cache, nblocks, bits, codec.cb_bits, k, m, stream);
+}
+
+extern "C" int tq_polar_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *scales_cache,
+                                              long long cache_head_stride, int num_heads, int tokens, void *out,
+                                              int out_dtype, int head_dim, int bits, size_t outlier_blocks,
+                                              int norm_mode, hipStream_t stream) {
+  int rc = check_shape(head_dim);
+  if (rc) return rc;
+  tqh::PolarCodec codec;
+  rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(out_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", out_dtype);
+  CacheMap m;
+  rc = cache_map(num_heads, tokens, head_dim, cache_head_stride, 0, m);
+  if (rc) return rc;
+  const long long nblocks = (long long)num_heads * tokens * (head_dim / 32);
+  if (nblocks == 0) return TQ_OK;
+  if (!packed_cache || !scales_cache || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  return launch_dequant<true>(packed_cache, scales_cache, out, out_dtype, nblocks, bits, make_dequant_consts(codec.cb),
+                              m, stream);
+}
+
+extern "C" int tq_pqo_quantize_to_cache(const void *x, int x_dtype, int num_heads, int tokens, uint8_t *packed_cache,
+                                        uint16_t *scales_cache, long long cache_head_stride, long long cache_offset,
+                                        int head_dim, int bits, hipStream_t stream) {
+  return tq_polar_quantize_to_cache(x, x_dtype, num_heads, tokens, packed_cache, scales_cache, cache_head_stride,
+                                    cache_offset, head_dim, bits, TQ_OUTLIER_ALL, TQ_NORM_MAXNORM, stream);
 }
 
 extern "C" int tq_pqo_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *scales_cache,
                                             long long cache_head_stride, int num_heads, int tokens, void *out,
                                             int out_dtype, int head_dim, int bits, hipStream_t stream) {
-  if (bits != 3 && bits != 4) return tqh::fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
-  if (!tqh::valid_dtype(out_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", out_dtype);
-  CacheMap m;
-  int rc = cache_map(num_heads, tokens, head_dim, cache_head_stride, 0, m);
-  if (rc) return rc;
-  const long long nblocks = (long long)num_heads * tokens * (head_dim / 32);
-  if (nblocks == 0) return TQ_OK;
-  if (!packed_cache || !scales_cache || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  const DequantConsts dc = make_dequant_consts(tqh::pqo_codebook(bits));
-  const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
-#define DM(B, D) hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false, true>), grid, block, 0, stream, packed_cache, \
-                                    scales_cache, out, nblocks, dc, nullptr, nullptr, m)
-  if (bits == 3) {
-    if (out_dtype == kF32) DM(3, kF32);
-    else if (out_dtype == kBF16) DM(3, kBF16);
-    else DM(3, kF16);
-  } else {
-    if (out_dtype == kF32) DM(4, kF32);
-    else if (out_dtype == kBF16) DM(4, kBF16);
-    else DM(4, kF16);
-  }
-#undef DM
-  return tqh::check_launch("pqo_dequant_kernel (cache)");
+  return tq_polar_dequantize_from_cache(packed_cache, scales_cache, cache_head_stride, num_heads, tokens, out,
+                                        out_dtype, head_dim, bits, TQ_OUTLIER_ALL, TQ_NORM_MAXNORM, stream);
 }

@@ -300,6 +300,215 @@ __global__ __launch_bounds__(kBlock) void qjl_wv_finish_kernel(const float *__re
   for (int e = 0; e < D; e++) out[qi * D + e] = (a[e] * k.polar.wht_norm) * ((e & 1) ? so : se);
 }
 
+// ---------------------------------------------------------------------------
+// TqCache on the device (reference src/cache/tq.rs): the sign matrix of R,
+// the sketch of cached keys' residuals, query projections and the logit bias.
+// ---------------------------------------------------------------------------
+
+// The d x d sign bits of R once, for kernels that read rather than hash them:
+// out[j * D/32 + w] bit b set <=> sign(j, 32 w + b) = -1.
+template <int D>
+__global__ __launch_bounds__(kBlock) void qjl_sign_matrix_kernel(uint32_t *__restrict__ out, uint64_t seed) {
+  const int it = blockIdx.x * kBlock + threadIdx.x;
+  if (it >= D * D / 32) return;
+  const int j = it / (D / 32), w = it % (D / 32);
+  const uint64_t rs = mix_seed(seed, (uint64_t)j);
+  uint32_t bits = 0;
+  for (int b = 0; b < 32; b++) bits |= (sign_negative(rs, (uint64_t)j, (uint64_t)(32 * w + b)) ? 1u : 0u) << b;
+  out[it] = bits;
+}
+
+// Lane j of a wave: p_j = (sum_c sign(j, c) v[c]) * inv for rows j = lane +
+// 64 m (rademacher_vector_product, qjl.rs:196-208: column order, the +-v
+// products exact), v read from LDS.
+template <int D>
+__device__ __forceinline__ void wave_row_products(const float *s_v, const uint32_t *__restrict__ rbits, float inv,
+                                                  int lane, float (&p)[D / 64]) {
+  constexpr int E = D / 64, NWR = D / 32;
+  uint32_t rb[E][NWR];
+#pragma unroll
+  for (int m = 0; m < E; m++)
+#pragma unroll
+    for (int w = 0; w < NWR; w++) rb[m][w] = rbits[(lane + 64 * m) * NWR + w];
+  float acc[E];
+#pragma unroll
+  for (int m = 0; m < E; m++) acc[m] = -0.0f;
+#pragma unroll
+  for (int c4 = 0; c4 < D / 4; c4++) {
+    const float4 v = reinterpret_cast<const float4 *>(s_v)[c4];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = 4 * c4 + i;
+#pragma unroll
+      for (int m = 0; m < E; m++)
+        acc[m] = __builtin_fmaf(((rb[m][c >> 5] >> (c & 31)) & 1u) ? -1.0f : 1.0f, vv[i], acc[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < E; m++) p[m] = acc[m] * inv;
+}
+
+struct SketchConsts {
+  float cb[16];      // the cache codec's centroids
+  uint32_t sign_mask;  // decode sign pattern (bit j set: -fl(R_fwd[0][j] * sqrt 32))
+  float decode_factor;
+  float inv_sqrt_d;
+  long long head_stride, offset;
+  int tokens;
+};
+
+// compute_qjl_signs_and_norms for keys just appended to a TqCache
+// (tq.rs:154-182, 373-412), one wave per key vector (h, t): the key's cache
+// record is dequantized exactly as polar_dequantize's CPU branch
+// (quantize_tensor.rs:197-219, 32-lane butterflies), the residual
+// r = k - k_hat is summed as sum r^2 in element order for the norm, and
+// sign bit j = (R r)_j >= 0 (qjl.rs:305-319) is one wave ballot per 64 rows.
+template <int D, int BITS, int IN_DT>
+__global__ __launch_bounds__(kBlock) void qjl_cache_sketch_kernel(
+    const void *__restrict__ x, const uint8_t *__restrict__ packed, const uint16_t *__restrict__ scales,
+    const uint32_t *__restrict__ rbits, uint8_t *__restrict__ signs, uint16_t *__restrict__ norms, long long nvec,
+    SketchConsts k) {
+  constexpr int E = D / 64, NQB = D / 32, WB = 4 * BITS;
+  __shared__ __attribute__((aligned(16))) float s_r[kBlock / 64][D];
+  __shared__ float s_cb[16];
+#pragma unroll
+  for (int q = 0; q < 16; q++)
+    if (threadIdx.x == q) s_cb[q] = k.cb[q];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long long v = (long long)blockIdx.x * (kBlock / 64) + wave;
+  if (v >= nvec) return;  // whole waves leave together
+  const long long h = v / k.tokens, t = v - h * k.tokens;
+  const long long rec = h * k.head_stride + k.offset + t;
+  const int i = lane & 31;
+  const float sg = ((k.sign_mask >> i) & 1u) ? -k.decode_factor : k.decode_factor;
+  float *r = s_r[wave];
+#pragma unroll
+  for (int m = 0; m < E; m++) {
+    const int e = 64 * m + lane, qb = e >> 5;
+    uint32_t w[BITS];
+#pragma unroll
+    for (int q = 0; q < BITS; q++) w[q] = reinterpret_cast<const uint32_t *>(packed + rec * (NQB * WB) + qb * WB)[q];
+    // field i of the block's LSB-first bitstream (select chains: no
+    // dynamically indexed registers)
+    const int pos = i * BITS, wi = pos >> 5, sh = pos & 31;
+    uint32_t lo = w[0], hi = w[1];
+#pragma unroll
+    for (int q = 1; q < BITS; q++) lo = (wi == q) ? w[q] : lo;
+#pragma unroll
+    for (int q = 2; q < BITS; q++) hi = (wi + 1 == q) ? w[q] : hi;
+    hi = (wi + 1 < BITS) ? hi : 0u;
+    const uint32_t code = __builtin_amdgcn_alignbit(hi, lo, sh) & ((1u << BITS) - 1u);
+    float y = s_cb[code] * sg;
+#pragma unroll
+    for (int hh = 1; hh < 32; hh <<= 1) {
+      const float o = __shfl_xor(y, hh, 64);
+      y = (i & hh) ? (o - y) : (y + o);
+    }
+    const float s = fabsf(f16_to_f32(scales[rec * NQB + qb]));
+    y = (y * 0x1.6a09e6p-3f) * s;
+    const long long xi = v * D + e;
+    float xv;
+    if constexpr (IN_DT == kF32) xv = static_cast<const float *>(x)[xi];
+    else if constexpr (IN_DT == kBF16) xv = bf16_to_f32(static_cast<const uint16_t *>(x)[xi]);
+    else xv = f16_to_f32(static_cast<const uint16_t *>(x)[xi]);
+    r[e] = xv - y;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float p[E];
+  wave_row_products<D>(r, rbits, k.inv_sqrt_d, lane, p);
+  uint64_t mask[E];
+#pragma unroll
+  for (int m = 0; m < E; m++) mask[m] = __builtin_amdgcn_ballot_w64(p[m] >= 0.0f);
+  if (lane == 0) {
+    float ss = 0.0f;
+    for (int e = 0; e < D; e++) ss = ss + r[e] * r[e];
+    norms[rec] = f32_to_f16(sqrtf(ss));
+    uint32_t *sp = reinterpret_cast<uint32_t *>(signs + rec * (D / 8));
+#pragma unroll
+    for (int m = 0; m < E; m++) {
+      sp[2 * m] = (uint32_t)mask[m];
+      sp[2 * m + 1] = (uint32_t)(mask[m] >> 32);
+    }
+  }
+}
+
+// rq = R q per row (precompute_query_projections, qjl.rs:488-492; r_q = q R^T
+// of tq.rs:233-234), one wave per row.
+template <int D, int IN_DT>
+__global__ __launch_bounds__(kBlock) void qjl_project_kernel(const void *__restrict__ q,
+                                                             const uint32_t *__restrict__ rbits,
+                                                             float *__restrict__ rq, long long nrows, float inv) {
+  constexpr int E = D / 64;
+  __shared__ __attribute__((aligned(16))) float s_q[kBlock / 64][D];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long long row = (long long)blockIdx.x * (kBlock / 64) + wave;
+  if (row >= nrows) return;
+#pragma unroll
+  for (int m = 0; m < E; m++) {
+    const long long xi = row * D + 64 * m + lane;
+    float xv;
+    if constexpr (IN_DT == kF32) xv = static_cast<const float *>(q)[xi];
+    else if constexpr (IN_DT == kBF16) xv = bf16_to_f32(static_cast<const uint16_t *>(q)[xi]);
+    else xv = f16_to_f32(static_cast<const uint16_t *>(q)[xi]);
+    s_q[wave][64 * m + lane] = xv;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float p[E];
+  wave_row_products<D>(s_q[wave], rbits, inv, lane, p);
+#pragma unroll
+  for (int m = 0; m < E; m++) rq[row * D + 64 * m + lane] = p[m];
+}
+
+// compute_logit_bias (tq.rs:185-253): bias[h][i][t] = (sum_j rq[h][i][j]
+// (2 b_tj - 1)) * (|r_t| * sf), sf = f32(sqrt(pi/2)) / sqrt(d), for query
+// head h over KV head h / (H / H_kv).  Lane = token; per workgroup QB
+// queries of one head, their +-rq nibble sums in LDS.
+template <int D, int QB>
+__global__ __launch_bounds__(kBlock) void qjl_logit_bias_kernel(const float *__restrict__ rq, int q_len,
+                                                                const uint32_t *__restrict__ signs,
+                                                                const uint16_t *__restrict__ norms, int kv_len,
+                                                                long long head_stride, int n_rep, float sf,
+                                                                void *__restrict__ out, int out_dtype) {
+  constexpr int CT = (D / 4) * 16;
+  __shared__ float s_tab[QB * CT];
+  const int h = blockIdx.z;
+  const int i0 = blockIdx.y * QB;
+  const int nql = min(QB, q_len - i0);
+  for (int e = threadIdx.x; e < nql * CT; e += kBlock) {
+    const int ql = e / CT, rr = e % CT, c = rr / 16, m = rr % 16;
+    const float *rp = rq + (((long long)h * q_len + i0 + ql) * D) + 4 * c;
+    float val = -0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; b++) val = val + (((m >> b) & 1) ? rp[b] : -rp[b]);
+    s_tab[e] = val;
+  }
+  __syncthreads();
+  const int t = blockIdx.x * kBlock + threadIdx.x;
+  if (t >= kv_len) return;
+  const long long rec = (long long)(h / n_rep) * head_stride + t;
+  uint32_t sgn[D / 32];
+#pragma unroll
+  for (int w = 0; w < D / 32; w++) sgn[w] = signs[rec * (D / 32) + w];
+  const float c = f16_to_f32(norms[rec]) * sf;
+  for (int ql = 0; ql < nql; ql++) {
+    const float *tb = s_tab + ql * CT;
+    float raw = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < D / 4; cc++) raw += tb[cc * 16 + ((sgn[cc >> 3] >> ((cc & 7) * 4)) & 15u)];
+    const float val = raw * c;
+    const long long oi = ((long long)h * q_len + i0 + ql) * kv_len + t;
+    if (out_dtype == kF32) static_cast<float *>(out)[oi] = val;
+    else if (out_dtype == kBF16) static_cast<uint16_t *>(out)[oi] = f32_to_bf16(val);
+    else static_cast<uint16_t *>(out)[oi] = f32_to_f16(val);
+  }
+}
+
 int qjl_consts(int polar_bits, int dim, uint64_t rot_seed, uint64_t qjl_seed, QjlConsts &k) {
   if (dim != 32 && dim != 64 && dim != 128)
     return tqh::fail(TQ_ERR_INVALID_DIMENSION, "QJL kernels take dim 32, 64 or 128 (got %d)", dim);
@@ -437,5 +646,151 @@ extern "C" int tq_qjl_weighted_values(const uint8_t *polar_packed, const uint16_
     hipLaunchKernelGGL((qjl_wv_finish_kernel<D>), dim3(grid_for(nq)), dim3(kBlock), 0, stream, partial, nchunks, out,
                        nq, k);
     return tqh::check_launch("qjl_wv_finish_kernel");
+  });
+}
+
+// ---------------------------------------------------------------------------
+// TqCache building blocks
+// ---------------------------------------------------------------------------
+
+namespace {
+float inv_sqrt_dim(int dim) {
+  volatile float fd = (float)dim;
+  volatile float sq = sqrtf(fd);
+  return 1.0f / sq;
+}
+int check_sketch_dim(int dim) {
+  if (dim != 64 && dim != 128 && dim != 256)
+    return tqh::fail(TQ_ERR_INVALID_DIMENSION, "cache QJL kernels take head_dim 64, 128 or 256 (got %d)", dim);
+  return TQ_OK;
+}
+template <typename F>
+int by_cache_dim(int dim, F &&f) {
+  switch (dim) {
+    case 64: return f(std::integral_constant<int, 64>{});
+    case 128: return f(std::integral_constant<int, 128>{});
+    case 256: return f(std::integral_constant<int, 256>{});
+  }
+  return tqh::fail(TQ_ERR_INVALID_DIMENSION, "unsupported head_dim %d", dim);
+}
+}  // namespace
+
+extern "C" int tq_qjl_sign_matrix(uint32_t *bits_out, int dim, uint64_t qjl_seed, hipStream_t stream) {
+  if (dim != 32 && dim != 64 && dim != 128 && dim != 256)
+    return tqh::fail(TQ_ERR_INVALID_DIMENSION, "sign matrix dim must be 32, 64, 128 or 256 (got %d)", dim);
+  if (!bits_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const unsigned grid = (unsigned)((dim * dim / 32 + kBlock - 1) / kBlock);
+  switch (dim) {
+    case 32: hipLaunchKernelGGL((qjl_sign_matrix_kernel<32>), dim3(grid), dim3(kBlock), 0, stream, bits_out, qjl_seed); break;
+    case 64: hipLaunchKernelGGL((qjl_sign_matrix_kernel<64>), dim3(grid), dim3(kBlock), 0, stream, bits_out, qjl_seed); break;
+    case 128: hipLaunchKernelGGL((qjl_sign_matrix_kernel<128>), dim3(grid), dim3(kBlock), 0, stream, bits_out, qjl_seed); break;
+    default: hipLaunchKernelGGL((qjl_sign_matrix_kernel<256>), dim3(grid), dim3(kBlock), 0, stream, bits_out, qjl_seed); break;
+  }
+  return tqh::check_launch("qjl_sign_matrix_kernel");
+}
+
+extern "C" int tq_qjl_cache_sketch(const void *k, int k_dtype, int num_heads, int tokens, const uint8_t *packed_cache,
+                                   const uint16_t *scales_cache, const uint32_t *sign_matrix, uint8_t *signs_cache,
+                                   uint16_t *norms_cache, long long cache_head_stride, long long cache_offset,
+                                   int head_dim, int bits, size_t outlier_blocks, int norm_mode, hipStream_t stream) {
+  int rc = check_sketch_dim(head_dim);
+  if (rc) return rc;
+  tqh::PolarCodec codec;
+  rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(k_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", k_dtype);
+  if (num_heads < 0 || tokens < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "negative shape");
+  if (cache_offset < 0 || cache_head_stride < cache_offset + tokens)
+    return tqh::fail(TQ_ERR_RANGE_OUT_OF_BOUNDS, "cache rows [%lld, %lld) exceed head stride %lld", cache_offset,
+                     cache_offset + tokens, cache_head_stride);
+  const long long nvec = (long long)num_heads * tokens;
+  if (nvec == 0) return TQ_OK;
+  if (!k || !packed_cache || !scales_cache || !sign_matrix || !signs_cache || !norms_cache)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  SketchConsts c{};
+  for (int i = 0; i < codec.cb.nc; i++) c.cb[i] = codec.cb.c[i];
+  c.sign_mask = kPqoSignMask;
+  {
+    volatile float thirty_two = 32.0f;
+    volatile float sq = sqrtf(thirty_two);
+    volatile float inv = 1.0f / sq;
+    c.decode_factor = inv * sq;  // fl(fl(1/sqrt 32) * sqrt 32) (wht_tensor.rs:28-41)
+  }
+  c.inv_sqrt_d = inv_sqrt_dim(head_dim);
+  c.head_stride = cache_head_stride;
+  c.offset = cache_offset;
+  c.tokens = tokens;
+  const unsigned grid = (unsigned)((nvec + kBlock / 64 - 1) / (kBlock / 64));
+  return by_cache_dim(head_dim, [&](auto d) {
+    constexpr int D = decltype(d)::value;
+#define SK(B, T) hipLaunchKernelGGL((qjl_cache_sketch_kernel<D, B, T>), dim3(grid), dim3(kBlock), 0, stream, k, \
+                                    packed_cache, scales_cache, sign_matrix, signs_cache, norms_cache, nvec, c)
+    if (bits == 3) {
+      if (k_dtype == kF32) SK(3, kF32);
+      else if (k_dtype == kBF16) SK(3, kBF16);
+      else SK(3, kF16);
+    } else {
+      if (k_dtype == kF32) SK(4, kF32);
+      else if (k_dtype == kBF16) SK(4, kBF16);
+      else SK(4, kF16);
+    }
+#undef SK
+    return tqh::check_launch("qjl_cache_sketch_kernel");
+  });
+}
+
+extern "C" int tq_qjl_project(const void *q, int q_dtype, const uint32_t *sign_matrix, float *rq, size_t num_rows,
+                              int dim, hipStream_t stream) {
+  int rc = check_sketch_dim(dim);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(q_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", q_dtype);
+  if (num_rows == 0) return TQ_OK;
+  if (!q || !sign_matrix || !rq) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const long long n = (long long)num_rows;
+  const float inv = inv_sqrt_dim(dim);
+  const unsigned grid = (unsigned)((n + kBlock / 64 - 1) / (kBlock / 64));
+  return by_cache_dim(dim, [&](auto d) {
+    constexpr int D = decltype(d)::value;
+    if (q_dtype == kF32)
+      hipLaunchKernelGGL((qjl_project_kernel<D, kF32>), dim3(grid), dim3(kBlock), 0, stream, q, sign_matrix, rq, n, inv);
+    else if (q_dtype == kBF16)
+      hipLaunchKernelGGL((qjl_project_kernel<D, kBF16>), dim3(grid), dim3(kBlock), 0, stream, q, sign_matrix, rq, n, inv);
+    else
+      hipLaunchKernelGGL((qjl_project_kernel<D, kF16>), dim3(grid), dim3(kBlock), 0, stream, q, sign_matrix, rq, n, inv);
+    return tqh::check_launch("qjl_project_kernel");
+  });
+}
+
+extern "C" float tq_qjl_bias_scale(int head_dim) {
+  // tq.rs:213-214: f32(sqrt(pi / 2)) / sqrt(head_dim as f32)
+  volatile float sp = (float)std::sqrt(3.14159265358979323846 / 2.0);
+  volatile float fd = (float)head_dim;
+  volatile float sq = sqrtf(fd);
+  return sp / sq;
+}
+
+extern "C" int tq_qjl_logit_bias(const float *rq, int num_q_heads, int q_len, const uint8_t *signs_cache,
+                                 const uint16_t *norms_cache, int num_kv_heads, int kv_len,
+                                 long long cache_head_stride, int head_dim, void *out, int out_dtype,
+                                 hipStream_t stream) {
+  int rc = check_sketch_dim(head_dim);
+  if (rc) return rc;
+  if (!tqh::valid_dtype(out_dtype)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype %d", out_dtype);
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_q_heads (%d) must be a multiple of num_kv_heads (%d)", num_q_heads,
+                     num_kv_heads);
+  if (q_len < 0 || kv_len < 0 || cache_head_stride < kv_len) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "bad shape");
+  if (q_len == 0 || kv_len == 0) return TQ_OK;
+  if (!rq || !signs_cache || !norms_cache || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  const float sf = tq_qjl_bias_scale(head_dim);
+  const int n_rep = num_q_heads / num_kv_heads;
+  return by_cache_dim(head_dim, [&](auto d) {
+    constexpr int D = decltype(d)::value;
+    constexpr int QB = 8;
+    const dim3 grid((unsigned)((kv_len + kBlock - 1) / kBlock), (unsigned)((q_len + QB - 1) / QB), (unsigned)num_q_heads);
+    hipLaunchKernelGGL((qjl_logit_bias_kernel<D, QB>), grid, dim3(kBlock), 0, stream, rq, q_len,
+                       reinterpret_cast<const uint32_t *>(signs_cache), norms_cache, kv_len, cache_head_stride, n_rep,
+                       sf, out, out_dtype);
+    return tqh::check_launch("qjl_logit_bias_kernel");
   });
 }
