@@ -53,8 +53,8 @@ def _load():
         "tqo_pqo_quantize": (C.c_int, [C.c_int, _sz, _sz, _f32p, _u8p, _u16p]),
         "tqo_pqo_dequantize": (C.c_int, [C.c_int, _sz, _sz, _u8p, _u16p, _f32p]),
         "tqo_attention_dense": (C.c_int, [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_float, _f32p]),
-        "tqo_polar_quantize": (C.c_int, [C.c_int, _sz, _sz, _sz, _f32p, _u8p, _u16p]),
-        "tqo_polar_dequantize": (C.c_int, [C.c_int, _sz, _sz, _sz, _u8p, _u16p, _f32p]),
+        "tqo_polar_quantize": (C.c_int, [C.c_int, _sz, C.c_int, _sz, _sz, _f32p, _u8p, _u16p]),
+        "tqo_polar_dequantize": (C.c_int, [C.c_int, _sz, C.c_int, _sz, _sz, _u8p, _u16p, _f32p]),
         "tqo_tq_signs_norms": (C.c_int, [_sz, _sz, _f32p, _f32p, _u8p, _u16p]),
         "tqo_tq_logit_bias": (C.c_int, [_sz, _sz, _sz, _sz, _sz, _f32p, _u8p, _u16p, _f32p]),
         "tqo_attention_dense_bias": (C.c_int, [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, C.c_float,
@@ -264,21 +264,22 @@ def pqo_dequantize(bits: int, packed: np.ndarray, scales: np.ndarray, head_dim: 
 OUTLIER_ALL = (1 << 64) - 1
 
 
-def polar_quantize(bits: int, outlier_blocks: int, x: np.ndarray, head_dim: int):
+def polar_quantize(bits: int, outlier_blocks: int, x: np.ndarray, head_dim: int, norm_mode: int = 0):
     x = _c(x, np.float32).reshape(-1, head_dim)
     n = x.shape[0]
     packed = np.zeros((n, head_dim * bits // 8), np.uint8)
     scales = np.zeros((n, head_dim // 32), np.uint16)
-    _check(lib.tqo_polar_quantize(bits, outlier_blocks, n, head_dim, x, packed, scales))
+    _check(lib.tqo_polar_quantize(bits, outlier_blocks, norm_mode, n, head_dim, x, packed, scales))
     return packed, scales
 
 
-def polar_dequantize(bits: int, outlier_blocks: int, packed: np.ndarray, scales: np.ndarray, head_dim: int):
+def polar_dequantize(bits: int, outlier_blocks: int, packed: np.ndarray, scales: np.ndarray, head_dim: int,
+                     norm_mode: int = 0):
     packed = _c(packed, np.uint8)
     scales = _c(scales, np.uint16)
     n = packed.size // (head_dim * bits // 8)
     out = np.zeros((n, head_dim), np.float32)
-    _check(lib.tqo_polar_dequantize(bits, outlier_blocks, n, head_dim, packed, scales, out))
+    _check(lib.tqo_polar_dequantize(bits, outlier_blocks, norm_mode, n, head_dim, packed, scales, out))
     return out
 
 

@@ -645,18 +645,38 @@ int tqo_pqo_dequantize(int bits, size_t n, size_t head_dim, const uint8_t *packe
    scale sign is -1 for the first min(outlier_blocks, nb) blocks of every
    vector (build_scale_sign_tensor, precomputed/mod.rs:102-114); codes are
    packed bits-wide (:73).  For outlier_blocks 0 or >= nb the two
-   orderings agree. */
-int tqo_polar_quantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim, const float *x,
+   orderings agree.  norm_mode 1 (L2Norm, :90-101): the block's norm
+   sqrt(sum x^2) (element order from +0, clamped to 1e-10) divides it before
+   the rotation and is its scale; the codebooks are get_codebook(b, 32) in
+   f32 (codebooks.rs:30-47). */
+static void polar_codebooks(int bits, int norm_mode, float *oc, float *ob, int *onc, float *nc_, float *nb_,
+                            int *nnc, float *outer)
+{
+    float outer_n;
+    if (norm_mode == 0) {
+        tqo_pqo_codebook(bits, oc, ob, onc, outer);
+        tqo_pqo_codebook(bits - 1, nc_, nb_, nnc, &outer_n);
+        return;
+    }
+    const double *c, *b;
+    tqo_get_codebook(bits, 32, &c, &b, onc);
+    for (int i = 0; i < *onc; i++) oc[i] = (float)c[i];
+    for (int i = 0; i + 1 < *onc; i++) ob[i] = (float)b[i];
+    tqo_get_codebook(bits - 1, 32, &c, &b, nnc);
+    for (int i = 0; i < *nnc; i++) nc_[i] = (float)c[i];
+    for (int i = 0; i + 1 < *nnc; i++) nb_[i] = (float)b[i];
+    *outer = oc[*onc - 1];
+}
+
+int tqo_polar_quantize(int bits, size_t outlier_blocks, int norm_mode, size_t n, size_t head_dim, const float *x,
                        uint8_t *packed_out, uint16_t *scales_out)
 {
     if (head_dim % QBLOCK != 0 || head_dim == 0) return TQO_ERR_INVALID_ARGUMENT;
     if (bits != 3 && bits != 4) return TQO_ERR_UNSUPPORTED_BITS;
-    float oc[16], ob[15], nc_[16], nb_[15], outer, outer_n;
+    if (norm_mode != 0 && norm_mode != 1) return TQO_ERR_INVALID_ARGUMENT;
+    float oc[16], ob[15], nc_[16], nb_[15], outer;
     int onc, nnc;
-    tqo_pqo_codebook(bits, oc, ob, &onc, &outer);
-    tqo_pqo_codebook(bits - 1, nc_, nb_, &nnc, &outer_n);
-    (void)oc;
-    (void)nc_;
+    polar_codebooks(bits, norm_mode, oc, ob, &onc, nc_, nb_, &nnc, &outer);
     const size_t nblk_v = head_dim / QBLOCK;
     const size_t eo = outlier_blocks < nblk_v ? outlier_blocks : nblk_v;
     const size_t rows = n * nblk_v, outlier_rows = n * eo;
@@ -665,19 +685,31 @@ int tqo_polar_quantize(int bits, size_t outlier_blocks, size_t n, size_t head_di
     float r[QBLOCK];
     uint8_t idx[QBLOCK];
     for (size_t row = 0; row < rows; row++) {
-        tqo_pqo_rotate_block(x + row * QBLOCK, r);
-        float amax = 0.0f;
-        for (int j = 0; j < QBLOCK; j++) {
-            float a = fabsf(r[j]);
-            amax = a > amax ? a : amax;
+        float s;
+        if (norm_mode == 1) {
+            const float *xb = x + row * QBLOCK;
+            float ss = 0.0f;
+            for (int j = 0; j < QBLOCK; j++) ss = ss + xb[j] * xb[j];
+            s = sqrtf(ss);
+            if (s < MIN_NORM) s = MIN_NORM;
+            float xn[QBLOCK];
+            for (int j = 0; j < QBLOCK; j++) xn[j] = xb[j] / s;
+            tqo_pqo_rotate_block(xn, r);
+        } else {
+            tqo_pqo_rotate_block(x + row * QBLOCK, r);
+            float amax = 0.0f;
+            for (int j = 0; j < QBLOCK; j++) {
+                float a = fabsf(r[j]);
+                amax = a > amax ? a : amax;
+            }
+            s = amax * mul;
+            if (s < MIN_NORM) s = MIN_NORM;
         }
-        float s = amax * mul;
-        if (s < MIN_NORM) s = MIN_NORM;
         const int outlier_row = row < outlier_rows;
         const float *bnd = outlier_row ? ob : nb_;
         const int nbnd = outlier_row ? onc - 1 : nnc - 1;
         for (int j = 0; j < QBLOCK; j++) {
-            float v = r[j] / s;
+            float v = norm_mode == 1 ? r[j] : r[j] / s;
             int k = 0;
             for (int t = 0; t < nbnd; t++) k += v > bnd[t];
             idx[j] = (uint8_t)k;
@@ -693,15 +725,15 @@ int tqo_polar_quantize(int bits, size_t outlier_blocks, size_t n, size_t head_di
    picks the outlier centroids for all-outlier configs, the standard ones
    for outlier_blocks 0, and per block by the scale's sign otherwise (with
    the index clamped into the standard codebook, :242-260). */
-int tqo_polar_dequantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim, const uint8_t *packed,
-                         const uint16_t *scales, float *out)
+int tqo_polar_dequantize(int bits, size_t outlier_blocks, int norm_mode, size_t n, size_t head_dim,
+                         const uint8_t *packed, const uint16_t *scales, float *out)
 {
     if (head_dim % QBLOCK != 0 || head_dim == 0) return TQO_ERR_INVALID_ARGUMENT;
     if (bits != 3 && bits != 4) return TQO_ERR_UNSUPPORTED_BITS;
-    float oc[16], ob[15], ncb[16], nbb[15], outer, outer_n;
+    if (norm_mode != 0 && norm_mode != 1) return TQO_ERR_INVALID_ARGUMENT;
+    float oc[16], ob[15], ncb[16], nbb[15], outer;
     int onc, nnc;
-    tqo_pqo_codebook(bits, oc, ob, &onc, &outer);
-    tqo_pqo_codebook(bits - 1, ncb, nbb, &nnc, &outer_n);
+    polar_codebooks(bits, norm_mode, oc, ob, &onc, ncb, nbb, &nnc, &outer);
     const size_t nblk_v = head_dim / QBLOCK;
     float sg[32];
     tqo_pqo_decode_signs(sg);

@@ -88,10 +88,10 @@ int tqo_pqo_dequantize(int bits, size_t n, size_t head_dim, const uint8_t *packe
                        const uint16_t *scales, float *out);
 
 /* polar_quantize / polar_dequantize for the cache modes (outlier_blocks:
- * >= num_blocks PQO, 0 PQ/TQ), MaxNorm. */
-int tqo_polar_quantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim, const float *x,
-                       uint8_t *packed_out, uint16_t *scales_out);
-int tqo_polar_dequantize(int bits, size_t outlier_blocks, size_t n, size_t head_dim,
+ * >= num_blocks PQO, 0 PQ/TQ, else mixed), norm_mode 0 MaxNorm / 1 L2Norm. */
+int tqo_polar_quantize(int bits, size_t outlier_blocks, int norm_mode, size_t n, size_t head_dim,
+                       const float *x, uint8_t *packed_out, uint16_t *scales_out);
+int tqo_polar_dequantize(int bits, size_t outlier_blocks, int norm_mode, size_t n, size_t head_dim,
                          const uint8_t *packed, const uint16_t *scales, float *out);
 
 /* ---- TqCache (src/cache/tq.rs) ---- */

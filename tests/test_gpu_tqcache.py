@@ -219,3 +219,72 @@ def test_reference_abi_qjl_enabled(tq):
 def test_tq_cache_rejects_outlier_config(tq):
     with pytest.raises(tq.TurboQuantError):
         tq.TqCache(tq.CacheConfig(bits=3, head_dim=D, num_kv_heads=2, num_layers=1))
+
+
+@pytest.mark.parametrize("bits,outlier,norm", [(3, 0, 1), (4, 0, 1), (3, orc.OUTLIER_ALL, 1), (4, orc.OUTLIER_ALL, 1),
+                                               (3, 1, 0), (4, 2, 0), (3, 3, 1)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_l2norm_and_mixed_codec_bit_exact(tq, bits, outlier, norm, dtype):
+    rng = np.random.default_rng(200 + bits + norm)
+    x = kv_outlier(rng, 3, 70).reshape(-1, D)
+    xd = _dev(bf16_bits(x)).view(torch.bfloat16) if dtype == "bf16" else _dev(x)
+    p, s = tq.polar_quantize(xd, bits, outlier_blocks=outlier, norm_mode=norm)
+    rp, rs = orc.polar_quantize(bits, outlier, x, D, norm_mode=norm)
+    assert (_host(p) == rp).all()
+    assert (_host(s).view(np.uint16) == rs).all()
+    y = tq.polar_dequantize(p, s, bits, D, outlier_blocks=outlier, norm_mode=norm)
+    ry = orc.polar_dequantize(bits, outlier, rp, rs, D, norm_mode=norm)
+    assert (_host(y).view(np.uint32) == ry.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("kind,bits", [("pqo", 3), ("pq", 4), ("tq", 3), ("tq", 4)])
+def test_l2norm_caches_decode(tq, kind, bits):
+    hkv, hq, t = 8, 16, 1200
+    rng = np.random.default_rng(300 + bits)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    outlier = orc.OUTLIER_ALL if kind == "pqo" else 0
+    cfg = tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1,
+                         norm_mode=tq.QuantNormMode.L2Norm, outlier_blocks=outlier)
+    cache = tq.TqCache(cfg) if kind == "tq" else tq.PqoCache(cfg)
+    qp = rng.standard_normal((hq, 1, D)).astype(np.float32)
+    if kind == "tq":
+        cache.prefill(0, _dev(k[None, :, :-1]), _dev(v[None, :, :-1]), _dev(qp[None]))
+    else:
+        cache.prefill(0, _dev(k[None, :, :-1]), _dev(v[None, :, :-1]))
+    q = bf16_round(rng.standard_normal((hq, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    scale = 1 / math.sqrt(D)
+    out = cache.decode(0, _dev(k[None, :, -1:]), _dev(v[None, :, -1:]), _dev(q).reshape(1, hq, 1, D),
+                       tq.AttendConfig(scale, 2))
+    pk, sk = orc.polar_quantize(bits, outlier, k.reshape(-1, D), D, norm_mode=1)
+    pv, sv = orc.polar_quantize(bits, outlier, v.reshape(-1, D), D, norm_mode=1)
+    kd = orc.polar_dequantize(bits, outlier, pk, sk, D, norm_mode=1)
+    vd = orc.polar_dequantize(bits, outlier, pv, sv, D, norm_mode=1).reshape(hkv, t, D)
+    if kind == "tq":
+        sg, nm = orc.tq_signs_norms(k.reshape(-1, D), kd)
+        bias = orc.tq_logit_bias(q[:, None, :], sg.reshape(hkv, t, -1), nm.reshape(hkv, t))[:, 0, :]
+        ref = orc.attention_dense_bias(q, kd.reshape(hkv, t, D), vd, bias, scale)
+    else:
+        ref = orc.attention_dense(q, kd.reshape(hkv, t, D), vd, scale)
+    err = np.abs(_host(out).reshape(hq, D) - ref).max()
+    assert err <= TOL, err
+
+
+def test_mixed_cache_dequantized_paths(tq):
+    bits, hkv, eo = 3, 4, 2
+    rng = np.random.default_rng(400)
+    k1, v1 = kv_outlier(rng, hkv, 30), kv_outlier(rng, hkv, 30)
+    k2, v2 = kv_outlier(rng, hkv, 9), kv_outlier(rng, hkv, 9)
+    cache = tq.PqoCache(tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1, outlier_blocks=eo))
+    cache.prefill(0, _dev(k1[None]), _dev(v1[None]))
+    r = cache.prefill(0, _dev(k2[None]), _dev(v2[None]))
+    # each append quantizes its own [H * T, D] block matrix (quantize_kv_pair per call)
+    ref = np.concatenate([orc.polar_dequantize(bits, eo, *orc.polar_quantize(bits, eo, kk.reshape(-1, D), D), D)
+                          .reshape(hkv, -1, D) for kk in (k1, k2)], 1)
+    assert (_host(r.k[0]).view(np.uint32) == ref.view(np.uint32)).all()
+    q = _dev(rng.standard_normal((1, 8, 1, D)).astype(np.float32))
+    k3, v3 = kv_outlier(rng, hkv, 1), kv_outlier(rng, hkv, 1)
+    with pytest.raises(tq.TurboQuantError):
+        cache.decode(0, _dev(k3[None]), _dev(v3[None]), q, tq.AttendConfig(1 / math.sqrt(D), 2))
+    out = cache.decode_output(0, _dev(k3[None]), _dev(v3[None]), q, tq.AttendConfig(1 / math.sqrt(D), 2))
+    assert isinstance(out, tq.Dequantized) and out.result.k.shape == (1, hkv, 40, D)

@@ -135,3 +135,62 @@ def test_dense_bias_attention_against_numpy():
     # zero bias reduces to the plain dense oracle
     z = orc.attention_dense_bias(q, k, v, np.zeros_like(bias), scale)
     np.testing.assert_allclose(z, orc.attention_dense(q, k, v, scale), rtol=1e-6, atol=1e-7)
+
+
+def l2_codebook(bits):
+    c, b = orc.get_codebook(bits, 32)
+    return np.asarray(c, np.float32).astype(np.float64), np.asarray(b, np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("bits,outlier", [(3, 0), (4, 0), (3, orc.OUTLIER_ALL), (4, orc.OUTLIER_ALL)])
+def test_l2norm_mode_against_float64_textbook(bits, outlier):
+    """L2Norm (quantize_tensor.rs:90-101): x / |x| rotated, bucketized against the
+    Beta tables of dimension 32, scale = |x|; dequant = centroids through R_fwd^T."""
+    rng = np.random.default_rng(30 + bits)
+    x = kv_outlier(rng, 2, 20).reshape(-1, 128)
+    packed, scales = orc.polar_quantize(bits, outlier, x, 128, norm_mode=1)
+    cb_bits = bits if outlier else bits - 1
+    cen, bnd = l2_codebook(cb_bits)
+    blocks = x.reshape(-1, 32).astype(np.float64)
+    nrm = np.linalg.norm(blocks, axis=1)
+    r = (blocks / nrm[:, None]) @ R_FWD
+    ref = np.searchsorted(bnd, r, side="left")
+    bpb = 4 * bits
+    got = np.stack([unpack(packed.reshape(-1, bpb)[i], bits, 32) for i in range(blocks.shape[0])])
+    near = np.min(np.abs(r[..., None] - bnd[None, None, :]), axis=-1) < 1e-6
+    assert (got[~near] == ref[~near]).all()
+    sc = orc.f16_bits_to_f32(scales.reshape(-1)).astype(np.float64)
+    np.testing.assert_allclose(np.abs(sc), nrm, rtol=1e-3)
+    assert ((sc < 0) == bool(outlier)).all()
+    y = orc.polar_dequantize(bits, outlier, packed, scales, 128, norm_mode=1).reshape(-1, 32)
+    yref = (cen[got] @ R_FWD.T) * np.abs(sc)[:, None]
+    np.testing.assert_allclose(y, yref, rtol=2e-6, atol=2e-6 * np.abs(yref).max())
+
+
+@pytest.mark.parametrize("eo", [1, 2, 3])
+def test_mixed_outlier_blocks_follow_reference_row_order(eo):
+    """0 < outlier_blocks < num_blocks: the first n * eo rows of the block matrix
+    take the outlier boundaries (bucketize_blocks, quantize_tensor.rs:118-150),
+    the scale sign marks blocks j < eo of every vector (precomputed/mod.rs:102-114)
+    and the dequantize picks the codebook by that sign, clamping standard codes
+    (quantize_tensor.rs:242-260)."""
+    bits, n = 3, 5
+    rng = np.random.default_rng(eo)
+    x = kv_outlier(rng, 1, n).reshape(-1, 128)
+    packed, scales = orc.polar_quantize(bits, eo, x, 128)
+    blocks = x.reshape(-1, 32).astype(np.float64)
+    r = blocks @ R_FWD
+    s = np.maximum(np.abs(r).max(1) / 2.1573, 1e-10)
+    v = r / s[:, None]
+    rows = np.arange(blocks.shape[0])
+    out_row = rows < n * eo
+    ref = np.where(out_row[:, None], np.searchsorted(B3, v, side="left"), np.searchsorted(B2, v, side="left"))
+    got = np.stack([unpack(packed.reshape(-1, 12)[i], bits, 32) for i in range(blocks.shape[0])])
+    near = np.min(np.abs(v[..., None] - B3[None, None, :]), axis=-1) < 1e-5
+    assert (got[~near] == ref[~near]).all()
+    sc = orc.f16_bits_to_f32(scales.reshape(-1))
+    assert ((sc < 0) == ((rows % 4) < eo)).all()
+    y = orc.polar_dequantize(bits, eo, packed, scales, 128).reshape(-1, 32)
+    cen = np.where((sc < 0)[:, None], C3[got], C2[np.minimum(got, 3)])
+    yref = (cen @ R_FWD.T) * np.abs(sc)[:, None]
+    np.testing.assert_allclose(y, yref, rtol=2e-6, atol=2e-6 * np.abs(yref).max())

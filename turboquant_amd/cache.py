@@ -230,7 +230,19 @@ class PqoCache(_DeviceCache):
         dtype (DecodeOutput::Fused, pqo.rs:202-222 on the device path)."""
         return self._decode_fused(layer, k, v, q, config)
 
+    def decode_dequantized(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> DequantResult:
+        """Stores k, v and returns the whole dequantized layer (the reference's
+        CPU decode path, pqo.rs:218-221)."""
+        return self._decode_dequantized(layer, k, v, None)
+
     def decode_output(self, layer: int, k, v, q, config: AttendConfig) -> DecodeOutput:
+        """DecodeOutput as the trait returns it: Fused for PQO and PQ configs;
+        Dequantized for mixed outlier configs, which the fused kernel does not
+        take (the reference's CUDA path would read them with the outlier
+        codebook only, pqo.rs:152)."""
+        ob = self.config.outlier_blocks
+        if 0 < ob < self.config.num_blocks():
+            return Dequantized(self.decode_dequantized(layer, k, v))
         return Fused(self.decode(layer, k, v, q, config))
 
 

@@ -93,6 +93,10 @@ struct AttnArgs {
   const uint32_t *qjl_signs;
   const uint16_t *qjl_norms;
   float qjl_c;
+  // cb_args: the codebook comes from cb (L2Norm tables) instead of the
+  // MaxNorm constants compiled in
+  int cb_args;
+  float cb[16];
 };
 
 // Query element as stored (f32 bits or a 16-bit pattern), converted
@@ -395,7 +399,20 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   for (int it = tid; it < NPAIR * PREP; it += kThreads) {
     const int e = it / PREP;
     constexpr int CM = (1 << CB) - 1;  // slot codes >= 2^CB never occur
-    const float c0 = pqo_centroid<CB>(e & (NC - 1) & CM), c1 = pqo_centroid<CB>((e >> BITS) & CM);
+    const int i0 = e & (NC - 1) & CM, i1 = (e >> BITS) & CM;
+    float c0, c1;
+    if (a.cb_args) {
+      c0 = a.cb[0];
+      c1 = a.cb[0];
+#pragma unroll
+      for (int kk = 1; kk <= CM; kk++) {
+        c0 = i0 == kk ? a.cb[kk] : c0;
+        c1 = i1 == kk ? a.cb[kk] : c1;
+      }
+    } else {
+      c0 = pqo_centroid<CB>(i0);
+      c1 = pqo_centroid<CB>(i1);
+    }
     const float h0 = split_hi(c0), h1 = split_hi(c1);
     s_pair[it] = make_uint2(pack_f16(h0, h1), pack_f16(c0 - h0, c1 - h1));
   }
@@ -926,6 +943,9 @@ extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8
   tqh::PolarCodec codec;
   rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
   if (rc) return rc;
+  if (codec.mixed)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT,
+                     "fused decode takes outlier_blocks 0 or all (mixed configs: dequantize and attend)");
   const bool qjl = qjl_signs != nullptr;
   if (qjl && codec.outlier)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL correction applies to the standard codebook (outlier_blocks 0)");
@@ -971,6 +991,10 @@ extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8
   a.qjl_signs = reinterpret_cast<const uint32_t *>(qjl_signs);
   a.qjl_norms = qjl_norms;
   a.qjl_c = tq_qjl_bias_scale(head_dim);
+  if (codec.norm_mode == TQ_NORM_L2NORM) {
+    a.cb_args = 1;
+    for (int i = 0; i < codec.cb.nc; i++) a.cb[i] = codec.cb.c[i];
+  }
   const int mode = codec.outlier ? kModePqo : (qjl ? kModeTq : kModePq);
   const dim3 grid((unsigned)w.P, (unsigned)num_kv_heads, (unsigned)batch);
   return launch_decode<true>(a, bits, mode, num_heads / num_kv_heads, grid, stream);

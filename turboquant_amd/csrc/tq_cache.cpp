@@ -377,6 +377,10 @@ extern "C" int tq_cache_decode(void *cache, int layer, const void *k, const void
   rc = check_q(c, q, q_dtype, num_q_heads);
   if (rc) return rc;
   if (tokens < 0 || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid arguments");
+  const CacheMode &m = c->mode();
+  if (m.outlier_blocks > 0 && m.outlier_blocks < (size_t)c->head_dim() / 32)  // checked before anything is stored
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT,
+                     "fused decode takes outlier_blocks 0 or all (mixed configs: tq_cache_decode_dequantized)");
   size_t old = 0;
   rc = c->append(layer, k, v, kv_dtype, tokens, &old, stream);
   if (rc) return rc;

@@ -1,5 +1,6 @@
 // tq_common.cpp -- error reporting and host-side constant tables.
 #include "tq_common.h"
+#include "tq_codebooks.h"
 #include "tq_device.h"
 
 #include <cmath>
@@ -65,21 +66,44 @@ PqoCodebook pqo_codebook(int bits) {
   return cb;
 }
 
+// get_codebook(bits, 32) as f32 (build_codebooks_l2, codebooks.rs:30-47)
+static PqoCodebook l2_codebook(int bits) {
+  PqoCodebook cb;
+  const double *c = nullptr, *b = nullptr;
+  int nc = 0;
+  if (!core_codebook(bits, 32, &c, &b, &nc)) return cb;
+  cb.bits = bits;
+  cb.nc = nc;
+  for (int i = 0; i < nc; i++) cb.c[i] = (float)c[i];
+  for (int i = 0; i + 1 < nc; i++) cb.b[i] = (float)b[i];
+  float m = cb.c[0];
+  for (int i = 1; i < nc; i++) m = cb.c[i] > m ? cb.c[i] : m;
+  cb.outer = m;
+  return cb;
+}
+
 int polar_codec(int bits, int norm_mode, size_t outlier_blocks, int num_blocks, PolarCodec &codec) {
   if (bits != 3 && bits != 4) return fail(TQ_ERR_UNSUPPORTED_BITS, "unsupported bits=%d, expected 3 or 4", bits);
-  if (norm_mode != TQ_NORM_MAXNORM)
-    return fail(TQ_ERR_INVALID_ARGUMENT, "norm mode %d is not implemented by this library (MaxNorm only)", norm_mode);
+  if (norm_mode != TQ_NORM_MAXNORM && norm_mode != TQ_NORM_L2NORM)
+    return fail(TQ_ERR_INVALID_ARGUMENT, "unknown norm mode %d", norm_mode);
   const bool all = outlier_blocks >= (size_t)num_blocks;
-  if (!all && outlier_blocks != 0)
-    return fail(TQ_ERR_INVALID_ARGUMENT,
-                "mixed outlier blocks (%zu of %d) are not implemented by this library (0 or all)", outlier_blocks,
-                num_blocks);
   codec.bits = bits;
-  codec.cb_bits = all ? bits : bits - 1;
+  codec.norm_mode = norm_mode;
   codec.outlier = all;
-  codec.cb = pqo_codebook(codec.cb_bits);
-  codec.outer = pqo_codebook(bits).outer;  // outlier codebook = polar_bits + 1 = bits (codebooks.rs:84-88)
-  codec.scale_sign = all ? -1.f : 1.f;     // build_scale_sign_tensor (precomputed/mod.rs:102-114)
+  codec.mixed = !all && outlier_blocks != 0;
+  codec.num_blocks = num_blocks;
+  codec.eo = all ? num_blocks : (int)outlier_blocks;
+  codec.cb_bits = all ? bits : bits - 1;
+  if (norm_mode == TQ_NORM_MAXNORM) {
+    codec.ocb = pqo_codebook(bits);  // outlier = polar_bits + 1 = bits (codebooks.rs:84-88)
+    codec.ncb = pqo_codebook(bits - 1);
+  } else {
+    codec.ocb = l2_codebook(bits);
+    codec.ncb = l2_codebook(bits - 1);
+  }
+  codec.cb = all ? codec.ocb : codec.ncb;
+  codec.outer = codec.ocb.outer;
+  codec.scale_sign = all ? -1.f : 1.f;  // build_scale_sign_tensor (precomputed/mod.rs:102-114)
   return TQ_OK;
 }
 

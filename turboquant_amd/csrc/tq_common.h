@@ -30,22 +30,32 @@ struct PqoCodebook {
 PqoCodebook pqo_codebook(int bits);
 
 // Codec of one cache mode (CacheConfig, src/cache/config.rs:50-85;
-// GpuPrecomputed, precomputed/mod.rs:45-98).  outlier_blocks >= num_blocks
-// (PQO): every block on the bits-bit outlier codebook, negative scales.
-// outlier_blocks == 0 (PQ / TQ): the standard (bits - 1)-bit codebook, its
-// codes in bits-wide slots (packed_dim = head_dim * bits / 8), positive
-// scales.  MaxNorm divides by the outlier codebook's largest centroid in both
-// (quantize_tensor.rs:103-108).
+// GpuPrecomputed, precomputed/mod.rs:45-98).  The outlier codebook has
+// `bits` bits, the standard one bits - 1, its codes in bits-wide slots
+// (packed_dim = head_dim * bits / 8).  outlier_blocks >= num_blocks (PQO):
+// every block on the outlier codebook; 0 (PQ / TQ): every block on the
+// standard one; in between, quantize_tensor.rs:118-150 sends the first
+// n * outlier_blocks rows of the [n * num_blocks, 32] block matrix to the
+// outlier boundaries while the scale sign (negative = outlier, which the
+// dequantize dispatches on) marks the first outlier_blocks blocks of each
+// vector.  MaxNorm divides by the outlier codebook's largest centroid
+// (quantize_tensor.rs:103-108); L2Norm uses the Beta-optimal tables of
+// dimension 32 (codebooks.rs:30-47).
 struct PolarCodec {
-  int bits = 0;     // slot width
-  int cb_bits = 0;  // codebook width (bits or bits - 1)
-  bool outlier = false;
-  PqoCodebook cb;   // centroids / boundaries of the blocks' codebook
-  float outer = 0.f;
+  int bits = 0;         // slot width
+  int cb_bits = 0;      // codebook width of uniform modes (bits or bits - 1)
+  int norm_mode = 0;
+  bool outlier = false; // every block on the outlier codebook
+  bool mixed = false;   // 0 < outlier_blocks < num_blocks
+  int num_blocks = 0;
+  int eo = 0;           // min(outlier_blocks, num_blocks)
+  PqoCodebook cb;       // the blocks' codebook in uniform modes
+  PqoCodebook ocb, ncb; // outlier (bits) and standard (bits - 1) codebooks
+  float outer = 0.f;    // MaxNorm divisor: the outlier codebook's largest centroid
   float scale_sign = 1.f;
 };
 // Fills `codec` for (bits, norm_mode, outlier_blocks) or returns an error
-// status for a mode this library does not implement.
+// status for an invalid mode.
 int polar_codec(int bits, int norm_mode, size_t outlier_blocks, int num_blocks, PolarCodec &codec);
 
 // Per-boundary constants of the exact division threshold (see

@@ -16,6 +16,8 @@
 #include "tq_common.h"
 #include "tq_device.h"
 
+#include <cstring>
+
 namespace {
 
 using namespace tqd;
@@ -25,10 +27,16 @@ constexpr float kInvSqrt32 = 0x1.6a09e6p-3f;  // fl(1 / fl(sqrt(32))) = 0.176776
 struct QuantConsts {
   double mu[15];
   float b[15];
+  float u[15];  // L2Norm: nextup(b), so x >= u <=> x > b
   uint32_t strict_mask;
   float mul;
   float scale_sign;
+  int mixed_sign;  // scale sign per block: -1 for block % nb < eo
+  int nb, eo;
+  long long blk0;  // first block of this launch
 };
+
+enum NormMode : int { kMaxNorm = 0, kL2Norm = 1 };
 
 template <int BITS>
 struct Packed {
@@ -139,6 +147,27 @@ __device__ __forceinline__ uint32_t push_bit(uint32_t acc, bool bit) {
 // is the last 32 bits pushed into it, so codes that straddle words need no
 // special case.  CB < BITS: CB-bit codes (the standard codebook) in BITS-wide
 // slots, whose top bits stay zero (quantize_tensor.rs:73, config.rs:82-84).
+template <int BITS, int CB>
+__device__ __forceinline__ void pack_codes(const float (&r)[32], const float (&U)[(1 << CB) - 1],
+                                           uint32_t (&w)[Packed<BITS>::kWords]) {
+  uint32_t acc[Packed<BITS>::kWords];
+#pragma unroll
+  for (int q = 0; q < Packed<BITS>::kWords; q++) acc[q] = 0;
+#pragma unroll
+  for (int j = 31; j >= 0; j--) {
+    bool bit[CB];
+    bucket_bits<CB>(r[j], U, bit);
+#pragma unroll
+    for (int t = 0; t < BITS; t++) {
+      const int pos = j * BITS + (BITS - 1 - t);
+      if (t < BITS - CB) acc[pos >> 5] <<= 1;
+      else acc[pos >> 5] = push_bit(acc[pos >> 5], bit[t - (BITS - CB)]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < Packed<BITS>::kWords; q++) w[q] = acc[q];
+}
+
 template <int BITS, int CB = BITS>
 __device__ __forceinline__ float quantize_block(const float (&r)[32], const QuantConsts &k,
                                                 uint32_t (&w)[Packed<BITS>::kWords]) {
@@ -155,22 +184,7 @@ __device__ __forceinline__ float quantize_block(const float (&r)[32], const Quan
     float U[NB];
 #pragma unroll
     for (int t = 0; t < NB; t++) U[t] = div_threshold(k.mu[t], (k.strict_mask >> t) & 1u, s);
-    uint32_t acc[Packed<BITS>::kWords];
-#pragma unroll
-    for (int q = 0; q < Packed<BITS>::kWords; q++) acc[q] = 0;
-#pragma unroll
-    for (int j = 31; j >= 0; j--) {
-      bool bit[CB];
-      bucket_bits<CB>(r[j], U, bit);
-#pragma unroll
-      for (int t = 0; t < BITS; t++) {
-        const int pos = j * BITS + (BITS - 1 - t);
-        if (t < BITS - CB) acc[pos >> 5] <<= 1;
-        else acc[pos >> 5] = push_bit(acc[pos >> 5], bit[t - (BITS - CB)]);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < Packed<BITS>::kWords; q++) w[q] = acc[q];
+    pack_codes<BITS, CB>(r, U, w);
     return s;
   } else {
     // Infinite scale (an infinite input): follow the reference's division.
@@ -228,25 +242,49 @@ __device__ __forceinline__ long long cache_block(uint32_t blk, const CacheMap &m
 // ROTATE: input is raw activations (fused forward rotation, butterfly order).
 // Otherwise input is already rotated f32 (the reference kernel's contract).
 // MAP: outputs go to cache records (CacheMap) instead of block order.
-template <int BITS, int CB, int IN_DT, bool ROTATE, bool MAP = false>
+// NORM = kL2Norm: the block's L2 norm (sum of squares in element order,
+// sqrt, clamped to 1e-10) divides it before the rotation and is its scale;
+// codes count the boundaries strictly below the rotated value
+// (normalize_and_rotate, quantize_tensor.rs:90-101, 161-176).
+template <int BITS, int CB, int IN_DT, bool ROTATE, bool MAP, int NORM>
 __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__ x,
                                                         uint8_t *__restrict__ packed,
                                                         uint16_t *__restrict__ scales,
-                                                        long long nblocks, QuantConsts k, CacheMap map = {}) {
-  const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (blk >= nblocks) return;
+                                                        long long nblocks, QuantConsts k, CacheMap map) {
+  const long long blk = k.blk0 + (long long)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= k.blk0 + nblocks) return;
   const long long ob = MAP ? cache_block((uint32_t)blk, map) : blk;
   float r[32];
   load_block<IN_DT>(x, blk, r);
+  float nrm = 0.f;
+  if constexpr (NORM == kL2Norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) ss = ss + r[j] * r[j];
+    nrm = sqrtf(ss);
+    nrm = nrm < 1e-10f ? 1e-10f : nrm;
+#pragma unroll
+    for (int j = 0; j < 32; j++) r[j] = r[j] / nrm;
+  }
   if constexpr (ROTATE) {
     butterfly<32>(r);
 #pragma unroll
     for (int j = 0; j < 32; j++) r[j] = r[j] * (pqo_neg(j) ? -kInvSqrt32 : kInvSqrt32);
   }
   uint32_t w[Packed<BITS>::kWords];
-  float s = quantize_block<BITS, CB>(r, k, w);
+  float s;
+  if constexpr (NORM == kL2Norm) {
+    float U[(1 << CB) - 1];
+#pragma unroll
+    for (int t = 0; t < (1 << CB) - 1; t++) U[t] = k.u[t];
+    pack_codes<BITS, CB>(r, U, w);
+    s = nrm;
+  } else {
+    s = quantize_block<BITS, CB>(r, k, w);
+  }
   store_packed<BITS>(packed, ob, w);
-  scales[ob] = f32_to_f16(s * k.scale_sign);
+  const float sign = k.mixed_sign ? (((int)(blk % k.nb) < k.eo) ? -1.0f : 1.0f) : k.scale_sign;
+  scales[ob] = f32_to_f16(s * sign);
 }
 
 // Reference-ABI variant: boundaries and outer centroid come from the caller
@@ -281,8 +319,11 @@ __global__ __launch_bounds__(256) void pqo_quant_rotated_dev_kernel(
 }
 
 struct DequantConsts {
-  float cb[16];  // codebook values (f32)
-  float sg[32];  // sign factor per element (the reference passes fl(R_fwd[0][j] * sqrt(32)))
+  float cb[16];   // codebook values (f32); the outlier codebook when mixed
+  float cbn[16];  // mixed: the standard codebook
+  float sg[32];   // sign factor per element (the reference passes fl(R_fwd[0][j] * sqrt(32)))
+  int mixed;      // codebook per block by the scale's sign (quantize_tensor.rs:242-260)
+  int nn;         // mixed: standard codebook size (codes are clamped into it)
 };
 
 // out_j = fl(fl(W_j * fl(1/sqrt(32))) * |scale|), W = butterfly(cb[idx] * sign):
@@ -296,9 +337,10 @@ __global__ __launch_bounds__(256) void pqo_dequant_kernel(const uint8_t *__restr
                                                           DequantConsts dc,
                                                           const float *__restrict__ dev_cb,
                                                           const float *__restrict__ dev_sg, CacheMap map = {}) {
-  __shared__ float lut[16];
+  __shared__ float lut[32];
   constexpr int NC = 1 << BITS;
   if (threadIdx.x < NC) lut[threadIdx.x] = DEV_CONSTS ? dev_cb[threadIdx.x] : dc.cb[threadIdx.x];
+  if (!DEV_CONSTS && threadIdx.x >= 16 && threadIdx.x < 32) lut[threadIdx.x] = dc.cbn[threadIdx.x - 16];
   __syncthreads();
   const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
   if (blk >= nblocks) return;
@@ -315,12 +357,16 @@ __global__ __launch_bounds__(256) void pqo_dequant_kernel(const uint8_t *__restr
 #pragma unroll
     for (int q = 0; q < 3; q++) w[q] = p[q];
   }
-  const float s = fabsf(f16_to_f32(scales[ib]));
+  const float ssig = f16_to_f32(scales[ib]);
+  const float s = fabsf(ssig);
+  // mixed: a non-negative scale selects the standard codebook, codes clamped
+  const bool std_cb = !DEV_CONSTS && dc.mixed && !(ssig < 0.0f);
+  const uint32_t base = std_cb ? 16u : 0u, cmax = std_cb ? (uint32_t)dc.nn - 1u : 15u;
   float z[32];
 #pragma unroll
   for (int j = 0; j < 32; j++) {
     const float sgn = DEV_CONSTS ? dev_sg[j] : dc.sg[j];
-    z[j] = lut[field<BITS>(w, j)] * sgn;
+    z[j] = lut[base + min(field<BITS>(w, j), cmax)] * sgn;
   }
   butterfly<32>(z);
 #pragma unroll
@@ -369,11 +415,12 @@ __global__ __launch_bounds__(256) void pack_indices_kernel(const uint8_t *__rest
 
 // One launch of pqo_quant_kernel for (slot bits, codebook bits, input type):
 // ROTATE for activations, MAP for cache placement.
-template <bool ROTATE, bool MAP>
+template <bool ROTATE, bool MAP, int NORM>
 int launch_quant(const void *x, int dt, uint8_t *packed, uint16_t *scales, long long nblocks, int bits, int cb_bits,
                  const QuantConsts &k, const CacheMap &m, hipStream_t st) {
+  if (nblocks <= 0) return TQ_OK;
   const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
-#define QL(B, C, D) hipLaunchKernelGGL((pqo_quant_kernel<B, C, D, ROTATE, MAP>), grid, block, 0, st, x, packed, \
+#define QL(B, C, D) hipLaunchKernelGGL((pqo_quant_kernel<B, C, D, ROTATE, MAP, NORM>), grid, block, 0, st, x, packed, \
                                        scales, nblocks, k, m)
 #define QD(B, C) \
   do {                                      \
@@ -397,6 +444,11 @@ QuantConsts make_quant_consts(const tqh::PqoCodebook &cb, float outer, float sca
   for (int i = 0; i < t.nb; i++) {
     k.mu[i] = t.mu[i];
     k.b[i] = cb.b[i];
+    uint32_t u;
+    std::memcpy(&u, &cb.b[i], 4);  // nextup(b) for finite b
+    if ((u & 0x7fffffffu) == 0) u = 1u;
+    else u = ((int32_t)u >= 0) ? u + 1u : u - 1u;
+    std::memcpy(&k.u[i], &u, 4);
   }
   k.strict_mask = t.strict_mask;
   k.mul = t.mul;
@@ -404,9 +456,45 @@ QuantConsts make_quant_consts(const tqh::PqoCodebook &cb, float outer, float sca
   return k;
 }
 
+// polar_quantize of nblocks blocks (vectors of codec.num_blocks blocks) in
+// one launch per codebook: a mixed config's first nblocks / nb * eo blocks
+// on the outlier codebook, the rest on the standard one.
+template <bool MAP>
+int launch_polar_quant(const void *x, int dt, uint8_t *packed, uint16_t *scales, long long nblocks,
+                       const tqh::PolarCodec &codec, const CacheMap &m, hipStream_t st) {
+  auto run = [&](const tqh::PqoCodebook &cb, int cb_bits, long long b0, long long n) {
+    QuantConsts k = make_quant_consts(cb, codec.outer, codec.scale_sign);
+    k.mixed_sign = codec.mixed ? 1 : 0;
+    k.nb = codec.num_blocks;
+    k.eo = codec.eo;
+    k.blk0 = b0;
+    if (codec.norm_mode == kL2Norm)
+      return launch_quant<true, MAP, kL2Norm>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
+    return launch_quant<true, MAP, kMaxNorm>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
+  };
+  if (!codec.mixed) return run(codec.cb, codec.cb_bits, 0, nblocks);
+  const long long nout = nblocks / codec.num_blocks * codec.eo;  // bucketize_blocks' outlier rows
+  int rc = run(codec.ocb, codec.bits, 0, nout);
+  if (rc) return rc;
+  return run(codec.ncb, codec.bits - 1, nout, nblocks - nout);
+}
+
+DequantConsts make_dequant_consts(const tqh::PqoCodebook &cb);
+
+DequantConsts dequant_consts(const tqh::PolarCodec &codec) {
+  DequantConsts dc = make_dequant_consts(codec.mixed ? codec.ocb : codec.cb);
+  if (codec.mixed) {
+    for (int i = 0; i < codec.ncb.nc; i++) dc.cbn[i] = codec.ncb.c[i];
+    dc.nn = codec.ncb.nc;
+    dc.mixed = 1;
+  }
+  return dc;
+}
+
 DequantConsts make_dequant_consts(const tqh::PqoCodebook &cb) {
   DequantConsts dc{};
   for (int i = 0; i < cb.nc; i++) dc.cb[i] = cb.c[i];
+  dc.nn = cb.nc;
   // fl(R_fwd[0][j] * sqrt(32)) = fl(+-fl(1/sqrt(32)) * fl(sqrt(32))) (wht_tensor.rs:28-41)
   volatile float thirty_two = 32.0f;
   volatile float sq = sqrtf(thirty_two);  // fl(sqrt(32)), IEEE sqrt
@@ -463,9 +551,7 @@ extern "C" int tq_polar_quantize(const void *x, int x_dtype, uint8_t *packed_out
   if (num_vectors == 0) return TQ_OK;
   if (!x || !packed_out || !scales_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   const long long nblocks = (long long)num_vectors * (head_dim / 32);
-  const QuantConsts k = make_quant_consts(codec.cb, codec.outer, codec.scale_sign);
-  return launch_quant<true, false>(x, x_dtype, packed_out, scales_out, nblocks, bits, codec.cb_bits, k, CacheMap{},
-                                   stream);
+  return launch_polar_quant<false>(x, x_dtype, packed_out, scales_out, nblocks, codec, CacheMap{}, stream);
 }
 
 extern "C" int tq_polar_dequantize(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype,
@@ -480,7 +566,7 @@ extern "C" int tq_polar_dequantize(const uint8_t *packed, const uint16_t *scales
   if (num_vectors == 0) return TQ_OK;
   if (!packed || !scales || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   const long long nblocks = (long long)num_vectors * (head_dim / 32);
-  return launch_dequant<false>(packed, scales, out, out_dtype, nblocks, bits, make_dequant_consts(codec.cb),
+  return launch_dequant<false>(packed, scales, out, out_dtype, nblocks, bits, dequant_consts(codec),
                                CacheMap{}, stream);
 }
 
@@ -602,8 +688,7 @@ extern "C" int tq_polar_quantize_to_cache(const void *x, int x_dtype, int num_he
   const long long nblocks = (long long)num_heads * tokens * (head_dim / 32);
   if (nblocks == 0) return TQ_OK;
   if (!x || !packed_cache || !scales_cache) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  const QuantConsts k = make_quant_consts(codec.cb, codec.outer, codec.scale_sign);
-  return launch_quant<true, true>(x, x_dtype, packed_cache, scales_cache, nblocks, bits, codec.cb_bits, k, m, stream);
+  return launch_polar_quant<true>(x, x_dtype, packed_cache, scales_cache, nblocks, codec, m, stream);
 }
 
 extern "C" int tq_polar_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *scales_cache,
@@ -622,7 +707,7 @@ extern "C" int tq_polar_dequantize_from_cache(const uint8_t *packed_cache, const
   const long long nblocks = (long long)num_heads * tokens * (head_dim / 32);
   if (nblocks == 0) return TQ_OK;
   if (!packed_cache || !scales_cache || !out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  return launch_dequant<true>(packed_cache, scales_cache, out, out_dtype, nblocks, bits, make_dequant_consts(codec.cb),
+  return launch_dequant<true>(packed_cache, scales_cache, out, out_dtype, nblocks, bits, dequant_consts(codec),
                               m, stream);
 }
 
