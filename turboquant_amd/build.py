@@ -64,9 +64,26 @@ def build(verbose: bool = True) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    _build_api_test()
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
     return LIB
+
+
+API_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "api_test.cpp")
+API_TEST_BIN = os.path.join(ROOT, "tests", "cpp", "api_test")
+
+
+def _build_api_test() -> None:
+    """The C++ host-API test driver (tests/cpp), linked against the library."""
+    if not os.path.exists(API_TEST_SRC):
+        return
+    cmd = [_hipcc(), "-O2", "-std=c++17", f"-I{INCLUDE}", API_TEST_SRC, f"-L{HERE}", "-lturboquant_amd",
+           "-Wl,-rpath,$ORIGIN/../../turboquant_amd", "-o", API_TEST_BIN + ".tmp"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"api_test build failed:\n{res.stderr}")
+    os.replace(API_TEST_BIN + ".tmp", API_TEST_BIN)
 
 
 if __name__ == "__main__":
