@@ -189,6 +189,57 @@ def bench_c4(torch, tq, args):
             "contexts": lens_np.tolist(), "copies": copies}
 
 
+def bench_tq_c3(torch, tq, args):
+    """The C3 shape over a TQ3 cache (TqCache: 2-bit standard codes in 3-bit
+    slots plus the 1-bit QJL sketch of every key's residual): fused decode
+    with the QJL correction in the logits.  Bytes per step = 8 x 32768 x
+    (56 + 56 + 16 + 2): codes and scales of K and V, the keys' sign words and
+    residual norms.  Also timed with the query projection R q launched before
+    each step (the TqCache decode sequence)."""
+    import numpy as np
+    from tq_testdata import kv_outlier
+
+    rng = np.random.default_rng(33)
+    hkv, t, hd, bits, h = C3["kv_heads"], C3["ctx"], C3["head_dim"], 3, C3["heads"]
+    k = torch.from_numpy(kv_outlier(rng, hkv, t, hd)).cuda().to(torch.bfloat16)
+    v = torch.from_numpy(kv_outlier(rng, hkv, t, hd)).cuda().to(torch.bfloat16)
+    pk, sk = tq.polar_quantize(k.reshape(-1, hd), bits, outlier_blocks=0)
+    pv, sv = tq.polar_quantize(v.reshape(-1, hd), bits, outlier_blocks=0)
+    rmat = tq.qjl_sign_matrix(hd, 12345)
+    sg = torch.empty((hkv * t, hd // 8), dtype=torch.uint8, device="cuda")
+    nm = torch.empty((hkv * t,), dtype=torch.int16, device="cuda")
+    tq.qjl_cache_sketch(k, pk, sk, rmat, sg, nm, t, 0, bits, 0)
+    del k, v
+    base = [pk, sk, pv, sv, sg, nm]
+    step_bytes = hkv * t * (2 * (hd * bits // 8 + 8) + hd // 8 + 2)
+    copies = max(1, math.ceil((1 << 30) / step_bytes) + 1)
+    caches = [base] + [[x.clone() for x in base] for _ in range(copies - 1)]
+    q = (torch.from_numpy(rng.standard_normal((1, h, hd)).astype(np.float32)) / math.sqrt(hd)).cuda().to(
+        torch.bfloat16)
+    rq = tq.qjl_project(q.reshape(h, hd), rmat).reshape(1, h, hd)
+    lens = torch.tensor([t], dtype=torch.int32, device="cuda")
+    ws = tq.AttentionWorkspace(1, h, hkv, hd, t)
+    scale = 1.0 / math.sqrt(hd)
+
+    def step(i):
+        kp, ks, vp, vs, g, n = caches[i % copies]
+        tq.cache_decode_attention(q, kp, ks, vp, vs, lens, hkv, bits, t, t, 0, scale, ws, 0, rq=rq, qjl_signs=g,
+                                  qjl_norms=n)
+
+    def step_proj(i):
+        tq.qjl_project(q.reshape(h, hd), rmat)
+        step(i)
+
+    ms, _ = time_steps(torch, step, args.steps, args.warmup)
+    ms_proj, _ = time_steps(torch, step_proj, max(10, args.steps // 2), max(2, args.warmup // 2))
+    del caches, base
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return {"metric": "TQ3 fused decode with inline QJL correction, C3 shape (GB/s of compressed bytes)",
+            "value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(ms, 6),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": step_bytes,
+            "ms_per_step_with_query_projection": round(ms_proj, 6), "copies": copies}
+
+
 def bench_c1(torch, tq, args):
     """Config 1 on the GPU: 10,000 N(0,1) vectors (seed 42), d=128, TQ3 with
     rotation seed 42: quantize_vec + dequantize_vec per step; nMSE of the
@@ -309,6 +360,7 @@ def main():
 
     del x, packed, scales
     c4 = bench_c4(torch, tq, args)
+    tq_c3 = bench_tq_c3(torch, tq, args)
     c1 = bench_c1(torch, tq, args)
     c5 = bench_c5(torch, tq, args)
 
@@ -349,6 +401,7 @@ def main():
                                   "traffic": traffic("pqo_quant_kernel")},
                      "cpu_baseline": qcpu},
         "c4_batched_decode": c4,
+        "tq_decode_c3": tq_c3,
         "c1_codec": c1,
         "c5_qjl": c5,
         "wall_s_timed": round(wall, 4),

@@ -246,13 +246,16 @@ __device__ __forceinline__ long long cache_block(uint32_t blk, const CacheMap &m
 // sqrt, clamped to 1e-10) divides it before the rotation and is its scale;
 // codes count the boundaries strictly below the rotated value
 // (normalize_and_rotate, quantize_tensor.rs:90-101, 161-176).
-template <int BITS, int CB, int IN_DT, bool ROTATE, bool MAP, int NORM>
+// MIXED: one of the two launches of a mixed-outlier config (blocks from
+// k.blk0, scale sign per block).
+template <int BITS, int CB, int IN_DT, bool ROTATE, bool MAP, int NORM, bool MIXED>
 __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__ x,
                                                         uint8_t *__restrict__ packed,
                                                         uint16_t *__restrict__ scales,
                                                         long long nblocks, QuantConsts k, CacheMap map) {
-  const long long blk = k.blk0 + (long long)blockIdx.x * 256 + threadIdx.x;
-  if (blk >= k.blk0 + nblocks) return;
+  const long long b0 = MIXED ? k.blk0 : 0;
+  const long long blk = b0 + (long long)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= b0 + nblocks) return;
   const long long ob = MAP ? cache_block((uint32_t)blk, map) : blk;
   float r[32];
   load_block<IN_DT>(x, blk, r);
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__
     s = quantize_block<BITS, CB>(r, k, w);
   }
   store_packed<BITS>(packed, ob, w);
-  const float sign = k.mixed_sign ? (((int)(blk % k.nb) < k.eo) ? -1.0f : 1.0f) : k.scale_sign;
+  const float sign = MIXED ? (((int)(blk % k.nb) < k.eo) ? -1.0f : 1.0f) : k.scale_sign;
   scales[ob] = f32_to_f16(s * sign);
 }
 
@@ -415,13 +418,13 @@ __global__ __launch_bounds__(256) void pack_indices_kernel(const uint8_t *__rest
 
 // One launch of pqo_quant_kernel for (slot bits, codebook bits, input type):
 // ROTATE for activations, MAP for cache placement.
-template <bool ROTATE, bool MAP, int NORM>
+template <bool ROTATE, bool MAP, int NORM, bool MIXED>
 int launch_quant(const void *x, int dt, uint8_t *packed, uint16_t *scales, long long nblocks, int bits, int cb_bits,
                  const QuantConsts &k, const CacheMap &m, hipStream_t st) {
   if (nblocks <= 0) return TQ_OK;
   const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
-#define QL(B, C, D) hipLaunchKernelGGL((pqo_quant_kernel<B, C, D, ROTATE, MAP, NORM>), grid, block, 0, st, x, packed, \
-                                       scales, nblocks, k, m)
+#define QL(B, C, D) hipLaunchKernelGGL((pqo_quant_kernel<B, C, D, ROTATE, MAP, NORM, MIXED>), grid, block, 0, st, x, \
+                                       packed, scales, nblocks, k, m)
 #define QD(B, C) \
   do {                                      \
     if (!ROTATE || dt == kF32) QL(B, C, kF32); \
@@ -468,9 +471,14 @@ int launch_polar_quant(const void *x, int dt, uint8_t *packed, uint16_t *scales,
     k.nb = codec.num_blocks;
     k.eo = codec.eo;
     k.blk0 = b0;
+    if (codec.mixed) {
+      if (codec.norm_mode == kL2Norm)
+        return launch_quant<true, MAP, kL2Norm, true>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
+      return launch_quant<true, MAP, kMaxNorm, true>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
+    }
     if (codec.norm_mode == kL2Norm)
-      return launch_quant<true, MAP, kL2Norm>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
-    return launch_quant<true, MAP, kMaxNorm>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
+      return launch_quant<true, MAP, kL2Norm, false>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
+    return launch_quant<true, MAP, kMaxNorm, false>(x, dt, packed, scales, n, codec.bits, cb_bits, k, m, st);
   };
   if (!codec.mixed) return run(codec.cb, codec.cb_bits, 0, nblocks);
   const long long nout = nblocks / codec.num_blocks * codec.eo;  // bucketize_blocks' outlier rows
