@@ -223,7 +223,7 @@ def bench_tq_c3(torch, tq, args):
 
     def step(i):
         kp, ks, vp, vs, g, n = caches[i % copies]
-        tq.cache_decode_attention(q, kp, ks, vp, vs, lens, hkv, bits, t, t, 0, scale, ws, 0, rq=rq, qjl_signs=g,
+        tq.cache_decode_attention(q, kp, ks, vp, vs, None, hkv, bits, t, t, 0, scale, ws, 0, rq=rq, qjl_signs=g,
                                   qjl_norms=n)
 
     def step_proj(i):
@@ -323,14 +323,18 @@ def main():
     out = torch.empty((1, h, hd), dtype=torch.float32, device="cuda")
     scale = 1.0 / math.sqrt(hd)
 
-    def attn_step(i):
+    # the sequence length is known on the host (batch 1, as PqoCache::decode
+    # holds it), so no length is read on the device; the variant with device
+    # lengths (kv_lens tensor, the batched form) is timed beside it
+    def attn_step(i, kv_lens=None):
         kidx, ksc, vidx, vsc = caches[i % copies]
-        tq.pqo_decode_attention(q, kidx, ksc, vidx, vsc, lens, hkv, bits, t, t, 0, scale, ws, out=out)
+        tq.pqo_decode_attention(q, kidx, ksc, vidx, vsc, kv_lens, hkv, bits, t, t, 0, scale, ws, out=out)
 
     # headline: K steps launched from the host API one after another; the same
     # K steps replayed from a HIP graph are reported beside it
     ms, wall = time_steps(torch, attn_step, args.steps, args.warmup)
     ms_graph, _ = time_steps(torch, attn_step, args.steps, 0, graph=True)
+    ms_devlen, _ = time_steps(torch, lambda i: attn_step(i, lens), args.steps, args.warmup)
     gbs = c3_bytes() / (ms * 1e-3) / 1e9
     del caches
 
@@ -387,7 +391,8 @@ def main():
                                "ctx 32768, bf16 query, f32 out; rotating >= 1 GiB of cache copies",
                    "copies": copies, "algorithmic_bytes_per_step": c3_bytes(),
                    "launch": "K consecutive launches from the host API, HIP events around them",
-                   "graph_ms_per_step": round(ms_graph, 6)},
+                   "graph_ms_per_step": round(ms_graph, 6),
+                   "device_lengths_ms_per_step": round(ms_devlen, 6)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic("attn_decode_kernel")},
         "cpu_baseline": cpu,

@@ -176,7 +176,9 @@ int tq_attention_workspace_init(void *workspace, size_t workspace_bytes, int bat
  * tq_fused_attention (pqo.rs:106-174, cuda/attention.rs:41-174).
  *   q   [batch][num_heads][head_dim] in q_dtype
  *   out [batch][num_heads][head_dim] in out_dtype
- *   kv_lens: device int[batch]; max_kv_len: host bound on every kv_lens[b]
+ *   kv_lens: device int[batch]; max_kv_len: host bound on every kv_lens[b].
+ *   kv_lens may be null when every sequence holds exactly max_kv_len tokens
+ *   (a length the host knows): the kernel then reads no length from memory.
  *   record strides in tokens: kv_head_stride (capacity), seq_stride. */
 int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                             const uint16_t *k_scales, const uint8_t *v_indices,
@@ -296,6 +298,16 @@ int tq_qjl_cache_sketch(const void *k, int k_dtype, int num_heads, int tokens,
                         const uint32_t *sign_matrix, uint8_t *signs_cache, uint16_t *norms_cache,
                         long long cache_head_stride, long long cache_offset, int head_dim, int bits,
                         size_t outlier_blocks, int norm_mode, hipStream_t stream);
+
+/* tq_qjl_cache_sketch plus rq = R q for num_q_rows rows of q (q_dtype) in
+ * the same launch (a TQ decode step's sketch and projection). */
+int tq_qjl_cache_sketch_project(const void *k, int k_dtype, int num_heads, int tokens,
+                                const uint8_t *packed_cache, const uint16_t *scales_cache,
+                                const uint32_t *sign_matrix, uint8_t *signs_cache,
+                                uint16_t *norms_cache, long long cache_head_stride,
+                                long long cache_offset, int head_dim, int bits,
+                                size_t outlier_blocks, int norm_mode, const void *q, int q_dtype,
+                                float *rq, size_t num_q_rows, hipStream_t stream);
 
 /* rq[row] = R q[row] (precompute_query_projections, qjl.rs:488-492; r_q of
  * tq.rs:233-234), q [num_rows][dim] in q_dtype, rq f32. */

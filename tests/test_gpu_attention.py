@@ -200,3 +200,22 @@ def test_decode_peaked_softmax(tq):
     ref = orc.attention_dense(q, cache[4], cache[5], 1.0 / math.sqrt(128))
     (out,) = _run_decode(tq, q, cache, hkv, t, bits, t)
     assert np.abs(out - ref).max() <= TOL
+
+
+def test_host_known_length_matches_device_lengths(tq):
+    """kv_lens = null (every sequence holds max_kv_len tokens, known on the host)
+    gives the same output as the device length array."""
+    bits, h, hkv, t = 3, 16, 8, 3000
+    rng = np.random.default_rng(515)
+    cache = _make_cache(rng, hkv, t, bits, t)
+    kidx, ksc, vidx, vsc, kd, vd = cache
+    q = bf16_round(rng.standard_normal((h, 128)).astype(np.float32) / np.float32(math.sqrt(128)))
+    qd = _dev(q).reshape(1, h, 128)
+    ws = tq.AttentionWorkspace(1, h, hkv, 128, t)
+    lens = torch.tensor([t], dtype=torch.int32, device="cuda")
+    a = tq.pqo_decode_attention(qd, kidx, ksc, vidx, vsc, lens, hkv, bits, t, t, 0, 1 / math.sqrt(128), ws)
+    b = tq.pqo_decode_attention(qd, kidx, ksc, vidx, vsc, None, hkv, bits, t, t, 0, 1 / math.sqrt(128), ws)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    ref = orc.attention_dense(q, kd, vd, 1 / math.sqrt(128))
+    assert np.abs(b.cpu().numpy().reshape(h, 128) - ref).max() <= TOL

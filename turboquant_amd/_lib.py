@@ -66,6 +66,8 @@ SIGNATURES = {
     "tq_qjl_sign_matrix": (_i, [_p, _i, _u64, _p]),
     "tq_qjl_cache_sketch": (_i, [_p, _i, _i, _i, _p, _p, _p, _p, _p, _ll, _ll, _i, _i, _sz, _i, _p]),
     "tq_qjl_project": (_i, [_p, _i, _p, _p, _sz, _i, _p]),
+    "tq_qjl_cache_sketch_project": (_i, [_p, _i, _i, _i, _p, _p, _p, _p, _p, _ll, _ll, _i, _i, _sz, _i, _p, _i, _p,
+                                         _sz, _p]),
     "tq_qjl_bias_scale": (_f, [_i]),
     "tq_qjl_logit_bias": (_i, [_p, _i, _i, _p, _p, _i, _i, _ll, _i, _p, _i, _p]),
     "tq_cache_create": (_i, [_i, _i, _i, _i, _i, _sz, _i, C.POINTER(C.c_void_p)]),

@@ -930,14 +930,15 @@ extern "C" int tq_attention_workspace_init(void *workspace, size_t workspace_byt
   return tqh::check_launch("fill_zero_kernel");
 }
 
-extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
-                                         const uint16_t *k_scales, const uint8_t *v_indices,
-                                         const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
-                                         const uint16_t *qjl_norms, const int *kv_lens, int batch, int num_heads,
-                                         int num_kv_heads, int head_dim, int bits, size_t outlier_blocks,
-                                         int norm_mode, int max_kv_len, long long kv_head_stride,
-                                         long long seq_stride, float softmax_scale, void *out, int out_dtype,
-                                         void *workspace, size_t workspace_bytes, hipStream_t stream) {
+// host_len >= 0 (with kv_lens null): every sequence holds host_len tokens;
+// max_kv_len fixes the workspace layout either way.
+int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
+                          const uint8_t *v_indices, const uint16_t *v_scales, const float *rq,
+                          const uint8_t *qjl_signs, const uint16_t *qjl_norms, const int *kv_lens, int host_len,
+                          int batch, int num_heads, int num_kv_heads, int head_dim, int bits, size_t outlier_blocks,
+                          int norm_mode, int max_kv_len, long long kv_head_stride, long long seq_stride,
+                          float softmax_scale, void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+                          hipStream_t stream) {
   int rc = check_common(num_heads, num_kv_heads, head_dim, bits);
   if (rc) return rc;
   tqh::PolarCodec codec;
@@ -952,8 +953,9 @@ extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8
   if (!tqh::valid_dtype(q_dtype) || !tqh::valid_dtype(out_dtype))
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype");
   if (batch <= 0 || max_kv_len <= 0) return TQ_OK;
-  if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !kv_lens || !out)
+  if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !out)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!kv_lens && host_len < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null kv_lens");
   if (qjl && (!rq || !qjl_norms)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL needs rq, signs and norms");
   if (kv_head_stride < max_kv_len)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_head_stride %lld < max_kv_len %d", kv_head_stride, max_kv_len);
@@ -973,7 +975,7 @@ extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8
   a.v_idx = v_indices;
   a.v_sc = v_scales;
   a.kv_lens = kv_lens;
-  a.single_len = 0;
+  a.single_len = kv_lens ? 0 : min(max(host_len, 0), max_kv_len);
   a.max_len = max_kv_len;
   a.num_heads = num_heads;
   a.num_kv_heads = num_kv_heads;
@@ -998,6 +1000,20 @@ extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8
   const int mode = codec.outlier ? kModePqo : (qjl ? kModeTq : kModePq);
   const dim3 grid((unsigned)w.P, (unsigned)num_kv_heads, (unsigned)batch);
   return launch_decode<true>(a, bits, mode, num_heads / num_kv_heads, grid, stream);
+}
+
+extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
+                                         const uint16_t *k_scales, const uint8_t *v_indices,
+                                         const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                                         const uint16_t *qjl_norms, const int *kv_lens, int batch, int num_heads,
+                                         int num_kv_heads, int head_dim, int bits, size_t outlier_blocks,
+                                         int norm_mode, int max_kv_len, long long kv_head_stride,
+                                         long long seq_stride, float softmax_scale, void *out, int out_dtype,
+                                         void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  return tqh::decode_attention(q, q_dtype, k_indices, k_scales, v_indices, v_scales, rq, qjl_signs, qjl_norms, kv_lens,
+                               max_kv_len, batch, num_heads, num_kv_heads, head_dim, bits, outlier_blocks, norm_mode,
+                               max_kv_len, kv_head_stride, seq_stride, softmax_scale, out, out_dtype, workspace,
+                               workspace_bytes, stream);
 }
 
 extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,

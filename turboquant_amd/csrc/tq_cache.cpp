@@ -22,10 +22,6 @@
 
 namespace {
 
-__global__ void set_len_kernel(int *p, int v) {
-  if (threadIdx.x == 0) p[0] = v;
-}
-
 struct LayerBuffers {
   uint8_t *k_idx = nullptr, *v_idx = nullptr;
   uint16_t *k_sc = nullptr, *v_sc = nullptr;
@@ -147,10 +143,8 @@ class KvCache {
  public:
   KvCache(int num_layers, int num_kv_heads, int head_dim, const CacheMode &mode)
       : layers_(num_layers), heads_(num_kv_heads), head_dim_(head_dim), mode_(mode),
-        storage_(num_kv_heads, head_dim, mode.bits, num_layers, mode.qjl), lens_(num_layers, nullptr) {}
+        storage_(num_kv_heads, head_dim, mode.bits, num_layers, mode.qjl) {}
   ~KvCache() {
-    for (int *p : lens_)
-      if (p) (void)hipFree(p);
     for (void *p : {ws_, rmat_, rq_})
       if (p) (void)hipFree(p);
   }
@@ -161,8 +155,11 @@ class KvCache {
   const CacheMode &mode() const { return mode_; }
   CompressedStorage &storage() { return storage_; }
 
-  // quantize_and_store (pqo.rs:64-100, tq.rs:97-145): k, v [num_kv_heads][tokens][head_dim]
-  int append(int l, const void *k, const void *v, int dtype, int tokens, size_t *old_seq, hipStream_t stream) {
+  // quantize_and_store (pqo.rs:64-100, tq.rs:97-145): k, v [num_kv_heads][tokens][head_dim].
+  // A TqCache given q (num_q_rows rows) also projects it into the rq scratch
+  // in the sketch's launch.
+  int append(int l, const void *k, const void *v, int dtype, int tokens, size_t *old_seq, hipStream_t stream,
+             const void *q = nullptr, int q_dtype = TQ_DTYPE_F32, size_t num_q_rows = 0) {
     const size_t old = storage_.seq_len(l);
     *old_seq = old;
     if (tokens == 0) return TQ_OK;
@@ -178,9 +175,14 @@ class KvCache {
     if (mode_.qjl) {
       rc = sign_matrix(stream);
       if (rc) return rc;
-      rc = tq_qjl_cache_sketch(k, dtype, heads_, tokens, L.k_idx, L.k_sc, static_cast<const uint32_t *>(rmat_),
-                               L.signs, L.norms, (long long)L.cap, (long long)old, head_dim_, mode_.bits,
-                               mode_.outlier_blocks, mode_.norm_mode, stream);
+      if (num_q_rows) {
+        rc = rq_scratch(num_q_rows, stream);
+        if (rc) return rc;
+      }
+      rc = tq_qjl_cache_sketch_project(k, dtype, heads_, tokens, L.k_idx, L.k_sc,
+                                       static_cast<const uint32_t *>(rmat_), L.signs, L.norms, (long long)L.cap,
+                                       (long long)old, head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode,
+                                       q, q_dtype, static_cast<float *>(rq_), num_q_rows, stream);
       if (rc) return rc;
     }
     storage_.set_seq(l, old + tokens);
@@ -197,19 +199,24 @@ class KvCache {
                                           head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode, stream);
   }
 
+  int rq_scratch(size_t num_rows, hipStream_t stream) {
+    const size_t need = num_rows * (size_t)head_dim_ * sizeof(float);
+    if (need <= rq_bytes_) return TQ_OK;
+    if (hipStreamSynchronize(stream) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "stream synchronize failed");
+    if (rq_) (void)hipFree(rq_);
+    rq_ = nullptr;
+    rq_bytes_ = 0;
+    if (hipMalloc(&rq_, need) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "rq allocation failed");
+    rq_bytes_ = need;
+    return TQ_OK;
+  }
+
   // rq = R q for num_rows query rows, in the cache's scratch
   int project(const void *q, int q_dtype, size_t num_rows, hipStream_t stream) {
     int rc = sign_matrix(stream);
     if (rc) return rc;
-    const size_t need = num_rows * (size_t)head_dim_ * sizeof(float);
-    if (need > rq_bytes_) {
-      if (hipStreamSynchronize(stream) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "stream synchronize failed");
-      if (rq_) (void)hipFree(rq_);
-      rq_ = nullptr;
-      rq_bytes_ = 0;
-      if (hipMalloc(&rq_, need) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "rq allocation failed");
-      rq_bytes_ = need;
-    }
+    rc = rq_scratch(num_rows, stream);
+    if (rc) return rc;
     return tq_qjl_project(q, q_dtype, static_cast<const uint32_t *>(rmat_), static_cast<float *>(rq_), num_rows,
                           head_dim_, stream);
   }
@@ -225,15 +232,12 @@ class KvCache {
   }
 
   // decode_cuda (pqo.rs:106-174) as one fused launch over the stored records;
-  // a TqCache adds the QJL correction inline
+  // a TqCache adds the QJL correction inline (rq_ready: the append already
+  // projected q)
   int attend(int l, const void *q, int q_dtype, int num_q_heads, float scale, void *out, int out_dtype,
-             hipStream_t stream) {
+             hipStream_t stream, bool rq_ready = false) {
     const LayerBuffers &L = storage_.layer(l);
-    if (!lens_[l] && hipMalloc(&lens_[l], sizeof(int)) != hipSuccess)
-      return tqh::fail(TQ_ERR_DEVICE, "length buffer allocation failed");
-    hipLaunchKernelGGL(set_len_kernel, dim3(1), dim3(64), 0, stream, lens_[l], (int)L.seq);
-    int rc = tqh::check_launch("set_len_kernel");
-    if (rc) return rc;
+    int rc = TQ_OK;
     const size_t need = tq_attention_workspace_size(1, num_q_heads, heads_, head_dim_, (int)L.cap);
     if (need == 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid attention shape");
     if (need > ws_bytes_) {
@@ -246,16 +250,16 @@ class KvCache {
       rc = tq_attention_workspace_init(ws_, ws_bytes_, 1, num_q_heads, heads_, head_dim_, (int)L.cap, stream);
       if (rc) return rc;
     }
-    if (mode_.qjl) {
+    if (mode_.qjl && !rq_ready) {
       rc = project(q, q_dtype, (size_t)num_q_heads, stream);
       if (rc) return rc;
     }
-    return tq_cache_decode_attention(q, q_dtype, L.k_idx, L.k_sc, L.v_idx, L.v_sc,
-                                     mode_.qjl ? static_cast<const float *>(rq_) : nullptr,
-                                     mode_.qjl ? L.signs : nullptr, mode_.qjl ? L.norms : nullptr, lens_[l], 1,
-                                     num_q_heads, heads_, head_dim_, mode_.bits, mode_.outlier_blocks,
-                                     mode_.norm_mode, (int)L.cap, (long long)L.cap, 0, scale, out, out_dtype, ws_,
-                                     ws_bytes_, stream);
+    // the length is known here: the kernel reads none from memory
+    return tqh::decode_attention(q, q_dtype, L.k_idx, L.k_sc, L.v_idx, L.v_sc,
+                                 mode_.qjl ? static_cast<const float *>(rq_) : nullptr,
+                                 mode_.qjl ? L.signs : nullptr, mode_.qjl ? L.norms : nullptr, nullptr, (int)L.seq, 1,
+                                 num_q_heads, heads_, head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode,
+                                 (int)L.cap, (long long)L.cap, 0, scale, out, out_dtype, ws_, ws_bytes_, stream);
   }
 
  private:
@@ -275,7 +279,6 @@ class KvCache {
   int layers_, heads_, head_dim_;
   CacheMode mode_;
   CompressedStorage storage_;
-  std::vector<int *> lens_;
   void *ws_ = nullptr;
   size_t ws_bytes_ = 0;
   void *rmat_ = nullptr;
@@ -382,10 +385,12 @@ extern "C" int tq_cache_decode(void *cache, int layer, const void *k, const void
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT,
                      "fused decode takes outlier_blocks 0 or all (mixed configs: tq_cache_decode_dequantized)");
   size_t old = 0;
-  rc = c->append(layer, k, v, kv_dtype, tokens, &old, stream);
+  const bool fuse_rq = m.qjl && tokens > 0;  // the sketch launch projects q too
+  rc = c->append(layer, k, v, kv_dtype, tokens, &old, stream, fuse_rq ? q : nullptr, q_dtype,
+                 fuse_rq ? (size_t)num_q_heads : 0);
   if (rc) return rc;
   if (!c->storage().is_active(layer)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "decode over an empty cache");
-  return c->attend(layer, q, q_dtype, num_q_heads, softmax_scale, out, out_dtype, stream);
+  return c->attend(layer, q, q_dtype, num_q_heads, softmax_scale, out, out_dtype, stream, fuse_rq);
 }
 
 extern "C" int tq_cache_decode_dequantized(void *cache, int layer, const void *k, const void *v, int dtype, int tokens,

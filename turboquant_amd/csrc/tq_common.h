@@ -58,6 +58,18 @@ struct PolarCodec {
 // status for an invalid mode.
 int polar_codec(int bits, int norm_mode, size_t outlier_blocks, int num_blocks, PolarCodec &codec);
 
+// Fused decode attention (tq_cache_decode_attention) with the length given
+// by the host: kv_lens null and host_len >= 0 means every sequence holds
+// host_len tokens, no length is read on the device; max_kv_len fixes the
+// workspace layout (a cache passes its capacity, so the layout stays put as
+// the sequence grows).
+int decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
+                     const uint8_t *v_indices, const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                     const uint16_t *qjl_norms, const int *kv_lens, int host_len, int batch, int num_heads,
+                     int num_kv_heads, int head_dim, int bits, size_t outlier_blocks, int norm_mode, int max_kv_len,
+                     long long kv_head_stride, long long seq_stride, float softmax_scale, void *out, int out_dtype,
+                     void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 // Per-boundary constants of the exact division threshold (see
 // tqd::div_threshold): mu = midpoint of b and nextup(b), strict = b even.
 struct DivThresholds {

@@ -364,11 +364,14 @@ struct SketchConsts {
 // (quantize_tensor.rs:197-219, 32-lane butterflies), the residual
 // r = k - k_hat is summed as sum r^2 in element order for the norm, and
 // sign bit j = (R r)_j >= 0 (qjl.rs:305-319) is one wave ballot per 64 rows.
+// Waves past the nvec keys project the nq query rows of `q` instead (rq = R q,
+// as qjl_project_kernel), so a decode step's sketch and projection share one
+// launch.
 template <int D, int BITS, int IN_DT>
 __global__ __launch_bounds__(kBlock) void qjl_cache_sketch_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ packed, const uint16_t *__restrict__ scales,
     const uint32_t *__restrict__ rbits, uint8_t *__restrict__ signs, uint16_t *__restrict__ norms, long long nvec,
-    SketchConsts k) {
+    SketchConsts k, const void *__restrict__ q, int q_dtype, float *__restrict__ rq, long long nq) {
   constexpr int E = D / 64, NQB = D / 32, WB = 4 * BITS;
   __shared__ __attribute__((aligned(16))) float s_r[kBlock / 64][D];
   __shared__ float s_cb[16];
@@ -378,7 +381,27 @@ __global__ __launch_bounds__(kBlock) void qjl_cache_sketch_kernel(
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const long long v = (long long)blockIdx.x * (kBlock / 64) + wave;
-  if (v >= nvec) return;  // whole waves leave together
+  if (v >= nvec + nq) return;  // whole waves leave together
+  if (v >= nvec) {
+    const long long row = v - nvec;
+#pragma unroll
+    for (int m = 0; m < E; m++) {
+      const long long xi = row * D + 64 * m + lane;
+      float xv;
+      if (q_dtype == kF32) xv = static_cast<const float *>(q)[xi];
+      else if (q_dtype == kBF16) xv = bf16_to_f32(static_cast<const uint16_t *>(q)[xi]);
+      else xv = f16_to_f32(static_cast<const uint16_t *>(q)[xi]);
+      s_r[wave][64 * m + lane] = xv;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float p[E];
+    wave_row_products<D>(s_r[wave], rbits, k.inv_sqrt_d, lane, p);
+#pragma unroll
+    for (int m = 0; m < E; m++) rq[row * D + 64 * m + lane] = p[m];
+    return;
+  }
   const long long h = v / k.tokens, t = v - h * k.tokens;
   const long long rec = h * k.head_stride + k.offset + t;
   const int i = lane & 31;
@@ -689,10 +712,12 @@ extern "C" int tq_qjl_sign_matrix(uint32_t *bits_out, int dim, uint64_t qjl_seed
   return tqh::check_launch("qjl_sign_matrix_kernel");
 }
 
-extern "C" int tq_qjl_cache_sketch(const void *k, int k_dtype, int num_heads, int tokens, const uint8_t *packed_cache,
-                                   const uint16_t *scales_cache, const uint32_t *sign_matrix, uint8_t *signs_cache,
-                                   uint16_t *norms_cache, long long cache_head_stride, long long cache_offset,
-                                   int head_dim, int bits, size_t outlier_blocks, int norm_mode, hipStream_t stream) {
+extern "C" int tq_qjl_cache_sketch_project(const void *k, int k_dtype, int num_heads, int tokens,
+                                           const uint8_t *packed_cache, const uint16_t *scales_cache,
+                                           const uint32_t *sign_matrix, uint8_t *signs_cache, uint16_t *norms_cache,
+                                           long long cache_head_stride, long long cache_offset, int head_dim, int bits,
+                                           size_t outlier_blocks, int norm_mode, const void *q, int q_dtype, float *rq,
+                                           size_t num_q_rows, hipStream_t stream) {
   int rc = check_sketch_dim(head_dim);
   if (rc) return rc;
   tqh::PolarCodec codec;
@@ -703,10 +728,12 @@ extern "C" int tq_qjl_cache_sketch(const void *k, int k_dtype, int num_heads, in
   if (cache_offset < 0 || cache_head_stride < cache_offset + tokens)
     return tqh::fail(TQ_ERR_RANGE_OUT_OF_BOUNDS, "cache rows [%lld, %lld) exceed head stride %lld", cache_offset,
                      cache_offset + tokens, cache_head_stride);
-  const long long nvec = (long long)num_heads * tokens;
-  if (nvec == 0) return TQ_OK;
-  if (!k || !packed_cache || !scales_cache || !sign_matrix || !signs_cache || !norms_cache)
+  const long long nvec = (long long)num_heads * tokens, nq = (long long)num_q_rows;
+  if (nvec + nq == 0) return TQ_OK;
+  if (!sign_matrix || (nvec && (!k || !packed_cache || !scales_cache || !signs_cache || !norms_cache)))
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  if (nq && (!q || !rq || !tqh::valid_dtype(q_dtype)))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "query projection needs q (f32/bf16/f16) and rq");
   SketchConsts c{};
   for (int i = 0; i < codec.cb.nc; i++) c.cb[i] = codec.cb.c[i];
   c.sign_mask = kPqoSignMask;
@@ -720,11 +747,12 @@ extern "C" int tq_qjl_cache_sketch(const void *k, int k_dtype, int num_heads, in
   c.head_stride = cache_head_stride;
   c.offset = cache_offset;
   c.tokens = tokens;
-  const unsigned grid = (unsigned)((nvec + kBlock / 64 - 1) / (kBlock / 64));
+  const unsigned grid = (unsigned)((nvec + nq + kBlock / 64 - 1) / (kBlock / 64));
   return by_cache_dim(head_dim, [&](auto d) {
     constexpr int D = decltype(d)::value;
 #define SK(B, T) hipLaunchKernelGGL((qjl_cache_sketch_kernel<D, B, T>), dim3(grid), dim3(kBlock), 0, stream, k, \
-                                    packed_cache, scales_cache, sign_matrix, signs_cache, norms_cache, nvec, c)
+                                    packed_cache, scales_cache, sign_matrix, signs_cache, norms_cache, nvec, c, q, \
+                                    q_dtype, rq, nq)
     if (bits == 3) {
       if (k_dtype == kF32) SK(3, kF32);
       else if (k_dtype == kBF16) SK(3, kBF16);
@@ -793,4 +821,13 @@ extern "C" int tq_qjl_logit_bias(const float *rq, int num_q_heads, int q_len, co
                        sf, out, out_dtype);
     return tqh::check_launch("qjl_logit_bias_kernel");
   });
+}
+
+extern "C" int tq_qjl_cache_sketch(const void *k, int k_dtype, int num_heads, int tokens, const uint8_t *packed_cache,
+                                   const uint16_t *scales_cache, const uint32_t *sign_matrix, uint8_t *signs_cache,
+                                   uint16_t *norms_cache, long long cache_head_stride, long long cache_offset,
+                                   int head_dim, int bits, size_t outlier_blocks, int norm_mode, hipStream_t stream) {
+  return tq_qjl_cache_sketch_project(k, k_dtype, num_heads, tokens, packed_cache, scales_cache, sign_matrix,
+                                     signs_cache, norms_cache, cache_head_stride, cache_offset, head_dim, bits,
+                                     outlier_blocks, norm_mode, nullptr, TQ_DTYPE_F32, nullptr, 0, stream);
 }
