@@ -207,6 +207,23 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
                               void *out, int out_dtype, void *workspace, size_t workspace_bytes,
                               hipStream_t stream);
 
+/* Multi-query (prefill) attention straight over a compressed cache, on the
+ * matrix cores (no dequantized K/V): q [num_heads][q_len][head_dim] in
+ * q_dtype, out the same shape in out_dtype; query i sits at position
+ * kv_len - q_len + i and, when causal, sees tokens t <= that position.
+ * Records as tq_cache_decode_attention (one sequence, kv_head_stride);
+ * qjl_signs non-null selects TQ (rq [num_heads][q_len][head_dim] f32 = R q,
+ * logits scale * (q.k + correction)).  head_dim 128, GQA 1/2/4, outlier_blocks
+ * 0 or all.  Replaces the reference's prefill result (dequantized K/V for
+ * SDPA, pqo.rs:184-200, tq.rs:258-273). */
+int tq_cache_prefill_attention(const void *q, int q_dtype, const uint8_t *k_indices,
+                               const uint16_t *k_scales, const uint8_t *v_indices,
+                               const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                               const uint16_t *qjl_norms, int num_heads, int q_len,
+                               int num_kv_heads, int head_dim, int bits, size_t outlier_blocks,
+                               int norm_mode, int kv_len, long long kv_head_stride, int causal,
+                               float softmax_scale, void *out, int out_dtype, hipStream_t stream);
+
 /* =========================================================================
  * Core full-vector codec (TurboQuantConfig{bits, dim, rotation_seed}),
  * batched over vectors.  A PackedBlock maps to one row of packed_out
@@ -371,6 +388,15 @@ int tq_cache_decode(void *cache, int layer, const void *k, const void *v, int kv
 int tq_cache_decode_dequantized(void *cache, int layer, const void *k, const void *v, int dtype,
                                 int tokens, const void *q, int q_dtype, int num_q_heads, int q_len,
                                 void *k_out, void *v_out, void *logit_bias_out, hipStream_t stream);
+
+/* Multi-query attention of q [num_q_heads][q_len][head_dim] over the whole
+ * layer (tq_cache_prefill_attention on the stored records; the queries sit at
+ * the layer's last q_len positions), without dequantizing it: the attention a
+ * caller runs on prefill's DequantResult (pqo.rs:184-200, tq.rs:258-273),
+ * with the QJL correction for a TqCache. */
+int tq_cache_attend_prefill(void *cache, int layer, const void *q, int q_dtype, int num_q_heads,
+                            int q_len, int causal, float softmax_scale, void *out, int out_dtype,
+                            hipStream_t stream);
 
 /* seq_len / reset / memory_usage (pqo.rs:224-236, tq.rs:299-323,
  * storage.rs:175-202). */

@@ -53,6 +53,8 @@ def _load():
         "tqo_pqo_quantize": (C.c_int, [C.c_int, _sz, _sz, _f32p, _u8p, _u16p]),
         "tqo_pqo_dequantize": (C.c_int, [C.c_int, _sz, _sz, _u8p, _u16p, _f32p]),
         "tqo_attention_dense": (C.c_int, [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_float, _f32p]),
+        "tqo_attention_prefill": (C.c_int, [_sz, _sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_void_p, C.c_float,
+                                            C.c_int, _f32p]),
         "tqo_polar_quantize": (C.c_int, [C.c_int, _sz, C.c_int, _sz, _sz, _f32p, _u8p, _u16p]),
         "tqo_polar_dequantize": (C.c_int, [C.c_int, _sz, C.c_int, _sz, _sz, _u8p, _u16p, _f32p]),
         "tqo_tq_signs_norms": (C.c_int, [_sz, _sz, _f32p, _f32p, _u8p, _u16p]),
@@ -313,6 +315,20 @@ def attention_dense_bias(q, k, v, bias, softmax_scale: float) -> np.ndarray:
     hkv, t, _ = k.shape
     out = np.zeros((h, d), np.float32)
     _check(lib.tqo_attention_dense_bias(h, hkv, d, t, q, k, v, bias, softmax_scale, out))
+    return out
+
+
+def attention_prefill(q, k, v, softmax_scale: float, causal: bool, bias=None) -> np.ndarray:
+    """q [H, L, D]; k, v [Hkv, S, D]; bias [H, L, S] or None -> out [H, L, D]."""
+    q, k, v = (_c(a, np.float32) for a in (q, k, v))
+    h, ql, d = q.shape
+    hkv, t, _ = k.shape
+    out = np.zeros((h, ql, d), np.float32)
+    b = None
+    if bias is not None:
+        bias = _c(bias, np.float32)
+        b = bias.ctypes.data_as(C.c_void_p)
+    _check(lib.tqo_attention_prefill(h, hkv, d, ql, t, q, k, v, b, softmax_scale, 1 if causal else 0, out))
     return out
 
 

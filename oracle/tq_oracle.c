@@ -904,6 +904,51 @@ int tqo_attention_dense(size_t num_heads, size_t num_kv_heads, size_t head_dim, 
     return TQO_OK;
 }
 
+/* Multi-query (prefill) attention over dequantized K/V, accumulated in
+   double: out[h][i] = softmax_t(scale * (q[h][i] . k_t + bias[h][i][t]))
+   v_t over t < kv_len, and t <= kv_len - q_len + i when causal (the SDPA a
+   caller runs on the reference's prefill result); bias may be NULL.
+   q, out [num_heads][q_len][d]; k, v [num_kv_heads][kv_len][d];
+   bias [num_heads][q_len][kv_len]. */
+int tqo_attention_prefill(size_t num_heads, size_t num_kv_heads, size_t d, size_t q_len, size_t kv_len,
+                          const float *q, const float *k, const float *v, const float *bias, float softmax_scale,
+                          int causal, float *out)
+{
+    if (num_kv_heads == 0 || num_heads % num_kv_heads != 0) return TQO_ERR_INVALID_ARGUMENT;
+    if (causal && q_len > kv_len) return TQO_ERR_INVALID_ARGUMENT;
+    const size_t rep = num_heads / num_kv_heads;
+    double *sc = malloc((kv_len ? kv_len : 1) * sizeof(double));
+    double *acc = malloc(d * sizeof(double));
+    for (size_t h = 0; h < num_heads; h++) {
+        const size_t g = h / rep;
+        const float *kg = k + g * kv_len * d, *vg = v + g * kv_len * d;
+        for (size_t i = 0; i < q_len; i++) {
+            const float *qv = q + (h * q_len + i) * d;
+            const size_t lim = causal ? kv_len - q_len + i + 1 : kv_len;
+            double mx = -INFINITY;
+            for (size_t t = 0; t < lim; t++) {
+                double s = 0.0;
+                for (size_t e = 0; e < d; e++) s += (double)qv[e] * (double)kg[t * d + e];
+                if (bias) s += (double)bias[(h * q_len + i) * kv_len + t];
+                s *= (double)softmax_scale;
+                sc[t] = s;
+                mx = s > mx ? s : mx;
+            }
+            double l = 0.0;
+            for (size_t e = 0; e < d; e++) acc[e] = 0.0;
+            for (size_t t = 0; t < lim; t++) {
+                const double p = exp(sc[t] - mx);
+                l += p;
+                for (size_t e = 0; e < d; e++) acc[e] += p * (double)vg[t * d + e];
+            }
+            for (size_t e = 0; e < d; e++) out[(h * q_len + i) * d + e] = lim ? (float)(acc[e] / l) : 0.0f;
+        }
+    }
+    free(sc);
+    free(acc);
+    return TQO_OK;
+}
+
 /* ------------------------------------------------------------------------
  * QJL -- src/qjl.rs
  * ---------------------------------------------------------------------- */

@@ -104,6 +104,9 @@ int tqo_attention_dense_bias(size_t num_heads, size_t num_kv_heads, size_t head_
                              float softmax_scale, float *out);
 
 /* ---- dense attention oracle over dequantized K/V ---- */
+int tqo_attention_prefill(size_t num_heads, size_t num_kv_heads, size_t d, size_t q_len,
+                          size_t kv_len, const float *q, const float *k, const float *v,
+                          const float *bias, float softmax_scale, int causal, float *out);
 int tqo_attention_dense(size_t num_heads, size_t num_kv_heads, size_t head_dim,
                         size_t kv_len, const float *q, const float *k, const float *v,
                         float softmax_scale, float *out);

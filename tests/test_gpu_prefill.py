@@ -1,0 +1,109 @@
+"""GPU parity of the multi-query (prefill) attention over compressed records
+against the oracle: dequantize with the CPU restatement, then dense
+(causal or full) softmax attention in double, with the QJL logit bias for a
+TQ cache.  Tolerance: 1e-3 max-abs (fp32 accumulation, f16 two-part
+operands)."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tq_testdata import bf16_bits, bf16_round, kv_outlier
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+D = 128
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def tq():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import turboquant_amd
+    return turboquant_amd
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _records(bits, outlier, x, cap):
+    h, t, _ = x.shape
+    p, s = orc.polar_quantize(bits, outlier, x.reshape(-1, D), D)
+    d = orc.polar_dequantize(bits, outlier, p, s, D).reshape(h, t, D)
+    pb = np.zeros((h, cap, p.shape[1]), np.uint8)
+    sb = np.zeros((h, cap, 4), np.uint16)
+    pb[:, :t] = p.reshape(h, t, -1)
+    sb[:, :t] = s.reshape(h, t, 4)
+    return _dev(pb), _dev(sb.view(np.int16)), d
+
+
+@pytest.mark.parametrize("bits,outlier,hq,hkv,ql,t,causal", [
+    (3, orc.OUTLIER_ALL, 16, 8, 100, 300, True),
+    (4, orc.OUTLIER_ALL, 32, 8, 70, 129, True),
+    (3, orc.OUTLIER_ALL, 8, 8, 64, 64, True),
+    (3, 0, 16, 8, 33, 200, False),
+    (4, 0, 16, 8, 1, 1000, True),
+    (3, orc.OUTLIER_ALL, 16, 8, 257, 257, True),
+])
+def test_prefill_matches_dense_oracle(tq, bits, outlier, hq, hkv, ql, t, causal):
+    rng = np.random.default_rng(700 + t + ql)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    cap = t + 5
+    ki, ks, kd = _records(bits, outlier, k, cap)
+    vi, vs, vd = _records(bits, outlier, v, cap)
+    q = bf16_round(rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    scale = 1 / math.sqrt(D)
+    out = tq.cache_prefill_attention(qd, ki, ks, vi, vs, hkv, bits, t, cap, scale, outlier, causal=causal)
+    torch.cuda.synchronize()
+    ref = orc.attention_prefill(q, kd, vd, scale, causal)
+    err = np.abs(out.cpu().numpy() - ref).max()
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_tq_cache_attend_prefill_with_qjl(tq, bits):
+    hkv, hq, t, ql = 4, 8, 400, 48
+    rng = np.random.default_rng(800 + bits)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    cache = tq.TqCache(tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1, outlier_blocks=0))
+    q = rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D))
+    r = cache.prefill(0, _dev(k[None]), _dev(v[None]), _dev(q[None]))
+    out = cache.attend_prefill(0, _dev(q[None]), 1 / math.sqrt(D))
+    torch.cuda.synchronize()
+    pk, sk = orc.polar_quantize(bits, 0, k.reshape(-1, D), D)
+    pv, sv = orc.polar_quantize(bits, 0, v.reshape(-1, D), D)
+    kd = orc.polar_dequantize(bits, 0, pk, sk, D)
+    vd = orc.polar_dequantize(bits, 0, pv, sv, D).reshape(hkv, t, D)
+    sg, nm = orc.tq_signs_norms(k.reshape(-1, D), kd)
+    bias = orc.tq_logit_bias(q, sg.reshape(hkv, t, -1), nm.reshape(hkv, t))
+    ref = orc.attention_prefill(q, kd.reshape(hkv, t, D), vd, 1 / math.sqrt(D), True, bias)
+    err = np.abs(out[0].cpu().numpy() - ref).max()
+    assert err <= TOL, err
+    # the caller's alternative: SDPA on the dequantized result plus the returned bias
+    np.testing.assert_allclose(r.logit_bias[0].cpu().numpy(), bias, rtol=0, atol=1e-5 * np.abs(bias).max())
+
+
+def test_pqo_cache_attend_prefill_full_layer(tq):
+    hkv, hq, t = 8, 16, 700
+    rng = np.random.default_rng(900)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    cache = tq.PqoCache(2, hkv, D, 3)
+    cache.prefill(1, _dev(k[None, :, :500]), _dev(v[None, :, :500]))
+    cache.prefill(1, _dev(k[None, :, 500:]), _dev(v[None, :, 500:]))
+    q = bf16_round(rng.standard_normal((hq, 200, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    out = cache.attend_prefill(1, _dev(q[None]), 1 / math.sqrt(D), out_dtype=torch.float32)
+    pk, sk = orc.pqo_quantize(3, k.reshape(-1, D), D)
+    pv, sv = orc.pqo_quantize(3, v.reshape(-1, D), D)
+    kd = orc.pqo_dequantize(3, pk, sk, D).reshape(hkv, t, D)
+    vd = orc.pqo_dequantize(3, pv, sv, D).reshape(hkv, t, D)
+    ref = orc.attention_prefill(q, kd, vd, 1 / math.sqrt(D), True)
+    err = np.abs(out[0].cpu().numpy() - ref).max()
+    assert err <= TOL, err

@@ -194,3 +194,26 @@ def test_mixed_outlier_blocks_follow_reference_row_order(eo):
     cen = np.where((sc < 0)[:, None], C3[got], C2[np.minimum(got, 3)])
     yref = (cen @ R_FWD.T) * np.abs(sc)[:, None]
     np.testing.assert_allclose(y, yref, rtol=2e-6, atol=2e-6 * np.abs(yref).max())
+
+
+def test_prefill_oracle_against_numpy():
+    rng = np.random.default_rng(12)
+    h, hkv, ql, t, d = 4, 2, 5, 19, 128
+    q = rng.standard_normal((h, ql, d)).astype(np.float32)
+    k = rng.standard_normal((hkv, t, d)).astype(np.float32)
+    v = rng.standard_normal((hkv, t, d)).astype(np.float32)
+    bias = rng.standard_normal((h, ql, t)).astype(np.float32)
+    scale = 1 / math.sqrt(d)
+    for causal in (False, True):
+        got = orc.attention_prefill(q, k, v, scale, causal, bias)
+        for hh in range(h):
+            g = hh // 2
+            lo = (q[hh].astype(np.float64) @ k[g].T.astype(np.float64) + bias[hh]) * scale
+            if causal:
+                lo = np.where(np.arange(t)[None, :] <= (t - ql + np.arange(ql))[:, None], lo, -np.inf)
+            p = np.exp(lo - lo.max(1, keepdims=True))
+            ref = (p / p.sum(1, keepdims=True)) @ v[g].astype(np.float64)
+            np.testing.assert_allclose(got[hh], ref, rtol=1e-5, atol=1e-6)
+    # one query at the end with the causal limit is the decode oracle
+    one = orc.attention_prefill(q[:, -1:], k, v, scale, True)
+    np.testing.assert_allclose(one[:, 0], orc.attention_dense(q[:, -1], k, v, scale), rtol=1e-6, atol=1e-7)

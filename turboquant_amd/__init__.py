@@ -24,7 +24,7 @@ __all__ = [
     "qjl_query_context", "qjl_scores", "softmax_rows", "qjl_weighted_values", "PqoCache", "AttendConfig",
     "DequantResult", "TqCache", "CacheConfig", "QuantNormMode", "DecodeOutput", "Fused", "Dequantized",
     "polar_quantize", "polar_dequantize", "cache_decode_attention", "qjl_sign_matrix", "qjl_project",
-    "qjl_cache_sketch", "qjl_logit_bias",
+    "qjl_cache_sketch", "qjl_logit_bias", "cache_prefill_attention",
 ]
 
 _DT = {torch.float32: TQ_DTYPE_F32, torch.bfloat16: TQ_DTYPE_BF16, torch.float16: TQ_DTYPE_F16}
@@ -185,6 +185,21 @@ def cache_decode_attention(q, k_idx, k_sc, v_idx, v_sc, kv_lens, num_kv_heads, b
                                         num_kv_heads, hd, bits, int(outlier_blocks), TQ_NORM_MAXNORM, max_kv_len,
                                         kv_head_stride, seq_stride, float(softmax_scale), _ptr(out), _DT[out.dtype],
                                         _ptr(workspace.buf), workspace.nbytes, _stream()))
+    return out
+
+
+def cache_prefill_attention(q, k_idx, k_sc, v_idx, v_sc, num_kv_heads, bits, kv_len, kv_head_stride, softmax_scale,
+                            outlier_blocks: int, causal: bool = True, rq=None, qjl_signs=None, qjl_norms=None,
+                            out_dtype: torch.dtype = torch.float32):
+    """Multi-query attention over compressed records: q [H, L, D] -> [H, L, D];
+    query i at position kv_len - L + i (causal: sees tokens up to it)."""
+    h, ql, hd = q.shape
+    out = torch.empty((h, ql, hd), dtype=out_dtype, device=q.device)
+    check(lib.tq_cache_prefill_attention(_ptr(q), _DT[q.dtype], _ptr(k_idx), _ptr(k_sc), _ptr(v_idx), _ptr(v_sc),
+                                         _ptr(rq), _ptr(qjl_signs), _ptr(qjl_norms), h, ql, num_kv_heads, hd, bits,
+                                         int(outlier_blocks), TQ_NORM_MAXNORM, kv_len, kv_head_stride,
+                                         1 if causal else 0, float(softmax_scale), _ptr(out), _DT[out.dtype],
+                                         _stream()))
     return out
 
 

@@ -154,6 +154,18 @@ class _DeviceCache:
         check(lib.tq_cache_buffers(self._h, layer, *[C.byref(p) for p in ptrs]))
         return [p.value for p in ptrs]
 
+    def attend_prefill(self, layer: int, q: torch.Tensor, softmax_scale: float, causal: bool = True,
+                       out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """Multi-query attention of q [1, Hq, q_len, D] over the whole layer (the
+        queries at its last q_len positions) straight from the compressed
+        records; a TqCache includes the QJL correction.  Returns [1, Hq, q_len, D]."""
+        qc = _check_q(q, self.num_kv_heads, self.head_dim)
+        hq, ql = qc.shape[1], qc.shape[2]
+        out = torch.empty((1, hq, ql, self.head_dim), dtype=out_dtype or qc.dtype, device=qc.device)
+        check(lib.tq_cache_attend_prefill(self._h, layer, qc.data_ptr(), _DT[qc.dtype], hq, ql, 1 if causal else 0,
+                                          float(softmax_scale), out.data_ptr(), _DT[out.dtype], _stream()))
+        return out
+
     def _prefill(self, layer, k, v, q):
         k, v = _check_kv(k, v, self.num_kv_heads, self.head_dim)
         t = k.shape[2]

@@ -262,6 +262,22 @@ class KvCache {
                                  (int)L.cap, (long long)L.cap, 0, scale, out, out_dtype, ws_, ws_bytes_, stream);
   }
 
+  // multi-query attention of q [num_q_heads][q_len][head_dim] over the whole
+  // layer, the queries at its last q_len positions
+  int attend_prefill(int l, const void *q, int q_dtype, int num_q_heads, int q_len, int causal, float scale, void *out,
+                     int out_dtype, hipStream_t stream) {
+    const LayerBuffers &L = storage_.layer(l);
+    if (mode_.qjl) {
+      int rc = project(q, q_dtype, (size_t)num_q_heads * q_len, stream);
+      if (rc) return rc;
+    }
+    return tq_cache_prefill_attention(q, q_dtype, L.k_idx, L.k_sc, L.v_idx, L.v_sc,
+                                      mode_.qjl ? static_cast<const float *>(rq_) : nullptr,
+                                      mode_.qjl ? L.signs : nullptr, mode_.qjl ? L.norms : nullptr, num_q_heads, q_len,
+                                      heads_, head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode,
+                                      (int)L.seq, (long long)L.cap, causal, scale, out, out_dtype, stream);
+  }
+
  private:
   // build_rademacher_matrix (precomputed/mod.rs:116-125) as sign bits, once
   int sign_matrix(hipStream_t stream) {
@@ -414,6 +430,17 @@ extern "C" int tq_cache_decode_dequantized(void *cache, int layer, const void *k
   if (rc) return rc;
   if (tq) return c->logit_bias(layer, q, q_dtype, num_q_heads, q_len, logit_bias_out, stream);
   return TQ_OK;
+}
+
+extern "C" int tq_cache_attend_prefill(void *cache, int layer, const void *q, int q_dtype, int num_q_heads, int q_len,
+                                       int causal, float softmax_scale, void *out, int out_dtype, hipStream_t stream) {
+  KvCache *c = as_cache(cache);
+  int rc = check_layer(c, layer);
+  if (rc) return rc;
+  rc = check_q(c, q, q_dtype, num_q_heads);
+  if (rc) return rc;
+  if (!out || !tqh::valid_dtype(out_dtype) || q_len < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid arguments");
+  return c->attend_prefill(layer, q, q_dtype, num_q_heads, q_len, causal, softmax_scale, out, out_dtype, stream);
 }
 
 extern "C" size_t tq_cache_seq_len(void *cache, int layer) {

@@ -1,0 +1,481 @@
+// tq_prefill.hip -- multi-query (prefill) attention straight over the
+// compressed cache, on the matrix cores.
+//
+// The reference hands prefill attention back to the caller as dequantized
+// K/V (pqo.rs:184-200, tq.rs:258-273; SDPA runs in mistral.rs).  This kernel
+// computes it without materializing K/V: out[h][i] = softmax_t(scale *
+// (q_hi . k_t + corr_hit)) v_t over the tokens t a query may see (all, or
+// t <= kv_len - q_len + i when causal), corr the QJL correction of a TQ
+// cache (tq.rs:185-253).
+//
+// One workgroup (4 waves) serves 64 rows = (query, head) pairs of one KV
+// head, query-major, so the NR query heads of a KV head share every decoded
+// tile.  Per 64-token tile the workgroup decodes K (token-major, per-token
+// exponent folded out) and V (element-major) into LDS as two-part f16
+// values (hi = 11 significant bits, lo = the remainder), then each wave
+// (16 rows) runs
+//   S^T = K Q^T          16x16x32 MFMAs, K's hi/lo along k against a
+//                        duplicated query value, query hi and lo as two
+//                        operands (22-bit products, f32 accumulation)
+//   corr^T = Sg RQ^T     TQ: the keys' +-1 sign bits against rq hi/lo
+//   O^T += V^T P^T       16x16x16 MFMAs whose B operand is exactly S^T's
+//                        accumulator layout (4 tokens per lane), V hi/lo x
+//                        P hi/lo (three products, lo x lo dropped)
+// with an online base-2 softmax per row.  Values stay in the rotated
+// domain; each row is inverse-rotated once at the end.  The next tile's
+// records are fetched while the current one is computed.
+#include "tq_common.h"
+#include "tq_device.h"
+#include "tq_mfma.h"
+
+namespace {
+
+using namespace tqd;
+using namespace tqm;
+
+constexpr int kPThreads = 256;
+constexpr int kRows = 64;   // (query, head) rows per workgroup
+constexpr int kTile = 64;   // tokens per tile
+constexpr int kKStride = 66;  // uint2 per token row of the K tile (64 pairs + pad)
+constexpr int kVStride = 68;  // halves per element row of the V tiles (64 tokens + pad)
+
+enum PMode : int { kPPqo = 0, kPPq = 1, kPTq = 2 };
+
+struct PrefillArgs {
+  const void *q;
+  int q_dtype;
+  const uint8_t *k_idx;
+  const uint16_t *k_sc;
+  const uint8_t *v_idx;
+  const uint16_t *v_sc;
+  const float *rq;           // TQ: [H][q_len][128] = R q
+  const uint32_t *signs;     // TQ: [record][4] sign words
+  const uint16_t *norms;     // TQ: [record] f16 residual norms
+  int num_heads, num_kv_heads, q_len, kv_len;
+  long long kv_head_stride;  // records between KV heads
+  int causal;
+  float softmax_scale;
+  float qjl_c;               // f32(sqrt(pi/2)) / sqrt(head_dim)
+  void *out;
+  int out_dtype;
+  int cb_args;               // codebook from cb (L2Norm) instead of the MaxNorm constants
+  float cb[16];
+};
+
+__device__ __forceinline__ f32x4 mfma16(u32x2 a, u32x2 b, f32x4 d) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, a), __builtin_bit_cast(half4, b), d, 0, 0,
+                                               0);
+}
+
+template <int BITS, int MODE, int NR>
+__global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
+  constexpr int CB = MODE == kPPqo ? BITS : BITS - 1;
+  constexpr bool QJL = MODE == kPTq;
+  constexpr int HD = 128, QW = BITS, PACKED = 16 * QW;
+  constexpr int QB = kRows / NR;  // queries per workgroup
+  // LDS: K tile | V tiles (hi, lo) | per-token and per-row scalars
+  constexpr int K_WORDS = kTile * kKStride * 2;
+  constexpr int V_HALVES = HD * kVStride;
+  constexpr int V_WORDS = V_HALVES;  // hi and lo planes, 2 halves per word each
+  __shared__ __attribute__((aligned(16))) uint32_t s_k[K_WORDS];
+  __shared__ __attribute__((aligned(16))) uint32_t s_v[V_WORDS];
+  __shared__ float s_ek[kTile];       // 2^E_k per token (key exponent folded out)
+  __shared__ int s_ev[kTile];         // V exponent per token
+  __shared__ float s_cn[kTile];       // TQ: |r_t| * qjl_c
+  __shared__ __attribute__((aligned(16))) uint32_t s_sg[kTile * 4];  // TQ: sign words
+  __shared__ float s_cb[16];
+  __shared__ int s_eq[kRows], s_er[kRows];
+  __shared__ uint2 s_nib[16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int g = blockIdx.y;
+  const int i0 = blockIdx.x * QB;
+  const long long rec0 = (long long)g * a.kv_head_stride;
+  const float lscale = a.softmax_scale * kLog2e;
+
+  if (tid < 16) {
+    constexpr int CM = (1 << CB) - 1;
+    float c = a.cb[0];
+    if (a.cb_args) {
+#pragma unroll
+      for (int kk = 1; kk <= CM; kk++) c = (tid == kk) ? a.cb[kk] : c;
+    } else {
+      c = pqo_centroid<CB>(tid & CM);
+    }
+    s_cb[tid] = c;
+    auto pm1 = [&](int bit) { return ((tid >> bit) & 1) ? 0x3C00u : 0xBC00u; };
+    s_nib[tid] = make_uint2(pm1(0) | (pm1(1) << 16), pm1(2) | (pm1(3) << 16));
+  }
+
+  // ---- query rows: thread (row, quarter) rotates one 32-element block ----
+  // (the V tile region holds the split query until the operands are built)
+  const int prow = tid >> 2, pq = tid & 3;
+  const int qi = i0 + prow / NR, qh = g * NR + prow % NR;
+  const bool row_ok = qi < a.q_len;
+  _Float16 *s_qh = reinterpret_cast<_Float16 *>(s_v);  // [row][128] hi
+  _Float16 *s_ql = s_qh + kRows * HD;                 // [row][128] lo
+  {
+    float x[32];
+    const long long base = ((long long)qh * a.q_len + (row_ok ? qi : 0)) * HD + 32 * pq;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      if (a.q_dtype == kF32) x[j] = static_cast<const float *>(a.q)[base + j];
+      else if (a.q_dtype == kBF16) x[j] = bf16_to_f32(static_cast<const uint16_t *>(a.q)[base + j]);
+      else x[j] = f16_to_f32(static_cast<const uint16_t *>(a.q)[base + j]);
+    }
+    butterfly<32>(x);
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      x[j] = x[j] * (decode_sign(j) * (kInvSqrt32 * lscale));
+      m = fmaxf(m, fabsf(x[j]));
+    }
+    m = fmaxf(m, dpp_quad_xor1(m));
+    m = fmaxf(m, dpp_quad_xor2(m));
+    const int eq = pow2_exponent(m);
+    const float sc = exp2i(-eq);
+    if (pq == 0) s_eq[prow] = eq;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      const float v = row_ok ? x[j] * sc : 0.f;
+      const float h = split_hi(v);
+      s_qh[prow * HD + 32 * pq + j] = (_Float16)h;
+      s_ql[prow * HD + 32 * pq + j] = (_Float16)(v - h);
+    }
+  }
+  // TQ: rq rows the same way (no rotation), into the K tile region
+  _Float16 *s_rh = reinterpret_cast<_Float16 *>(s_k);
+  _Float16 *s_rl = s_rh + kRows * HD;
+  if constexpr (QJL) {
+    float x[32];
+    const long long base = ((long long)qh * a.q_len + (row_ok ? qi : 0)) * HD + 32 * pq;
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      x[j] = a.rq[base + j] * lscale;
+      m = fmaxf(m, fabsf(x[j]));
+    }
+    m = fmaxf(m, dpp_quad_xor1(m));
+    m = fmaxf(m, dpp_quad_xor2(m));
+    const int er = pow2_exponent(m);
+    const float sc = exp2i(-er);
+    if (pq == 0) s_er[prow] = er;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      const float v = row_ok ? x[j] * sc : 0.f;
+      const float h = split_hi(v);
+      s_rh[prow * HD + 32 * pq + j] = (_Float16)h;
+      s_rl[prow * HD + 32 * pq + j] = (_Float16)(v - h);
+    }
+  }
+  __syncthreads();
+
+  // ---- per-wave operands for its 16 rows (lane column = row 16 wave + l16) ----
+  const int myrow = 16 * wave + l16;
+  u32x4 qop[8][2];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int e = myrow * HD + 16 * j + 4 * lg;
+    const uint2 h = *reinterpret_cast<const uint2 *>(s_qh + e);
+    const uint2 l = *reinterpret_cast<const uint2 *>(s_ql + e);
+    qop[j][0] = u32x4{h.x, h.x, h.y, h.y};
+    qop[j][1] = u32x4{l.x, l.x, l.y, l.y};
+  }
+  u32x4 rop[4][2];
+  if constexpr (QJL) {
+#pragma unroll
+    for (int sl = 0; sl < 4; sl++) {
+      const int e = myrow * HD + 32 * sl + 8 * lg;
+      const uint4 h = *reinterpret_cast<const uint4 *>(s_rh + e);
+      const uint4 l = *reinterpret_cast<const uint4 *>(s_rl + e);
+      rop[sl][0] = u32x4{h.x, h.y, h.z, h.w};
+      rop[sl][1] = u32x4{l.x, l.y, l.z, l.w};
+    }
+  }
+  const int my_qi = i0 + myrow / NR;
+  const bool my_ok = my_qi < a.q_len;
+  const float eq_scale = exp2i(s_eq[myrow]);
+  const float er_scale = QJL ? exp2i(s_er[myrow]) : 0.f;
+  const int qpos = a.kv_len - a.q_len + my_qi;  // causal limit of this row
+  __syncthreads();  // operands built: the tiles may overwrite the query staging
+
+  // ---- tiles ----
+  const int last_q = min(a.q_len - 1, i0 + QB - 1);
+  const int kv_end = a.causal ? min(a.kv_len, a.kv_len - a.q_len + last_q + 1) : a.kv_len;
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+
+  // thread (token, qblock) fetches one record of K and V per tile
+  const int ftok = tid >> 2, fqb = tid & 3;
+  uint32_t kw[QW], vw[QW], sgw = 0;
+  uint16_t ks = 0, vs = 0, nm = 0;
+  auto fetch = [&](int t0) {
+    const int t = min(t0 + ftok, a.kv_len - 1);
+    const long long rec = rec0 + t;
+#pragma unroll
+    for (int w = 0; w < QW; w++) {
+      kw[w] = reinterpret_cast<const uint32_t *>(a.k_idx + rec * PACKED + fqb * 4 * QW)[w];
+      vw[w] = reinterpret_cast<const uint32_t *>(a.v_idx + rec * PACKED + fqb * 4 * QW)[w];
+    }
+    ks = a.k_sc[rec * 4 + fqb];
+    vs = a.v_sc[rec * 4 + fqb];
+    if constexpr (QJL) {
+      sgw = a.signs[rec * 4 + fqb];
+      nm = a.norms[rec];
+    }
+  };
+  if (ntiles > 0) fetch(0);
+
+  float m_run = -INFINITY, l_run = 0.f;
+  int ev_cur = -1000;
+  f32x4 o[8];
+#pragma unroll
+  for (int eb = 0; eb < 8; eb++) o[eb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint2 *kt = reinterpret_cast<uint2 *>(s_k);
+  _Float16 *vth = reinterpret_cast<_Float16 *>(s_v);
+  _Float16 *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
+  static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
+  static_assert(2 * kRows * HD <= 2 * V_WORDS, "the split query fits the V region");
+  static_assert(2 * kRows * HD <= 2 * K_WORDS && kRows * HD <= K_WORDS, "rq and the output fit the K region");
+
+  for (int tile = 0; tile < ntiles; tile++) {
+    const int t0 = tile * kTile;
+    // ---- decode this thread's record into the tiles ----
+    {
+      const float sk = fabsf(f16_to_f32(ks)), sv = fabsf(f16_to_f32(vs));
+      float mk = fmaxf(sk, dpp_quad_xor1(sk));
+      mk = fmaxf(mk, dpp_quad_xor2(mk));
+      float mv = fmaxf(sv, dpp_quad_xor1(sv));
+      mv = fmaxf(mv, dpp_quad_xor2(mv));
+      const int ek = pow2_exponent(mk), ev = pow2_exponent(mv);
+      const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
+      if (fqb == 0) {
+        s_ek[ftok] = exp2i(ek);
+        s_ev[ftok] = ev;
+        if constexpr (QJL) s_cn[ftok] = f16_to_f32(nm) * a.qjl_c;
+      }
+      if constexpr (QJL) s_sg[ftok * 4 + fqb] = sgw;
+#pragma unroll
+      for (int p = 0; p < 16; p++) {
+        const uint32_t code = pair_code<BITS>(kw, p);
+        const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * kf;
+        const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * kf;
+        const float h0 = split_hi(x0), h1 = split_hi(x1);
+        kt[ftok * kKStride + 16 * fqb + p] = make_uint2(pack_f16(h0, h1), pack_f16(x0 - h0, x1 - h1));
+      }
+#pragma unroll
+      for (int p = 0; p < 16; p++) {
+        const uint32_t code = pair_code<BITS>(vw, p);
+        const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * vf;
+        const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * vf;
+        const float h0 = split_hi(x0), h1 = split_hi(x1);
+        const int e = 32 * fqb + 2 * p;
+        vth[e * kVStride + ftok] = (_Float16)h0;
+        vth[(e + 1) * kVStride + ftok] = (_Float16)h1;
+        vtl[e * kVStride + ftok] = (_Float16)(x0 - h0);
+        vtl[(e + 1) * kVStride + ftok] = (_Float16)(x1 - h1);
+      }
+    }
+    __syncthreads();
+    if (tile + 1 < ntiles) fetch(t0 + kTile);  // next tile's records arrive during the compute
+
+    // ---- S^T = K Q^T (+ corr), four 16-token blocks ----
+    float x[4][4];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) {
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint2 *krow = kt + (16 * tb + l16) * kKStride;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint4 kk = *reinterpret_cast<const uint4 *>(krow + 8 * j + 2 * lg);
+        const u32x4 ka = {kk.x, kk.y, kk.z, kk.w};
+        d = mfma(ka, qop[j][0], d);
+        d = mfma(ka, qop[j][1], d);
+      }
+      f32x4 dc = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (QJL) {
+        const uint32_t *sgrow = s_sg + (16 * tb + l16) * 4;
+#pragma unroll
+        for (int sl = 0; sl < 4; sl++) {
+          const uint32_t byte = (sgrow[sl] >> (8 * lg)) & 0xffu;
+          const uint2 n0 = s_nib[byte & 15u], n1 = s_nib[byte >> 4];
+          const u32x4 sa = {n0.x, n0.y, n1.x, n1.y};
+          dc = mfma(sa, rop[sl][0], dc);
+          dc = mfma(sa, rop[sl][1], dc);
+        }
+      }
+      const float4 ekv = *reinterpret_cast<const float4 *>(s_ek + 16 * tb + 4 * lg);
+      const float ek4[4] = {ekv.x, ekv.y, ekv.z, ekv.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int tp = t0 + 16 * tb + 4 * lg + i;
+        float v = d[i] * (ek4[i] * eq_scale);
+        if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[16 * tb + 4 * lg + i] * er_scale, v);
+        const bool ok = my_ok && tp < a.kv_len && (!a.causal || tp <= qpos);
+        x[tb][i] = ok ? v : -INFINITY;
+      }
+    }
+    // ---- online softmax of this row (its 64 logits sit in the 4 lanes l16 + 16 k) ----
+    float mt = -INFINITY;
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) mt = fmaxf(mt, x[tb][i]);
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    // V exponent of the tile (each wave reads all 64)
+    int evt = s_ev[lane];
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1) evt = max(evt, __shfl_xor(evt, o2, 64));
+    const int ev_new = max(ev_cur, evt);
+    const float rescale = alpha * exp2i(max(ev_cur - ev_new, -126));
+    ev_cur = ev_new;
+    m_run = m_new;
+    float ls = 0.f;
+    u32x2 pb[4][2];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float e = (x[tb][i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[tb][i] - m_new);
+        ls += e;
+        p[i] = e * exp2i(max(s_ev[16 * tb + 4 * lg + i] - ev_new, -126));
+      }
+      float ph[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) ph[i] = split_hi(p[i]);
+      pb[tb][0] = u32x2{pack_f16(ph[0], ph[1]), pack_f16(ph[2], ph[3])};
+      pb[tb][1] = u32x2{pack_f16(p[0] - ph[0], p[1] - ph[1]), pack_f16(p[2] - ph[2], p[3] - ph[3])};
+    }
+    l_run = l_run * alpha + ls;
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int eb = 0; eb < 8; eb++) {
+      f32x4 acc = o[eb] * rescale;
+      const int e = 16 * eb + l16;
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) {
+        const uint2 vh = *reinterpret_cast<const uint2 *>(vth + e * kVStride + 16 * tb + 4 * lg);
+        const uint2 vl = *reinterpret_cast<const uint2 *>(vtl + e * kVStride + 16 * tb + 4 * lg);
+        const u32x2 ah = {vh.x, vh.y}, al = {vl.x, vl.y};
+        acc = mfma16(ah, pb[tb][0], acc);
+        acc = mfma16(ah, pb[tb][1], acc);
+        acc = mfma16(al, pb[tb][0], acc);
+      }
+      o[eb] = acc;
+    }
+    __syncthreads();  // the next decode overwrites the tiles
+  }
+
+  // ---- finish: row sums, inverse rotation per 32-element block, store ----
+  float L = l_run;
+  L += __shfl_xor(L, 16, 64);
+  L += __shfl_xor(L, 32, 64);
+  float *s_o = reinterpret_cast<float *>(s_k);  // [row][128] (rotated, in units of 2^ev_cur)
+  const float ofac = exp2i(max(min(ev_cur, 126), -126));
+#pragma unroll
+  for (int eb = 0; eb < 8; eb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) s_o[myrow * HD + 16 * eb + 4 * lg + i] = o[eb][i] * ofac;
+  float *s_rowl = s_ek;  // [rows] (the tiles are done)
+  if (lg == 0) s_rowl[myrow] = L;
+  __syncthreads();
+  {
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) v[j] = s_o[prow * HD + 32 * pq + j] * decode_sign(j);
+    butterfly<32>(v);
+    const float Lr = s_rowl[prow];
+    if (row_ok) {
+      const long long ob = ((long long)qh * a.q_len + qi) * HD + 32 * pq;
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const float res = Lr > 0.f ? v[j] * kInvSqrt32 / Lr : 0.f;
+        if (a.out_dtype == kF32) static_cast<float *>(a.out)[ob + j] = res;
+        else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[ob + j] = f32_to_bf16(res);
+        else static_cast<uint16_t *>(a.out)[ob + j] = f32_to_f16(res);
+      }
+    }
+  }
+}
+
+template <int BITS, int MODE>
+int launch_prefill_m(const PrefillArgs &a, int nr, hipStream_t st) {
+  const int qb = kRows / nr;
+  const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
+  if (nr == 1) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1>), grid, dim3(kPThreads), 0, st, a);
+  else if (nr == 2) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 2>), grid, dim3(kPThreads), 0, st, a);
+  else hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 4>), grid, dim3(kPThreads), 0, st, a);
+  return tqh::check_launch("prefill_attn_kernel");
+}
+
+}  // namespace
+
+extern "C" int tq_cache_prefill_attention(const void *q, int q_dtype, const uint8_t *k_indices,
+                                          const uint16_t *k_scales, const uint8_t *v_indices,
+                                          const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                                          const uint16_t *qjl_norms, int num_heads, int q_len, int num_kv_heads,
+                                          int head_dim, int bits, size_t outlier_blocks, int norm_mode, int kv_len,
+                                          long long kv_head_stride, int causal, float softmax_scale, void *out,
+                                          int out_dtype, hipStream_t stream) {
+  if (head_dim != 128)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "prefill attention supports head_dim 128, got %d", head_dim);
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_heads (%d) must be a multiple of num_kv_heads (%d)", num_heads,
+                     num_kv_heads);
+  const int nr = num_heads / num_kv_heads;
+  if (nr != 1 && nr != 2 && nr != 4) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "GQA ratio %d not supported", nr);
+  tqh::PolarCodec codec;
+  int rc = tqh::polar_codec(bits, norm_mode, outlier_blocks, head_dim / 32, codec);
+  if (rc) return rc;
+  if (codec.mixed)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "prefill attention takes outlier_blocks 0 or all");
+  const bool qjl = qjl_signs != nullptr;
+  if (qjl && (codec.outlier || !rq || !qjl_norms))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL correction needs outlier_blocks 0, rq, signs and norms");
+  if (!tqh::valid_dtype(q_dtype) || !tqh::valid_dtype(out_dtype))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (q_len < 0 || kv_len < 0 || kv_head_stride < kv_len) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "bad shape");
+  if (causal && q_len > kv_len)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "causal prefill needs q_len (%d) <= kv_len (%d)", q_len, kv_len);
+  if (q_len == 0) return TQ_OK;
+  if (!q || !out || (kv_len > 0 && (!k_indices || !k_scales || !v_indices || !v_scales)))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+  PrefillArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.k_idx = k_indices;
+  a.k_sc = k_scales;
+  a.v_idx = v_indices;
+  a.v_sc = v_scales;
+  a.rq = rq;
+  a.signs = reinterpret_cast<const uint32_t *>(qjl_signs);
+  a.norms = qjl_norms;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.q_len = q_len;
+  a.kv_len = kv_len;
+  a.kv_head_stride = kv_head_stride;
+  a.causal = causal ? 1 : 0;
+  a.softmax_scale = softmax_scale;
+  a.qjl_c = tq_qjl_bias_scale(head_dim);
+  a.out = out;
+  a.out_dtype = out_dtype;
+  if (norm_mode == TQ_NORM_L2NORM) {
+    a.cb_args = 1;
+    for (int i = 0; i < codec.cb.nc; i++) a.cb[i] = codec.cb.c[i];
+  }
+  const int mode = codec.outlier ? kPPqo : (qjl ? kPTq : kPPq);
+  if (bits == 3) {
+    if (mode == kPPqo) return launch_prefill_m<3, kPPqo>(a, nr, stream);
+    if (mode == kPPq) return launch_prefill_m<3, kPPq>(a, nr, stream);
+    return launch_prefill_m<3, kPTq>(a, nr, stream);
+  }
+  if (mode == kPPqo) return launch_prefill_m<4, kPPqo>(a, nr, stream);
+  if (mode == kPPq) return launch_prefill_m<4, kPPq>(a, nr, stream);
+  return launch_prefill_m<4, kPTq>(a, nr, stream);
+}
