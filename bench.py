@@ -240,6 +240,38 @@ def bench_tq_c3(torch, tq, args):
             "ms_per_step_with_query_projection": round(ms_proj, 6), "copies": copies}
 
 
+def bench_prefill(torch, tq, args):
+    """Causal prefill attention straight over a PQO3 cache: 16 q-heads / 8 KV
+    heads, d=128, 4096 queries over the 4096 tokens they were appended as (the
+    C2 model shape, one layer).  Useful work = 2 products x 2 flops x H x
+    (sum over queries of visible tokens) x 128."""
+    import numpy as np
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    h, hkv, hd, t, bits = 16, 8, 128, 4096, 3
+    x = torch.randn((2, hkv * t, hd), generator=gen, device="cuda")
+    x[:, :, torch.tensor([3, 40, 77, 101], device="cuda")] *= 8.0
+    pk, sk = tq.pqo_quantize(x[0].to(torch.bfloat16), bits)
+    pv, sv = tq.pqo_quantize(x[1].to(torch.bfloat16), bits)
+    q = (torch.randn((h, t, hd), generator=gen, device="cuda") / math.sqrt(hd)).to(torch.bfloat16)
+    out = torch.empty((h, t, hd), dtype=torch.bfloat16, device="cuda")
+    scale = 1.0 / math.sqrt(hd)
+
+    def step(i):
+        tq.check(tq.lib.tq_cache_prefill_attention(q.data_ptr(), 1, pk.data_ptr(), sk.data_ptr(), pv.data_ptr(),
+                                                   sv.data_ptr(), None, None, None, h, t, hkv, hd, bits,
+                                                   (1 << 64) - 1, 0, t, t, 1, scale, out.data_ptr(), 1,
+                                                   torch.cuda.current_stream().cuda_stream))
+
+    ms, _ = time_steps(torch, step, max(5, args.steps // 20), 2)
+    flops = 4.0 * h * hd * (t * (t + 1) / 2)
+    tflops = flops / (ms * 1e-3) / 1e12
+    del x, pk, sk, pv, sv, q, out
+    return {"metric": "causal prefill attention over a PQO3 cache (16/8 heads, d=128, 4096 x 4096)",
+            "ms_per_step": round(ms, 4), "useful_tflops": round(tflops, 1),
+            "roofline": {"bound": "mfma", "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
+                         "note": "f16 dense peak; every product runs as hi/lo parts (3-4 MFMAs per useful one)"}}
+
+
 def bench_c1(torch, tq, args):
     """Config 1 on the GPU: 10,000 N(0,1) vectors (seed 42), d=128, TQ3 with
     rotation seed 42: quantize_vec + dequantize_vec per step; nMSE of the
@@ -365,6 +397,7 @@ def main():
     del x, packed, scales
     c4 = bench_c4(torch, tq, args)
     tq_c3 = bench_tq_c3(torch, tq, args)
+    pf = bench_prefill(torch, tq, args)
     c1 = bench_c1(torch, tq, args)
     c5 = bench_c5(torch, tq, args)
 
@@ -407,6 +440,7 @@ def main():
                      "cpu_baseline": qcpu},
         "c4_batched_decode": c4,
         "tq_decode_c3": tq_c3,
+        "prefill_attention": pf,
         "c1_codec": c1,
         "c5_qjl": c5,
         "wall_s_timed": round(wall, 4),
