@@ -327,8 +327,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   // groups: group k issues only once the records of group k - 1 have
   // arrived, so device-wide the early groups' bytes come back first and their
   // passes overlap the later transfers.  Group 0 is the highest waves (the
-  // query waves above fetch last).  Codes: tile tt of this wave, lane
-  // (l16, lg) holds qblock lg of token 16 tt + l16; scales: lane = token, all
+  // query waves above fetch last).  Codes, tile tt of this wave: for the
+  // keys lane (l16, lg) holds qblock lg of token 16 tt + l16, for the values
+  // qblock l16 % 4 of token 16 tt + 4 lg + l16 / 4 (one contiguous run of
+  // four records per 16 lanes); scales: lane = token, all
   // four qblock scales in one load.  Addresses are a per-(b, g) base plus a
   // 32-bit offset inside the head. ----
   constexpr int GW = kWaves / kLoadGroups;  // waves per load group
@@ -344,10 +346,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   auto issue_loads = [&](bool real) {
     const int tw = t0 + wave * WT;
     const uint32_t soff = (uint32_t)(real ? min(tw + lane, len - 1) : t0) * (NQB * 2);
-    uint32_t off[NT];
+    uint32_t off[NT], voff[NT];
 #pragma unroll
-    for (int tt = 0; tt < NT; tt++)
+    for (int tt = 0; tt < NT; tt++) {
       off[tt] = (uint32_t)(real ? min(tw + 16 * tt + l16, len - 1) : t0) * PACKED + lg * (QW * 4);
+      voff[tt] = (uint32_t)(real ? min(tw + 16 * tt + 4 * lg + (l16 >> 2), len - 1) : t0) * PACKED + (l16 & 3) * (QW * 4);
+    }
 #pragma unroll
     for (int tt = 0; tt < NT; tt++)
 #pragma unroll
@@ -363,7 +367,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int tt = 0; tt < NT; tt++)
 #pragma unroll
-      for (int w = 0; w < QW; w++) vq[tt][w] = *reinterpret_cast<const uint32_t *>(vbase + off[tt] + 4 * w);
+      for (int w = 0; w < QW; w++) vq[tt][w] = *reinterpret_cast<const uint32_t *>(vbase + voff[tt] + 4 * w);
     vsc = *reinterpret_cast<const uint2 *>(vsbase + soff);
   };
   // Every wave issues the same load sequence here (later groups fetch the
@@ -568,59 +572,69 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- V pass.  Weight operands, one per 16-token tile: lane (n, kg) holds
-  // for column n = (qblock bq, head 2 gi + brl, part) the weights of tokens
-  // 4 kg + (0, 1, 0, 1, 2, 3, 2, 3) of the tile (each twice: against the hi
-  // and the lo part of the value) ----
+  // ---- V pass.  Weight operands, one per pair of 16-token tiles: lane
+  // (n, kg) holds for column n = (qblock bq, head 2 gi + brl, part) the
+  // weights of tokens 4 kg .. 4 kg + 3 of tile 2 tp and of tile 2 tp + 1 ----
+  static_assert(NT % 2 == 0, "tiles pair up along the value contraction");
   const int bq = l16 >> 2, brl = (l16 >> 1) & 1, bpart = l16 & 1;
-  u32x4 bw[NT][NG];
+  u32x4 bw[NT / 2][NG];
 #pragma unroll
-  for (int tt = 0; tt < NT; tt++) {
+  for (int tp = 0; tp < NT / 2; tp++) {
 #pragma unroll
     for (int gi = 0; gi < NG; gi++) {
       const int r = min(2 * gi + brl, NR - 1);  // NR == 1: the second head's columns are never read
-      const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * tt + 4 * lg);
-      const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * tt + 4 * lg);
-      const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
-      const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
-      const uint32_t w01 = bpart ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
-      const uint32_t w23 = bpart ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
-      bw[tt][gi] = u32x4{w01, w01, w23, w23};
+      uint32_t w[4];
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int tt = 2 * tp + u;
+        const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * tt + 4 * lg);
+        const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * tt + 4 * lg);
+        const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
+        const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
+        w[2 * u] = bpart ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
+        w[2 * u + 1] = bpart ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
+      }
+      bw[tp][gi] = u32x4{w[0], w[1], w[2], w[3]};
     }
   }
-  // The value codes are decoded where they were loaded (lane (t, q): qblock
-  // q of token t), two pair-table reads per 4-element slice j as for the
-  // keys, and turned to element-major order on the matrix core: V_hi x I
-  // and V_lo x I (16 x 16 x 16, exact) leave lane (n, g) with element
-  // (qblock n / 4, 4 j + n % 4) of tokens 4 g .. 4 g + 3, which is the value
-  // operand's row n.  D then holds rows = those elements, columns (qblock,
-  // head, part); a lane's rows count only under its own qblock's columns.
-  const int idk = l16 - 4 * lg;  // the identity's single 1 in this lane, if 0 <= idk < 4
-  const uint32_t one = 0x3C00u << (16 * (idk & 1));
-  const u32x2 ident = {(idk == 0 || idk == 1) ? one : 0u, (idk == 2 || idk == 3) ? one : 0u};
+  // The value codes are decoded by the same pair-table lookup as the keys,
+  // read through the transposing LDS read: lane l of a 16-lane group holds
+  // qblock l % 4 of token 4 g + l / 4 (g = lane group), so lane 4 a + b
+  // receives part b (hi c0, hi c1, lo c0, lo c1) of the entries of qblock a
+  // for tokens 4 g .. 4 g + 3 -- the value operand's row (a, b) at those
+  // tokens, two tiles per 16 x 16 x 32 product.  D then holds rows =
+  // (qblock, value part), columns (qblock, head, weight part); a lane's rows
+  // count only under its own qblock's columns, and hi + lo of a value sum
+  // inside the lane (rows 4 g + i and 4 g + i + 2).
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    f32x4 dv[NG];
+    f32x4 dv[2][NG];
 #pragma unroll
-    for (int gi = 0; gi < NG; gi++) dv[gi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-    for (int tt = 0; tt < NT; tt++) {
-      const uint2 e0 = s_pair_l[pair_code<BITS>(vq[tt], 2 * j) * PREP];
-      const uint2 e1 = s_pair_l[pair_code<BITS>(vq[tt], 2 * j + 1) * PREP];
-      const f32x4 th = mfma_t(u32x2{e0.x, e1.x}, ident);
-      const f32x4 tl = mfma_t(u32x2{e0.y, e1.y}, ident);
-      const u32x4 va = {pack_f16(th[0], th[1]), pack_f16(tl[0], tl[1]), pack_f16(th[2], th[3]),
-                        pack_f16(tl[2], tl[3])};
+      for (int gi = 0; gi < NG; gi++) dv[h][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int gi = 0; gi < NG; gi++) dv[gi] = mfma(va, bw[tt][gi], dv[gi]);
+    for (int tp = 0; tp < NT / 2; tp++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const u32x2 r0 = lds_read_tr16(s_pair_l + pair_code<BITS>(vq[2 * tp], 2 * j + h) * PREP);
+        const u32x2 r1 = lds_read_tr16(s_pair_l + pair_code<BITS>(vq[2 * tp + 1], 2 * j + h) * PREP);
+        const u32x4 va = {r0[0], r0[1], r1[0], r1[1]};
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) dv[h][gi] = mfma(va, bw[tp][gi], dv[h][gi]);
+      }
     }
-    // lane (n, lg) holds column n at elements (qblock lg, 4 j + i); the parts
-    // of one head sit in lanes n and n ^ 1
+    // lane (n, lg) holds column n at rows (qblock lg, parts hi c0, hi c1,
+    // lo c0, lo c1) of pairs 2 j and 2 j + 1; the weight parts of one head
+    // sit in lanes n and n ^ 1
 #pragma unroll
     for (int gi = 0; gi < NG; gi++) {
       f32x4 o;
 #pragma unroll
-      for (int i = 0; i < 4; i++) o[i] = dpp_quad_xor1(dv[gi][i]) + dv[gi][i];
+      for (int i = 0; i < 4; i++) {
+        const float x = dv[i >> 1][gi][i & 1] + dv[i >> 1][gi][(i & 1) + 2];
+        o[i] = dpp_quad_xor1(x) + x;
+      }
       __builtin_amdgcn_sched_barrier(0);  // the sums stay outside the store's branch (DPP adds)
       const int r = 2 * gi + brl;
       if (bpart == 0 && bq == lg && r < NR) *reinterpret_cast<f32x4 *>(comb + r * HD + 32 * lg + 4 * j) = o;

@@ -112,6 +112,16 @@ __device__ __forceinline__ f32x4 mfma_t(u32x2 a, u32x2 b) {
                                                f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16): inside each group of 16 lanes,
+// lane 4 a + b receives item b (16-bit) of the 8-byte rows addressed by
+// lanes a, a + 4, a + 8 and a + 12 of its group, in that order (item 0 in
+// the low half of the first word).  p must point into LDS.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_read_tr16(const void *p) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)p));
+}
+
 // Upper part of the two-part f16 split: x with its significand cut to 11
 // bits (exact in f16 while |x| is in f16's normal range); x - hi is exact in
 // f32 and is the lower part.
