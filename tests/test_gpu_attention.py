@@ -72,7 +72,10 @@ def _run_decode(tq, q_np, cache, hkv, t, bits, cap, qdtype=torch.float32, out_dt
 
 
 @pytest.mark.parametrize("bits,h,hkv,t", [(3, 16, 8, 1000), (4, 32, 8, 777), (3, 8, 8, 1), (4, 4, 4, 256),
-                                          (3, 16, 8, 257), (4, 32, 8, 5000)])
+                                          (3, 16, 8, 257), (4, 32, 8, 5000),
+                                          (3, 32, 8, 17000),
+                                          # more chunks than the merge's first round (32)
+                                          (4, 8, 8, 33000)])
 def test_decode_matches_dense_oracle(tq, bits, h, hkv, t):
     rng = np.random.default_rng(1000 + t + bits)
     cap = t + 37

@@ -103,82 +103,101 @@ __device__ __forceinline__ float q_value(uint32_t bits, int qt) {
 // ---------------------------------------------------------------------------
 // Split-K merge and final inverse rotation for NR heads of one (b, g):
 //   o = inv * H(sg * sum_c 2^(m_c - M) acc_c) / sum_c 2^(m_c - M) l_c
-// All partial loads of a lane are independent (one latency round).
+// Each lane folds four consecutive elements of every PARTS-th chunk (one
+// 16-byte device-coherent load per chunk) under a local maximum; the PARTS
+// lane sets meet once in LDS.  The first-round loads of a lane are
+// independent (one latency round); longer contexts continue with an online
+// update.
 // ---------------------------------------------------------------------------
-constexpr int kMergeCap = 2048;  // max NR * chunks merged (LDS floats)
-constexpr int kMiscFloats = 2 * kMergeCap + kThreads + 8;
+constexpr int kMiscFloats = 2 * kThreads + 64;
+
+// 16-byte load with the coherence of an agent-scope atomic load (SC1): the
+// partials were written by other workgroups, possibly on other dies.
+__device__ __forceinline__ float4 ld_agent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+}
 
 template <int NR>
 __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, float *lds) {
   constexpr int HD = 128;
   constexpr int OUTS = NR * HD;
-  constexpr int PARTS = kThreads / OUTS;   // lanes sharing one output element
-  constexpr int MAXC = 8;                  // partial values per lane per round
+  constexpr int QUADS = OUTS / 4;          // four consecutive elements per lane
+  constexpr int PARTS = 4;                 // lane sets, each folding every PARTS-th chunk
+  constexpr int MAXC = 8;                  // chunks per lane in the first round
+  static_assert(PARTS * OUTS <= 2 * kThreads && 2 * PARTS * NR <= 64, "merge scratch");
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  float *s_w = lds;                     // [NR][nchunks]: m_c, then weights 2^(m_c - M)
-  float *s_ls = s_w + kMergeCap;        // [NR][nchunks]: l_c
-  float *s_part = s_ls + kMergeCap;     // [kThreads] partial sums
-  float *s_l = s_part + kThreads;       // [NR]
-  const int o = tid % OUTS, part = tid / OUTS;
-  const int r = o / HD, d = o % HD;
-  const long long bh = (long long)b * a.num_heads + g * NR + r;
-  // first round of this lane's partial accumulators, issued together with
-  // the (m, l) loads so the whole merge costs one memory round trip when
-  // nchunks <= MAXC * PARTS
-  float pv[MAXC];
+  float *s_a = lds;                        // [PARTS][OUTS] partial sums
+  float *s_ml = s_a + PARTS * OUTS;        // [PARTS][NR] (local max, local l)
+  const int quad = tid % QUADS, part = tid / QUADS;
+  const int r = quad / (HD / 4), d0 = 4 * (quad % (HD / 4));
+  const long long bh0 = (long long)b * a.num_heads + g * NR;  // first head of this KV head
+  const long long c0 = (bh0 + r) * a.P;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      a.po + bh0 * a.P * HD, (short)0, NR * a.P * HD * (int)sizeof(float), 0x00020000);
+  const bool active = tid < PARTS * QUADS;
+  float4 pv[MAXC];
+  float pm[MAXC], pl[MAXC];
 #pragma unroll
   for (int k = 0; k < MAXC; k++) {
     const int cc = part + k * PARTS;
-    pv[k] = cc < nchunks ? ld_agent(&a.po[(bh * a.P + cc) * HD + d]) : 0.f;
+    const bool ok = active && cc < nchunks;
+    pv[k] = ok ? ld_agent16(rsrc, (uint32_t)(((r * a.P + cc) * HD + d0) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    pm[k] = ok ? ld_agent(&a.pm[c0 + cc]) : -INFINITY;
+    pl[k] = ok ? ld_agent(&a.ps[c0 + cc]) : 0.f;
   }
-  for (int e = tid; e < NR * nchunks; e += kThreads) {
-    const int rr = e / nchunks, cc = e % nchunks;
-    const long long bh2 = (long long)b * a.num_heads + g * NR + rr;
-    s_w[e] = ld_agent(&a.pm[bh2 * a.P + cc]);
-    s_ls[e] = ld_agent(&a.ps[bh2 * a.P + cc]);
-  }
-  __syncthreads();
-  if (wave < NR) {  // wave rr reduces head rr
-    const int rr = wave;
-    float M = -INFINITY;
-    for (int cc = lane; cc < nchunks; cc += 64) M = fmaxf(M, s_w[rr * nchunks + cc]);
-    M = wave_reduce(M, [](float x, float y) { return fmaxf(x, y); });
-    float L = 0.f;
-    for (int cc = lane; cc < nchunks; cc += 64) {
-      const float w = exp2f(s_w[rr * nchunks + cc] - M);
-      s_w[rr * nchunks + cc] = w;
-      L = __builtin_fmaf(s_ls[rr * nchunks + cc], w, L);
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < MAXC; k++) M = fmaxf(M, pm[k]);
+  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+  float L = 0.f;
+  auto fold = [&](const float4 &v, float l, float w) {
+    A.x = __builtin_fmaf(v.x, w, A.x);
+    A.y = __builtin_fmaf(v.y, w, A.y);
+    A.z = __builtin_fmaf(v.z, w, A.z);
+    A.w = __builtin_fmaf(v.w, w, A.w);
+    L = __builtin_fmaf(l, w, L);
+  };
+#pragma unroll
+  for (int k = 0; k < MAXC; k++) fold(pv[k], pl[k], pm[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[k] - M));
+  for (int cc = part + MAXC * PARTS; active && cc < nchunks; cc += PARTS) {  // long contexts only
+    const float m = ld_agent(&a.pm[c0 + cc]), l = ld_agent(&a.ps[c0 + cc]);
+    const float4 v = ld_agent16(rsrc, (uint32_t)(((r * a.P + cc) * HD + d0) * 4));
+    if (m == -INFINITY) continue;
+    if (m > M) {
+      const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - m);
+      A.x *= f;
+      A.y *= f;
+      A.z *= f;
+      A.w *= f;
+      L *= f;
+      M = m;
     }
-    L = wave_reduce(L, [](float x, float y) { return x + y; });
-    if (lane == 0) s_l[rr] = L;
+    fold(v, l, __builtin_amdgcn_exp2f(m - M));
   }
-  __syncthreads();
-  float acc = 0.f;
-#pragma unroll
-  for (int k = 0; k < MAXC; k++) {
-    const int cc = part + k * PARTS;
-    if (cc < nchunks) acc = __builtin_fmaf(pv[k], s_w[r * nchunks + cc], acc);
+  if (active) *reinterpret_cast<float4 *>(s_a + part * OUTS + 4 * quad) = A;
+  if (active && d0 == 0) {
+    s_ml[2 * (part * NR + r)] = M;
+    s_ml[2 * (part * NR + r) + 1] = L;
   }
-  for (int cc = part + MAXC * PARTS; cc < nchunks; cc += PARTS)  // long contexts only
-    acc = __builtin_fmaf(ld_agent(&a.po[(bh * a.P + cc) * HD + d]), s_w[r * nchunks + cc], acc);
-  s_part[tid] = acc;
   __syncthreads();
   if (tid < OUTS) {
-    float A = 0.f;
+    const int ro = tid / HD, d = tid % HD;
+    float Mx = -INFINITY;
 #pragma unroll
-    for (int p = 0; p < PARTS; p++) A += s_part[p * OUTS + tid];
+    for (int p = 0; p < PARTS; p++) Mx = fmaxf(Mx, s_ml[2 * (p * NR + ro)]);
+    float At = 0.f, Lt = 0.f;
+#pragma unroll
+    for (int p = 0; p < PARTS; p++) {
+      const float mp = s_ml[2 * (p * NR + ro)];
+      const float f = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - Mx);
+      At = __builtin_fmaf(s_a[p * OUTS + tid], f, At);
+      Lt = __builtin_fmaf(s_ml[2 * (p * NR + ro) + 1], f, Lt);
+    }
     // inverse rotation over the 32 lanes of this block (lane bits 0..4 = i)
     const int i = d & 31;
-    float v = A * decode_sign(i);
-#pragma unroll
-    for (int hh = 1; hh < 32; hh <<= 1) {
-      float ov = __shfl_xor(v, hh, 64);
-      v = (i & hh) ? (ov - v) : (v + ov);
-    }
-    const float L = s_l[r];
-    const float res = (L > 0.f) ? v * kInvSqrt32 / L : 0.f;
-    const long long oi = bh * HD + d;
+    const float v = wht32_lanes(At * decode_sign(i), i);
+    const float res = (Lt > 0.f) ? v * kInvSqrt32 / Lt : 0.f;
+    const long long oi = (bh0 + ro) * HD + d;
     if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = res;
     else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(res);
     else static_cast<uint16_t *>(a.out)[oi] = f32_to_f16(res);
@@ -304,13 +323,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const float qscale = a.softmax_scale * kLog2e * kInvSqrt32;
   if (tid < NR * HD) {
     const int d = tid % HD;
-    float v = q_value(qbits, a.q_dtype);
     const int i = d & 31;
-#pragma unroll
-    for (int hh = 1; hh < 32; hh <<= 1) {
-      float ov = __shfl_xor(v, hh, 64);
-      v = (i & hh) ? (ov - v) : (v + ov);
-    }
+    const float v = wht32_lanes(q_value(qbits, a.q_dtype), i);
     const float qt = v * (decode_sign(i) * qscale);
     s_q[tid] = qt;
     const float am = wave_max(fabsf(qt));
@@ -852,8 +866,6 @@ int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, 
   const WsLayout w = ws_layout(batch, num_heads, num_kv_heads, head_dim, max_kv_len);
   if (!workspace || workspace_bytes < w.total)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
-  if ((long long)(num_heads / num_kv_heads) * w.P > kMergeCap)
-    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "max_kv_len %d too long for one merge", max_kv_len);
   AttnArgs a = base_args();
   char *ws = static_cast<char *>(workspace);
   a.q = q;
@@ -972,7 +984,6 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
   a.qjl_c = tq_qjl_bias_scale(head_dim);
   const int nr = num_attention_heads / num_kv_heads;
   const int P = (kv_len + kChunk - 1) / kChunk;
-  if ((long long)nr * P > kMergeCap) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_len %d too long for one merge", kv_len);
   rc = launch_decode<false>(a, bits, qjl_enabled ? kModeTq : kModePqo, nr, dim3((unsigned)P, (unsigned)num_kv_heads, 1u),
                             stream);
   if (rc) return rc;

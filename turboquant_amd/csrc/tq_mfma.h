@@ -27,6 +27,36 @@ __device__ __forceinline__ float dpp_quad_xor2(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
 }
 
+// Value of lane l ^ 8 (DPP row_ror:8 inside rows of 16) and of lane l ^ 4 or
+// l ^ 16 inside halves of 32 (ds_swizzle bit mode: source lane
+// ((l & 31) ^ x), no address operand).
+__device__ __forceinline__ float dpp_row_xor8(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, true));
+}
+template <int X>
+__device__ __forceinline__ float swizzle_xor(float v) {
+  static_assert(X > 0 && X < 32, "inside 32 lanes");
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (X << 10)));
+}
+template <int X>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (X == 1) return dpp_quad_xor1(v);
+  else if constexpr (X == 2) return dpp_quad_xor2(v);
+  else if constexpr (X == 8) return dpp_row_xor8(v);
+  else return swizzle_xor<X>(v);
+}
+// Unnormalised 32-point Walsh-Hadamard transform across lanes: lane i (bits
+// 0..4 of the lane index) ends with sum_j (-1)^popcount(i & j) v_j.
+__device__ __forceinline__ float wht32_lanes(float v, int i) {
+  auto stage = [&](float ov, int h) { return (i & h) ? (ov - v) : (v + ov); };
+  v = stage(lane_xor<1>(v), 1);
+  v = stage(lane_xor<2>(v), 2);
+  v = stage(lane_xor<4>(v), 4);
+  v = stage(lane_xor<8>(v), 8);
+  v = stage(lane_xor<16>(v), 16);
+  return v;
+}
+
 template <typename Op>
 __device__ __forceinline__ float wave_reduce(float v, Op op) {
 #pragma unroll
