@@ -288,6 +288,57 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   float *st_s = st_p + PW;                                // [NQB][WT]
   float *comb = st_s + SW;                                // [NR][HD], m[NR], l[NR], 2^Ev
 
+  // ---- K/V records.  The tile's waves fetch them in kLoadGroups staggered
+  // groups: group k issues only once the records of group k - 1 have
+  // arrived, so device-wide the early groups' bytes come back first and their
+  // passes overlap the later transfers.  Group 0 is the highest waves (the
+  // query waves fetch last).  Codes, tile tt of this wave: for the
+  // keys lane (l16, lg) holds qblock lg of token 16 tt + l16, for the values
+  // qblock l16 % 4 of token 16 tt + 4 lg + l16 / 4 (one contiguous run of
+  // four records per 16 lanes); scales: lane = token, all
+  // four qblock scales in one load.  Addresses are a per-(b, g) base plus a
+  // 32-bit offset inside the head. ----
+  constexpr int GW = kWaves / kLoadGroups;  // waves per load group
+  const int grp = (kWaves - 1 - wave) / GW;
+  const uint8_t *ksbase = reinterpret_cast<const uint8_t *>(a.k_sc + rec0 * NQB);
+  const uint8_t *vsbase = reinterpret_cast<const uint8_t *>(a.v_sc + rec0 * NQB);
+  uint32_t kq[NT][QW], vq[NT][QW];
+  uint2 ksc, vsc;
+  uint32_t sq[NT];   // QJL: sign word lg of token 16 tt + l16
+  uint32_t nrm = 0;  // QJL: residual norm of token lane
+  const uint8_t *sgbase = reinterpret_cast<const uint8_t *>(a.qjl_signs) + rec0 * 16;
+  const uint16_t *nmbase = a.qjl_norms + rec0;
+  auto issue_loads = [&]() {
+    const int tw = t0 + wave * WT;
+    const uint32_t soff = (uint32_t)min(tw + lane, len - 1) * (NQB * 2);
+    uint32_t off[NT], voff[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+      off[tt] = (uint32_t)min(tw + 16 * tt + l16, len - 1) * PACKED + lg * (QW * 4);
+      voff[tt] = (uint32_t)min(tw + 16 * tt + 4 * lg + (l16 >> 2), len - 1) * PACKED + (l16 & 3) * (QW * 4);
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+      for (int w = 0; w < QW; w++) kq[tt][w] = *reinterpret_cast<const uint32_t *>(kbase + off[tt] + 4 * w);
+    ksc = *reinterpret_cast<const uint2 *>(ksbase + soff);
+    if constexpr (QJL) {
+#pragma unroll
+      for (int tt = 0; tt < NT; tt++)
+        sq[tt] = *reinterpret_cast<const uint32_t *>(
+            sgbase + (uint32_t)min(tw + 16 * tt + l16, len - 1) * 16 + lg * 4);
+      nrm = nmbase[min(tw + lane, len - 1)];
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+      for (int w = 0; w < QW; w++) vq[tt][w] = *reinterpret_cast<const uint32_t *>(vbase + voff[tt] + 4 * w);
+    vsc = *reinterpret_cast<const uint2 *>(vsbase + soff);
+  };
+  // Group 0 fetches before the shared setup below, so its records are on the
+  // way while the pair table and the query operands are built.
+  if (grp == 0) issue_loads();
+
   // ---- pair table from the constant codebook ----
   for (int it = tid; it < NPAIR * PREP; it += kThreads) {
     const int e = it / PREP;
@@ -337,57 +388,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     }
   }
 
-  // ---- K/V records.  The tile's waves fetch them in kLoadGroups staggered
-  // groups: group k issues only once the records of group k - 1 have
-  // arrived, so device-wide the early groups' bytes come back first and their
-  // passes overlap the later transfers.  Group 0 is the highest waves (the
-  // query waves above fetch last).  Codes, tile tt of this wave: for the
-  // keys lane (l16, lg) holds qblock lg of token 16 tt + l16, for the values
-  // qblock l16 % 4 of token 16 tt + 4 lg + l16 / 4 (one contiguous run of
-  // four records per 16 lanes); scales: lane = token, all
-  // four qblock scales in one load.  Addresses are a per-(b, g) base plus a
-  // 32-bit offset inside the head. ----
-  constexpr int GW = kWaves / kLoadGroups;  // waves per load group
-  const int grp = (kWaves - 1 - wave) / GW;
-  const uint8_t *ksbase = reinterpret_cast<const uint8_t *>(a.k_sc + rec0 * NQB);
-  const uint8_t *vsbase = reinterpret_cast<const uint8_t *>(a.v_sc + rec0 * NQB);
-  uint32_t kq[NT][QW], vq[NT][QW];
-  uint2 ksc, vsc;
-  uint32_t sq[NT];   // QJL: sign word lg of token 16 tt + l16
-  uint32_t nrm = 0;  // QJL: residual norm of token lane
-  const uint8_t *sgbase = reinterpret_cast<const uint8_t *>(a.qjl_signs) + rec0 * 16;
-  const uint16_t *nmbase = a.qjl_norms + rec0;
-  auto issue_loads = [&](bool real) {
-    const int tw = t0 + wave * WT;
-    const uint32_t soff = (uint32_t)(real ? min(tw + lane, len - 1) : t0) * (NQB * 2);
-    uint32_t off[NT], voff[NT];
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++) {
-      off[tt] = (uint32_t)(real ? min(tw + 16 * tt + l16, len - 1) : t0) * PACKED + lg * (QW * 4);
-      voff[tt] = (uint32_t)(real ? min(tw + 16 * tt + 4 * lg + (l16 >> 2), len - 1) : t0) * PACKED + (l16 & 3) * (QW * 4);
-    }
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++)
-#pragma unroll
-      for (int w = 0; w < QW; w++) kq[tt][w] = *reinterpret_cast<const uint32_t *>(kbase + off[tt] + 4 * w);
-    ksc = *reinterpret_cast<const uint2 *>(ksbase + soff);
-    if constexpr (QJL) {
-#pragma unroll
-      for (int tt = 0; tt < NT; tt++)
-        sq[tt] = *reinterpret_cast<const uint32_t *>(
-            sgbase + (uint32_t)(real ? min(tw + 16 * tt + l16, len - 1) : t0) * 16 + lg * 4);
-      nrm = nmbase[real ? min(tw + lane, len - 1) : t0];
-    }
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++)
-#pragma unroll
-      for (int w = 0; w < QW; w++) vq[tt][w] = *reinterpret_cast<const uint32_t *>(vbase + voff[tt] + 4 * w);
-    vsc = *reinterpret_cast<const uint2 *>(vsbase + soff);
-  };
-  // Every wave issues the same load sequence here (later groups fetch the
-  // tile's first record as a placeholder), so the number of loads in flight
-  // does not depend on the group.
-  issue_loads(grp == 0);
   __syncthreads();
   // Key-pass query operands.  MFMA j covers elements 4 j .. 4 j + 3 of every
   // qblock, each twice along k (against the hi and the lo part of the key
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         __builtin_amdgcn_s_sleep(2);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    issue_loads(true);
+    issue_loads();
   }
   if constexpr (kLoadGroups > 1) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's records are in registers
