@@ -9,6 +9,11 @@ cache.  Algorithmic bytes per step: 8 heads x 32768 tokens x (56 + 56) B =
 cache (29 MB) fits the 256 MB Infinity Cache, so steps rotate through
 >= 1 GiB of distinct cache copies.
 
+Beside it, "read_ceiling": the time of a plain streaming read of the same
+29,360,128 B (turboquant_amd/probe/read_probe.hip, also rotating over
+>= 1 GiB), i.e. what any kernel that reads those bytes once can reach here,
+and the decode's fraction of it.
+
 Secondary: PQO3 quantize Mvec/s at d=128 (config 2: 28 layers x 8 KV heads x
 4096 tokens, K and V, bf16 in) with the fused rotation, reported in the same
 JSON line under "quantize".
@@ -319,6 +324,32 @@ def bench_c5(torch, tq, args):
             "estimates_per_s": round(64 * 8192 / (times["scores_64x8192_ms"] * 1e-3), 1)}
 
 
+def read_ceiling(torch, nbytes: int, steps: int, warmup: int):
+    """Attainable read rate at nbytes: a plain streaming read of nbytes
+    (turboquant_amd/probe/read_probe.hip), rotating over >= 1 GiB so nothing
+    is cache-resident, best of three grid sizes.  A reference for the decode's
+    bytes, not a figure of this library."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "turboquant_amd", "libtq_read_probe.so"))
+    lib.tq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    nsl = max(1, math.ceil((1 << 30) / nbytes) + 1)
+    buf = torch.ones(nsl * nbytes, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.uint32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    best = None
+    for grid in (1024, 2048, 4096):
+        def step(i, grid=grid):
+            if lib.tq_probe_read(buf.data_ptr() + (i % nsl) * nbytes, nbytes, grid, sink.data_ptr(), stream) != 0:
+                raise RuntimeError("read probe launch failed")
+        ms, _ = time_steps(torch, step, steps, warmup)
+        if best is None or ms < best[0]:
+            best = (ms, grid)
+    del buf
+    gbs = nbytes / (best[0] * 1e-3) / 1e9
+    return {"bytes": nbytes, "us": round(best[0] * 1e3, 3), "gbs": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "grid": best[1], "slices": nsl}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +400,8 @@ def main():
     ms_devlen, _ = time_steps(torch, lambda i: attn_step(i, lens), args.steps, args.warmup)
     gbs = c3_bytes() / (ms * 1e-3) / 1e9
     del caches
+    ceiling = read_ceiling(torch, c3_bytes(), args.steps, args.warmup)
+    ceiling["decode_frac_of_read"] = round(gbs / ceiling["gbs"], 4)
 
     # ---- config 2: PQO3 quantize (fused rotation), bf16 in ----
     n_vec = C2["layers"] * C2["kv_heads"] * C2["tokens"] * 2
@@ -429,6 +462,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic("attn_decode_kernel")},
         "cpu_baseline": cpu,
+        "read_ceiling": ceiling,
         "quantize": {"metric": "PQO3 quantize Mvec/s at d=128 (C2, bf16 in, fused rotation)",
                      "value": round(mvec, 2), "unit": "Mvec/s", "ms_per_step": round(qms, 6),
                      "launch": "consecutive launches from the host API, HIP events around them",

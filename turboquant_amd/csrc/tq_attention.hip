@@ -213,10 +213,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   constexpr int PACKED = NQB * QW * 4;           // bytes per token record
   constexpr int NC = 1 << BITS;
   constexpr int NPAIR = 1 << (2 * BITS);         // pair-table entries
-  // Pair-table copies: with 16, entry e of copy s sits at word 32 e + 2 s, so
-  // the 16 lanes of a row, each reading copy l % 16, always hit 16 distinct
-  // bank pairs whatever codes they look up (PQO3: 8 KB; PQO4 keeps one copy).
-  constexpr int PREP = BITS == 3 ? 16 : 1;
+  // One pair table (512 B for 3-bit codes, 2 KB for 4-bit): per-lane copies
+  // measured no faster, as 8-byte LDS reads are served 32 lanes at a time.
   constexpr int WT = 64;                         // tokens per wave
   constexpr int NT = WT / 16;                    // 16-token tiles per wave
   constexpr int NG = NR > 2 ? NR / 2 : 1;        // MFMA head groups: 16 rows = 4 qblocks x 2 heads x 2 parts
@@ -227,8 +225,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   constexpr int CW = (NR * HD + 2 * NR + 1 + 3) & ~3;  // combine record: acc [head][d], m, l, 2^Ev
   constexpr int WSTAGE = RA + PW + SW + CW;
   // LDS carve (32-bit words)
-  constexpr int OFF_PAIR = 0;                    // uint2 [NPAIR][PREP]
-  constexpr int OFF_QA = OFF_PAIR + 2 * NPAIR * PREP;  // u32x4 [NG][8][64]: key-pass query operands
+  constexpr int OFF_PAIR = 0;                    // uint2 [NPAIR]
+  constexpr int OFF_QA = OFF_PAIR + 2 * NPAIR;   // u32x4 [NG][8][64]: key-pass query operands
   constexpr int OFF_Q = OFF_QA + NG * 8 * 64 * 4;
   constexpr int OFF_QMAX = OFF_Q + NR * HD;      // [2 NR] max |qt| per half head
   // QJL: u32x4 [4][64] correction operands, uint2 [16] +-1 f16 nibble table,
@@ -258,7 +256,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;  // matrix-core column / row group of this lane
-  const uint2 *s_pair_l = s_pair + (l16 % PREP);  // this lane's copy: entry e at s_pair_l[e * PREP]
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int t0 = c * CH;
   const long long rec0 = (long long)b * a.seq_stride + (long long)g * a.kv_head_stride;
@@ -340,8 +337,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   if (grp == 0) issue_loads();
 
   // ---- pair table from the constant codebook ----
-  for (int it = tid; it < NPAIR * PREP; it += kThreads) {
-    const int e = it / PREP;
+  for (int it = tid; it < NPAIR; it += kThreads) {
+    const int e = it;
     constexpr int CM = (1 << CB) - 1;  // slot codes >= 2^CB never occur
     const int i0 = e & (NC - 1) & CM, i1 = (e >> BITS) & CM;
     float c0, c1;
@@ -474,8 +471,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     for (int gi = 0; gi < NG; gi++) qa[gi] = s_qa[(gi * 8 + j) * 64 + lane];
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
-      const uint2 e0 = s_pair_l[pair_code<BITS>(kq[tt], 2 * j) * PREP];
-      const uint2 e1 = s_pair_l[pair_code<BITS>(kq[tt], 2 * j + 1) * PREP];
+      const uint2 e0 = s_pair[pair_code<BITS>(kq[tt], 2 * j)];
+      const uint2 e1 = s_pair[pair_code<BITS>(kq[tt], 2 * j + 1)];
       const u32x4 kb = {e0.x, e0.y, e1.x, e1.y};
 #pragma unroll
       for (int gi = 0; gi < NG; gi++) dk[tt][gi] = mfma(qa[gi], kb, dk[tt][gi]);
@@ -631,8 +628,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     for (int tp = 0; tp < NT / 2; tp++) {
 #pragma unroll
       for (int h = 0; h < 2; h++) {
-        const u32x2 r0 = lds_read_tr16(s_pair_l + pair_code<BITS>(vq[2 * tp], 2 * j + h) * PREP);
-        const u32x2 r1 = lds_read_tr16(s_pair_l + pair_code<BITS>(vq[2 * tp + 1], 2 * j + h) * PREP);
+        const u32x2 r0 = lds_read_tr16(s_pair + pair_code<BITS>(vq[2 * tp], 2 * j + h));
+        const u32x2 r1 = lds_read_tr16(s_pair + pair_code<BITS>(vq[2 * tp + 1], 2 * j + h));
         const u32x4 va = {r0[0], r0[1], r1[0], r1[1]};
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) dv[h][gi] = mfma(va, bw[tp][gi], dv[h][gi]);
