@@ -45,6 +45,18 @@ __device__ __forceinline__ float lane_xor(float v) {
   else if constexpr (X == 8) return dpp_row_xor8(v);
   else return swizzle_xor<X>(v);
 }
+// max(v, v of lane l ^ 16) and max(v, v of lane l ^ 32) on the permlane
+// swaps: with both operands v, the two results of a swap are v of lane l
+// and of its partner, in some order.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
 // Unnormalised 32-point Walsh-Hadamard transform across lanes: lane i (bits
 // 0..4 of the lane index) ends with sum_j (-1)^popcount(i & j) v_j.
 __device__ __forceinline__ float wht32_lanes(float v, int i) {

@@ -10,17 +10,19 @@
 //
 // One workgroup (4 waves) serves 64 rows = (query, head) pairs of one KV
 // head, query-major, so the NR query heads of a KV head share every decoded
-// tile.  Per 64-token tile the workgroup decodes K (token-major, per-token
-// exponent folded out) and V (element-major) into LDS as two-part f16
-// values (hi = 11 significant bits, lo = the remainder), then each wave
+// tile.  Per 64-token tile the workgroup decodes K and V (token-major,
+// per-token exponents folded out) into LDS as two-part f16 values (hi = 11
+// significant bits, lo = the remainder), then each wave
 // (16 rows) runs
 //   S^T = K Q^T          16x16x32 MFMAs, K's hi/lo along k against a
 //                        duplicated query value, query hi and lo as two
 //                        operands (22-bit products, f32 accumulation)
 //   corr^T = Sg RQ^T     TQ: the keys' +-1 sign bits against rq hi/lo
-//   O^T += V^T P^T       16x16x16 MFMAs whose B operand is exactly S^T's
-//                        accumulator layout (4 tokens per lane), V hi/lo x
-//                        P hi/lo (three products, lo x lo dropped)
+//   O^T += V^T P^T       16x16x32 MFMAs over two 16-token blocks whose B
+//                        operand is S^T's accumulator layout (4 tokens per
+//                        lane and block), the V operand read through the
+//                        transposing LDS read, V hi/lo x P hi/lo (three
+//                        products, lo x lo dropped)
 // with an online base-2 softmax per row.  Values stay in the rotated
 // domain; each row is inverse-rotated once at the end.  The next tile's
 // records are fetched while the current one is computed.
@@ -37,7 +39,8 @@ constexpr int kPThreads = 256;
 constexpr int kRows = 64;   // (query, head) rows per workgroup
 constexpr int kTile = 64;   // tokens per tile
 constexpr int kKStride = 66;  // uint2 per token row of the K tile (64 pairs + pad)
-constexpr int kVStride = 68;  // halves per element row of the V tiles (64 tokens + pad)
+constexpr int kVRow = 144;    // halves per token row of the V tiles (128 elements + pad: the
+                              // transposing reads of 4 tokens x 4 element quads hit 32 distinct banks)
 
 enum PMode : int { kPPqo = 0, kPPq = 1, kPTq = 2 };
 
@@ -62,11 +65,6 @@ struct PrefillArgs {
   float cb[16];
 };
 
-__device__ __forceinline__ f32x4 mfma16(u32x2 a, u32x2 b, f32x4 d) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, a), __builtin_bit_cast(half4, b), d, 0, 0,
-                                               0);
-}
-
 template <int BITS, int MODE, int NR>
 __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
   constexpr int CB = MODE == kPPqo ? BITS : BITS - 1;
@@ -75,12 +73,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   constexpr int QB = kRows / NR;  // queries per workgroup
   // LDS: K tile | V tiles (hi, lo) | per-token and per-row scalars
   constexpr int K_WORDS = kTile * kKStride * 2;
-  constexpr int V_HALVES = HD * kVStride;
+  constexpr int V_HALVES = kTile * kVRow;
   constexpr int V_WORDS = V_HALVES;  // hi and lo planes, 2 halves per word each
   __shared__ __attribute__((aligned(16))) uint32_t s_k[K_WORDS];
   __shared__ __attribute__((aligned(16))) uint32_t s_v[V_WORDS];
   __shared__ float s_ek[kTile];       // 2^E_k per token (key exponent folded out)
   __shared__ int s_ev[kTile];         // V exponent per token
+  __shared__ int s_evw[4];            // max V exponent over each wave's 16 tokens
   __shared__ float s_cn[kTile];       // TQ: |r_t| * qjl_c
   __shared__ __attribute__((aligned(16))) uint32_t s_sg[kTile * 4];  // TQ: sign words
   __shared__ float s_cb[16];
@@ -255,6 +254,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
         s_ev[ftok] = ev;
         if constexpr (QJL) s_cn[ftok] = f16_to_f32(nm) * a.qjl_c;
       }
+      {
+        const float wm = wave_max((float)ev);  // exact: |ev| <= 100
+        if (lane == 0) s_evw[wave] = (int)wm;
+      }
       if constexpr (QJL) s_sg[ftok * 4 + fqb] = sgw;
 #pragma unroll
       for (int p = 0; p < 16; p++) {
@@ -264,17 +267,23 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
         const float h0 = split_hi(x0), h1 = split_hi(x1);
         kt[ftok * kKStride + 16 * fqb + p] = make_uint2(pack_f16(h0, h1), pack_f16(x0 - h0, x1 - h1));
       }
+      uint32_t hw[16], lw[16];
 #pragma unroll
       for (int p = 0; p < 16; p++) {
         const uint32_t code = pair_code<BITS>(vw, p);
         const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * vf;
         const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * vf;
         const float h0 = split_hi(x0), h1 = split_hi(x1);
-        const int e = 32 * fqb + 2 * p;
-        vth[e * kVStride + ftok] = (_Float16)h0;
-        vth[(e + 1) * kVStride + ftok] = (_Float16)h1;
-        vtl[e * kVStride + ftok] = (_Float16)(x0 - h0);
-        vtl[(e + 1) * kVStride + ftok] = (_Float16)(x1 - h1);
+        hw[p] = pack_f16(h0, h1);
+        lw[p] = pack_f16(x0 - h0, x1 - h1);
+      }
+      // token-major rows: this thread's 32 elements, four 16-byte stores per plane
+      uint4 *vrh = reinterpret_cast<uint4 *>(vth + ftok * kVRow + 32 * fqb);
+      uint4 *vrl = reinterpret_cast<uint4 *>(vtl + ftok * kVRow + 32 * fqb);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        vrh[i] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
+        vrl[i] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
       }
     }
     __syncthreads();
@@ -322,14 +331,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     for (int tb = 0; tb < 4; tb++)
 #pragma unroll
       for (int i = 0; i < 4; i++) mt = fmaxf(mt, x[tb][i]);
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = max_xor32(max_xor16(mt));
     const float m_new = fmaxf(m_run, mt);
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
     // V exponent of the tile (each wave reads all 64)
-    int evt = s_ev[lane];
-#pragma unroll
-    for (int o2 = 32; o2 > 0; o2 >>= 1) evt = max(evt, __shfl_xor(evt, o2, 64));
+    const int evt = max(max(s_evw[0], s_evw[1]), max(s_evw[2], s_evw[3]));
     const int ev_new = max(ev_cur, evt);
     const float rescale = alpha * exp2i(max(ev_cur - ev_new, -126));
     ev_cur = ev_new;
@@ -352,19 +358,25 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       pb[tb][1] = u32x2{pack_f16(p[0] - ph[0], p[1] - ph[1]), pack_f16(p[2] - ph[2], p[3] - ph[3])};
     }
     l_run = l_run * alpha + ls;
-    // ---- O^T += V^T P^T ----
+    // ---- O^T += V^T P^T, two 16-token blocks per 16x16x32 product.  The
+    // value operand comes through the transposing LDS read: lane (4 a + b)
+    // of group lg receives element 16 eb + 4 a + b of tokens 16 tb + 4 lg ..
+    // + 3 from the token-major rows addressed by lanes a + 4 j. ----
+    const int vrow = 4 * lg + (l16 >> 2), vcol = 4 * (l16 & 3);
 #pragma unroll
     for (int eb = 0; eb < 8; eb++) {
       f32x4 acc = o[eb] * rescale;
-      const int e = 16 * eb + l16;
 #pragma unroll
-      for (int tb = 0; tb < 4; tb++) {
-        const uint2 vh = *reinterpret_cast<const uint2 *>(vth + e * kVStride + 16 * tb + 4 * lg);
-        const uint2 vl = *reinterpret_cast<const uint2 *>(vtl + e * kVStride + 16 * tb + 4 * lg);
-        const u32x2 ah = {vh.x, vh.y}, al = {vl.x, vl.y};
-        acc = mfma16(ah, pb[tb][0], acc);
-        acc = mfma16(ah, pb[tb][1], acc);
-        acc = mfma16(al, pb[tb][0], acc);
+      for (int tp = 0; tp < 2; tp++) {
+        const int r0 = (32 * tp + vrow) * kVRow + 16 * eb + vcol, r1 = r0 + 16 * kVRow;
+        const u32x2 h0 = lds_read_tr16(vth + r0), h1 = lds_read_tr16(vth + r1);
+        const u32x2 q0 = lds_read_tr16(vtl + r0), q1 = lds_read_tr16(vtl + r1);
+        const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {q0[0], q0[1], q1[0], q1[1]};
+        const u32x4 bh = {pb[2 * tp][0][0], pb[2 * tp][0][1], pb[2 * tp + 1][0][0], pb[2 * tp + 1][0][1]};
+        const u32x4 bl = {pb[2 * tp][1][0], pb[2 * tp][1][1], pb[2 * tp + 1][1][0], pb[2 * tp + 1][1][1]};
+        acc = mfma(ah, bh, acc);
+        acc = mfma(ah, bl, acc);
+        acc = mfma(al, bh, acc);
       }
       o[eb] = acc;
     }
