@@ -4,8 +4,9 @@
 // chunk of CH = 1024 tokens) and serves all NR = num_heads / num_kv_heads
 // query heads of that KV head, so every compressed byte is read from HBM
 // exactly once (GQA sharing).  Each wave owns 64 tokens, fetched as four
-// 16-token tiles in which lane (t, q) loads qblock q of token t, so one load
-// instruction reads one contiguous run of 16 records.
+// 16-token tiles, each load instruction one contiguous run of records (key
+// codes: lane (t, q) loads qblock q of token t; value codes: lane l of a
+// 16-lane group loads qblock l % 4 of token 4 g + l / 4).
 //
 // Keys are never inverse-rotated.  With the block dequantization
 //   k_j = |s| * inv * (H (cb[idx] * sg))_j               (wht_tensor.rs:38-64)
@@ -17,9 +18,9 @@
 //   scores  D[(qblock, head, part)][token] = sum_k Q[..][k] K[k][token], the
 //           query operand block-diagonal over qblocks so that the
 //           per-(token, qblock) key scale applies after the contraction;
-//   values  D[element][(qblock, head, part)] = sum_t V[element][t] W[t][..],
-//           W = p * |s_V|, with the codes transposed to token-major order in
-//           LDS.
+//   values  D[(qblock, value part)][(qblock, head, part)] = sum_t V W,
+//           W = p * |s_V|, the value operand taken element-major straight
+//           from the pair table through the transposing LDS read.
 // A pair of codes is decoded by one 8-byte LDS read from a 2^(2 BITS)-entry
 // table of (hi(cb[c0]), hi(cb[c1]), lo(cb[c0]), lo(cb[c1])).  Values are
 // accumulated in the rotated domain and inverse-rotated once per head after

@@ -146,14 +146,6 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 d) {
                                                 0);
 }
 
-// A B over 16 x 16 x 16 (f16 in, f32 out): lane l holds A row l % 16 and B
-// column l % 16 at k = 4 (l / 16) .. 4 (l / 16) + 3, and D column l % 16 at
-// rows 4 (l / 16) .. 4 (l / 16) + 3.  With B = I it is an exact transpose.
-__device__ __forceinline__ f32x4 mfma_t(u32x2 a, u32x2 b) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, a), __builtin_bit_cast(half4, b),
-                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-}
-
 // Transposing LDS read (ds_read_b64_tr_b16): inside each group of 16 lanes,
 // lane 4 a + b receives item b (16-bit) of the 8-byte rows addressed by
 // lanes a, a + 4, a + 8 and a + 12 of its group, in that order (item 0 in
