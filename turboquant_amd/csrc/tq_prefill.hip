@@ -30,19 +30,23 @@
 #include "tq_device.h"
 #include "tq_mfma.h"
 
+#include <type_traits>
+
 namespace {
 
 using namespace tqd;
 using namespace tqm;
 
-constexpr int kPThreads = 256;
-constexpr int kRows = 64;   // (query, head) rows per workgroup
+// (query, head) rows per workgroup: 128 (8 waves) share each decoded tile;
+// the TQ mode, whose wave needs 256 registers, keeps 64 (4 waves)
+constexpr int prefill_rows(int mode) { return mode == 2 ? 64 : 128; }
 constexpr int kTile = 64;   // tokens per tile
 constexpr int kKStride = 66;  // uint2 per token row of the K tile (64 pairs + pad)
 constexpr int kVRow = 144;    // halves per token row of the V tiles (128 elements + pad: the
                               // transposing reads of 4 tokens x 4 element quads hit 32 distinct banks)
 
 enum PMode : int { kPPqo = 0, kPPq = 1, kPTq = 2 };
+constexpr int kPrefillModeTq = kPTq;
 
 struct PrefillArgs {
   const void *q;
@@ -66,20 +70,27 @@ struct PrefillArgs {
 };
 
 template <int BITS, int MODE, int NR>
-__global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(PrefillArgs a) {
   constexpr int CB = MODE == kPPqo ? BITS : BITS - 1;
   constexpr bool QJL = MODE == kPTq;
   constexpr int HD = 128, QW = BITS, PACKED = 16 * QW;
+  constexpr int kRows = prefill_rows(MODE);
+  constexpr int NW = kRows / 16;            // waves
+  constexpr int SPLIT = NW / 4;             // waves per 16-token slice of a tile's decode
+  constexpr int NP = 16 / SPLIT;            // code pairs per decoding thread
   constexpr int QB = kRows / NR;  // queries per workgroup
+  static_assert(kPrefillModeTq == 2, "prefill_rows keys on the TQ mode");
   // LDS: K tile | V tiles (hi, lo) | per-token and per-row scalars
   constexpr int K_WORDS = kTile * kKStride * 2;
   constexpr int V_HALVES = kTile * kVRow;
   constexpr int V_WORDS = V_HALVES;  // hi and lo planes, 2 halves per word each
-  __shared__ __attribute__((aligned(16))) uint32_t s_k[K_WORDS];
-  __shared__ __attribute__((aligned(16))) uint32_t s_v[V_WORDS];
+  // K tile | V tiles; before the tiles the split query (and rq) rows, after
+  // them the output rows
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[K_WORDS + V_WORDS];
+  uint32_t *s_k = s_tile, *s_v = s_tile + K_WORDS;
   __shared__ float s_ek[kTile];       // 2^E_k per token (key exponent folded out)
   __shared__ int s_ev[kTile];         // V exponent per token
-  __shared__ int s_evw[4];            // max V exponent over each wave's 16 tokens
+  __shared__ int s_evw[NW];           // max V exponent over each wave's 16 tokens
   __shared__ float s_cn[kTile];       // TQ: |r_t| * qjl_c
   __shared__ __attribute__((aligned(16))) uint32_t s_sg[kTile * 4];  // TQ: sign words
   __shared__ float s_cb[16];
@@ -112,7 +123,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   const int prow = tid >> 2, pq = tid & 3;
   const int qi = i0 + prow / NR, qh = g * NR + prow % NR;
   const bool row_ok = qi < a.q_len;
-  _Float16 *s_qh = reinterpret_cast<_Float16 *>(s_v);  // [row][128] hi
+  _Float16 *s_qh = reinterpret_cast<_Float16 *>(s_tile);  // [row][128] hi
   _Float16 *s_ql = s_qh + kRows * HD;                 // [row][128] lo
   {
     float x[32];
@@ -144,7 +155,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     }
   }
   // TQ: rq rows the same way (no rotation), into the K tile region
-  _Float16 *s_rh = reinterpret_cast<_Float16 *>(s_k);
+  _Float16 *s_rh = reinterpret_cast<_Float16 *>(s_tile + kRows * HD);
   _Float16 *s_rl = s_rh + kRows * HD;
   if constexpr (QJL) {
     float x[32];
@@ -205,7 +216,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   const int ntiles = (kv_end + kTile - 1) / kTile;
 
   // thread (token, qblock) fetches one record of K and V per tile
-  const int ftok = tid >> 2, fqb = tid & 3;
+  // thread (token, qblock, part): wave w decodes tokens 16 (w / SPLIT) ..
+  // + 15, code pairs NP (w % SPLIT) .. + NP - 1 of every qblock
+  const int ftok = 16 * (wave / SPLIT) + (lane >> 2), fqb = lane & 3, fpart = wave % SPLIT;
   uint32_t kw[QW], vw[QW], sgw = 0;
   uint16_t ks = 0, vs = 0, nm = 0;
   auto fetch = [&](int t0) {
@@ -235,8 +248,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   _Float16 *vth = reinterpret_cast<_Float16 *>(s_v);
   _Float16 *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
-  static_assert(2 * kRows * HD <= 2 * V_WORDS, "the split query fits the V region");
-  static_assert(2 * kRows * HD <= 2 * K_WORDS && kRows * HD <= K_WORDS, "rq and the output fit the K region");
+  static_assert((QJL ? 2 : 1) * kRows * HD <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
+  static_assert(kRows * HD + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
 
   for (int tile = 0; tile < ntiles; tile++) {
     const int t0 = tile * kTile;
@@ -249,7 +262,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       mv = fmaxf(mv, dpp_quad_xor2(mv));
       const int ek = pow2_exponent(mk), ev = pow2_exponent(mv);
       const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
-      if (fqb == 0) {
+      if (fqb == 0 && fpart == 0) {
         s_ek[ftok] = exp2i(ek);
         s_ev[ftok] = ev;
         if constexpr (QJL) s_cn[ftok] = f16_to_f32(nm) * a.qjl_c;
@@ -259,31 +272,43 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
         if (lane == 0) s_evw[wave] = (int)wm;
       }
       if constexpr (QJL) s_sg[ftok * 4 + fqb] = sgw;
+      // this thread's code pairs P0 .. P0 + NP - 1 (a wave-uniform part, so
+      // every pair index folds to a constant)
+      auto decode_pairs = [&](auto p0c) {
+        constexpr int P0 = decltype(p0c)::value;
 #pragma unroll
-      for (int p = 0; p < 16; p++) {
-        const uint32_t code = pair_code<BITS>(kw, p);
-        const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * kf;
-        const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * kf;
-        const float h0 = split_hi(x0), h1 = split_hi(x1);
-        kt[ftok * kKStride + 16 * fqb + p] = make_uint2(pack_f16(h0, h1), pack_f16(x0 - h0, x1 - h1));
-      }
-      uint32_t hw[16], lw[16];
+        for (int pp = 0; pp < NP; pp++) {
+          const int p = P0 + pp;
+          const uint32_t code = pair_code<BITS>(kw, p);
+          const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * kf;
+          const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * kf;
+          const float h0 = split_hi(x0), h1 = split_hi(x1);
+          kt[ftok * kKStride + 16 * fqb + p] = make_uint2(pack_f16(h0, h1), pack_f16(x0 - h0, x1 - h1));
+        }
+        uint32_t hw[NP], lw[NP];
 #pragma unroll
-      for (int p = 0; p < 16; p++) {
-        const uint32_t code = pair_code<BITS>(vw, p);
-        const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * vf;
-        const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * vf;
-        const float h0 = split_hi(x0), h1 = split_hi(x1);
-        hw[p] = pack_f16(h0, h1);
-        lw[p] = pack_f16(x0 - h0, x1 - h1);
-      }
-      // token-major rows: this thread's 32 elements, four 16-byte stores per plane
-      uint4 *vrh = reinterpret_cast<uint4 *>(vth + ftok * kVRow + 32 * fqb);
-      uint4 *vrl = reinterpret_cast<uint4 *>(vtl + ftok * kVRow + 32 * fqb);
+        for (int pp = 0; pp < NP; pp++) {
+          const uint32_t code = pair_code<BITS>(vw, P0 + pp);
+          const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * vf;
+          const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * vf;
+          const float h0 = split_hi(x0), h1 = split_hi(x1);
+          hw[pp] = pack_f16(h0, h1);
+          lw[pp] = pack_f16(x0 - h0, x1 - h1);
+        }
+        // token-major rows: this thread's 2 NP elements, 16-byte stores per plane
+        uint4 *vrh = reinterpret_cast<uint4 *>(vth + ftok * kVRow + 32 * fqb + 2 * P0);
+        uint4 *vrl = reinterpret_cast<uint4 *>(vtl + ftok * kVRow + 32 * fqb + 2 * P0);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        vrh[i] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
-        vrl[i] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
+        for (int i = 0; i < NP / 4; i++) {
+          vrh[i] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
+          vrl[i] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
+        }
+      };
+      if constexpr (SPLIT == 1) {
+        decode_pairs(std::integral_constant<int, 0>{});
+      } else {
+        if (fpart == 0) decode_pairs(std::integral_constant<int, 0>{});
+        else decode_pairs(std::integral_constant<int, NP>{});
       }
     }
     __syncthreads();
@@ -335,7 +360,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     const float m_new = fmaxf(m_run, mt);
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
     // V exponent of the tile (each wave reads all 64)
-    const int evt = max(max(s_evw[0], s_evw[1]), max(s_evw[2], s_evw[3]));
+    int evt = s_evw[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) evt = max(evt, s_evw[w]);
     const int ev_new = max(ev_cur, evt);
     const float rescale = alpha * exp2i(max(ev_cur - ev_new, -126));
     ev_cur = ev_new;
@@ -387,13 +414,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   float L = l_run;
   L += __shfl_xor(L, 16, 64);
   L += __shfl_xor(L, 32, 64);
-  float *s_o = reinterpret_cast<float *>(s_k);  // [row][128] (rotated, in units of 2^ev_cur)
+  float *s_o = reinterpret_cast<float *>(s_tile);  // [row][128] (rotated, in units of 2^ev_cur)
   const float ofac = exp2i(max(min(ev_cur, 126), -126));
 #pragma unroll
   for (int eb = 0; eb < 8; eb++)
 #pragma unroll
     for (int i = 0; i < 4; i++) s_o[myrow * HD + 16 * eb + 4 * lg + i] = o[eb][i] * ofac;
-  float *s_rowl = s_ek;  // [rows] (the tiles are done)
+  float *s_rowl = s_o + kRows * HD;  // [rows] (the tiles are done)
   if (lg == 0) s_rowl[myrow] = L;
   __syncthreads();
   {
@@ -417,11 +444,12 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
 
 template <int BITS, int MODE>
 int launch_prefill_m(const PrefillArgs &a, int nr, hipStream_t st) {
-  const int qb = kRows / nr;
+  const int qb = prefill_rows(MODE) / nr;
+  const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
-  if (nr == 1) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1>), grid, dim3(kPThreads), 0, st, a);
-  else if (nr == 2) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 2>), grid, dim3(kPThreads), 0, st, a);
-  else hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 4>), grid, dim3(kPThreads), 0, st, a);
+  if (nr == 1) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1>), grid, block, 0, st, a);
+  else if (nr == 2) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 2>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 4>), grid, block, 0, st, a);
   return tqh::check_launch("prefill_attn_kernel");
 }
 
