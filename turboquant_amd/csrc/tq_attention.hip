@@ -35,6 +35,8 @@
 #include "tq_device.h"
 #include "tq_mfma.h"
 
+#include <type_traits>
+
 namespace {
 
 using namespace tqd;
@@ -298,6 +300,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   // 32-bit offset inside the head. ----
   constexpr int GW = kWaves / kLoadGroups;  // waves per load group
   const int grp = (kWaves - 1 - wave) / GW;
+  using I0 = std::integral_constant<int, 0>;
+  using INT = std::integral_constant<int, NT>;
+  const int tw_a = t0 + wave * WT;
   const uint8_t *ksbase = reinterpret_cast<const uint8_t *>(a.k_sc + rec0 * NQB);
   const uint8_t *vsbase = reinterpret_cast<const uint8_t *>(a.v_sc + rec0 * NQB);
   uint32_t kq[NT][QW], vq[NT][QW];
@@ -306,36 +311,37 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   uint32_t nrm = 0;  // QJL: residual norm of token lane
   const uint8_t *sgbase = reinterpret_cast<const uint8_t *>(a.qjl_signs) + rec0 * 16;
   const uint16_t *nmbase = a.qjl_norms + rec0;
-  auto issue_loads = [&]() {
-    const int tw = t0 + wave * WT;
+  // NTC tiles from token tw into tile registers TT0 ..
+  auto issue_tiles = [&](const int tw, auto tt0c, auto ntc, uint2 &ks_, uint2 &vs_, uint32_t &nm_) {
+    constexpr int TT0 = decltype(tt0c)::value, NTC = decltype(ntc)::value;
     const uint32_t soff = (uint32_t)min(tw + lane, len - 1) * (NQB * 2);
-    uint32_t off[NT], voff[NT];
+    uint32_t off[NTC], voff[NTC];
 #pragma unroll
-    for (int tt = 0; tt < NT; tt++) {
+    for (int tt = 0; tt < NTC; tt++) {
       off[tt] = (uint32_t)min(tw + 16 * tt + l16, len - 1) * PACKED + lg * (QW * 4);
       voff[tt] = (uint32_t)min(tw + 16 * tt + 4 * lg + (l16 >> 2), len - 1) * PACKED + (l16 & 3) * (QW * 4);
     }
 #pragma unroll
-    for (int tt = 0; tt < NT; tt++)
+    for (int tt = 0; tt < NTC; tt++)
 #pragma unroll
-      for (int w = 0; w < QW; w++) kq[tt][w] = *reinterpret_cast<const uint32_t *>(kbase + off[tt] + 4 * w);
-    ksc = *reinterpret_cast<const uint2 *>(ksbase + soff);
+      for (int w = 0; w < QW; w++) kq[TT0 + tt][w] = *reinterpret_cast<const uint32_t *>(kbase + off[tt] + 4 * w);
+    ks_ = *reinterpret_cast<const uint2 *>(ksbase + soff);
     if constexpr (QJL) {
 #pragma unroll
-      for (int tt = 0; tt < NT; tt++)
-        sq[tt] = *reinterpret_cast<const uint32_t *>(
+      for (int tt = 0; tt < NTC; tt++)
+        sq[TT0 + tt] = *reinterpret_cast<const uint32_t *>(
             sgbase + (uint32_t)min(tw + 16 * tt + l16, len - 1) * 16 + lg * 4);
-      nrm = nmbase[min(tw + lane, len - 1)];
+      nm_ = nmbase[min(tw + lane, len - 1)];
     }
 #pragma unroll
-    for (int tt = 0; tt < NT; tt++)
+    for (int tt = 0; tt < NTC; tt++)
 #pragma unroll
-      for (int w = 0; w < QW; w++) vq[tt][w] = *reinterpret_cast<const uint32_t *>(vbase + voff[tt] + 4 * w);
-    vsc = *reinterpret_cast<const uint2 *>(vsbase + soff);
+      for (int w = 0; w < QW; w++) vq[TT0 + tt][w] = *reinterpret_cast<const uint32_t *>(vbase + voff[tt] + 4 * w);
+    vs_ = *reinterpret_cast<const uint2 *>(vsbase + soff);
   };
   // Group 0 fetches before the shared setup below, so its records are on the
   // way while the pair table and the query operands are built.
-  if (grp == 0) issue_loads();
+  if (grp == 0) issue_tiles(tw_a, I0{}, INT{}, ksc, vsc, nrm);
 
   // ---- pair table from the constant codebook ----
   for (int it = tid; it < NPAIR; it += kThreads) {
@@ -441,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         __builtin_amdgcn_s_sleep(2);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    issue_loads();
+    issue_tiles(tw_a, I0{}, INT{}, ksc, vsc, nrm);
   }
   if constexpr (kLoadGroups > 1) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's records are in registers
@@ -455,203 +461,224 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     if constexpr (QJL) erscale[r] = exp2i(pow2_exponent(fmaxf(s_rqmax[2 * r], s_rqmax[2 * r + 1])));
   }
 
-  // ---- K pass: D[tile][(qblock, head, part)][token] over the eight
-  // 4-element slices j of every qblock.  The key operand of lane (t, q) for
-  // slice j is (hi pair, lo pair) of codes 4j, 4j+1 and of codes 4j+2, 4j+3
-  // of qblock q of token t: two pair-table reads.  Lane (t, q) ends with
-  // token t's (unscaled) qblock-q partial of each head. ----
-  f32x4 dk[NT][NG];
-#pragma unroll
-  for (int tt = 0; tt < NT; tt++)
-#pragma unroll
-    for (int gi = 0; gi < NG; gi++) dk[tt][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    u32x4 qa[NG];
-#pragma unroll
-    for (int gi = 0; gi < NG; gi++) qa[gi] = s_qa[(gi * 8 + j) * 64 + lane];
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++) {
-      const uint2 e0 = s_pair[pair_code<BITS>(kq[tt], 2 * j)];
-      const uint2 e1 = s_pair[pair_code<BITS>(kq[tt], 2 * j + 1)];
-      const u32x4 kb = {e0.x, e0.y, e1.x, e1.y};
-#pragma unroll
-      for (int gi = 0; gi < NG; gi++) dk[tt][gi] = mfma(qa[gi], kb, dk[tt][gi]);
-    }
-  }
-  if constexpr (QJL) {
-    // sum_j rq_j (2 b_j - 1) per (head, token) on the matrix core: the sign
-    // operand of lane (t, kg) for MFMA s is the +-1 pairs of byte s of its
-    // sign word; the (unscaled) sums go to st_p, which the softmax
-    // overwrites only after they are read
-    f32x4 dq[NT];
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++) dq[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int sl = 0; sl < 4; sl++) {
-      const u32x4 ra = s_ra[sl * 64 + lane];
-#pragma unroll
-      for (int tt = 0; tt < NT; tt++) {
-        const uint32_t byte = (sq[tt] >> (8 * sl)) & 0xffu;
-        const uint2 n0 = s_nib[byte & 15u], n1 = s_nib[byte >> 4];
-        dq[tt] = mfma(ra, u32x4{n0.x, n0.y, n1.x, n1.y}, dq[tt]);
-      }
-    }
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++)
-#pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int r = 2 * lg + u;
-        if (r < NR) st_p[r * WT + 16 * tt + l16] = dq[tt][2 * u] + dq[tt][2 * u + 1];
-      }
-  }
-#pragma unroll
-  for (int tt = 0; tt < NT; tt++) {
-    uint32_t *dst = st_x + (lg * WT + 16 * tt + l16) * NR;
-    uint32_t xv[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) xv[r] = f2u(dk[tt][r >> 1][2 * (r & 1)] + dk[tt][r >> 1][2 * (r & 1) + 1]);
-    if constexpr (NR == 1) {
-      dst[0] = xv[0];
-    } else if constexpr (NR == 2) {
-      *reinterpret_cast<uint2 *>(dst) = make_uint2(xv[0], xv[1]);
-    } else {
-      *reinterpret_cast<uint4 *>(dst) = make_uint4(xv[0], xv[1], xv[2], xv[3]);
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // lane = token: the four qblock partials times the token's key scales
-  float score[NR];
-#pragma unroll
-  for (int r = 0; r < NR; r++) score[r] = 0.f;
-#pragma unroll
-  for (int qb = 0; qb < NQB; qb++) {
-    const uint32_t sbits = (qb < 2 ? ksc.x : ksc.y) >> ((qb & 1) ? 16 : 0);
-    const float sk = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
-    const uint32_t *src = st_x + (qb * WT + lane) * NR;
-    uint32_t xv[NR];
-    if constexpr (NR == 1) {
-      xv[0] = src[0];
-    } else if constexpr (NR == 2) {
-      const uint2 t = *reinterpret_cast<const uint2 *>(src);
-      xv[0] = t.x; xv[1] = t.y;
-    } else {
-      const uint4 t = *reinterpret_cast<const uint4 *>(src);
-      xv[0] = t.x; xv[1] = t.y; xv[2] = t.z; xv[3] = t.w;
-    }
-#pragma unroll
-    for (int r = 0; r < NR; r++) score[r] = __builtin_fmaf(u2f(xv[r]), sk, score[r]);
-  }
-
-  // ---- wave-local softmax (base 2): m = max over the wave's tokens ----
-  const int tok = t0 + wave * WT + lane;
-  const bool valid = tok < len;
-  float m_w[NR], p[NR], l_w[NR];
-  float corr[NR];
-#pragma unroll
-  for (int r = 0; r < NR; r++) corr[r] = 0.f;
-  if constexpr (QJL) {
-    const float cn = f16_to_f32((uint16_t)nrm) * a.qjl_c;
-#pragma unroll
-    for (int r = 0; r < NR; r++) corr[r] = st_p[r * WT + lane] * (cn * erscale[r]);
-  }
+  // ---- the wave's NTB tiles from token tw (tile registers TT0 ..): its
+  // record (m, l, acc in units of 2^-Ev) goes to comb ----
+  float m_w[NR], l_w[NR];
 #pragma unroll
   for (int r = 0; r < NR; r++) {
-    const float sc = valid ? (QJL ? __builtin_fmaf(score[r], escale[r], corr[r]) : score[r] * escale[r]) : -INFINITY;
-    m_w[r] = wave_max(sc);
-    p[r] = valid ? __builtin_amdgcn_exp2f(sc - m_w[r]) : 0.f;
-    st_p[r * WT + lane] = p[r];
+    m_w[r] = -INFINITY;
+    l_w[r] = 0.f;
   }
-#pragma unroll
-  for (int r = 0; r < NR; r++) l_w[r] = wave_sum(p[r]);
-
-  // ---- V scales * 2^-Ev to LDS (lane = token) ----
-  float sv[NQB];
-  float smax = 0.f;
-#pragma unroll
-  for (int qb = 0; qb < NQB; qb++) {
-    const uint32_t sbits = (qb < 2 ? vsc.x : vsc.y) >> ((qb & 1) ? 16 : 0);
-    sv[qb] = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
-    smax = fmaxf(smax, sv[qb]);
-  }
-  const int ev = pow2_exponent(wave_max(smax));
-  const float vinv = exp2i(-ev);
-#pragma unroll
-  for (int qb = 0; qb < NQB; qb++) st_s[qb * WT + lane] = sv[qb] * vinv;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---- V pass.  Weight operands, one per pair of 16-token tiles: lane
-  // (n, kg) holds for column n = (qblock bq, head 2 gi + brl, part) the
-  // weights of tokens 4 kg .. 4 kg + 3 of tile 2 tp and of tile 2 tp + 1 ----
-  static_assert(NT % 2 == 0, "tiles pair up along the value contraction");
+  int ev = 0;
   const int bq = l16 >> 2, brl = (l16 >> 1) & 1, bpart = l16 & 1;
-  u32x4 bw[NT / 2][NG];
+  auto run_batch = [&](const int tw, auto tt0c, auto ntbc, const uint2 ks_, const uint2 vs_, const uint32_t nm_) {
+    constexpr int TT0 = decltype(tt0c)::value, NTB = decltype(ntbc)::value;
+    // ---- K pass: D[tile][(qblock, head, part)][token] over the eight
+    // 4-element slices j of every qblock.  The key operand of lane (t, q) for
+    // slice j is (hi pair, lo pair) of codes 4j, 4j+1 and of codes 4j+2, 4j+3
+    // of qblock q of token t: two pair-table reads.  Lane (t, q) ends with
+    // token t's (unscaled) qblock-q partial of each head. ----
+    f32x4 dk[NTB][NG];
 #pragma unroll
-  for (int tp = 0; tp < NT / 2; tp++) {
+    for (int tt = 0; tt < NTB; tt++)
 #pragma unroll
-    for (int gi = 0; gi < NG; gi++) {
-      const int r = min(2 * gi + brl, NR - 1);  // NR == 1: the second head's columns are never read
-      uint32_t w[4];
+      for (int gi = 0; gi < NG; gi++) dk[tt][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int tt = 2 * tp + u;
-        const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * tt + 4 * lg);
-        const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * tt + 4 * lg);
-        const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
-        const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
-        w[2 * u] = bpart ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
-        w[2 * u + 1] = bpart ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
-      }
-      bw[tp][gi] = u32x4{w[0], w[1], w[2], w[3]};
-    }
-  }
-  // The value codes are decoded by the same pair-table lookup as the keys,
-  // read through the transposing LDS read: lane l of a 16-lane group holds
-  // qblock l % 4 of token 4 g + l / 4 (g = lane group), so lane 4 a + b
-  // receives part b (hi c0, hi c1, lo c0, lo c1) of the entries of qblock a
-  // for tokens 4 g .. 4 g + 3 -- the value operand's row (a, b) at those
-  // tokens, two tiles per 16 x 16 x 32 product.  D then holds rows =
-  // (qblock, value part), columns (qblock, head, weight part); a lane's rows
-  // count only under its own qblock's columns, and hi + lo of a value sum
-  // inside the lane (rows 4 g + i and 4 g + i + 2).
+    for (int j = 0; j < 8; j++) {
+      u32x4 qa[NG];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    f32x4 dv[2][NG];
+      for (int gi = 0; gi < NG; gi++) qa[gi] = s_qa[(gi * 8 + j) * 64 + lane];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+      for (int tt = 0; tt < NTB; tt++) {
+        const uint2 e0 = s_pair[pair_code<BITS>(kq[TT0 + tt], 2 * j)];
+        const uint2 e1 = s_pair[pair_code<BITS>(kq[TT0 + tt], 2 * j + 1)];
+        const u32x4 kb = {e0.x, e0.y, e1.x, e1.y};
 #pragma unroll
-      for (int gi = 0; gi < NG; gi++) dv[h][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int tp = 0; tp < NT / 2; tp++) {
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const u32x2 r0 = lds_read_tr16(s_pair + pair_code<BITS>(vq[2 * tp], 2 * j + h));
-        const u32x2 r1 = lds_read_tr16(s_pair + pair_code<BITS>(vq[2 * tp + 1], 2 * j + h));
-        const u32x4 va = {r0[0], r0[1], r1[0], r1[1]};
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) dv[h][gi] = mfma(va, bw[tp][gi], dv[h][gi]);
+        for (int gi = 0; gi < NG; gi++) dk[tt][gi] = mfma(qa[gi], kb, dk[tt][gi]);
       }
     }
-    // lane (n, lg) holds column n at rows (qblock lg, parts hi c0, hi c1,
-    // lo c0, lo c1) of pairs 2 j and 2 j + 1; the weight parts of one head
-    // sit in lanes n and n ^ 1
+    if constexpr (QJL) {
+      // sum_j rq_j (2 b_j - 1) per (head, token) on the matrix core: the sign
+      // operand of lane (t, kg) for MFMA s is the +-1 pairs of byte s of its
+      // sign word; the (unscaled) sums go to st_p, which the softmax
+      // overwrites only after they are read
+      f32x4 dq[NTB];
 #pragma unroll
-    for (int gi = 0; gi < NG; gi++) {
-      f32x4 o;
+      for (int tt = 0; tt < NTB; tt++) dq[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float x = dv[i >> 1][gi][i & 1] + dv[i >> 1][gi][(i & 1) + 2];
-        o[i] = dpp_quad_xor1(x) + x;
+      for (int sl = 0; sl < 4; sl++) {
+        const u32x4 ra = s_ra[sl * 64 + lane];
+#pragma unroll
+        for (int tt = 0; tt < NTB; tt++) {
+          const uint32_t byte = (sq[TT0 + tt] >> (8 * sl)) & 0xffu;
+          const uint2 n0 = s_nib[byte & 15u], n1 = s_nib[byte >> 4];
+          dq[tt] = mfma(ra, u32x4{n0.x, n0.y, n1.x, n1.y}, dq[tt]);
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);  // the sums stay outside the store's branch (DPP adds)
-      const int r = 2 * gi + brl;
-      if (bpart == 0 && bq == lg && r < NR) *reinterpret_cast<f32x4 *>(comb + r * HD + 32 * lg + 4 * j) = o;
+#pragma unroll
+      for (int tt = 0; tt < NTB; tt++)
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const int r = 2 * lg + u;
+          if (r < NR) st_p[r * WT + 16 * tt + l16] = dq[tt][2 * u] + dq[tt][2 * u + 1];
+        }
     }
-  }
+#pragma unroll
+    for (int tt = 0; tt < NTB; tt++) {
+      uint32_t *dst = st_x + (lg * WT + 16 * tt + l16) * NR;
+      uint32_t xv[NR];
+#pragma unroll
+      for (int r = 0; r < NR; r++) xv[r] = f2u(dk[tt][r >> 1][2 * (r & 1)] + dk[tt][r >> 1][2 * (r & 1) + 1]);
+      if constexpr (NR == 1) {
+        dst[0] = xv[0];
+      } else if constexpr (NR == 2) {
+        *reinterpret_cast<uint2 *>(dst) = make_uint2(xv[0], xv[1]);
+      } else {
+        *reinterpret_cast<uint4 *>(dst) = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane = token: the four qblock partials times the token's key scales
+    float score[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) score[r] = 0.f;
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) {
+      const uint32_t sbits = (qb < 2 ? ks_.x : ks_.y) >> ((qb & 1) ? 16 : 0);
+      const float sk = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+      const uint32_t *src = st_x + (qb * WT + lane) * NR;
+      uint32_t xv[NR];
+      if constexpr (NR == 1) {
+        xv[0] = src[0];
+      } else if constexpr (NR == 2) {
+        const uint2 t = *reinterpret_cast<const uint2 *>(src);
+        xv[0] = t.x; xv[1] = t.y;
+      } else {
+        const uint4 t = *reinterpret_cast<const uint4 *>(src);
+        xv[0] = t.x; xv[1] = t.y; xv[2] = t.z; xv[3] = t.w;
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++) score[r] = __builtin_fmaf(u2f(xv[r]), sk, score[r]);
+    }
+
+    // ---- softmax (base 2) of this batch's tokens ----
+    const int tok = tw + lane;
+    const bool valid = lane < 16 * NTB && tok < len;
+    float mb[NR], p[NR], lb[NR];
+    float corr[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) corr[r] = 0.f;
+    if constexpr (QJL) {
+      const float cn = f16_to_f32((uint16_t)nm_) * a.qjl_c;
+#pragma unroll
+      for (int r = 0; r < NR; r++) corr[r] = st_p[r * WT + lane] * (cn * erscale[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const float sc = valid ? (QJL ? __builtin_fmaf(score[r], escale[r], corr[r]) : score[r] * escale[r]) : -INFINITY;
+      mb[r] = wave_max(sc);
+      p[r] = valid ? __builtin_amdgcn_exp2f(sc - mb[r]) : 0.f;
+      st_p[r * WT + lane] = p[r];
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) lb[r] = wave_sum(p[r]);
+
+    // ---- V scales * 2^-Ev to LDS (lane = token) ----
+    float sv[NQB];
+    float smax = 0.f;
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) {
+      const uint32_t sbits = (qb < 2 ? vs_.x : vs_.y) >> ((qb & 1) ? 16 : 0);
+      sv[qb] = fabsf(f16_to_f32((uint16_t)(sbits & 0xffffu)));
+      smax = fmaxf(smax, sv[qb]);
+    }
+    const int evb = pow2_exponent(wave_max(smax));
+    const float vinv = exp2i(-evb);
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) st_s[qb * WT + lane] = sv[qb] * vinv;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- V pass.  Weight operands, one per pair of 16-token tiles: lane
+    // (n, kg) holds for column n = (qblock bq, head 2 gi + brl, part) the
+    // weights of tokens 4 kg .. 4 kg + 3 of tile 2 tp and of tile 2 tp + 1 ----
+    static_assert(NTB % 2 == 0, "tiles pair up along the value contraction");
+    u32x4 bw[NTB / 2][NG];
+#pragma unroll
+    for (int tp = 0; tp < NTB / 2; tp++) {
+#pragma unroll
+      for (int gi = 0; gi < NG; gi++) {
+        const int r = min(2 * gi + brl, NR - 1);  // NR == 1: the second head's columns are never read
+        uint32_t w[4];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const int tt = 2 * tp + u;
+          const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * tt + 4 * lg);
+          const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * tt + 4 * lg);
+          const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
+          const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
+          w[2 * u] = bpart ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
+          w[2 * u + 1] = bpart ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
+        }
+        bw[tp][gi] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    }
+    // The value codes are decoded by the same pair-table lookup as the keys,
+    // read through the transposing LDS read: lane l of a 16-lane group holds
+    // qblock l % 4 of token 4 g + l / 4 (g = lane group), so lane 4 a + b
+    // receives part b (hi c0, hi c1, lo c0, lo c1) of the entries of qblock a
+    // for tokens 4 g .. 4 g + 3 -- the value operand's row (a, b) at those
+    // tokens, two tiles per 16 x 16 x 32 product.  D then holds rows =
+    // (qblock, value part), columns (qblock, head, weight part); a lane's rows
+    // count only under its own qblock's columns, and hi + lo of a value sum
+    // inside the lane (rows 4 g + i and 4 g + i + 2).
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      f32x4 dv[2][NG];
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) dv[h][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int tp = 0; tp < NTB / 2; tp++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const u32x2 r0 = lds_read_tr16(s_pair + pair_code<BITS>(vq[TT0 + 2 * tp], 2 * j + h));
+          const u32x2 r1 = lds_read_tr16(s_pair + pair_code<BITS>(vq[TT0 + 2 * tp + 1], 2 * j + h));
+          const u32x4 va = {r0[0], r0[1], r1[0], r1[1]};
+#pragma unroll
+          for (int gi = 0; gi < NG; gi++) dv[h][gi] = mfma(va, bw[tp][gi], dv[h][gi]);
+        }
+      }
+      // lane (n, lg) holds column n at rows (qblock lg, parts hi c0, hi c1,
+      // lo c0, lo c1) of pairs 2 j and 2 j + 1; the weight parts of one head
+      // sit in lanes n and n ^ 1
+#pragma unroll
+      for (int gi = 0; gi < NG; gi++) {
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float x = dv[i >> 1][gi][i & 1] + dv[i >> 1][gi][(i & 1) + 2];
+          o[i] = dpp_quad_xor1(x) + x;
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the sums stay outside the store's branch (DPP adds)
+        const int r = 2 * gi + brl;
+        if (bpart == 0 && bq == lg && r < NR) {
+          *reinterpret_cast<f32x4 *>(comb + r * HD + 32 * lg + 4 * j) = o;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      m_w[r] = mb[r];
+      l_w[r] = lb[r];
+    }
+    ev = evb;
+  };
+  run_batch(tw_a, I0{}, INT{}, ksc, vsc, nrm);
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < NR; r++) {
