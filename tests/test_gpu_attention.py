@@ -178,6 +178,43 @@ def test_decode_batched_varlen(tq):
         assert np.abs(out[bi] - refs[bi]).max() <= TOL, bi
 
 
+def test_decode_c4_full_size(tq):
+    """BASELINE config 4 at full size: PQO4, 32 q-heads / 8 KV heads, batch 16
+    with contexts drawn uniformly from [4096, 16384] (seeded), bf16 queries,
+    split-K over each context; every sequence against the dense oracle."""
+    rng = np.random.default_rng(44)
+    bits, h, hkv, bsz = 4, 32, 8, 16
+    lens = [int(x) for x in rng.integers(4096, 16385, bsz)]
+    cap = max(lens)
+    pd = 128 * bits // 8
+    kidx = np.zeros((bsz, hkv, cap, pd), np.uint8)
+    vidx = np.zeros_like(kidx)
+    ksc = np.zeros((bsz, hkv, cap, 4), np.int16)
+    vsc = np.zeros_like(ksc)
+    qs = bf16_round(rng.standard_normal((bsz, h, 128)).astype(np.float32) / np.float32(math.sqrt(128)))
+    refs = []
+    for bi, t in enumerate(lens):
+        k = kv_outlier(rng, hkv, t)
+        v = kv_outlier(rng, hkv, t)
+        pk, sk = orc.pqo_quantize(bits, k.reshape(-1, 128), 128)
+        pv, sv = orc.pqo_quantize(bits, v.reshape(-1, 128), 128)
+        kidx[bi, :, :t] = pk.reshape(hkv, t, pd)
+        vidx[bi, :, :t] = pv.reshape(hkv, t, pd)
+        ksc[bi, :, :t] = sk.view(np.int16).reshape(hkv, t, 4)
+        vsc[bi, :, :t] = sv.view(np.int16).reshape(hkv, t, 4)
+        kd = orc.pqo_dequantize(bits, pk, sk, 128).reshape(hkv, t, 128)
+        vd = orc.pqo_dequantize(bits, pv, sv, 128).reshape(hkv, t, 128)
+        refs.append(orc.attention_dense(qs[bi], kd, vd, 1.0 / math.sqrt(128)))
+    ws = tq.AttentionWorkspace(bsz, h, hkv, 128, cap)
+    out = tq.pqo_decode_attention(_dev(bf16_bits(qs)).view(torch.bfloat16), _dev(kidx), _dev(ksc), _dev(vidx),
+                                  _dev(vsc), torch.tensor(lens, dtype=torch.int32, device="cuda"), hkv, bits, cap,
+                                  cap, hkv * cap, 1.0 / math.sqrt(128), ws)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for bi in range(bsz):
+        assert np.abs(out[bi] - refs[bi]).max() <= TOL, (bi, lens[bi])
+
+
 @pytest.mark.parametrize("bits", [3, 4])
 def test_fused_attention_reference_abi(tq, bits):
     """tq_fused_attention (reference FFI shape, two launches, 512-token partitions)."""

@@ -6,9 +6,12 @@ import numpy as np
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
     """Round f32 to bf16 (nearest-even) and return the f32 values."""
-    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    return r.astype(np.uint32).view(np.float32)
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    r = (u >> 16) & np.uint32(1)   # ties to even
+    r += u
+    r += np.uint32(0x7FFF)           # wraps mod 2^32 like the truncating 64-bit form
+    r &= np.uint32(0xFFFF0000)
+    return r.view(np.float32)
 
 
 def bf16_bits(x: np.ndarray) -> np.ndarray:
