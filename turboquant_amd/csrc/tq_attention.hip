@@ -663,8 +663,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         for (int i = 0; i < 4; i++) {
           const float x = dv[i >> 1][gi][i & 1] + dv[i >> 1][gi][(i & 1) + 2];
           o[i] = dpp_quad_xor1(x) + x;
+          asm volatile("" : "+v"(o[i]));  // the add stays beside its DPP read (one v_add_f32_dpp), not sunk into the store's branch
         }
-        __builtin_amdgcn_sched_barrier(0);  // the sums stay outside the store's branch (DPP adds)
         const int r = 2 * gi + brl;
         if (bpart == 0 && bq == lg && r < NR) {
           *reinterpret_cast<f32x4 *>(comb + r * HD + 32 * lg + 4 * j) = o;
