@@ -607,6 +607,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     // weights of tokens 4 kg .. 4 kg + 3 of tile 2 tp and of tile 2 tp + 1 ----
     static_assert(NTB % 2 == 0, "tiles pair up along the value contraction");
     u32x4 bw[NTB / 2][NG];
+    const float kpart = bpart ? -1.f : 0.f;
 #pragma unroll
     for (int tp = 0; tp < NTB / 2; tp++) {
 #pragma unroll
@@ -619,9 +620,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
           const float4 p4 = *reinterpret_cast<const float4 *>(st_p + r * WT + 16 * tt + 4 * lg);
           const float4 s4 = *reinterpret_cast<const float4 *>(st_s + bq * WT + 16 * tt + 4 * lg);
           const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
-          const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
-          w[2 * u] = bpart ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
-          w[2 * u + 1] = bpart ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
+          w[2 * u] = pack_rem(x0, x1, pack_f16(x0, x1), kpart);          // hi (part 0) or lo (part 1)
+          w[2 * u + 1] = pack_rem(x2, x3, pack_f16(x2, x3), kpart);
         }
         bw[tp][gi] = u32x4{w[0], w[1], w[2], w[3]};
       }

@@ -163,6 +163,14 @@ __device__ __forceinline__ float split_hi(float x) { return u2f(f2u(x) & 0xffffe
 __device__ __forceinline__ uint32_t pack_f16(float lo_half, float hi_half) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo_half, hi_half));
 }
+// The same split from the f16 side: hi = pack_f16(x0, x1) (round toward zero
+// is the 11-bit cut), and pack_rem(x0, x1, hi, k) = the f16 pair of x + k * hi,
+// i.e. the lower parts for k = -1 (x - hi is exact in f32; the f16 -> f32
+// widening folds into v_fma_mix_f32) and the upper parts again for k = 0.
+__device__ __forceinline__ uint32_t pack_rem(float x0, float x1, uint32_t hi, float k) {
+  const auto h = __builtin_bit_cast(__fp16 __attribute__((ext_vector_type(2))), hi);
+  return pack_f16(__builtin_fmaf((float)h[0], k, x0), __builtin_fmaf((float)h[1], k, x1));
+}
 // E with m * 2^-E in [0.5, 1) for finite m > 0 (0 for m == 0), clamped so
 // that 2^E and 2^-E are normal f32.
 __device__ __forceinline__ int pow2_exponent(float m) {

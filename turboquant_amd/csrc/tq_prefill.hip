@@ -98,6 +98,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   __shared__ uint2 s_nib[16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // -1 in a register the compiler cannot see through, so x + (-1) * hi stays
+  // one v_fma_mix_f32 instead of a widening convert and a subtraction
+  float mone = -1.f;
+  asm volatile("" : "+v"(mone));
   const int l16 = lane & 15, lg = lane >> 4;
   const int g = blockIdx.y;
   const int i0 = blockIdx.x * QB;
@@ -282,8 +286,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
           const uint32_t code = pair_code<BITS>(kw, p);
           const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * kf;
           const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * kf;
-          const float h0 = split_hi(x0), h1 = split_hi(x1);
-          kt[ftok * kKStride + 16 * fqb + p] = make_uint2(pack_f16(h0, h1), pack_f16(x0 - h0, x1 - h1));
+          const uint32_t hi = pack_f16(x0, x1);
+          kt[ftok * kKStride + 16 * fqb + p] = make_uint2(hi, pack_rem(x0, x1, hi, mone));
         }
         uint32_t hw[NP], lw[NP];
 #pragma unroll
@@ -291,9 +295,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
           const uint32_t code = pair_code<BITS>(vw, P0 + pp);
           const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * vf;
           const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * vf;
-          const float h0 = split_hi(x0), h1 = split_hi(x1);
-          hw[pp] = pack_f16(h0, h1);
-          lw[pp] = pack_f16(x0 - h0, x1 - h1);
+          hw[pp] = pack_f16(x0, x1);
+          lw[pp] = pack_rem(x0, x1, hw[pp], mone);
         }
         // token-major rows: this thread's 2 NP elements, 16-byte stores per plane
         uint4 *vrh = reinterpret_cast<uint4 *>(vth + ftok * kVRow + 32 * fqb + 2 * P0);
@@ -378,11 +381,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         ls += e;
         p[i] = e * exp2i(max(s_ev[16 * tb + 4 * lg + i] - ev_new, -126));
       }
-      float ph[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) ph[i] = split_hi(p[i]);
-      pb[tb][0] = u32x2{pack_f16(ph[0], ph[1]), pack_f16(ph[2], ph[3])};
-      pb[tb][1] = u32x2{pack_f16(p[0] - ph[0], p[1] - ph[1]), pack_f16(p[2] - ph[2], p[3] - ph[3])};
+      pb[tb][0] = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
+      pb[tb][1] = u32x2{pack_rem(p[0], p[1], pb[tb][0][0], mone), pack_rem(p[2], p[3], pb[tb][0][1], mone)};
     }
     l_run = l_run * alpha + ls;
     // ---- O^T += V^T P^T, two 16-token blocks per 16x16x32 product.  The
