@@ -635,13 +635,15 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     // (qblock, value part), columns (qblock, head, weight part); a lane's rows
     // count only under its own qblock's columns, and hi + lo of a value sum
     // inside the lane (rows 4 g + i and 4 g + i + 2).
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      f32x4 dv[2][NG];
+    // Software-pipelined over the eight pair slices: slice j + 1's products
+    // are issued before slice j's sums and store, so their latency overlaps.
+    f32x4 dv[2][2][NG];  // [slice parity][h][gi]
+    auto v_products = [&](auto jc) {
+      constexpr int j = decltype(jc)::value, sl = j & 1;
 #pragma unroll
       for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int gi = 0; gi < NG; gi++) dv[h][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int gi = 0; gi < NG; gi++) dv[sl][h][gi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int tp = 0; tp < NTB / 2; tp++) {
 #pragma unroll
@@ -650,18 +652,21 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
           const u32x2 r1 = lds_read_tr16(s_pair + pair_code<BITS>(vq[TT0 + 2 * tp + 1], 2 * j + h));
           const u32x4 va = {r0[0], r0[1], r1[0], r1[1]};
 #pragma unroll
-          for (int gi = 0; gi < NG; gi++) dv[h][gi] = mfma(va, bw[tp][gi], dv[h][gi]);
+          for (int gi = 0; gi < NG; gi++) dv[sl][h][gi] = mfma(va, bw[tp][gi], dv[sl][h][gi]);
         }
       }
-      // lane (n, lg) holds column n at rows (qblock lg, parts hi c0, hi c1,
-      // lo c0, lo c1) of pairs 2 j and 2 j + 1; the weight parts of one head
-      // sit in lanes n and n ^ 1
+    };
+    // lane (n, lg) holds column n at rows (qblock lg, parts hi c0, hi c1,
+    // lo c0, lo c1) of pairs 2 j and 2 j + 1; the weight parts of one head
+    // sit in lanes n and n ^ 1
+    auto v_store = [&](auto jc) {
+      constexpr int j = decltype(jc)::value, sl = j & 1;
 #pragma unroll
       for (int gi = 0; gi < NG; gi++) {
         f32x4 o;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const float x = dv[i >> 1][gi][i & 1] + dv[i >> 1][gi][(i & 1) + 2];
+          const float x = dv[sl][i >> 1][gi][i & 1] + dv[sl][i >> 1][gi][(i & 1) + 2];
           o[i] = dpp_quad_xor1(x) + x;
           asm volatile("" : "+v"(o[i]));  // the add stays beside its DPP read (one v_add_f32_dpp), not sunk into the store's branch
         }
@@ -670,7 +675,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
           *reinterpret_cast<f32x4 *>(comb + r * HD + 32 * lg + 4 * j) = o;
         }
       }
-    }
+    };
+    v_products(std::integral_constant<int, 0>{});
+    static_for<0, 8>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if constexpr (j + 1 < 8) v_products(std::integral_constant<int, j + 1>{});
+      v_store(jc);
+    });
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       m_w[r] = mb[r];

@@ -3,6 +3,7 @@
 // DPP wave reductions and the PQO decode constants.
 #pragma once
 
+#include <type_traits>
 #include "tq_device.h"
 
 namespace tqm {
@@ -187,6 +188,15 @@ __device__ __forceinline__ uint32_t pair_code(const uint32_t (&w)[BITS], int p) 
   const int pos = W * p, wi = pos >> 5, sh = pos & 31;
   if (sh + W <= 32) return __builtin_amdgcn_ubfe(w[wi], sh, W);
   return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & ((1u << W) - 1u);
+}
+
+// f(integral_constant<int, I>) for I = B .. E - 1, in order, at compile time.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 }  // namespace tqm
