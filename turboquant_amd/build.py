@@ -27,6 +27,8 @@ COMMON = [
     "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}", f"-I{CSRC}", "-Wall", "-Wno-unused-function",
+    # the first 13 kernel-argument dwords arrive in SGPRs at wave launch
+    "-mllvm", "-amdgpu-kernarg-preload-count=13",
 ]
 
 

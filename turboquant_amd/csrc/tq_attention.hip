@@ -207,8 +207,16 @@ __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, fl
   }
 }
 
+// The record pointers and strides also come as leading scalar arguments
+// (copies of a's fields, plus the single length or -1 when the lengths are
+// per sequence in device memory): the build preloads the first kernel-argument dwords
+// into SGPRs at wave launch, so the first record loads need no kernel-argument
+// fetch.
 template <int BITS, int MODE, int NR, bool INLINE_MERGE>
-__global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_idx, const uint8_t *v_idx,
+                                                               const uint16_t *k_sc, const uint16_t *v_sc,
+                                                               long long seq_stride, long long kv_head_stride,
+                                                               int len_hint, AttnArgs a) {
   constexpr int CB = MODE == kModePqo ? BITS : BITS - 1;  // codebook bits
   constexpr bool QJL = MODE == kModeTq;
   constexpr int NQB = 4, HD = 128, CH = kChunk;
@@ -261,8 +269,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int l16 = lane & 15, lg = lane >> 4;  // matrix-core column / row group of this lane
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int t0 = c * CH;
-  const long long rec0 = (long long)b * a.seq_stride + (long long)g * a.kv_head_stride;
-  const uint8_t *kbase = a.k_idx + rec0 * PACKED, *vbase = a.v_idx + rec0 * PACKED;
+  const long long rec0 = (long long)b * seq_stride + (long long)g * kv_head_stride;
+  const uint8_t *kbase = k_idx + rec0 * PACKED, *vbase = v_idx + rec0 * PACKED;
 
   // ---- the query goes out first (it does not depend on the sequence
   // length), loaded by the waves that rotate it, one element per lane (whole
@@ -276,7 +284,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     else qbits = static_cast<const uint16_t *>(a.q)[qidx];
     if constexpr (QJL) rqv = a.rq[qidx];
   }
-  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
+  // len_hint: the single length, or -1 for per-sequence device lengths
+  const int len = len_hint >= 0 ? len_hint : min(max(a.kv_lens[b], 0), a.max_len);
   if (t0 >= len) {  // empty tile: not counted by the merge
     __builtin_amdgcn_s_waitcnt(0);
     return;
@@ -303,8 +312,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   using I0 = std::integral_constant<int, 0>;
   using INT = std::integral_constant<int, NT>;
   const int tw_a = t0 + wave * WT;
-  const uint8_t *ksbase = reinterpret_cast<const uint8_t *>(a.k_sc + rec0 * NQB);
-  const uint8_t *vsbase = reinterpret_cast<const uint8_t *>(a.v_sc + rec0 * NQB);
+  const uint8_t *ksbase = reinterpret_cast<const uint8_t *>(k_sc + rec0 * NQB);
+  const uint8_t *vsbase = reinterpret_cast<const uint8_t *>(v_sc + rec0 * NQB);
   uint32_t kq[NT][QW], vq[NT][QW];
   uint2 ksc, vsc;
   uint32_t sq[NT];   // QJL: sign word lg of token 16 tt + l16
@@ -816,9 +825,15 @@ AttnArgs base_args() {
 
 template <int BITS, int MODE, bool INLINE>
 int launch_decode_m(const AttnArgs &a, int nr, dim3 grid, hipStream_t st) {
-  if (nr == 1) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 1, INLINE>), grid, dim3(kThreads), 0, st, a);
-  else if (nr == 2) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 2, INLINE>), grid, dim3(kThreads), 0, st, a);
-  else hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 4, INLINE>), grid, dim3(kThreads), 0, st, a);
+  if (nr == 1) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 1, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
+                       a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
+                       a.kv_lens ? -1 : a.single_len, a);
+  else if (nr == 2) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 2, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
+                       a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
+                       a.kv_lens ? -1 : a.single_len, a);
+  else hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 4, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
+                       a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
+                       a.kv_lens ? -1 : a.single_len, a);
   return tqh::check_launch("attn_decode_kernel");
 }
 
