@@ -827,13 +827,13 @@ template <int BITS, int MODE, bool INLINE>
 int launch_decode_m(const AttnArgs &a, int nr, dim3 grid, hipStream_t st) {
   if (nr == 1) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 1, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
                        a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
-                       a.kv_lens ? -1 : a.single_len, a);
+                       a.kv_lens ? -1 : max(a.single_len, 0), a);
   else if (nr == 2) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 2, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
                        a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
-                       a.kv_lens ? -1 : a.single_len, a);
+                       a.kv_lens ? -1 : max(a.single_len, 0), a);
   else hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 4, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
                        a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
-                       a.kv_lens ? -1 : a.single_len, a);
+                       a.kv_lens ? -1 : max(a.single_len, 0), a);
   return tqh::check_launch("attn_decode_kernel");
 }
 
