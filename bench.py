@@ -354,10 +354,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # default warmup: more than two passes over the rotating cache copies, so
-    # the timed steps see no first-touch (page-table) misses and the clock has
-    # left idle
-    ap.add_argument("--warmup", type=int, default=100)
+    # default warmup: ~30 ms of decode launches (many passes over the rotating
+    # cache copies), so the timed steps see no first-touch (page-table) misses
+    # and the clock has come up from idle after the host-side setup
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the reference kernel for "
