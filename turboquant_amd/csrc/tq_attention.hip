@@ -677,7 +677,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_
         for (int i = 0; i < 4; i++) {
           const float x = dv[sl][i >> 1][gi][i & 1] + dv[sl][i >> 1][gi][(i & 1) + 2];
           o[i] = dpp_quad_xor1(x) + x;
-          asm volatile("" : "+v"(o[i]));  // the add stays beside its DPP read (one v_add_f32_dpp), not sunk into the store's branch
+          // keeps the add beside its DPP read (one v_add_f32_dpp), not sunk
+          // into the store's branch
+          asm volatile("" : "+v"(o[i]));
         }
         const int r = 2 * gi + brl;
         if (bpart == 0 && bq == lg && r < NR) {
@@ -823,17 +825,19 @@ AttnArgs base_args() {
   return a;
 }
 
+template <int BITS, int MODE, int NR, bool INLINE>
+void launch_decode_nr(const AttnArgs &a, dim3 grid, hipStream_t st) {
+  // len_hint: the single length, or -1 when the lengths are per sequence
+  const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
+  hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, NR, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
+                     a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+}
+
 template <int BITS, int MODE, bool INLINE>
 int launch_decode_m(const AttnArgs &a, int nr, dim3 grid, hipStream_t st) {
-  if (nr == 1) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 1, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
-                       a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
-                       a.kv_lens ? -1 : max(a.single_len, 0), a);
-  else if (nr == 2) hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 2, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
-                       a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
-                       a.kv_lens ? -1 : max(a.single_len, 0), a);
-  else hipLaunchKernelGGL((attn_decode_kernel<BITS, MODE, 4, INLINE>), grid, dim3(kThreads), 0, st, a.k_idx, a.v_idx,
-                       a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride,
-                       a.kv_lens ? -1 : max(a.single_len, 0), a);
+  if (nr == 1) launch_decode_nr<BITS, MODE, 1, INLINE>(a, grid, st);
+  else if (nr == 2) launch_decode_nr<BITS, MODE, 2, INLINE>(a, grid, st);
+  else launch_decode_nr<BITS, MODE, 4, INLINE>(a, grid, st);
   return tqh::check_launch("attn_decode_kernel");
 }
 
