@@ -49,6 +49,8 @@ def _load():
         "tqo_pqo_decode_signs": (None, [_f32p]),
         "tqo_pqo_rotate_block": (None, [_f32p, _f32p]),
         "tqo_pqo_rotate_block_gemm": (None, [_f32p, _f32p]),
+        "tqo_pqo_rotate_block_fma": (None, [_f32p, _f32p]),
+        "tqo_pqo_rotate_blocks": (C.c_int, [C.c_int, _sz, _f32p, _f32p]),
         "tqo_pqo_quantize_rotated": (C.c_int, [C.c_int, _sz, _f32p, _u8p, _u16p, C.c_float]),
         "tqo_pqo_quantize": (C.c_int, [C.c_int, _sz, _sz, _f32p, _u8p, _u16p]),
         "tqo_pqo_dequantize": (C.c_int, [C.c_int, _sz, _sz, _u8p, _u16p, _f32p]),
@@ -224,15 +226,17 @@ def pqo_decode_signs() -> np.ndarray:
     return out
 
 
-def pqo_rotate(x: np.ndarray, gemm: bool = False) -> np.ndarray:
+ROTATE_ORDERS = {"butterfly": 0, "dot": 1, "fma": 2}
+
+
+def pqo_rotate(x: np.ndarray, gemm: bool = False, order: str | None = None) -> np.ndarray:
+    """Forward block rotation x @ R_fwd of [n, 32] blocks in one f32 evaluation
+    order: "butterfly" (the oracle's), "dot" (separately rounded products
+    summed in k order; gemm=True) or "fma" (one fused multiply-add chain)."""
     x = _c(x, np.float32).reshape(-1, 32)
     out = np.zeros_like(x)
-    fn = lib.tqo_pqo_rotate_block_gemm if gemm else lib.tqo_pqo_rotate_block
-    for i in range(x.shape[0]):
-        row = np.ascontiguousarray(x[i])
-        o = np.zeros(32, np.float32)
-        fn(row, o)
-        out[i] = o
+    o = ROTATE_ORDERS[order or ("dot" if gemm else "butterfly")]
+    _check(lib.tqo_pqo_rotate_blocks(o, x.shape[0], x, out))
     return out
 
 

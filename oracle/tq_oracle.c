@@ -551,6 +551,38 @@ void tqo_pqo_rotate_block_gemm(const float *x, float *r)
     }
 }
 
+/* The same product as one fused multiply-add chain per output, k = 0..31 in
+   order from +0: the accumulation a K=32 gemm microkernel on FMA hardware
+   most plausibly performs for quantize_tensor.rs:100,104 (candle's CPU
+   matmul; its order is not in the reference tree). */
+void tqo_pqo_rotate_block_fma(const float *x, float *r)
+{
+    float s[32];
+    tqo_pqo_sign32(s);
+    float c = 1.0f / sqrtf(32.0f);
+    for (int j = 0; j < 32; j++) {
+        float acc = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            float h = (__builtin_popcount((unsigned)(i & j)) & 1) ? -c : c;
+            acc = fmaf(x[i], h * s[j], acc);
+        }
+        r[j] = acc;
+    }
+}
+
+/* n blocks of 32 in one of the orders above: 0 butterfly, 1 separately
+   rounded dot products, 2 fused multiply-add chains. */
+int tqo_pqo_rotate_blocks(int order, size_t n, const float *x, float *r)
+{
+    if (order < 0 || order > 2) return TQO_ERR_INVALID_ARGUMENT;
+    for (size_t b = 0; b < n; b++) {
+        if (order == 0) tqo_pqo_rotate_block(x + 32 * b, r + 32 * b);
+        else if (order == 1) tqo_pqo_rotate_block_gemm(x + 32 * b, r + 32 * b);
+        else tqo_pqo_rotate_block_fma(x + 32 * b, r + 32 * b);
+    }
+    return TQO_OK;
+}
+
 /* quantize_tensor.rs:103-110 (MaxNorm scale), :161-176 (bucketize),
    :68-70 (signed f16 scale), :264-274 (packing); the same contract as the
    reference kernel entry tq_quant_maxnorm_batch (ffi.rs:24-37).

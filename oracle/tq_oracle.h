@@ -80,6 +80,8 @@ void tqo_pqo_sign32(float *out);
 void tqo_pqo_decode_signs(float *out);
 void tqo_pqo_rotate_block(const float *x, float *r);
 void tqo_pqo_rotate_block_gemm(const float *x, float *r);
+void tqo_pqo_rotate_block_fma(const float *x, float *r);
+int tqo_pqo_rotate_blocks(int order, size_t n, const float *x, float *r);
 int tqo_pqo_quantize_rotated(int bits, size_t num_blocks, const float *rotated,
                              uint8_t *packed_out, uint16_t *scales_out, float scale_sign);
 int tqo_pqo_quantize(int bits, size_t n, size_t head_dim, const float *x,

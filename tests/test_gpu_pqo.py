@@ -184,3 +184,40 @@ def test_pqo_full_size_c2_properties(tq):
         assert np.array_equal(p[idx].cpu().numpy(), p_ref)
         assert np.array_equal(_u16(s[idx]), s_ref)
         del p, s, d
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_end_to_end_codes_against_gemm_rotation_orders(tq, bits):
+    """End-to-end code parity on C2-shaped data (bf16 N(0,1) K/V with 4 of 128
+    channels x8; 65,536 vectors): the HIP quantize (butterfly rotation) against
+    the codes of the rotation evaluated as separately rounded dot products and
+    as fused multiply-add chains (the reference rotates with candle's matmul,
+    quantize_tensor.rs:100,104, whose f32 order is not in the reference tree).
+    Every differing code is one bin away, with the two quotients r/s on either
+    side of the boundary between (within 1e-6 of it); at most 2e-5 of the
+    codes differ (about 4-7e-6 measured)."""
+    x = kv_outlier(np.random.default_rng(0), 8, 8192).reshape(-1, 128)
+    p, s = tq.pqo_quantize(_dev(bf16_bits(x)).view(torch.bfloat16), bits)
+    u_hip = np.unpackbits(p.cpu().numpy().reshape(-1, 4 * bits), axis=1, bitorder="little")
+    u_hip = (u_hip.reshape(-1, 32, bits) * (1 << np.arange(bits))).sum(2)
+    c, bnd, outer = orc.pqo_codebook(bits)
+    mul = np.float32(1.0 / np.float64(outer))
+    blocks = x.reshape(-1, 32)
+    for order in ("dot", "fma"):
+        r = orc.pqo_rotate(blocks, order=order)
+        pr, _ = orc.pqo_quantize_rotated(bits, r)
+        u_ref = (np.unpackbits(pr, axis=1, bitorder="little").reshape(-1, 32, bits) * (1 << np.arange(bits))).sum(2)
+        sc = np.maximum((np.abs(r).max(1) * mul).astype(np.float32), np.float32(1e-10))
+        v_ref = (r / sc[:, None]).astype(np.float32)
+        rb = orc.pqo_rotate(blocks, order="butterfly")
+        scb = np.maximum((np.abs(rb).max(1) * mul).astype(np.float32), np.float32(1e-10))
+        v_hip = (rb / scb[:, None]).astype(np.float32)
+        diff = np.argwhere(u_hip != u_ref)
+        rate = len(diff) / u_ref.size
+        assert rate <= 2e-5, (order, rate)
+        for i, j in diff:
+            k = min(u_hip[i, j], u_ref[i, j])
+            lo, hi = sorted((v_hip[i, j], v_ref[i, j]))
+            assert abs(int(u_hip[i, j]) - int(u_ref[i, j])) == 1 and lo <= bnd[k] <= hi, (order, i, j)
+            assert abs(v_hip[i, j] - bnd[k]) <= 1e-6, (order, i, j)
+        print(f"PQO{bits} HIP vs {order}-order rotation: {len(diff)} of {u_ref.size} codes differ ({rate:.2e})")

@@ -116,3 +116,40 @@ def test_c5_full_size(tq):
     assert abs(((s - true) / nat).mean()) < 0.01
     p = tq.softmax_rows(sc, 1 / math.sqrt(dim)).cpu().numpy()
     assert np.allclose(p.sum(1), 1.0, atol=1e-5) and (p >= 0).all()
+
+
+def test_c5_estimator_statistics(tq):
+    """The reference's statistical gates on the GPU estimates at the C5 size (one
+    QJL projection, 64 x 8192 = 524,288 query-key pairs, TQ3 = 2-bit polar +
+    1-bit QJL, d = 128):
+      * relative variance E[(est - ip)^2] / E[ip^2] < 2 (inner_product_tests.rs:152-195);
+      * distortion of the normalised pairs E[((est - ip) / (|q| |k|))^2] below
+        twice Theorem 2's bound 3 pi^2 / (d 4^b), b = 3 (paper_verification_tests.rs:237-317);
+      * regression slope E[est ip] / E[ip^2] in (0.95, 1.05), the polar-only
+        estimate <q, x_mse> with slope < 0.99 and farther from 1
+        (paper_verification_tests.rs:336-402);
+      * mean normalised bias below 0.01 (paper_verification_tests.rs:142-175 uses 0.03)."""
+    dim, nk, nq = 128, 8192, 64
+    keys = orc.lcg_normal_vecs(2024, dim, nk)
+    qs = orc.lcg_normal_vecs(2025, dim, nq)
+    got = tq.qjl_quantize_batch(_dev(keys), 3, 42, 4242)
+    ctx = tq.qjl_query_context(_dev(qs), 42, 4242)
+    est = tq.qjl_scores(ctx, *got, 2, 42).cpu().numpy().astype(np.float64)
+    q64, k64 = qs.astype(np.float64), keys.astype(np.float64)
+    true = q64 @ k64.T
+    nat = np.linalg.norm(q64, axis=1)[:, None] * np.linalg.norm(k64, axis=1)[None, :]
+    err = est - true
+    rel_var = (err ** 2).mean() / (true ** 2).mean()
+    distortion = ((err / nat) ** 2).mean()
+    bound = 3 * math.pi ** 2 / (dim * 4 ** 3)
+    qjl_slope = (est * true).sum() / (true ** 2).sum()
+    xhat = tq.dequantize_vec_batch(got[0], got[1], 2, dim, 42).cpu().numpy().astype(np.float64)
+    polar_slope = ((q64 @ xhat.T) * true).sum() / (true ** 2).sum()
+    bias = (err / nat).mean()
+    print(f"C5 estimator: relative variance {rel_var:.4f}, distortion {distortion:.6f} (2x bound "
+          f"{2 * bound:.6f}), QJL slope {qjl_slope:.4f}, polar-only slope {polar_slope:.4f}, bias {bias:.2e}")
+    assert rel_var < 2.0
+    assert distortion < 2 * bound
+    assert 0.95 < qjl_slope < 1.05
+    assert polar_slope < 0.99 and abs(qjl_slope - 1) < abs(polar_slope - 1)
+    assert abs(bias) < 0.01

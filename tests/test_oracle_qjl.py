@@ -15,7 +15,9 @@ Independent checks:
     paper_verification_tests.rs:142-175), the d=64 pair bias (< 0.02,
     inner_product_tests.rs:78-111) and the residual-norm identity.
 """
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -151,3 +153,106 @@ def test_scores_batch_and_weighted_values_match_single_calls():
     out = orc.weighted_values(2, dim, 42, packed, scales, w)
     ref = (w.astype(np.float64)[:, None] * orc.dequantize_vec_batch(2, dim, 42, packed, scales)).sum(0)
     assert np.abs(out - ref).max() < 1e-4
+
+
+# ---- the seed mixer and hash constants, against the reference's own source
+# text (src/qjl.rs:44-98, 143-147 and src/cache/cuda/kernels/tq_common.h:
+# 171-183): no mathematical property fixes them, so a mistyped constant or
+# shift is caught only by the reference's two copies.  The committed vectors
+# (tests/golden/qjl_vectors.json, written by
+# tests/golden/qjl_reference_constants.py from those copies) pin the oracle
+# wherever the reference is absent. ----
+GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _golden_qjl():
+    with open(os.path.join(GOLDEN_DIR, "qjl_vectors.json")) as f:
+        return json.load(f)
+
+
+def test_mix_seed_and_signs_match_committed_reference_vectors():
+    g = _golden_qjl()
+    assert len(g["mix_seed"]) >= 100 and len(g["signs"]) >= 100
+    for seed, row, want in g["mix_seed"]:
+        assert orc.lib.tqo_qjl_mix_seed(int(seed, 16), row) == int(want, 16), (seed, row)
+    for seed, row, col, want in g["signs"]:
+        rs = orc.lib.tqo_qjl_mix_seed(int(seed, 16), row)
+        assert orc.lib.tqo_rademacher_sign(rs, row, col) == want, (seed, row, col)
+
+
+def test_committed_vectors_follow_from_their_constants():
+    """The fixture's vectors are what its constants give under the restated
+    functions (so the constants, not the vectors, are what the reference pins)."""
+    import sys
+    sys.path.insert(0, GOLDEN_DIR)
+    import qjl_reference_constants as qrc
+    g = _golden_qjl()
+    k = {n: int(v, 16) for n, v in g["constants"].items()}
+    assert qrc.vectors(k)["mix_seed"] == g["mix_seed"]
+    assert qrc.vectors(k)["signs"] == g["signs"]
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/src"), reason="reference sources not mounted")
+def test_qjl_constants_read_from_both_reference_copies():
+    import sys
+    sys.path.insert(0, GOLDEN_DIR)
+    import qjl_reference_constants as qrc
+    both = qrc.extract()
+    assert both["rust"] == both["cuda"]  # the reference's Rust and CUDA copies agree
+    g = _golden_qjl()
+    assert {n: hex(v) for n, v in both["rust"].items()} == g["constants"]
+    k = both["rust"]
+    rng = np.random.default_rng(2)
+    for _ in range(2000):
+        seed = int(rng.integers(0, 1 << 63)) * 2 + int(rng.integers(0, 2))
+        row = int(rng.integers(0, 4096))
+        assert orc.lib.tqo_qjl_mix_seed(seed, row) == qrc.mix_seed(k, seed, row)
+        col = int(rng.integers(0, 256))
+        rs = qrc.mix_seed(k, seed, row)
+        assert orc.lib.tqo_rademacher_sign(rs, row, col) == qrc.rademacher_sign(k, rs, row, col)
+
+
+def test_a_planted_mixing_mistake_is_caught():
+    """The pin is sensitive: the restated mixer with one constant off by one bit,
+    or the shift off by one, disagrees with the committed vectors."""
+    import sys
+    sys.path.insert(0, GOLDEN_DIR)
+    import qjl_reference_constants as qrc
+    g = _golden_qjl()
+    k = {n: int(v, 16) for n, v in g["constants"].items()}
+    for name, delta in (("SEED_MIX_MULTIPLIER", 1 << 17), ("SEED_MIX_XOR", 1), ("SEED_MIX_SHIFT", 1)):
+        bad = dict(k)
+        bad[name] = k[name] ^ delta if name != "SEED_MIX_SHIFT" else k[name] + delta
+        assert qrc.vectors(bad)["mix_seed"] != g["mix_seed"], name
+
+
+def test_estimator_variance_distortion_and_slopes_over_projections():
+    """The reference's gates with its own sampling (a fresh QJL seed per pair,
+    so the statistics average over R): relative variance < 2
+    (inner_product_tests.rs:152-195), distortion of unit pairs < 2 x
+    3 pi^2 / (d 4^3) (paper_verification_tests.rs:237-317), QJL slope in
+    (0.95, 1.05) with the polar-only slope < 0.99 and farther from 1
+    (paper_verification_tests.rs:336-402); d = 128, TQ3, 600 pairs."""
+    dim, n = 128, 600
+    xs = orc.lcg_normal_vecs(3000, dim, n).astype(np.float64)
+    ys = orc.lcg_normal_vecs(4000, dim, n).astype(np.float64)
+    xs /= np.linalg.norm(xs, axis=1, keepdims=True)
+    ys /= np.linalg.norm(ys, axis=1, keepdims=True)
+    xs, ys = xs.astype(np.float32), ys.astype(np.float32)
+    est = np.zeros(n)
+    pol = np.zeros(n)
+    for i in range(n):
+        seed = 55555 + i
+        polar, scales, signs, norms = orc.qjl_quantize_batch(3, dim, 42, seed, xs[i:i + 1])
+        ry = orc.query_projections(ys[i], seed)
+        est[i] = orc.estimate_inner_product(2, dim, 42, ys[i], ry, polar[0], scales[0], signs[0], norms[0])
+        xhat = orc.dequantize_vec_batch(2, dim, 42, polar, scales)[0]
+        pol[i] = float(ys[i].astype(np.float64) @ xhat.astype(np.float64))
+    true = (xs.astype(np.float64) * ys.astype(np.float64)).sum(1)
+    err = est - true
+    assert (err ** 2).mean() / (true ** 2).mean() < 2.0
+    assert (err ** 2).mean() < 2 * 3 * math.pi ** 2 / (dim * 4 ** 3)
+    qjl_slope = (est * true).sum() / (true ** 2).sum()
+    polar_slope = (pol * true).sum() / (true ** 2).sum()
+    assert 0.95 < qjl_slope < 1.05
+    assert polar_slope < 0.99 and abs(qjl_slope - 1) < abs(polar_slope - 1)

@@ -78,7 +78,18 @@ struct AttnArgs {
   float *po;                 // partial acc  [(b*H + h) * P + c][head_dim]
   float *pm;                 // partial max  [(b*H + h) * P + c]   (base-2 logits)
   float *ps;                 // partial sum  [(b*H + h) * P + c]
-  int *counters;             // [(b * Hkv + g) * kCounterStride], zero between launches
+  // Split-K arrival counters, one 256-byte line per (sequence, KV head),
+  // zero between launches: counter i = b * Hkv + g sits at
+  // cnt_top - (i + 1) * kCounterStride; *ws_hdr = the number of counters
+  // below cnt_top that were zeroed.  A launch merges only if its ws_pairs =
+  // batch * num_kv_heads counters were zeroed (ws_pairs <= *ws_hdr) and its
+  // partials end below them (*ws_hdr <= ws_room, the counter lines between
+  // its partials and cnt_top); otherwise it stores nothing and writes NaN
+  // outputs.
+  int *cnt_top;
+  const int *ws_hdr;
+  int ws_pairs;
+  int ws_room;
   int P;                     // chunk stride per (b, h) in the partial arrays
   void *out;
   int out_dtype;
@@ -93,6 +104,11 @@ struct AttnArgs {
   // MaxNorm constants compiled in
   int cb_args;
   float cb[16];
+  // reference ABI (tq_fused_attention): the caller's device codebook
+  // (indexed by code, tq_attention_kernel.cu:129) and 32 decode signs
+  // (applied before the WHT, tq_attention_kernel.cu:45), or null
+  const float *cb_dev;
+  const float *sg_dev;
 };
 
 // Query element as stored (f32 bits or a 16-bit pattern), converted
@@ -198,7 +214,8 @@ __device__ void merge_and_store(const AttnArgs &a, int b, int g, int nchunks, fl
     }
     // inverse rotation over the 32 lanes of this block (lane bits 0..4 = i)
     const int i = d & 31;
-    const float v = wht32_lanes(At * decode_sign(i), i);
+    const float sg = a.sg_dev ? a.sg_dev[i] : decode_sign(i);
+    const float v = wht32_lanes(At * sg, i);
     const float res = (Lt > 0.f) ? v * kInvSqrt32 / Lt : 0.f;
     const long long oi = (bh0 + ro) * HD + d;
     if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = res;
@@ -284,9 +301,20 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_
     else qbits = static_cast<const uint16_t *>(a.q)[qidx];
     if constexpr (QJL) rqv = a.rq[qidx];
   }
+  float qsign = 0.f;  // decode sign of this lane's query element
+  if (tid < NR * HD) qsign = a.sg_dev ? a.sg_dev[tid & 31] : decode_sign(tid & 31);
+  // workspace header (inline merge): the counters the init zeroed
+  int ws_hdr = 0;
+  if (INLINE_MERGE && tid == 0) ws_hdr = *a.ws_hdr;
   // len_hint: the single length, or -1 for per-sequence device lengths
   const int len = len_hint >= 0 ? len_hint : min(max(a.kv_lens[b], 0), a.max_len);
   if (t0 >= len) {  // empty tile: not counted by the merge
+    if (len == 0 && c == 0 && tid < NR * HD) {
+      // an empty sequence attends to nothing: zero output (cuda/attention.rs:65-68)
+      const long long oi = ((long long)b * a.num_heads + g * NR) * HD + tid;
+      if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = 0.f;
+      else static_cast<uint16_t *>(a.out)[oi] = 0;
+    }
     __builtin_amdgcn_s_waitcnt(0);
     return;
   }
@@ -358,7 +386,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_
     constexpr int CM = (1 << CB) - 1;  // slot codes >= 2^CB never occur
     const int i0 = e & (NC - 1) & CM, i1 = (e >> BITS) & CM;
     float c0, c1;
-    if (a.cb_args) {
+    if (a.cb_dev) {
+      c0 = a.cb_dev[i0];
+      c1 = a.cb_dev[i1];
+    } else if (a.cb_args) {
       c0 = a.cb[0];
       c1 = a.cb[0];
 #pragma unroll
@@ -389,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_
     const int d = tid % HD;
     const int i = d & 31;
     const float v = wht32_lanes(q_value(qbits, a.q_dtype), i);
-    const float qt = v * (decode_sign(i) * qscale);
+    const float qt = v * (qsign * qscale);
     s_q[tid] = qt;
     const float am = wave_max(fabsf(qt));
     if (lane == 0) s_qmax[wave] = am;
@@ -709,11 +740,16 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_
     }
     comb[NR * HD + 2 * NR] = exp2i(ev);
   }
+  // s_flag 2: the workspace was initialised for fewer (sequence, KV head)
+  // pairs, or for so many that this launch's partials would reach their
+  // counters: this tile stores no partial and touches no counter
+  if (tid == 0) s_flag = (INLINE_MERGE && (ws_hdr < a.ws_pairs || ws_hdr > a.ws_room)) ? 2 : 0;
 
   // ---- combine the 16 waves' records: CP consecutive lanes share one output
   // (head r, element d), each folding kWaves / CP waves, then a DPP reduction
   // over the CP lanes ----
   __syncthreads();
+  const bool ws_ok = s_flag != 2;
   {
     constexpr int OUTS = NR * HD;
     constexpr int CP = kThreads / OUTS;  // 8, 4 or 2 lanes per output
@@ -750,7 +786,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_
       A += __shfl_xor(A, 4, 64);
       L += __shfl_xor(L, 4, 64);
     }
-    if (part == 0) {
+    if (part == 0 && ws_ok) {
       const long long bh = (long long)b * a.num_heads + g * NR + r;
       st_agent(&a.po[(bh * a.P + c) * HD + d], A);
       if (d == 0) {
@@ -769,17 +805,21 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const uint8_t *k_
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
-    if (tid == 0) {
-      const int prev = __hip_atomic_fetch_add(&a.counters[(b * a.num_kv_heads + g) * kCounterStride], 1, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
+    int *counter = a.cnt_top - (1 + b * a.num_kv_heads + g) * kCounterStride;
+    if (tid == 0 && ws_ok) {
+      const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_flag = (prev == nchunks - 1);
     }
     __syncthreads();
-    if (s_flag) {
+    if (!ws_ok) {
+      if (tid < NR * HD) {
+        const long long oi = ((long long)b * a.num_heads + g * NR) * HD + tid;
+        if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = __builtin_nanf("");
+        else static_cast<uint16_t *>(a.out)[oi] = 0x7e00;  // quiet NaN in f16 and bf16 alike
+      }
+    } else if (s_flag) {
       merge_and_store<NR>(a, b, g, nchunks, lds + OFF_MISC);
-      if (tid == 0)
-        __hip_atomic_store(&a.counters[(b * a.num_kv_heads + g) * kCounterStride], 0, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -800,22 +840,46 @@ __global__ void fill_zero_kernel(int *p, long long n) {
   if (i < n) p[i] = 0;
 }
 
-// Workspace layout: po | pm | ps | counters (each 256-byte aligned).
+// Zeroes `elems` outputs of the given dtype (a fill kernel, not a memset, so
+// that a captured graph replays it faithfully).
+int zero_output(void *out, long long elems, int dtype, hipStream_t stream) {
+  const long long bytes = elems * (dtype == kF32 ? 4 : 2);
+  const long long words = (bytes + 3) / 4;  // head_dim is a multiple of 32: whole words
+  if (words == 0) return TQ_OK;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<int *>(out), words);
+  return tqh::check_launch("fill_zero_kernel");
+}
+
+// Fills n ints with zeros, except the first of the last kCounterStride
+// (the header line) = hdr.
+__global__ void fill_header_kernel(int *p, long long n, int hdr) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = i == n - kCounterStride ? hdr : 0;
+}
+
+// Workspace layout: po | pm | ps from the start; the header in the last
+// 256-byte line below end = workspace_bytes rounded down to 256, and the
+// counters (one line per (sequence, KV head)) below it.  The counters'
+// place depends on workspace_bytes only, so a workspace initialised for the
+// largest batch and length serves every smaller call: their partials end
+// lower and their counters are a subset of the zeroed ones.
+constexpr size_t kLine = kCounterStride * sizeof(int);
 struct WsLayout {
-  size_t po, pm, ps, cnt, total;
+  size_t po, pm, ps, parts, total;
   int P;
 };
 
 WsLayout ws_layout(int batch, int num_heads, int num_kv_heads, int head_dim, int max_len) {
-  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  auto al = [](size_t x) { return (x + kLine - 1) & ~(kLine - 1); };
   WsLayout w{};
   w.P = (max_len + kChunk - 1) / kChunk;
   const size_t bhp = (size_t)batch * num_heads * w.P;
   w.po = 0;
   w.pm = al(w.po + bhp * head_dim * sizeof(float));
   w.ps = al(w.pm + bhp * sizeof(float));
-  w.cnt = al(w.ps + bhp * sizeof(float));
-  w.total = al(w.cnt + (size_t)batch * num_kv_heads * kCounterStride * sizeof(int));
+  w.parts = al(w.ps + bhp * sizeof(float));
+  w.total = w.parts + ((size_t)batch * num_kv_heads + 1) * kLine;
   return w;
 }
 
@@ -881,11 +945,52 @@ extern "C" int tq_attention_workspace_init(void *workspace, size_t workspace_byt
   const WsLayout w = ws_layout(batch, num_heads, num_kv_heads, head_dim, max_kv_len);
   if (!workspace || workspace_bytes < w.total)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
-  const long long n = (long long)batch * num_kv_heads * kCounterStride;
-  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     reinterpret_cast<int *>(static_cast<char *>(workspace) + w.cnt), n);
-  return tqh::check_launch("fill_zero_kernel");
+  // header = batch * num_kv_heads, the counters below it zero
+  const size_t end = workspace_bytes & ~(kLine - 1);
+  const int pairs = batch * num_kv_heads;
+  const long long n = (long long)((size_t)(pairs + 1) * kLine / sizeof(int));
+  int *hdr = reinterpret_cast<int *>(static_cast<char *>(workspace) + end - kLine);
+  hipLaunchKernelGGL(fill_header_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     hdr - (long long)pairs * kCounterStride, n, pairs);
+  return tqh::check_launch("fill_header_kernel");
 }
+
+namespace {
+
+// Where a decode launch keeps its split-K partials and counters: the
+// partials from `base`, the counter of pair i at cnt_top - (i + 1) lines,
+// *hdr = the number of zeroed counters below cnt_top.
+struct DecodeWs {
+  char *base = nullptr;
+  int *cnt_top = nullptr;
+  const int *hdr = nullptr;
+  // host-side view of the same: bytes the partials may use (up to the lowest
+  // zeroed counter a valid call can have), and the zeroed pairs (0: the
+  // caller's workspace, known to the device only)
+  size_t part_bytes = 0;
+  int pairs = 0;
+};
+
+// A caller's workspace: header in the last line below the rounded-down end,
+// counters below it.
+DecodeWs caller_ws(void *workspace, size_t workspace_bytes) {
+  DecodeWs d;
+  d.base = static_cast<char *>(workspace);
+  const size_t end = workspace_bytes & ~(kLine - 1);
+  d.cnt_top = end >= kLine ? reinterpret_cast<int *>(d.base + end - kLine) : nullptr;
+  d.hdr = d.cnt_top;
+  d.part_bytes = end >= kLine ? end - kLine : 0;
+  return d;
+}
+
+int decode_attention_ws(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
+                        const uint8_t *v_indices, const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                        const uint16_t *qjl_norms, const int *kv_lens, int host_len, int batch, int num_heads,
+                        int num_kv_heads, int head_dim, int bits, size_t outlier_blocks, int norm_mode,
+                        int max_kv_len, long long kv_head_stride, long long seq_stride, float softmax_scale, void *out,
+                        int out_dtype, const DecodeWs *wsd, size_t workspace_bytes, hipStream_t stream);
+
+}  // namespace
 
 // host_len >= 0 (with kv_lens null): every sequence holds host_len tokens;
 // max_kv_len fixes the workspace layout either way.
@@ -896,6 +1001,21 @@ int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, 
                           int norm_mode, int max_kv_len, long long kv_head_stride, long long seq_stride,
                           float softmax_scale, void *out, int out_dtype, void *workspace, size_t workspace_bytes,
                           hipStream_t stream) {
+  const DecodeWs d = caller_ws(workspace, workspace_bytes);
+  return decode_attention_ws(q, q_dtype, k_indices, k_scales, v_indices, v_scales, rq, qjl_signs, qjl_norms, kv_lens,
+                             host_len, batch, num_heads, num_kv_heads, head_dim, bits, outlier_blocks, norm_mode,
+                             max_kv_len, kv_head_stride, seq_stride, softmax_scale, out, out_dtype,
+                             workspace ? &d : nullptr, workspace_bytes, stream);
+}
+
+namespace {
+
+int decode_attention_ws(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
+                        const uint8_t *v_indices, const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,
+                        const uint16_t *qjl_norms, const int *kv_lens, int host_len, int batch, int num_heads,
+                        int num_kv_heads, int head_dim, int bits, size_t outlier_blocks, int norm_mode,
+                        int max_kv_len, long long kv_head_stride, long long seq_stride, float softmax_scale, void *out,
+                        int out_dtype, const DecodeWs *wsd, size_t workspace_bytes, hipStream_t stream) {
   int rc = check_common(num_heads, num_kv_heads, head_dim, bits);
   if (rc) return rc;
   tqh::PolarCodec codec;
@@ -909,7 +1029,12 @@ int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, 
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL correction applies to the standard codebook (outlier_blocks 0)");
   if (!tqh::valid_dtype(q_dtype) || !tqh::valid_dtype(out_dtype))
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "unknown dtype");
-  if (batch <= 0 || max_kv_len <= 0) return TQ_OK;
+  if (batch <= 0) return TQ_OK;
+  if (max_kv_len <= 0) {
+    // nothing to attend to: zero output (cuda/attention.rs:65-68)
+    if (!out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
+    return zero_output(out, (long long)batch * num_heads * head_dim, out_dtype, stream);
+  }
   if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !out)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   if (!kv_lens && host_len < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null kv_lens");
@@ -919,10 +1044,19 @@ int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, 
   if (batch > 1 && seq_stride < (long long)num_kv_heads * kv_head_stride)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "seq_stride %lld overlaps the KV heads of a sequence", seq_stride);
   const WsLayout w = ws_layout(batch, num_heads, num_kv_heads, head_dim, max_kv_len);
-  if (!workspace || workspace_bytes < w.total)
-    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
+  const long long pairs = (long long)batch * num_kv_heads;
+  if (!wsd) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null workspace");
+  if (wsd->pairs == 0) {  // the caller's workspace
+    if (workspace_bytes < w.total)
+      return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "workspace too small: %zu < %zu", workspace_bytes, w.total);
+  } else if (pairs > wsd->pairs || w.parts > wsd->part_bytes) {
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT,
+                     "decode needs %zu bytes of split-K partials and %lld counters; the library's scratch holds "
+                     "%zu bytes and %d counters",
+                     w.parts, pairs, wsd->part_bytes, wsd->pairs);
+  }
   AttnArgs a = base_args();
-  char *ws = static_cast<char *>(workspace);
+  char *ws = wsd->base;
   a.q = q;
   a.q_dtype = q_dtype;
   a.k_idx = k_indices;
@@ -940,7 +1074,10 @@ int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, 
   a.po = reinterpret_cast<float *>(ws + w.po);
   a.pm = reinterpret_cast<float *>(ws + w.pm);
   a.ps = reinterpret_cast<float *>(ws + w.ps);
-  a.counters = reinterpret_cast<int *>(ws + w.cnt);
+  a.cnt_top = wsd->cnt_top;
+  a.ws_hdr = wsd->hdr;
+  a.ws_pairs = (int)pairs;
+  a.ws_room = (int)(((size_t)(reinterpret_cast<char *>(wsd->cnt_top) - ws) - w.parts) / kLine);
   a.P = w.P;
   a.out = out;
   a.out_dtype = out_dtype;
@@ -956,6 +1093,8 @@ int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, 
   const dim3 grid((unsigned)w.P, (unsigned)num_kv_heads, (unsigned)batch);
   return launch_decode<true>(a, bits, mode, num_heads / num_kv_heads, grid, stream);
 }
+
+}  // namespace
 
 extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                                          const uint16_t *k_scales, const uint8_t *v_indices,
@@ -990,6 +1129,8 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
                                   const float *rq, int qjl_enabled, int num_attention_heads, int num_kv_heads,
                                   int head_dim, int kv_len, int kv_stride, int packed_dim, int num_qblocks, int bits,
                                   float softmax_scale, int num_partitions, hipStream_t stream) {
+  if (kv_len == 0 && output && num_attention_heads > 0 && head_dim > 0)  // attention.rs:65-68
+    return zero_output(output, (long long)num_attention_heads * head_dim, kF32, stream);
   if (kv_len == 0 || num_kv_heads == 0) return TQ_OK;  // tq_attention_kernel.cu:366
   if (qjl_enabled && (!qjl_signs || !qjl_residual_norms || !rq))
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "qjl_enabled needs signs, residual norms and rq");
@@ -1003,15 +1144,17 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
   if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !codebook || !sign_pattern || !output ||
       !partial_out || !partial_max || !partial_sum)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
-  // The codebook and sign pattern are device tensors in the reference
-  // (pqo.rs:134-160) holding the PQO constants, which this entry applies from
-  // its own copy; with qjl_enabled the records are TQ records (standard
-  // (bits-1)-bit codebook, the QJL branch of tq_attention_kernel.cu:192-231).
-  // The caller's partial buffers (sized for 512-token partitions) hold this
+  // The codebook (indexed by code: 2^bits entries, 2^(bits-1) used by TQ
+  // records) and the 32 decode signs are the caller's device tensors, read by
+  // the kernels as tq_attention_kernel.cu:127-130 reads them (pqo.rs:134-160
+  // passes pre.outlier_centroids, so an L2Norm cache brings its Beta tables);
+  // with qjl_enabled the records are TQ records (standard (bits-1)-bit
+  // codebook, the QJL branch of tq_attention_kernel.cu:192-231).  The
+  // caller's partial buffers (sized for 512-token partitions) hold this
   // entry's 1024-token partials.
-  (void)codebook;
-  (void)sign_pattern;
   AttnArgs a = base_args();
+  a.cb_dev = codebook;
+  a.sg_dev = sign_pattern;
   a.q = q;
   a.q_dtype = kF32;
   a.k_idx = k_indices;
@@ -1029,7 +1172,8 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
   a.po = partial_out;
   a.pm = partial_max;
   a.ps = partial_sum;
-  a.counters = nullptr;
+  a.cnt_top = nullptr;
+  a.ws_hdr = nullptr;
   a.P = num_partitions;
   a.out = output;
   a.out_dtype = kF32;
