@@ -9,14 +9,21 @@ cache.  Algorithmic bytes per step: 8 heads x 32768 tokens x (56 + 56) B =
 cache (29 MB) fits the 256 MB Infinity Cache, so steps rotate through
 >= 1 GiB of distinct cache copies.
 
-Beside it, "read_ceiling": the time of a plain streaming read of the same
-29,360,128 B (turboquant_amd/probe/read_probe.hip, also rotating over
->= 1 GiB), i.e. what any kernel that reads those bytes once can reach here,
-and the decode's fraction of it.
+Beside it, "read_ceiling": the time of a plain read of the same
+29,360,128 B (bench_read_probe.hip beside this file, also rotating over
+>= 1 GiB; best of several access shapes and loads in flight), i.e. what any
+kernel that reads those bytes once can reach here, and the decode's fraction
+of it.
 
-Secondary: PQO3 quantize Mvec/s at d=128 (config 2: 28 layers x 8 KV heads x
-4096 tokens, K and V, bf16 in) with the fused rotation, reported in the same
-JSON line under "quantize".
+Secondary (same JSON line): config 2 (28 layers x 8 KV heads x 4096 tokens,
+K and V, bf16) PQO3 quantize Mvec/s at d=128 with the fused rotation under
+"quantize", and PQO3 / PQO4 quantize and dequantize (bf16 out) GB/s under
+"c2_codec"; configs 4, 1 and 5 and the TQ3 decode and prefill records.
+
+CPU baselines: the oracle (oracle/tq_oracle.c, the C restatement of the
+reference CPU path) timed on this host's cores, one thread ("cores": 1) and
+all-cores (threads = min(16, nproc): the oracle's ctypes calls release the
+GIL), on bounded samples stated in each record.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -109,49 +116,221 @@ def traffic(kernel: str):
     return None if rec is None else rec.get("hbm_bytes_per_launch")
 
 
+def _cores():
+    """(threads used for the all-cores baselines, nproc): at most 16 threads,
+    the GPU box's CPU share."""
+    n = os.cpu_count() or 1
+    return max(1, min(16, n)), n
+
+
+def _parallel_wall(fn, threads: int) -> float:
+    """Wall seconds of fn(i) for i < threads, all at once on `threads` threads."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(threads) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(fn, range(threads)))
+        return time.perf_counter() - t0
+
+
+def _repeat(fn, budget_s: float, max_reps: int):
+    """(mean seconds per call, calls) of fn() repeated up to budget_s / max_reps."""
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= max_reps:
+            return el / reps, reps
+
+
+def _pqo_sample(rng, bits, heads, tokens, hd):
+    from oracle import oracle as orc
+    from tq_testdata import kv_outlier
+    k = kv_outlier(rng, heads, tokens, hd).reshape(-1, hd)
+    v = kv_outlier(rng, heads, tokens, hd).reshape(-1, hd)
+    pk, sk = orc.pqo_quantize(bits, k, hd)
+    pv, sv = orc.pqo_quantize(bits, v, hd)
+    return pk, sk, pv, sv
+
+
+def _attend_head(orc, bits, rec, q, t, hd):
+    pk, sk, pv, sv = rec
+    kd = orc.pqo_dequantize(bits, pk, sk, hd).reshape(1, t, hd)
+    vd = orc.pqo_dequantize(bits, pv, sv, hd).reshape(1, t, hd)
+    orc.attention_dense(q, kd, vd, 1.0 / math.sqrt(hd))
+
+
 def cpu_baseline_c3():
-    """Oracle (C restatement of the reference CPU path: polar_dequantize then
-    dense softmax attention, single thread) on a bounded sample: one KV head
-    (2 query heads) at the full 32K context; scaled to the 8-head config."""
+    """Oracle polar_dequantize then dense softmax attention on one KV head (2
+    query heads) at the full 32K context, scaled to the 8-head config; one
+    thread, then `threads` such heads at once."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(33)
+    t, hd, bits = C3["ctx"], C3["head_dim"], C3["bits"]
+    threads, nproc = _cores()
+    recs = [_pqo_sample(rng, bits, 1, t, hd) for _ in range(threads)]
+    q = rng.standard_normal((2, hd)).astype(np.float32) / np.float32(math.sqrt(hd))
+    per_head, reps = _repeat(lambda: _attend_head(orc, bits, recs[0], q, t, hd), 3.0, 20)
+    head_bytes = c3_bytes() / C3["kv_heads"]
+    wall = _parallel_wall(lambda i: _attend_head(orc, bits, recs[i], q, t, hd), threads)
+    return {"value": round(head_bytes / per_head / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"1 of 8 KV heads (2 q-heads) x 32768 tokens, {reps} reps, as GB/s of the config's bytes; "
+                      "oracle/tq_oracle.c pqo_dequantize + attention_dense",
+            "all_cores": {"value": round(threads * head_bytes / wall / 1e9, 4), "unit": "GB/s", "cores": threads,
+                          "nproc": nproc, "sample": f"{threads} KV heads x 32768 tokens at once, one per thread"}}
+
+
+def cpu_baseline_c2(bits: int):
+    """Oracle pqo_quantize (rotation + MaxNorm + pack) and pqo_dequantize of
+    100,000 C2-shaped vectors (d=128) per thread; one thread, then all."""
     import numpy as np
     from oracle import oracle as orc
     from tq_testdata import kv_outlier
 
-    rng = np.random.default_rng(33)
-    t, hd, bits = C3["ctx"], C3["head_dim"], C3["bits"]
-    k = kv_outlier(rng, 1, t, hd).reshape(-1, hd)
-    v = kv_outlier(rng, 1, t, hd).reshape(-1, hd)
-    pk, sk = orc.pqo_quantize(bits, k, hd)
-    pv, sv = orc.pqo_quantize(bits, v, hd)
-    q = rng.standard_normal((2, hd)).astype(np.float32) / np.float32(math.sqrt(hd))
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        kd = orc.pqo_dequantize(bits, pk, sk, hd).reshape(1, t, hd)
-        vd = orc.pqo_dequantize(bits, pv, sv, hd).reshape(1, t, hd)
-        orc.attention_dense(q, kd, vd, 1.0 / math.sqrt(hd))
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > 3.0 or reps >= 20:
-            break
-    per_head = el / reps
-    full = per_head * C3["kv_heads"]
-    return {"value": round(c3_bytes() / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"1 of 8 KV heads (2 q-heads) x 32768 tokens, {reps} reps, scaled x8; "
-                      "oracle/tq_oracle.c pqo_dequantize + attention_dense"}
+    n = 100_000
+    threads, nproc = _cores()
+    rng = np.random.default_rng(22)
+    xs = [kv_outlier(rng, 1, n, 128).reshape(-1, 128) for _ in range(threads)]
+    codes = [orc.pqo_quantize(bits, x, 128) for x in xs]
+    out_b = 128 * bits // 8 + 8
+    tq1, _ = _repeat(lambda: orc.pqo_quantize(bits, xs[0], 128), 1.0, 5)
+    td1, _ = _repeat(lambda: orc.pqo_dequantize(bits, *codes[0], 128), 1.0, 5)
+    tqa = _parallel_wall(lambda i: orc.pqo_quantize(bits, xs[i], 128), threads)
+    tda = _parallel_wall(lambda i: orc.pqo_dequantize(bits, *codes[i], 128), threads)
+    sample = f"{n:,} vectors d=128 per thread (bf16-valued N(0,1), 4 of 128 channels x8)"
+    quant = {"value": round(n / tq1 / 1e6, 4), "unit": "Mvec/s", "cores": 1, "kind": "port",
+             "gbs": round(n * (256 + out_b) / tq1 / 1e9, 4),
+             "sample": sample + ", oracle/tq_oracle.c pqo_quantize (bf16 bytes in)",
+             "all_cores": {"value": round(threads * n / tqa / 1e6, 4), "unit": "Mvec/s", "cores": threads,
+                           "nproc": nproc}}
+    deq = {"value": round(n * (out_b + 256) / td1 / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+           "mvec_s": round(n / td1 / 1e6, 4),
+           "sample": sample + ", oracle/tq_oracle.c pqo_dequantize (bytes as bf16 out)",
+           "all_cores": {"value": round(threads * n * (out_b + 256) / tda / 1e9, 4), "unit": "GB/s",
+                         "cores": threads, "nproc": nproc}}
+    return quant, deq
 
 
-def cpu_baseline_quantize():
+def cpu_baseline_c4(contexts):
+    """Oracle dequantize + dense attention for one KV head (4 query heads) of the
+    first C4 sequence, scaled by the contexts to the whole batch (16 sequences
+    x 8 KV heads); one thread, then one sequence's KV head per thread."""
     import numpy as np
     from oracle import oracle as orc
 
-    rng = np.random.default_rng(22)
-    x = rng.standard_normal((200_000, 128)).astype(np.float32)
-    t0 = time.perf_counter()
-    orc.pqo_quantize(3, x, 128)
-    el = time.perf_counter() - t0
-    return {"value": round(x.shape[0] / el / 1e6, 4), "unit": "Mvec/s", "cores": 1, "kind": "port",
-            "sample": "200,000 vectors d=128, oracle/tq_oracle.c pqo_quantize (rotation + MaxNorm + pack)"}
+    rng = np.random.default_rng(40)
+    hd, bits = 128, 4
+    t0 = int(contexts[0])
+    threads, nproc = _cores()
+    recs = [_pqo_sample(rng, bits, 1, t0, hd) for _ in range(threads)]
+    q = rng.standard_normal((4, hd)).astype(np.float32) / np.float32(math.sqrt(hd))
+    per, reps = _repeat(lambda: _attend_head(orc, bits, recs[0], q, t0, hd), 3.0, 10)
+    scale = 8 * float(sum(contexts)) / t0
+    full = per * scale
+    step_bytes = int(sum(contexts)) * 8 * 2 * (hd * bits // 8 + 8)
+    wall = _parallel_wall(lambda i: _attend_head(orc, bits, recs[i], q, t0, hd), threads)
+    full_all = wall / threads * scale
+    return {"tokens_per_s_per_layer": round(len(contexts) / full, 3), "gbs": round(step_bytes / full / 1e9, 4),
+            "ms_per_step": round(full * 1e3, 3), "cores": 1, "kind": "port",
+            "sample": f"1 KV head (4 q-heads) x {t0} tokens, {reps} reps, scaled x{scale:.1f} to the batch; "
+                      "oracle/tq_oracle.c pqo_dequantize + attention_dense",
+            "all_cores": {"tokens_per_s_per_layer": round(len(contexts) / full_all, 3),
+                          "gbs": round(step_bytes / full_all / 1e9, 4), "cores": threads, "nproc": nproc}}
+
+
+def cpu_baseline_c1():
+    """Oracle quantize_vec / dequantize_vec over config 1's 10,000 vectors (LCG
+    N(0,1), d=128, TQ3, rotation seed 42): us per vector and the round trip's nMSE."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    x = orc.lcg_normal_vecs(42, 128, 10_000)
+    tq_, _ = _repeat(lambda: orc.quantize_vec_batch(3, 128, 42, x), 1.0, 5)
+    p, s = orc.quantize_vec_batch(3, 128, 42, x)
+    td_, _ = _repeat(lambda: orc.dequantize_vec_batch(3, 128, 42, p, s), 1.0, 5)
+    y = orc.dequantize_vec_batch(3, 128, 42, p, s).astype(np.float64)
+    xd = x.astype(np.float64)
+    nmse = float((((xd - y) ** 2).sum(1) / (xd ** 2).sum(1)).mean())
+    return {"us_per_vector_quantize": round(tq_ * 1e6 / 10_000, 4),
+            "us_per_vector_dequantize": round(td_ * 1e6 / 10_000, 4), "nmse": round(nmse, 5), "cores": 1,
+            "kind": "port", "sample": "config 1 in full (10,000 vectors), oracle/tq_oracle.c quantize_vec_batch / "
+                                      "dequantize_vec_batch; the reference's README quotes ~1.1 / ~0.8 us"}
+
+
+def cpu_baseline_c5():
+    """Oracle QJL stages on bounded samples of config 5 (d=128, TQ3): the key
+    sketch of 1,024 keys, query contexts and scores of 8 queries over 8,192
+    keys, weighted values of 4 queries; each scaled to the config's counts."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    keys = orc.lcg_normal_vecs(2024, 128, 8192)
+    qs = orc.lcg_normal_vecs(2025, 128, 8)
+    ts, _ = _repeat(lambda: orc.qjl_quantize_batch(3, 128, 42, 4242, keys[:1024]), 1.0, 3)
+    kb = orc.qjl_quantize_batch(3, 128, 42, 4242, keys)
+    tc, _ = _repeat(lambda: [orc.query_projections(q, 4242) for q in qs], 1.0, 3)
+    tsc, _ = _repeat(lambda: orc.qjl_scores(2, 128, 42, 4242, qs, *kb), 2.0, 3)
+    w = np.full(8192, 1.0 / 8192, np.float32)
+    tw, _ = _repeat(lambda: [orc.weighted_values(2, 128, 42, kb[0], kb[1], w) for _ in range(4)], 2.0, 3)
+    return {"sketch_8192_keys_ms": round(ts * 8 * 1e3, 3), "query_context_64_ms": round(tc * 8 * 1e3, 3),
+            "scores_64x8192_ms": round(tsc * 8 * 1e3, 3), "weighted_values_64_ms": round(tw * 16 * 1e3, 3),
+            "us_per_estimate": round(tsc * 1e6 / (8 * 8192), 4), "cores": 1, "kind": "port",
+            "sample": "sketch of 1,024 keys x8; projections and scores of 8 queries x8; weighted values of 4 "
+                      "queries x16 (oracle/tq_oracle.c qjl_* functions)"}
+
+
+def bench_c2_codec(torch, tq, args, x, bits: int):
+    """Config 2 at full size for one PQO width: quantize every vector (bf16 in,
+    fused rotation), then dequantize all (bf16 out).  Algorithmic bytes per
+    vector: quantize 256 in + (48|64 codes + 8 scale) out; dequantize the
+    reverse.  Each step is one launch over all 1,835,008 vectors (> the
+    256 MB MALL, no rotation needed)."""
+    from turboquant_amd import _lib
+    n = x.shape[0]
+    pd = 128 * bits // 8
+    packed = torch.empty((n, pd), dtype=torch.uint8, device="cuda")
+    scales = torch.empty((n, 4), dtype=torch.int16, device="cuda")
+    y = torch.empty((n, 128), dtype=torch.bfloat16, device="cuda")
+    steps = max(5, args.steps // 10)
+    warm = max(2, args.warmup // 10)
+
+    def quant_step(i):
+        st = torch.cuda.current_stream().cuda_stream  # read at call time: a capture records the launch
+        _lib.check(_lib.lib.tq_pqo_quantize(x.data_ptr(), _lib.TQ_DTYPE_BF16, packed.data_ptr(), scales.data_ptr(),
+                                            n, 128, bits, st))
+
+    def deq_step(i):
+        st = torch.cuda.current_stream().cuda_stream
+        _lib.check(_lib.lib.tq_pqo_dequantize(packed.data_ptr(), scales.data_ptr(), y.data_ptr(), _lib.TQ_DTYPE_BF16,
+                                              n, 128, bits, st))
+
+    qms, _ = time_steps(torch, quant_step, steps, warm)
+    dms, _ = time_steps(torch, deq_step, steps, warm)
+    code_b = pd + 8
+    qb = n * (256 + code_b)
+    db = n * (code_b + 256)
+    q_gbs = qb / (qms * 1e-3) / 1e9
+    d_gbs = db / (dms * 1e-3) / 1e9
+    del packed, scales, y
+    return {
+        "quantize": {"metric": f"PQO{bits} quantize (C2, bf16 in, fused rotation)",
+                     "mvec_s": round(n / (qms * 1e-3) / 1e6, 2), "ms_per_step": round(qms, 6),
+                     "gbs_in": round(n * 256 / (qms * 1e-3) / 1e9, 2),
+                     "gbs_out": round(n * code_b / (qms * 1e-3) / 1e9, 2), "algorithmic_bytes_per_step": qb,
+                     "roofline": {"bound": "hbm", "achieved": round(q_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(q_gbs / HBM_PEAK_GBS, 4),
+                                  "traffic": traffic(f"pqo_quant_kernel_pqo{bits}")}},
+        "dequantize": {"metric": f"PQO{bits} dequantize (C2, bf16 out)",
+                       "mvec_s": round(n / (dms * 1e-3) / 1e6, 2), "ms_per_step": round(dms, 6),
+                       "gbs_in": round(n * code_b / (dms * 1e-3) / 1e9, 2),
+                       "gbs_out": round(n * 256 / (dms * 1e-3) / 1e9, 2), "algorithmic_bytes_per_step": db,
+                       "roofline": {"bound": "hbm", "achieved": round(d_gbs, 2), "peak": HBM_PEAK_GBS,
+                                    "unit": "GB/s", "frac": round(d_gbs / HBM_PEAK_GBS, 4),
+                                    "traffic": traffic(f"pqo_dequant_kernel_pqo{bits}")}},
+    }
 
 
 def bench_c4(torch, tq, args):
@@ -325,29 +504,35 @@ def bench_c5(torch, tq, args):
 
 
 def read_ceiling(torch, nbytes: int, steps: int, warmup: int):
-    """Attainable read rate at nbytes: a plain streaming read of nbytes
-    (turboquant_amd/probe/read_probe.hip), rotating over >= 1 GiB so nothing
-    is cache-resident, best of three grid sizes.  A reference for the decode's
-    bytes, not a figure of this library."""
+    """Attainable read rate at nbytes: a plain read of nbytes (bench_read_probe.hip,
+    built beside this file by __graft_entry__.build), rotating over >= 1 GiB so
+    nothing is cache-resident; the best of grid-stride and per-workgroup
+    contiguous spans, 1 / 4 / 8 loads in flight per lane and three grid sizes.
+    A reference for the decode's bytes, not a figure of this library."""
     import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "turboquant_amd", "libtq_read_probe.so"))
-    lib.tq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib = ctypes.CDLL(os.path.join(ROOT, "libtq_read_probe.so"))
+    lib.tq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_void_p, ctypes.c_void_p]
     nsl = max(1, math.ceil((1 << 30) / nbytes) + 1)
     buf = torch.ones(nsl * nbytes, dtype=torch.uint8, device="cuda")
     sink = torch.zeros(4, dtype=torch.uint32, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     best = None
-    for grid in (1024, 2048, 4096):
-        def step(i, grid=grid):
-            if lib.tq_probe_read(buf.data_ptr() + (i % nsl) * nbytes, nbytes, grid, sink.data_ptr(), stream) != 0:
-                raise RuntimeError("read probe launch failed")
-        ms, _ = time_steps(torch, step, steps, warmup)
-        if best is None or ms < best[0]:
-            best = (ms, grid)
+    for mode in (0, 1):
+        for unroll in (1, 4, 8):
+            for grid in (256, 1024, 2048):
+                def step(i, grid=grid, unroll=unroll, mode=mode):
+                    if lib.tq_probe_read(buf.data_ptr() + (i % nsl) * nbytes, nbytes, grid, unroll, mode,
+                                         sink.data_ptr(), stream) != 0:
+                        raise RuntimeError("read probe launch failed")
+                ms, _ = time_steps(torch, step, max(20, steps // 4), max(20, warmup // 10))
+                if best is None or ms < best[0]:
+                    best = (ms, grid, unroll, mode)
     del buf
     gbs = nbytes / (best[0] * 1e-3) / 1e9
     return {"bytes": nbytes, "us": round(best[0] * 1e3, 3), "gbs": round(gbs, 1),
-            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "grid": best[1], "slices": nsl}
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "grid": best[1], "loads_in_flight": best[2],
+            "access": ["grid stride", "contiguous span per workgroup"][best[3]], "slices": nsl}
 
 
 def main():
@@ -430,7 +615,9 @@ def main():
     q_gbs = q_bytes / (qms * 1e-3) / 1e9
     mvec = n_vec / (qms * 1e-3) / 1e6
 
-    del x, packed, scales
+    del packed, scales
+    c2 = {f"pqo{b}": bench_c2_codec(torch, tq, args, x, b) for b in (3, 4)}
+    del x
     c4 = bench_c4(torch, tq, args)
     tq_c3 = bench_tq_c3(torch, tq, args)
     pf = bench_prefill(torch, tq, args)
@@ -441,7 +628,14 @@ def main():
     qcpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_c3()
-        qcpu = cpu_baseline_quantize()
+        for b in (3, 4):
+            cq, cd = cpu_baseline_c2(b)
+            c2[f"pqo{b}"]["quantize"]["cpu_baseline"] = cq
+            c2[f"pqo{b}"]["dequantize"]["cpu_baseline"] = cd
+        qcpu = c2["pqo3"]["quantize"]["cpu_baseline"]
+        c4["cpu_baseline"] = cpu_baseline_c4(c4["contexts"])
+        c1["cpu_baseline"] = cpu_baseline_c1()
+        c5["cpu_baseline"] = cpu_baseline_c5()
 
     rec = {
         "metric": "PQO3 fused decode attn GB/s (%HBM peak) @32K ctx; quantize Mvec/s at d=128",
@@ -475,6 +669,7 @@ def main():
                                   "unit": "GB/s", "frac": round(q_gbs / HBM_PEAK_GBS, 4),
                                   "traffic": traffic("pqo_quant_kernel")},
                      "cpu_baseline": qcpu},
+        "c2_codec": c2,
         "c4_batched_decode": c4,
         "tq_decode_c3": tq_c3,
         "prefill_attention": pf,

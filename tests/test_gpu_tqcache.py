@@ -183,7 +183,9 @@ def test_pq_cache_decode_matches_dense(tq, bits):
 
 def test_reference_abi_qjl_enabled(tq):
     """tq_fused_attention with qjl_enabled = 1 over TQ records (the reference
-    kernel's dormant branch, tq_attention_kernel.cu:192-231)."""
+    kernel's dormant branch, tq_attention_kernel.cu:192-231), given the
+    records' codebook (the standard (bits-1)-bit MaxNorm codebook, indexed by
+    code as the kernel reads it) and the 32 decode signs."""
     bits, hkv, hq, t = 3, 4, 8, 900
     rng = np.random.default_rng(123)
     k = kv_outlier(rng, hkv, t)
@@ -199,8 +201,9 @@ def test_reference_abi_qjl_enabled(tq):
     po = torch.zeros((hq * p, D), dtype=torch.float32, device="cuda")
     pm = torch.zeros((hq * p,), dtype=torch.float32, device="cuda")
     ps = torch.zeros((hq * p,), dtype=torch.float32, device="cuda")
-    cb = dev(np.zeros(8, np.float32))
-    sgp = dev(np.ones(32, np.float32))
+    c_std, _, _ = orc.pqo_codebook(bits - 1)
+    cb = dev(np.concatenate([c_std, np.zeros(8 - c_std.size, np.float32)]))
+    sgp = dev(orc.pqo_decode_signs())
     ki, ks = dev(rp), dev(rs.view(np.int16))
     vi, vs = dev(pv), dev(sv.view(np.int16))
     sgd, nmd, rqd, qd = dev(rsg), dev(rnm.view(np.int16)), dev(rq), dev(q)

@@ -67,24 +67,9 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
     _build_api_test()
-    _build_probe()
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
     return LIB
-
-
-PROBE_SRC = os.path.join(HERE, "probe", "read_probe.hip")
-PROBE_LIB = os.path.join(HERE, "libtq_read_probe.so")
-
-
-def _build_probe() -> None:
-    """bench.py's read-bandwidth reference (a separate library, not the ABI)."""
-    tmp = PROBE_LIB + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", *COMMON, "-shared", PROBE_SRC, "-o", tmp]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"read probe build failed:\n{res.stderr}")
-    os.replace(tmp, PROBE_LIB)
 
 
 API_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "api_test.cpp")
