@@ -88,8 +88,11 @@ int tq_pack_indices(const uint8_t *indices, uint8_t *packed_out, int num_vectors
  * [num_attention_heads * num_partitions][head_dim], partial_max/sum
  * [num_attention_heads * num_partitions] are caller scratch, with
  * num_partitions = ceil(kv_len / 512) as in cuda/attention.rs:13,70.  The
- * codebook and sign pattern arguments are validated non-null and the PQO
- * constants applied.  qjl_enabled = 1 attends TQ records (standard
+ * codebook (device f32, indexed by code: 2^bits entries, or 2^(bits-1) for
+ * TQ records) and the 32 decode signs (device f32, applied before the
+ * inverse WHT) are read as tq_attention_kernel.cu:127-130 reads them, so an
+ * L2Norm cache's Beta tables decode correctly.  kv_len 0 zeroes the output
+ * (cuda/attention.rs:65-68).  qjl_enabled = 1 attends TQ records (standard
  * (bits-1)-bit codebook) with the QJL correction of the kernel's dormant
  * branch (tq_attention_kernel.cu:192-231): qjl_signs [num_kv_heads]
  * [kv_stride][head_dim/8], qjl_residual_norms [num_kv_heads][kv_stride] f16,
@@ -160,11 +163,19 @@ int tq_polar_dequantize_from_cache(const uint8_t *packed_cache, const uint16_t *
                                    void *out, int out_dtype, int head_dim, int bits,
                                    size_t outlier_blocks, int norm_mode, hipStream_t stream);
 
-/* Workspace for tq_pqo_decode_attention (partials + merge counters). */
+/* Workspace for tq_pqo_decode_attention: split-K partials from its start;
+ * a header line and one merge counter line per (sequence, KV head) below its
+ * end (workspace_bytes rounded down to 256).  A workspace sized and
+ * initialised for the largest (batch, num_heads, max_kv_len) serves every
+ * call with no more sequences x KV heads and no larger partials, in any
+ * order, given the same pointer and workspace_bytes each time.  A call whose
+ * counters the init did not zero, or whose partials would reach them, stores
+ * nothing and writes NaN outputs (the workspace stays usable). */
 size_t tq_attention_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
                                    int max_kv_len);
-/* Zero-fills the merge counters of a workspace (once after allocation; every
- * call leaves them zero again).  Uses a fill kernel, no memset node. */
+/* Writes the header (batch * num_kv_heads) and zero-fills those merge
+ * counters (once after allocation; every call leaves its counters zero
+ * again).  Uses a fill kernel, no memset node. */
 int tq_attention_workspace_init(void *workspace, size_t workspace_bytes, int batch,
                                 int num_heads, int num_kv_heads, int head_dim, int max_kv_len,
                                 hipStream_t stream);
@@ -179,7 +190,10 @@ int tq_attention_workspace_init(void *workspace, size_t workspace_bytes, int bat
  *   kv_lens: device int[batch]; max_kv_len: host bound on every kv_lens[b].
  *   kv_lens may be null when every sequence holds exactly max_kv_len tokens
  *   (a length the host knows): the kernel then reads no length from memory.
- *   record strides in tokens: kv_head_stride (capacity), seq_stride. */
+ *   record strides in tokens: kv_head_stride (capacity), seq_stride.
+ *   A sequence of length 0 (and every sequence when max_kv_len is 0) gets
+ *   zero outputs, as the reference's fused_attention zero-fills its output
+ *   (cuda/attention.rs:65-68). */
 int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                             const uint16_t *k_scales, const uint8_t *v_indices,
                             const uint16_t *v_scales, const int *kv_lens, int batch,
