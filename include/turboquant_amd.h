@@ -202,6 +202,24 @@ int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices
                             float softmax_scale, void *out, int out_dtype, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
+/* tq_pqo_decode_attention without the workspace arguments, for callers that
+ * cannot allocate (HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The split-K partials
+ * and merge counters live in the library's file-scope device array of 8 MiB
+ * per device (held until the process ends; room for 1,024 (sequence, KV
+ * head) pairs and 7.75 MiB of partials = batch * num_heads *
+ * ceil(max_kv_len / 1024) * (head_dim + 2) * 4 bytes, each part rounded up
+ * to 256); larger shapes are rejected with TQ_ERR_INVALID_ARGUMENT.  No
+ * hipMalloc, hipFree or other allocation.  Every call on a device shares that
+ * device's array: calls that overlap in time on one device race. */
+int tq_pqo_decode_attention_noalloc(const void *q, int q_dtype, const uint8_t *k_indices,
+                                    const uint16_t *k_scales, const uint8_t *v_indices,
+                                    const uint16_t *v_scales, const int *kv_lens, int batch,
+                                    int num_heads, int num_kv_heads, int head_dim, int bits,
+                                    int max_kv_len, long long kv_head_stride, long long seq_stride,
+                                    float softmax_scale, void *out, int out_dtype,
+                                    hipStream_t stream);
+
 /* Fused decode attention over any cache mode: outlier_blocks TQ_OUTLIER_ALL
  * (PQO) or 0 (PQ), norm_mode TQ_NORM_MAXNORM; arguments as
  * tq_pqo_decode_attention.  qjl_signs non-null selects TQ: the logits get

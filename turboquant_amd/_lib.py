@@ -46,6 +46,8 @@ SIGNATURES = {
     "tq_attention_workspace_init": (_i, [_p, _sz, _i, _i, _i, _i, _i, _p]),
     "tq_pqo_decode_attention": (_i, [_p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _ll, _ll, _f, _p, _i,
                                      _p, _sz, _p]),
+    "tq_pqo_decode_attention_noalloc": (_i, [_p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _ll, _ll, _f, _p,
+                                             _i, _p]),
     "tq_quantize_vec_batch": (_i, [_p, _p, _p, _sz, _i, _i, _u64, _p]),
     "tq_dequantize_vec_batch": (_i, [_p, _p, _p, _sz, _i, _i, _u64, _p]),
     "tq_dequantize_rotated_batch": (_i, [_p, _p, _p, _sz, _i, _i, _p]),

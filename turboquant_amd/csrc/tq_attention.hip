@@ -35,6 +35,7 @@
 #include "tq_device.h"
 #include "tq_mfma.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -1120,6 +1121,78 @@ extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t
                                    kv_lens, batch, num_heads, num_kv_heads, head_dim, bits, TQ_OUTLIER_ALL,
                                    TQ_NORM_MAXNORM, max_kv_len, kv_head_stride, seq_stride, softmax_scale, out,
                                    out_dtype, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Decode without a caller workspace and without any allocation: the split-K
+// partials and counters live in a file-scope device array.  Static storage
+// starts zeroed, so the counters are zero before the first call; every call
+// leaves the counters it used at zero again (the merging tile re-arms them)
+// and overwrites the partials it reads.  scratch_pairs holds the number of
+// counters below the array's end (the kernels' workspace header), set by
+// its static initializer.  All calls on one device share that device's
+// copy: calls that overlap in time on one device race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = size_t(8) << 20;  // 8 MiB per device
+constexpr int kScratchPairs = 1024;                // (sequence, KV head) pairs
+static_assert(kScratchPairs * kLine < kScratchBytes, "room for partials");
+
+__device__ __align__(256) int scratch[kScratchBytes / sizeof(int)];
+__device__ int scratch_pairs = kScratchPairs;
+
+constexpr int kMaxDevices = 64;
+struct ScratchDev {
+  char *base = nullptr;
+  int *pairs = nullptr;
+};
+std::mutex g_scratch_mu;
+ScratchDev g_scratch[kMaxDevices];
+
+// The device addresses of scratch and scratch_pairs on the current device,
+// looked up once per device (host code never passes the arrays' names).
+int scratch_for_current_device(DecodeWs *d) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return tqh::fail(TQ_ERR_DEVICE, "no current device (or device index %d beyond %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchDev &s = g_scratch[dev];
+  if (!s.base) {
+    void *p = nullptr, *c = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return tqh::fail(TQ_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    e = hipGetSymbolAddress(&c, HIP_SYMBOL(scratch_pairs));
+    if (e != hipSuccess || !c)
+      return tqh::fail(TQ_ERR_DEVICE, "hipGetSymbolAddress(scratch_pairs) on device %d: %s", dev,
+                       hipGetErrorString(e));
+    s.base = static_cast<char *>(p);
+    s.pairs = static_cast<int *>(c);
+  }
+  d->base = s.base;
+  d->cnt_top = reinterpret_cast<int *>(s.base + kScratchBytes);
+  d->hdr = s.pairs;
+  d->part_bytes = kScratchBytes - (size_t)kScratchPairs * kLine;
+  d->pairs = kScratchPairs;
+  return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" int tq_pqo_decode_attention_noalloc(const void *q, int q_dtype, const uint8_t *k_indices,
+                                               const uint16_t *k_scales, const uint8_t *v_indices,
+                                               const uint16_t *v_scales, const int *kv_lens, int batch,
+                                               int num_heads, int num_kv_heads, int head_dim, int bits,
+                                               int max_kv_len, long long kv_head_stride, long long seq_stride,
+                                               float softmax_scale, void *out, int out_dtype, hipStream_t stream) {
+  DecodeWs d;
+  int rc = scratch_for_current_device(&d);
+  if (rc) return rc;
+  return decode_attention_ws(q, q_dtype, k_indices, k_scales, v_indices, v_scales, nullptr, nullptr, nullptr, kv_lens,
+                             max_kv_len, batch, num_heads, num_kv_heads, head_dim, bits, TQ_OUTLIER_ALL,
+                             TQ_NORM_MAXNORM, max_kv_len, kv_head_stride, seq_stride, softmax_scale, out, out_dtype,
+                             &d, 0, stream);
 }
 
 extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, const uint16_t *k_scales,
