@@ -1,0 +1,867 @@
+// tq_decode_kernel.h -- the streaming fused decode kernel; included by
+// tq_attention.hip inside its anonymous namespace (after AttnArgs and the
+// split-K helpers).
+//
+// One workgroup of WAVES waves (4 or 8) owns a chunk of CHUNK = WAVES * TPW tokens of
+// one (sequence b, KV head g) for a group of HG query heads of that KV head;
+// every compressed byte of the chunk is read once for all HG heads.  Wave w
+// owns the TPW consecutive tokens starting at chunk + w * TPW, as NKT 16-token
+// K tiles and NVP 32-token V tile pairs.
+//
+// Schedule.  At entry every lane issues the loads of its query and of the K
+// records and scales of all its tiles; once the query setup has passed the
+// workgroup barrier (every wave has requested its keys), the V scales and V
+// records.  The keys thus arrive before the values chip-wide.  Each K tile is
+// scored as soon as its records have arrived (the loads return in order), so
+// the keys' arithmetic overlaps the transfer of the later keys; after the last
+// K tile the wave's softmax weights are final (a two-pass softmax over the
+// wave's tokens: no running rescale), and each V tile pair is accumulated as
+// it arrives, overlapping the values' transfer.  What remains after the last
+// byte is one tile pair's value products, the waves' combine and the split-K
+// arrival.
+//
+// Arithmetic (the same decomposition as the reference's per-qblock dequant,
+// tq_attention_kernel.cu:33-53, k_j = |s| inv (H (cb[idx] d))_j): keys are
+// never inverse-rotated; q.k = |s| sum_i cb[idx_i] qt_i with qt the rotated
+// query.  Both contractions run on v_mfma_f32_16x16x32_f16 with every f32
+// operand split into two f16 parts (hi = 11 significant bits, lo = the exact
+// remainder), 22-bit products accumulated in f32; a pair of codes is decoded
+// by one 8-byte LDS read of a 2^(2 BITS)-entry table (hi c0, hi c1, lo c0,
+// lo c1).
+//   K: D[(qblock, head, part)][token] = Q[..][k] K[k][token], the query
+//      operand block-diagonal over QPM qblocks per instruction (so the
+//      per-(token, qblock) key scale applies after the contraction).  QPM
+//      and HPM = 8 / QPM heads per instruction follow from HG, so one
+//      instruction serves every head of the group; lanes (token, k group)
+//      hold the key stream of their qblock's ES-th part (ES = 4 / QPM).
+//   V: D[(qblock, pair, part)][(qblock, head, weight part)] = V W, V through
+//      the transposing LDS read (ds_read_b64_tr_b16) of the same table, W =
+//      p |s_V| 2^-Ev; lanes (token, row set) hold the value stream of their
+//      row set's qblock part.  Accumulated over the wave's tiles in MFMA
+//      registers; the useful (block-diagonal) outputs are extracted once.
+
+constexpr int dmin(int x, int y) { return x < y ? x : y; }
+// LDS of the split-K merge (merge_heads) for a workgroup of `waves` waves
+constexpr int merge_lds(int waves) { return waves * 256 * 4 + waves * 8 * 2 * 4; }
+
+template <int BITS_, int MODE_, int NQB_, int HG_, int TPW_, int WAVES_>
+struct DecCfg {
+  static constexpr int BITS = BITS_, MODE = MODE_, NQB = NQB_, HG = HG_, TPW = TPW_, WAVES = WAVES_;
+  static constexpr int CB = MODE == kModePqo ? BITS : BITS - 1;  // codebook bits
+  static constexpr bool QJL = MODE == kModeTq;
+  static constexpr int HD = 32 * NQB;
+  static constexpr int QW = BITS;                // 32-bit words per qblock record
+  static constexpr int PACKED = NQB * QW * 4;    // bytes per token record
+  // qblocks per instruction (K and V) and heads per instruction
+  static constexpr int QPM = dmin(NQB, HG <= 2 ? 4 : (HG <= 4 ? 2 : 1));
+  static constexpr int HPM = 8 / QPM;
+  static constexpr int QG = NQB / QPM;           // qblock groups (K) / sets (V)
+  static constexpr int ES = 4 / QPM;             // parts of a qblock stream (lanes per qblock)
+  static constexpr int KJ = 2 * QPM;             // K slices (4 elements each) per group
+  static constexpr int PPL = 16 / ES;            // pairs per lane part (= V slices per set)
+  static constexpr int NW = ES == 1 ? QW : 2;    // record words a lane holds per group
+  static constexpr int NKT = TPW / 16, NVP = TPW / 32;
+#ifndef TQ_DECODE_LOOKAHEAD
+#define TQ_DECODE_LOOKAHEAD 2
+#endif
+  static constexpr int LOOKAHEAD = TQ_DECODE_LOOKAHEAD;  // load groups in flight per wave
+  static constexpr int THREADS = 64 * WAVES, CHUNK = WAVES * TPW;
+  static constexpr int NPAIR = 1 << (2 * BITS);
+  static constexpr int SW4 = (NQB + 3) / 4;      // QJL: sign words per lane and tile
+  static constexpr int TPL = TPW / 64;           // V-scale tokens per lane
+  static constexpr bool QA_REGS = QG * KJ <= 8;  // query operands in registers (else LDS)
+  // LDS carve (32-bit words)
+  static constexpr int OFF_PAIR = 0;                                  // uint2 [NPAIR]
+  static constexpr int OFF_NIB = OFF_PAIR + 2 * NPAIR;                // QJL uint2 [16]
+  static constexpr int OFF_QA = (OFF_NIB + (QJL ? 32 : 0) + 3) & ~3;  // u32x4 [QG*KJ][64] (LDS operands)
+  static constexpr int OFF_W = OFF_QA + (QA_REGS ? 0 : QG * KJ * 64 * 4);
+  // the query setup lives in the wave staging area until the K pass starts
+  static constexpr int OFF_Q = OFF_W;                                 // [HG][HD] scaled rotated query
+  static constexpr int OFF_QMAX = OFF_Q + HG * HD;                    // [HG][NQB] block max |qt|
+  static constexpr int OFF_RQ = OFF_QMAX + HG * NQB;                  // QJL [HG][HD]
+  static constexpr int OFF_RQMAX = OFF_RQ + (QJL ? HG * HD : 0);      // QJL [HG][NQB]
+  static constexpr int SETUP_END = OFF_RQMAX + (QJL ? HG * NQB : 0);
+  // register query operands are built once per workgroup, staged here
+  static constexpr int OFF_QAS = (SETUP_END + 3) & ~3;               // u32x4 [QG*KJ][64]
+  // per wave: weights p [HG][TPW] and |s_V| 2^-Ev [NQB][TPW] for the V pass;
+  // after it, the wave's output acc [HG][HD] over them; then m [HG], l [HG], 2^Ev
+  static constexpr int WP = HG * TPW;
+  static constexpr int WS = NQB * TPW;
+  static constexpr int WA = WP + WS > HG * HD ? WP + WS : HG * HD;
+  static constexpr int WSTAGE = (WA + 2 * HG + 1 + 3) & ~3;
+  static constexpr int TOTAL = OFF_W + WAVES * WSTAGE;
+  static constexpr int MERGE_LDS = merge_lds(WAVES);
+  static_assert(SETUP_END <= TOTAL, "the query setup fits the staging area");
+  static_assert(!QA_REGS || OFF_QAS + QG * KJ * 64 * 4 <= TOTAL, "the operand staging fits the staging area");
+  static_assert(HG >= 1 && HG <= 8, "heads per group");
+  static_assert(TPW % 64 == 0, "whole V-scale loads per lane");
+  static_assert(QPM * HPM == 8 && HPM >= HG, "one instruction serves every head");
+  static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "waves per workgroup");
+  // does the workgroup's LDS (with the merge's scratch) fit 64 KiB?
+  static constexpr bool LDS_FITS = TOTAL * 4 + MERGE_LDS <= 64 * 1024;
+};
+
+// A buffer resource over the bytes [off, total) of the records at base:
+// loads past the end return zeros.  The tile offset moves the base (scalar
+// arithmetic) rather than riding in the instruction's scalar offset, so
+// every byte a load touches is inside the range check.
+// (The arguments are wave-uniform; readfirstlane keeps the descriptor in
+// scalar registers, where a buffer instruction takes it.)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rec_rsrc(const void *base, uint32_t total, uint32_t off = 0) {
+  const int d = (int)(total - off);  // both below 2^31 (the host bounds a sequence's records)
+  const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane(d > 0 ? d : 0);
+  const uint64_t p = reinterpret_cast<uint64_t>(base) + off;
+  const uint64_t ps = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(ps), (short)0, (int)n, 0x00020000);
+}
+// N consecutive 32-bit words at voff + soff of a buffer
+template <int N>
+__device__ __forceinline__ void buf_words(uint32_t (&w)[N], __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  if constexpr (N == 1) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  } else if constexpr (N == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    w[0] = v[0];
+    w[1] = v[1];
+  } else if constexpr (N == 3) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
+    w[0] = v[0];
+    w[1] = v[1];
+    w[2] = v[2];
+  } else {
+    static_assert(N == 4, "1 to 4 words");
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    w[0] = v[0];
+    w[1] = v[1];
+    w[2] = v[2];
+    w[3] = v[3];
+  }
+}
+
+// BITS-bit code pair p of a lane's stream w (little-endian words), as the
+// byte offset of its pair-table entry (code * 8): two VALU per pair.
+template <int BITS, int NWD>
+__device__ __forceinline__ uint32_t pair_off(const uint32_t (&w)[NWD], int p) {
+  constexpr int W = 2 * BITS;
+  constexpr uint32_t M = ((1u << W) - 1u) << 3;
+  const int pos = W * p;
+  if (pos < 3) return (w[0] << 3) & M;
+  const int s = pos - 3, wi = s >> 5, sh = s & 31;
+  if (sh + W + 3 <= 32) return (w[wi] >> sh) & M;
+  return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & M;
+}
+
+// Stream of part `es` (of ES) of a qblock record held in w: for ES > 1 the
+// lane loaded the two words from word w0 = min(bo / 32, QW - 2); shift them so
+// that its pairs start at bit 0.
+template <class C>
+__device__ __forceinline__ int part_word(int es) {
+  if constexpr (C::ES == 1) return 0;
+  else return dmin((es * C::PPL * 2 * C::BITS) >> 5, C::QW - 2);
+}
+template <class C>
+__device__ __forceinline__ void align_part(uint32_t (&w)[C::NW], int es) {
+  if constexpr (C::ES > 1) {
+    const int sh = es * C::PPL * 2 * C::BITS - 32 * part_word<C>(es);
+    const uint64_t x = ((((uint64_t)w[1]) << 32) | w[0]) >> sh;
+    w[0] = (uint32_t)x;
+    w[1] = (uint32_t)(x >> 32);
+  }
+}
+
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_quad_xor1(v));
+  v = fmaxf(v, dpp_quad_xor2(v));
+  v = fmaxf(v, swizzle_xor<4>(v));
+  return fmaxf(v, dpp_row_xor8(v));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_quad_xor1(v);
+  v += dpp_quad_xor2(v);
+  v += swizzle_xor<4>(v);
+  return v + dpp_row_xor8(v);
+}
+// v + v of lane l ^ 32 / l ^ 16
+__device__ __forceinline__ float sum_xor32(float v) {
+  float a, b;
+  swap_pair32(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  float a, b;
+  swap_pair16(v, a, b);
+  return a + b;
+}
+
+// ---------------------------------------------------------------------------
+// Split-K merge and inverse rotation of the nr query heads of (b, g):
+//   o = inv * H(sg * sum_c 2^(m_c - M) acc_c) / sum_c 2^(m_c - M) l_c
+// (tq_attention_kernel.cu:299-332; 0 when the sum is 0).  Outputs go in
+// rounds of 256; in a round each of the W waves is one lane set folding every
+// W-th chunk of four consecutive outputs per lane (one 16-byte device-coherent
+// load per chunk, MAXC chunks per lane in one latency round, an online
+// update beyond); the W sets meet once in LDS.
+// ---------------------------------------------------------------------------
+template <int HD, int W>
+__device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
+  constexpr int MAXC = 64 / W;
+  __shared__ __attribute__((aligned(16))) float s_ma[W * 256];
+  __shared__ float s_mml[W * 8 * 2];
+  static_assert(sizeof(s_ma) + sizeof(s_mml) == merge_lds(W), "merge scratch");
+  const int tid = threadIdx.x, part = tid >> 6, quad = tid & 63;
+  const long long bh0 = (long long)b * a.num_heads + (long long)g * a.nr;
+  const int outs = a.nr * HD;
+  for (int o0 = 0; o0 < outs; o0 += 256) {
+    const int oq = o0 + 4 * quad;  // this lane's first output
+    const bool active = oq < outs;
+    const int r = active ? oq / HD : 0, d0 = oq - r * HD;
+    const long long c0 = (bh0 + r) * a.P;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(a.po + c0 * HD, (short)0, a.P * HD * (int)sizeof(float), 0x00020000);
+    float4 pv[MAXC];
+    float pm[MAXC], pl[MAXC];
+#pragma unroll
+    for (int k = 0; k < MAXC; k++) {
+      const int cc = part + W * k;
+      const bool ok = active && cc < nchunks;
+      pv[k] = ok ? ld_agent16(rsrc, (uint32_t)((cc * HD + d0) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+      pm[k] = ok ? ld_agent(&a.pm[c0 + cc]) : -INFINITY;
+      pl[k] = ok ? ld_agent(&a.ps[c0 + cc]) : 0.f;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < MAXC; k++) M = fmaxf(M, pm[k]);
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.f;
+    auto fold = [&](const float4 &v, float l, float w) {
+      A.x = __builtin_fmaf(v.x, w, A.x);
+      A.y = __builtin_fmaf(v.y, w, A.y);
+      A.z = __builtin_fmaf(v.z, w, A.z);
+      A.w = __builtin_fmaf(v.w, w, A.w);
+      L = __builtin_fmaf(l, w, L);
+    };
+#pragma unroll
+    for (int k = 0; k < MAXC; k++) fold(pv[k], pl[k], pm[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[k] - M));
+    for (int cc = part + W * MAXC; active && cc < nchunks; cc += W) {  // long contexts only
+      const float m = ld_agent(&a.pm[c0 + cc]), l = ld_agent(&a.ps[c0 + cc]);
+      const float4 v = ld_agent16(rsrc, (uint32_t)((cc * HD + d0) * 4));
+      if (m == -INFINITY) continue;
+      if (m > M) {
+        const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - m);
+        A.x *= f;
+        A.y *= f;
+        A.z *= f;
+        A.w *= f;
+        L *= f;
+        M = m;
+      }
+      fold(v, l, __builtin_amdgcn_exp2f(m - M));
+    }
+    if (active) {
+      *reinterpret_cast<float4 *>(s_ma + part * 256 + 4 * quad) = A;
+      if (d0 == 0) {
+        const int rl = (oq - o0) / HD;
+        s_mml[2 * (part * 8 + rl)] = M;
+        s_mml[2 * (part * 8 + rl) + 1] = L;
+      }
+    }
+    __syncthreads();
+    const int o = o0 + tid;
+    if (tid < 256 && o < outs) {  // whole 32-lane blocks
+      const int rl = tid / HD, d = o - (o / HD) * HD;
+      float Mx = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < W; p++) Mx = fmaxf(Mx, s_mml[2 * (p * 8 + rl)]);
+      float At = 0.f, Lt = 0.f;
+#pragma unroll
+      for (int p = 0; p < W; p++) {
+        const float mp = s_mml[2 * (p * 8 + rl)];
+        const float f = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - Mx);
+        At = __builtin_fmaf(s_ma[p * 256 + tid], f, At);
+        Lt = __builtin_fmaf(s_mml[2 * (p * 8 + rl) + 1], f, Lt);
+      }
+      const int i = d & 31;
+      const float sg = a.sg_dev ? a.sg_dev[i] : decode_sign(i);
+      const float v = wht32_lanes(At * sg, i);
+      const float res = (Lt > 0.f) ? v * kInvSqrt32 / Lt : 0.f;
+      const long long oi = bh0 * HD + o;
+      if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = res;
+      else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(res);
+      else static_cast<uint16_t *>(a.out)[oi] = f32_to_f16(res);
+    }
+    __syncthreads();
+  }
+}
+
+// The reference ABI's second launch: the split-K merge alone.
+template <int HD>
+__global__ __launch_bounds__(256) void stream_merge_kernel(AttnArgs a) {
+  const int g = blockIdx.x, b = blockIdx.y;
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
+  const int nchunks = (len + a.chunk - 1) / a.chunk;
+  if (nchunks == 0) return;
+  merge_heads<HD, 4>(a, b, g, nchunks);
+}
+
+template <class C, bool INLINE_MERGE>
+#ifndef TQ_DECODE_WPE
+#define TQ_DECODE_WPE 2
+#endif
+__global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kernel(const uint8_t *k_idx, const uint8_t *v_idx,
+                                                               const uint16_t *k_sc, const uint16_t *v_sc,
+                                                               long long seq_stride, long long kv_head_stride,
+                                                               int len_hint, AttnArgs a) {
+  constexpr int BITS = C::BITS, HD = C::HD, NQB = C::NQB, HG = C::HG, TPW = C::TPW, QW = C::QW, NW = C::NW;
+  static_assert(C::LDS_FITS, "the workgroup's LDS (with the merge's scratch) fits 64 KiB");
+  constexpr int QPM = C::QPM, HPM = C::HPM, QG = C::QG, ES = C::ES, KJ = C::KJ, PPL = C::PPL;
+  constexpr int NKT = C::NKT, NVP = C::NVP, PACKED = C::PACKED;
+  __shared__ __attribute__((aligned(16))) float lds[C::TOTAL];
+  __shared__ int s_flag;
+  uint2 *s_pair = reinterpret_cast<uint2 *>(lds + C::OFF_PAIR);
+  float *s_q = lds + C::OFF_Q;
+  float *s_qmax = lds + C::OFF_QMAX;
+  float *s_rq = lds + C::OFF_RQ;
+  float *s_rqmax = lds + C::OFF_RQMAX;
+  uint2 *s_nib = reinterpret_cast<uint2 *>(lds + C::OFF_NIB);
+  u32x4 *s_qa = reinterpret_cast<u32x4 *>(lds + C::OFF_QA);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the wave's scalar offsets
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int c = blockIdx.x, b = blockIdx.z;
+  const int g = blockIdx.y / a.ngroups, gh = blockIdx.y - g * a.ngroups;
+  const int nh = min(HG, a.nr - gh * HG);                    // heads of this group
+  const long long hq0 = (long long)b * a.num_heads + (long long)g * a.nr + gh * HG;  // its first q head
+  const int t0 = c * C::CHUNK, tw = t0 + wave * TPW;
+
+  // ---- the query (and for TQ its projection) goes out first: later waits
+  // for it count no record load ----
+  constexpr int QE = HG * HD;                 // query elements of the group
+  constexpr int QIT = (QE + C::THREADS - 1) / C::THREADS;
+  uint32_t qbits[QIT];
+  float rqv[QIT];
+#pragma unroll
+  for (int k = 0; k < QIT; k++) {
+    const int e = tid + C::THREADS * k, hl = e / HD;
+    qbits[k] = 0;
+    rqv[k] = 0.f;
+    if (e < QE && hl < nh) {
+      const long long qi = hq0 * HD + e;
+      if (a.q_dtype == kF32) qbits[k] = static_cast<const uint32_t *>(a.q)[qi];
+      else qbits[k] = static_cast<const uint16_t *>(a.q)[qi];
+      if constexpr (C::QJL) rqv[k] = a.rq[qi];
+    }
+  }
+  // the caller's decode sign for this lane (selected at its use: a select
+  // here would make the constant path wait for the load before any record
+  // load goes out)
+  float sgl = 0.f;
+  if (a.sg_dev) sgl = a.sg_dev[tid & 31];
+  // the caller's codebook entries for this lane's pair-table entry, also
+  // before any record load (a wait for them then waits for nothing else)
+  constexpr int CM = (1 << C::CB) - 1;  // slot codes >= 2^CB never occur
+  const int pi0 = tid & ((1 << BITS) - 1) & CM, pi1 = (tid >> BITS) & CM;
+  float pc0 = 0.f, pc1 = 0.f;
+  if (a.cb_dev && tid < C::NPAIR) {
+    pc0 = a.cb_dev[pi0];
+    pc1 = a.cb_dev[pi1];
+  }
+  int ws_hdr = 0;
+  if (INLINE_MERGE && tid == 0) ws_hdr = *a.ws_hdr;
+
+  const int len = len_hint >= 0 ? len_hint : min(max(a.kv_lens[b], 0), a.max_len);
+  if (t0 >= len) {  // an empty chunk is not counted by the merge
+    if (len == 0 && c == 0) {
+      // an empty sequence attends to nothing: zero output (cuda/attention.rs:65-68)
+      for (int e = tid; e < nh * HD; e += C::THREADS) {
+        const long long oi = hq0 * HD + e;
+        if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = 0.f;
+        else static_cast<uint16_t *>(a.out)[oi] = 0;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
+  }
+  const int nchunks = (len + C::CHUNK - 1) / C::CHUNK;
+
+  // ---- records.  K tile i, lane (l16, lg): token tw + 16 i + l16, for
+  // group qg the stream part lg % ES of qblock qg * QPM + lg / ES; its key
+  // scale.  V tile i, lane (l16, lg): token tw + 16 i + 4 lg + l16 / 4, row
+  // set rs = l16 & 3 -> stream part rs % ES of qblock vs * QPM + rs / ES.
+  // Buffer loads bounded by the sequence's len records: a token past the end
+  // reads zeros (its score is masked and its weight is 0), and a tile's
+  // offset is a scalar constant. ----
+  const long long rec0 = (long long)b * seq_stride + (long long)g * kv_head_stride;
+  const uint32_t nrec = (uint32_t)len;
+  const uint8_t *kbase = k_idx + rec0 * PACKED, *vbase = v_idx + rec0 * PACKED;
+  const uint16_t *ksbase = k_sc + rec0 * NQB, *vsbase = v_sc + rec0 * NQB;
+  const int kes = lg % ES, kqb = lg / ES;
+  const int rs = l16 & 3, ves = rs % ES, vqb = rs / ES;
+  // per-lane offsets from the wave's first token tw
+  const uint32_t kvo = (uint32_t)l16 * PACKED + (uint32_t)(kqb * QW + part_word<C>(kes)) * 4u;
+  const uint32_t kso = ((uint32_t)l16 * NQB + kqb) * 2u;
+  const uint32_t vvo = (uint32_t)(4 * lg + (l16 >> 2)) * PACKED + (uint32_t)(vqb * QW + part_word<C>(ves)) * 4u;
+  const uint32_t tw0 = (uint32_t)tw;
+  uint32_t kw[NKT][QG][NW], vw[NKT][QG][NW];
+  uint32_t ksv[NKT][QG];
+  uint32_t sgw[NKT][C::SW4];
+  uint32_t nrm[NKT];
+  uint32_t vsr[C::TPL][(NQB + 1) / 2];
+  // The wave's loads form one stream of NG groups, consumed in order: K tile
+  // i (records, scales, QJL signs and norms) is group i, the V scales group
+  // NKT, V tile i group NKT + 1 + i.  LA groups stay in flight: group c + LA
+  // is issued as group c is consumed, so no load instruction waits at issue
+  // for the CU's memory queue while arithmetic could run.
+  constexpr int NG = 2 * NKT + 1;
+  auto issue = [&](int grp) {
+    if (grp < NKT) {
+      const int i = grp;
+      const uint32_t t16 = tw0 + 16u * i;  // the tile's first token
+      const auto rk = rec_rsrc(kbase, nrec * PACKED, t16 * PACKED);
+      const auto rks = rec_rsrc(ksbase, nrec * NQB * 2u, t16 * NQB * 2u);
+#pragma unroll
+      for (int qg = 0; qg < QG; qg++) {
+        buf_words<NW>(kw[i][qg], rk, kvo + qg * QPM * QW * 4, 0);
+        ksv[i][qg] = __builtin_amdgcn_raw_buffer_load_b16(rks, kso + qg * QPM * 2, 0, 0);
+      }
+      if constexpr (C::QJL) {
+        const auto rsg = rec_rsrc(reinterpret_cast<const uint8_t *>(a.qjl_signs) + rec0 * (HD / 8), nrec * (HD / 8),
+                                  t16 * (HD / 8));
+        const auto rnm = rec_rsrc(a.qjl_norms + rec0, nrec * 2u, t16 * 2u);
+#pragma unroll
+        for (int s4 = 0; s4 < C::SW4; s4++) {
+          const int wi = min(s4 * 4 + lg, NQB - 1);
+          sgw[i][s4] = __builtin_amdgcn_raw_buffer_load_b32(rsg, (uint32_t)l16 * (HD / 8) + wi * 4, 0, 0);
+        }
+        nrm[i] = __builtin_amdgcn_raw_buffer_load_b16(rnm, (uint32_t)l16 * 2u, 0, 0);
+      }
+    } else if (grp == NKT) {
+      // V scales of the wave: tokens tw + TPL lane + u, all NQB per token
+      const auto rvs = rec_rsrc(vsbase, nrec * NQB * 2u, tw0 * NQB * 2u);
+      const uint32_t vso = (uint32_t)(C::TPL * lane) * NQB * 2u;
+#pragma unroll
+      for (int u = 0; u < C::TPL; u++) {
+        if constexpr (NQB == 1) vsr[u][0] = __builtin_amdgcn_raw_buffer_load_b16(rvs, vso + u * 2, 0, 0);
+        else buf_words<NQB / 2>(vsr[u], rvs, vso + u * NQB * 2, 0);
+      }
+    } else if (grp < NG) {
+      const int i = grp - NKT - 1;
+      const auto rv = rec_rsrc(vbase, nrec * PACKED, (tw0 + 16u * i) * PACKED);
+#pragma unroll
+      for (int qg = 0; qg < QG; qg++) buf_words<NW>(vw[i][qg], rv, vvo + qg * QPM * QW * 4, 0);
+    }
+  };
+  constexpr int LA = dmin(C::LOOKAHEAD, NG);
+#pragma unroll
+  for (int grp = 0; grp < LA; grp++) issue(grp);
+  // ---- pair table (the caller's device codebook, L2Norm tables from the
+  // arguments, or the PQO constants) ----
+  static_assert(C::NPAIR <= 256, "one pair-table entry per lane");
+  if (tid < C::NPAIR) {
+    const int e = tid, i0 = pi0, i1 = pi1;
+    float c0, c1;
+    if (a.cb_dev) {
+      c0 = pc0;
+      c1 = pc1;
+    } else if (a.cb_args) {
+      c0 = a.cb[0];
+      c1 = a.cb[0];
+#pragma unroll
+      for (int kk = 1; kk <= CM; kk++) {
+        c0 = i0 == kk ? a.cb[kk] : c0;
+        c1 = i1 == kk ? a.cb[kk] : c1;
+      }
+    } else {
+      c0 = pqo_centroid<C::CB>(i0);
+      c1 = pqo_centroid<C::CB>(i1);
+    }
+    const float h0 = split_hi(c0), h1 = split_hi(c1);
+    s_pair[e] = make_uint2(pack_f16(h0, h1), pack_f16(c0 - h0, c1 - h1));
+  }
+  if constexpr (C::QJL) {
+    // +-1 in f16 for the four sign bits of a nibble, LSB first
+    if (tid < 16) {
+      auto pm1 = [&](int bit) { return ((tid >> bit) & 1) ? 0x3C00u : 0xBC00u; };
+      s_nib[tid] = make_uint2(pm1(0) | (pm1(1) << 16), pm1(2) | (pm1(3) << 16));
+    }
+  }
+  // ---- rotated, scaled query: 32-lane butterflies (elements of a qblock sit
+  // in 32 consecutive lanes; absent heads are whole zero blocks) ----
+  const float qscale = a.softmax_scale * kLog2e * kInvSqrt32;
+  const float qsign = a.sg_dev ? sgl : decode_sign(tid & 31);
+#pragma unroll
+  for (int k = 0; k < QIT; k++) {
+    const int e = tid + C::THREADS * k;
+    if (e < QE) {  // uniform per 32-lane block
+      const float v = wht32_lanes(q_value(qbits[k], a.q_dtype), e & 31);
+      const float qt = v * (qsign * qscale);
+      s_q[e] = qt;
+      float m = fabsf(qt);
+      m = fmaxf(m, lane_xor<1>(m));
+      m = fmaxf(m, lane_xor<2>(m));
+      m = fmaxf(m, lane_xor<4>(m));
+      m = fmaxf(m, lane_xor<8>(m));
+      m = fmaxf(m, lane_xor<16>(m));
+      if ((e & 31) == 0) s_qmax[e >> 5] = m;
+      if constexpr (C::QJL) {
+        const float rsv = rqv[k] * (a.softmax_scale * kLog2e);
+        s_rq[e] = rsv;
+        float r = fabsf(rsv);
+        r = fmaxf(r, lane_xor<1>(r));
+        r = fmaxf(r, lane_xor<2>(r));
+        r = fmaxf(r, lane_xor<4>(r));
+        r = fmaxf(r, lane_xor<8>(r));
+        r = fmaxf(r, lane_xor<16>(r));
+        if ((e & 31) == 0) s_rqmax[e >> 5] = r;
+      }
+    }
+  }
+  __syncthreads();
+  auto head_exp = [&](const float *mx, int hl) {
+    float m = 0.f;
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) m = fmaxf(m, mx[hl * NQB + qb]);
+    return pow2_exponent(m);
+  };
+  // Key-pass query operands: for group qg and slice j, lane (m, kg) supplies
+  // k = 8 kg + (x0, x1, x0, x1, x2, x3, x2, x3), x_i = part(Q[head][e + i])
+  // with row m = (qbl, hl, part), e = element 4 j of stream part kg % ES of
+  // qblock qg * QPM + qbl, when kg / ES == qbl and hl < nh; Q = qt * 2^-Eq,
+  // scaled per head into f16's range.
+  auto make_qa = [&](int qg, int j, int m, int kg) -> u32x4 {
+    const int qbl = m / (2 * HPM), hl = (m >> 1) % HPM, part = m & 1;
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (kg / ES == qbl && hl < nh) {
+      const float sc = exp2i(-head_exp(s_qmax, hl));
+      const float4 q4 = *reinterpret_cast<const float4 *>(s_q + hl * HD + (qg * QPM + qbl) * 32 +
+                                                          (kg % ES) * (32 / ES) + 4 * j);
+      const float x0 = q4.x * sc, x1 = q4.y * sc, x2 = q4.z * sc, x3 = q4.w * sc;
+      const float h0 = split_hi(x0), h1 = split_hi(x1), h2 = split_hi(x2), h3 = split_hi(x3);
+      const uint32_t w01 = part ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
+      const uint32_t w23 = part ? pack_f16(x2 - h2, x3 - h3) : pack_f16(h2, h3);
+      val = u32x4{w01, w01, w23, w23};
+    }
+    return val;
+  };
+  u32x4 qa[C::QA_REGS ? QG * KJ : 1];
+  if constexpr (C::QA_REGS) {
+    // each operand is the same for every wave: the workgroup's lanes build
+    // them once, each wave then reads its registers
+    u32x4 *s_qas = reinterpret_cast<u32x4 *>(lds + C::OFF_QAS);
+    for (int e = tid; e < QG * KJ * 64; e += C::THREADS) {
+      const int sl = e >> 6, ln = e & 63;
+      s_qas[e] = make_qa(sl / KJ, sl % KJ, ln & 15, ln >> 4);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < QG * KJ; k++) qa[k] = s_qas[k * 64 + lane];
+  } else {
+    for (int e = tid; e < QG * KJ * 64; e += C::THREADS) {
+      const int sl = e >> 6, ln = e & 63;
+      s_qa[e] = make_qa(sl / KJ, sl % KJ, ln & 15, ln >> 4);
+    }
+  }
+  // score rows of this lane's MFMA outputs: heads hl0 + u (u = 0, 1) of
+  // qblock row qbl.  After the cross-qblock sum a lane keeps NS scores: both
+  // heads (QPM 1, one qblock per row group: nothing to sum) or head hl0 + uh
+  // (QPM 2 and 4: the sum trades the register halves, lanes 0-31 keep head
+  // hl0 and lanes 32-63 head hl0 + 1).
+  const int hl0 = (2 * lg) % HPM, uh = lane >> 5;
+  constexpr int NS = QPM == 1 ? 2 : 1;
+  float escale[NS], erscale[NS];
+#pragma unroll
+  for (int v = 0; v < NS; v++) {
+    const int hl = min(hl0 + (NS == 2 ? v : uh), HG - 1);
+    escale[v] = exp2i(head_exp(s_qmax, hl));
+    erscale[v] = C::QJL ? exp2i(head_exp(s_rqmax, hl)) : 0.f;
+  }
+  // QJL correction operands: MFMA s = 4 s4 + sb covers sign byte sb of sign
+  // word 4 s4 + kg (k = 8 kg + i <-> element 32 (4 s4 + kg) + 8 sb + i); row
+  // m = 4 r + 2 u + part holds part(rq) of head hl0(r) + u, so the sums land
+  // in the lanes whose scores they correct
+  u32x4 ra[C::QJL ? 4 * C::SW4 : 1];
+  if constexpr (C::QJL) {
+    const int r = l16 >> 2, u = (l16 >> 1) & 1, part = l16 & 1;
+    const int hl = (2 * r) % HPM + u;
+#pragma unroll
+    for (int s = 0; s < 4 * C::SW4; s++) {
+      const int wi = (s >> 2) * 4 + lg, sb = s & 3;
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if (hl < nh && wi < NQB) {
+        const float sc = exp2i(-head_exp(s_rqmax, hl));
+        const float *src = s_rq + hl * HD + 32 * wi + 8 * sb;
+        uint32_t wv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float x0 = src[2 * i] * sc, x1 = src[2 * i + 1] * sc;
+          const float h0 = split_hi(x0), h1 = split_hi(x1);
+          wv[i] = part ? pack_f16(x0 - h0, x1 - h1) : pack_f16(h0, h1);
+        }
+        val = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      }
+      ra[s] = val;
+    }
+  }
+  // the query setup is dead from here: the staging area it lives in is the waves' own
+  __syncthreads();
+
+  // ---- K pass, tile by tile as the records arrive ----
+  float sc[NKT][NS];
+#pragma unroll
+  for (int i = 0; i < NKT; i++) {
+    issue(i + LA);
+    f32x4 dk[QG];
+#pragma unroll
+    for (int qg = 0; qg < QG; qg++) {
+      dk[qg] = f32x4{0.f, 0.f, 0.f, 0.f};
+      align_part<C>(kw[i][qg], kes);
+    }
+    // every pair-table read of the tile goes out before its first MFMA, so
+    // the LDS latency is paid once per tile, not once per instruction
+    uint2 e[QG][KJ][2];
+#pragma unroll
+    for (int qg = 0; qg < QG; qg++)
+#pragma unroll
+      for (int j = 0; j < 2 * KJ; j++)
+        e[qg][j >> 1][j & 1] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(s_pair) +
+                                                                pair_off<BITS, NW>(kw[i][qg], j));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int qg = 0; qg < QG; qg++)
+#pragma unroll
+      for (int j = 0; j < KJ; j++) {
+        const u32x4 qv = C::QA_REGS ? qa[C::QA_REGS ? qg * KJ + j : 0] : s_qa[(qg * KJ + j) * 64 + lane];
+        dk[qg] = mfma(qv, u32x4{e[qg][j][0].x, e[qg][j][0].y, e[qg][j][1].x, e[qg][j][1].y}, dk[qg]);
+      }
+    f32x4 dq = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (C::QJL) {
+#pragma unroll
+      for (int s = 0; s < 4 * C::SW4; s++) {
+        const uint32_t byte = (sgw[i][s >> 2] >> (8 * (s & 3))) & 0xffu;
+        const uint2 n0 = s_nib[byte & 15u], n1 = s_nib[byte >> 4];
+        dq = mfma(ra[s], u32x4{n0.x, n0.y, n1.x, n1.y}, dq);
+      }
+    }
+    // lane (token l16, row group lg): rows (qbl, head hl0 + u, part)
+    float x[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      x[u] = 0.f;
+#pragma unroll
+      for (int qg = 0; qg < QG; qg++) {
+        const float sk = fabsf(f16_to_f32((uint16_t)ksv[i][qg]));
+        x[u] = __builtin_fmaf(dk[qg][2 * u] + dk[qg][2 * u + 1], sk, x[u]);
+      }
+    }
+    // sum over the qblocks of the instruction (row groups lg ^ 2 and, for
+    // QPM 4, lg ^ 1): one trade of the register halves covers both heads
+    float y[NS];
+    if constexpr (NS == 2) {
+      y[0] = x[0];
+      y[1] = x[1];
+    } else {
+      trade_halves32(x[0], x[1]);
+      y[0] = x[0] + x[1];
+      if constexpr (QPM == 4) y[0] = sum_xor16(y[0]);
+    }
+    const bool tok_ok = tw + 16 * i + l16 < len;
+#pragma unroll
+    for (int v = 0; v < NS; v++) {
+      float s = y[v] * escale[v];
+      const int u = NS == 2 ? v : uh;
+      if constexpr (C::QJL) {
+        const float cn = f16_to_f32((uint16_t)nrm[i]) * a.qjl_c;
+        const float dqs = NS == 2 ? dq[2 * v] + dq[2 * v + 1] : (uh ? dq[2] + dq[3] : dq[0] + dq[1]);
+        s = __builtin_fmaf(dqs, cn * erscale[v], s);
+      }
+      sc[i][v] = (tok_ok && hl0 + u < nh) ? s : -INFINITY;
+    }
+  }
+
+  // ---- softmax over the wave's tokens (base 2): per head row max and sum ----
+  issue(NKT + LA);
+  float* stage = lds + C::OFF_W + wave * C::WSTAGE;
+  float *st_p = stage;                 // [HG][TPW]
+  float *st_s = stage + C::WP;         // [NQB][TPW]
+  float *comb = stage;                 // [HG][HD] after the V pass
+  float *cml = stage + C::WA;          // m[HG], l[HG], 2^Ev
+  float mrow[NS], lrow[NS];
+  // 16-lane rows holding the same head: R replicas (QPM 4: the row groups
+  // lg and lg ^ 1; else one), replica ri stores every R-th tile's weights
+  constexpr int R = QPM == 4 ? 2 : 1;
+  const int ri = QPM == 4 ? (lg & 1) : 0;
+#pragma unroll
+  for (int v = 0; v < NS; v++) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NKT; i++) m = fmaxf(m, sc[i][v]);
+    m = row_max16(m);
+    float l = 0.f;
+    const int hl = hl0 + (NS == 2 ? v : uh);
+#pragma unroll
+    for (int i = 0; i < NKT; i++) {
+      const float p = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[i][v] - m);
+      l += p;
+      if (hl < HG && i % R == ri) st_p[hl * TPW + 16 * i + l16] = p;
+    }
+    mrow[v] = m;
+    lrow[v] = row_sum16(l);
+  }
+  // V scales (lane: tokens TPL lane + u) as |s| 2^-Ev, Ev from the wave's largest
+  float svv[C::TPL][NQB];
+  float smax = 0.f;
+#pragma unroll
+  for (int u = 0; u < C::TPL; u++)
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) {
+      const uint32_t bits = NQB == 1 ? vsr[u][0] : (vsr[u][qb >> 1] >> (16 * (qb & 1)));
+      svv[u][qb] = fabsf(f16_to_f32((uint16_t)(bits & 0xffffu)));
+      smax = fmaxf(smax, svv[u][qb]);
+    }
+  const int ev = pow2_exponent(wave_max(smax));
+  const float vinv = exp2i(-ev);
+#pragma unroll
+  for (int u = 0; u < C::TPL; u++)
+#pragma unroll
+    for (int qb = 0; qb < NQB; qb++) st_s[qb * TPW + C::TPL * lane + u] = svv[u][qb] * vinv;
+  if (l16 == 0) {
+#pragma unroll
+    for (int v = 0; v < NS; v++) {
+      const int hl = hl0 + (NS == 2 ? v : uh);
+      if (hl < HG && ri == 0) {
+        cml[hl] = mrow[v];
+        cml[HG + hl] = lrow[v];
+      }
+    }
+    if (lane == 0) cml[2 * HG] = exp2i(ev);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- V pass, tile pair by tile pair.  Weight operand of lane (n, kg),
+  // column n = (qblock qsp of the set, head hv, weight part): the weights of
+  // tokens 4 kg .. 4 kg + 3 of both tiles ----
+  const int qsp = l16 / (2 * HPM), hv = (l16 >> 1) % HPM, wpart = l16 & 1;
+  const float kpart = wpart ? -1.f : 0.f;
+  f32x4 dv[QG][PPL];
+#pragma unroll
+  for (int vs = 0; vs < QG; vs++)
+#pragma unroll
+    for (int j = 0; j < PPL; j++) dv[vs][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int vp = 0; vp < NVP; vp++) {
+    issue(NKT + 1 + 2 * vp + LA);
+    issue(NKT + 2 + 2 * vp + LA);
+    u32x4 bw[QG];
+#pragma unroll
+    for (int vs = 0; vs < QG; vs++) {
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      if (hv < nh) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const int t = 32 * vp + 16 * u + 4 * lg;
+          const float4 p4 = *reinterpret_cast<const float4 *>(st_p + hv * TPW + t);
+          const float4 s4 = *reinterpret_cast<const float4 *>(st_s + (vs * QPM + qsp) * TPW + t);
+          const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
+          w[2 * u] = pack_rem(x0, x1, pack_f16(x0, x1), kpart);
+          w[2 * u + 1] = pack_rem(x2, x3, pack_f16(x2, x3), kpart);
+        }
+      }
+      bw[vs] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+#pragma unroll
+    for (int vs = 0; vs < QG; vs++) {
+      align_part<C>(vw[2 * vp][vs], ves);
+      align_part<C>(vw[2 * vp + 1][vs], ves);
+      // the set's transposing reads all go out ahead of its MFMAs
+      u32x2 r[PPL][2];
+#pragma unroll
+      for (int j = 0; j < PPL; j++) {
+        r[j][0] = lds_read_tr16(reinterpret_cast<const char *>(s_pair) + pair_off<BITS, NW>(vw[2 * vp][vs], j));
+        r[j][1] = lds_read_tr16(reinterpret_cast<const char *>(s_pair) + pair_off<BITS, NW>(vw[2 * vp + 1][vs], j));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < PPL; j++) dv[vs][j] = mfma(u32x4{r[j][0][0], r[j][0][1], r[j][1][0], r[j][1][1]}, bw[vs], dv[vs][j]);
+    }
+  }
+  // useful outputs: lane (n, lg) holds rows (row set lg: qblock lg / ES, pair
+  // part lg % ES; parts hi c0, hi c1, lo c0, lo c1) under column n; the two
+  // weight parts of a head sit in lanes n, n ^ 1
+  {
+    const int oqb = lg / ES, ops = lg % ES;
+    const bool keep = qsp == oqb && wpart == 0 && hv < nh;
+#pragma unroll
+    for (int vs = 0; vs < QG; vs++)
+#pragma unroll
+      for (int j = 0; j < PPL; j++) {
+        float o[2];
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+          const float xx = dv[vs][j][cc] + dv[vs][j][cc + 2];
+          o[cc] = dpp_quad_xor1(xx) + xx;
+          asm volatile("" : "+v"(o[cc]));  // keeps the add beside its DPP read
+        }
+        if (keep)
+          *reinterpret_cast<float2 *>(comb + hv * HD + (vs * QPM + oqb) * 32 + 2 * (ops * PPL + j)) =
+              make_float2(o[0], o[1]);
+      }
+  }
+
+  // ---- combine the waves' records; the workgroup's partial goes out ----
+  if (tid == 0) s_flag = (INLINE_MERGE && (ws_hdr < a.ws_pairs || ws_hdr > a.ws_room)) ? 2 : 0;
+  __syncthreads();
+  const bool ws_ok = s_flag != 2;
+  for (int e = tid; e < nh * HD; e += C::THREADS) {
+    const int hl = e / HD, d = e - hl * HD;
+    float mw[C::WAVES], M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < C::WAVES; w++) {
+      mw[w] = lds[C::OFF_W + w * C::WSTAGE + C::WA + hl];
+      M = fmaxf(M, mw[w]);
+    }
+    float A = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < C::WAVES; w++) {
+      const float *cw = lds + C::OFF_W + w * C::WSTAGE;
+      const float f = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
+      A = __builtin_fmaf(cw[hl * HD + d], f * cw[C::WA + 2 * HG], A);
+      L = __builtin_fmaf(cw[C::WA + HG + hl], f, L);
+    }
+    if (ws_ok) {
+      const long long bh = hq0 + hl;
+      st_agent(&a.po[(bh * a.P + c) * HD + d], A);
+      if (d == 0) {
+        st_agent(&a.pm[bh * a.P + c], M);
+        st_agent(&a.ps[bh * a.P + c], L);
+      }
+    }
+  }
+
+  // ---- split-K arrival: the last of the (sequence, KV head)'s chunks x
+  // head groups merges every head of the KV head ----
+  if constexpr (!INLINE_MERGE) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  int *counter = a.cnt_top - (1 + b * a.num_kv_heads + g) * kCounterStride;
+  if (tid == 0 && ws_ok) {
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_flag = (prev == nchunks * a.ngroups - 1);
+  }
+  __syncthreads();
+  if (!ws_ok) {
+    for (int e = tid; e < nh * HD; e += C::THREADS) {
+      const long long oi = hq0 * HD + e;
+      if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = __builtin_nanf("");
+      else static_cast<uint16_t *>(a.out)[oi] = 0x7e00;  // quiet NaN in f16 and bf16 alike
+    }
+  } else if (s_flag) {
+    if constexpr (INLINE_MERGE) {
+      merge_heads<HD, C::WAVES>(a, b, g, nchunks);
+      if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}

@@ -46,16 +46,41 @@ __device__ __forceinline__ float lane_xor(float v) {
   else if constexpr (X == 8) return dpp_row_xor8(v);
   else return swizzle_xor<X>(v);
 }
-// max(v, v of lane l ^ 16) and max(v, v of lane l ^ 32) on the permlane
-// swaps: with both operands v, the two results of a swap are v of lane l
-// and of its partner, in some order.
+// The values of lane l and of lane l ^ 16 (l ^ 32), by one permlane swap of v
+// with a copy of itself (v_permlane16_swap: the odd rows of the first
+// operand trade places with the even rows of the second; v_permlane32_swap:
+// the upper half of the first with the lower half of the second), so the
+// two registers end as v of lane l and of its partner, in some order.  The
+// swap is written in assembly: this toolchain's lowering of the
+// __builtin_amdgcn_permlane*_swap pair result hands back the first register
+// for both elements.  The s_nop gives the two wait states a VALU write needs
+// before a permlane reads the register.
+__device__ __forceinline__ void swap_pair16(float v, float &a, float &b) {
+  a = v;
+  b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_pair32(float v, float &a, float &b) {
+  a = v;
+  b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+// Two registers' halves traded in place: afterwards a = (a of lanes 0-31,
+// b of lanes 0-31) and b = (a of lanes 32-63, b of lanes 32-63), so a + b is
+// a's sum over the halves in lanes 0-31 and b's in lanes 32-63.
+__device__ __forceinline__ void trade_halves32(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+// max(v, v of lane l ^ 16) and max(v, v of lane l ^ 32)
 __device__ __forceinline__ float max_xor16(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+  float a, b;
+  swap_pair16(v, a, b);
+  return fmaxf(a, b);
 }
 __device__ __forceinline__ float max_xor32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+  float a, b;
+  swap_pair32(v, a, b);
+  return fmaxf(a, b);
 }
 
 // Unnormalised 32-point Walsh-Hadamard transform across lanes: lane i (bits
