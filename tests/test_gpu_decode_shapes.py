@@ -138,3 +138,48 @@ def test_reference_abi_shapes(tq, d, nr):
     out = tq.fused_attention(_dev(q), *recs, cb, sg, hkv, t, cap, bits, 1 / math.sqrt(d))
     torch.cuda.synchronize()
     assert np.abs(out.cpu().numpy() - ref).max() <= TOL
+
+
+@pytest.mark.parametrize("bits,nr", [(3, 2), (4, 4)])
+def test_batched_ragged_grid_over_the_compute_units(tq, bits, nr):
+    """A batch whose grid of 8-wave workgroups exceeds the compute units runs
+    the 4-wave form (twice the chunks per sequence, each merged the same
+    way); ragged lengths, one of them empty, one a single token."""
+    bsz, hkv, d, cap = 24, 8, 128, 1400
+    rng = np.random.default_rng(70 + bits + nr)
+    lens = rng.integers(1100, cap + 1, size=bsz)
+    lens[3], lens[7] = 0, 1
+    h = hkv * nr
+    pd, nb = d * bits // 8, d // 32
+    kp = np.zeros((bsz, hkv, cap, pd), np.uint8)
+    ks = np.zeros((bsz, hkv, cap, nb), np.int16)
+    vp = np.zeros_like(kp)
+    vs = np.zeros_like(ks)
+    q = bf16_round(rng.standard_normal((bsz, h, d)).astype(np.float32) / np.float32(math.sqrt(d)))
+    refs = []
+    for b in range(bsz):
+        t = int(lens[b])
+        if t == 0:
+            refs.append(np.zeros((h, d), np.float32))
+            continue
+        k = kv_outlier(rng, hkv, t, d).reshape(-1, d)
+        v = kv_outlier(rng, hkv, t, d).reshape(-1, d)
+        pk, sk = orc.polar_quantize(bits, orc.OUTLIER_ALL, k, d)
+        pv, sv = orc.polar_quantize(bits, orc.OUTLIER_ALL, v, d)
+        kd = orc.polar_dequantize(bits, orc.OUTLIER_ALL, pk, sk, d).reshape(hkv, t, d)
+        vd = orc.polar_dequantize(bits, orc.OUTLIER_ALL, pv, sv, d).reshape(hkv, t, d)
+        kp[b, :, :t] = pk.reshape(hkv, t, pd)
+        ks[b, :, :t] = sk.view(np.int16).reshape(hkv, t, nb)
+        vp[b, :, :t] = pv.reshape(hkv, t, pd)
+        vs[b, :, :t] = sv.view(np.int16).reshape(hkv, t, nb)
+        refs.append(orc.attention_dense(q[b], kd, vd, 1 / math.sqrt(d)))
+    assert bsz * hkv * -(-cap // 1024) > 256  # the 8-wave grid would exceed 256 compute units
+    ws = tq.AttentionWorkspace(bsz, h, hkv, d, cap)
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    out = tq.cache_decode_attention(qd, _dev(kp), _dev(ks), _dev(vp), _dev(vs),
+                                    _dev(lens.astype(np.int32)), hkv, bits, cap, cap, hkv * cap,
+                                    1 / math.sqrt(d), ws, orc.OUTLIER_ALL)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for b in range(bsz):
+        assert np.abs(out[b] - refs[b]).max() <= TOL, b

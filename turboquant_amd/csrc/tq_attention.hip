@@ -156,14 +156,16 @@ constexpr int stream_waves_c() {
 }
 template <int BITS, int MODE, int NQB, int HG>
 using StreamCfg = DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), stream_waves_c<BITS, MODE, NQB, HG>()>;
+template <int BITS, int MODE, int NQB, int HG>
+using StreamCfg4 = DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), 4>;
 // The workspace layout is fixed by the shape alone: its chunk is the
-// smallest any bit width or mode uses, so every launch's chunks fit its
-// partial rows.
+// smallest any bit width, mode or workgroup size uses (the 4-wave form), so
+// every launch's chunks fit its partial rows.
 template <int NQB, int HG>
 constexpr int stream_chunk_c() {
-  return dmin(dmin(dmin(StreamCfg<3, kModePqo, NQB, HG>::CHUNK, StreamCfg<4, kModePqo, NQB, HG>::CHUNK),
-                   dmin(StreamCfg<3, kModePq, NQB, HG>::CHUNK, StreamCfg<4, kModePq, NQB, HG>::CHUNK)),
-              dmin(StreamCfg<3, kModeTq, NQB, HG>::CHUNK, StreamCfg<4, kModeTq, NQB, HG>::CHUNK));
+  return dmin(dmin(dmin(StreamCfg4<3, kModePqo, NQB, HG>::CHUNK, StreamCfg4<4, kModePqo, NQB, HG>::CHUNK),
+                   dmin(StreamCfg4<3, kModePq, NQB, HG>::CHUNK, StreamCfg4<4, kModePq, NQB, HG>::CHUNK)),
+              dmin(StreamCfg4<3, kModeTq, NQB, HG>::CHUNK, StreamCfg4<4, kModeTq, NQB, HG>::CHUNK));
 }
 template <int NQB>
 int stream_chunk_hg(int hg) {
@@ -227,15 +229,41 @@ AttnArgs base_args() {
   return a;
 }
 
-template <int BITS, int MODE, int NQB, int HG, bool INLINE>
-void launch_stream_cfg(AttnArgs &a, dim3 grid, hipStream_t st) {
-  using C = StreamCfg<BITS, MODE, NQB, HG>;
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
+template <class C, bool INLINE>
+void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
   a.chunk = C::CHUNK;
   grid.x = (unsigned)((a.max_len + C::CHUNK - 1) / C::CHUNK);
   if (grid.x == 0) grid.x = 1;  // an empty batch still zeroes its outputs
   const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
   hipLaunchKernelGGL((stream_decode_kernel<C, INLINE>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx, a.k_sc,
                      a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+}
+// The cache decode picks the workgroup size per launch: 8 waves while the
+// grid of 8-wave workgroups leaves compute units idle (one long sequence:
+// the halved split-K merge is on the critical path), else 4 waves (several
+// workgroups per compute unit keep more waves per SIMD in flight).  The
+// reference ABI (a separate merge launch) always takes the 8-wave form.
+template <int BITS, int MODE, int NQB, int HG, bool INLINE>
+void launch_stream_cfg(AttnArgs &a, dim3 grid, hipStream_t st) {
+  using C = StreamCfg<BITS, MODE, NQB, HG>;
+  using C4 = StreamCfg4<BITS, MODE, NQB, HG>;
+  if constexpr (INLINE && C::WAVES != 4) {
+    const long long wgs = (long long)((a.max_len + C::CHUNK - 1) / C::CHUNK) * grid.y * grid.z;
+    if (wgs > device_cus()) return launch_stream_c<C4, INLINE>(a, grid, st);
+  }
+  launch_stream_c<C, INLINE>(a, grid, st);
 }
 template <int BITS, int MODE, int NQB, bool INLINE>
 void launch_stream_hg(AttnArgs &a, int hg, dim3 grid, hipStream_t st) {
