@@ -50,7 +50,7 @@ def test_qjl_quantize_bit_exact(tq, tb, dim):
 def test_query_context_bit_exact(tq, dim):
     q = orc.lcg_normal_vecs(5 + dim, dim, 50)
     ctx = tq.qjl_query_context(_dev(q), 42, 999).cpu().numpy()
-    for i in (0, 17, 49):
+    for i in range(len(q)):  # 50 queries: the last block of 8 is partial
         assert np.array_equal(ctx[i, dim:], orc.query_projections(q[i], 999))
         assert np.array_equal(ctx[i, :dim], orc.rotate(q[i], orc.sign_pattern(dim, 42)))
 

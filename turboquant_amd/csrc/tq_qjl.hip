@@ -15,6 +15,7 @@
 // tables of qt-pair x centroid-pair products and of +-rq nibble sums, so a
 // score is one table read per two key elements plus one per four sign bits.
 #include "tq_codec_dev.h"
+#include "tq_mfma.h"
 
 #include <type_traits>
 
@@ -73,86 +74,203 @@ struct QjlConsts {
   float sqrt_d;        // fl(sqrt(d))
 };
 
-// quantize_with_qjl (qjl.rs:355-377) per key, lane = key.
+// +-1 for the four sign bits of a nibble (bit i set <=> element i negative)
+__device__ __forceinline__ float4 nibble_signs(int nib) {
+  return make_float4((nib & 1) ? -1.0f : 1.0f, (nib & 2) ? -1.0f : 1.0f, (nib & 4) ? -1.0f : 1.0f,
+                     (nib & 8) ? -1.0f : 1.0f);
+}
+
+// quantize_with_qjl (qjl.rs:355-377) for KB = 32 keys per workgroup.  One lane
+// of each group of 8 quantizes its key (polar codes, scale, residual r = x -
+// dequantized x, |r|) and stages r in LDS; then the 8 lanes of the key share
+// its D sign projections, D / 8 rows each.  A row is summed in column order
+// from -0.0 exactly as rademacher_vector_product (qjl.rs:196-208): the signs
+// of four columns come from one table read by the nibble of the row's bits,
+// and fma(+-1, r_c, s) is the reference's fl(s + sign * r_c).  Four rows at a
+// time keep four independent sums in flight.
 template <int D, int PB>
 __global__ __launch_bounds__(kBlock) void qjl_quant_kernel(const float *__restrict__ x, uint8_t *__restrict__ polar,
                                                            uint16_t *__restrict__ polar_scales,
                                                            uint32_t *__restrict__ signs,
                                                            uint16_t *__restrict__ residual_norms, long long n,
                                                            QjlConsts k) {
+  constexpr int LPK = 8, KB = kBlock / LPK, RPL = D / LPK, RI = RPL < 4 ? RPL : 4;
   constexpr int NW = D * PB / 32;
   constexpr int U = StoreUnit<D * PB / 8>::value;
+  constexpr int RS = D + 4;  // residual row stride (floats): rows of different keys in different banks
   __shared__ uint32_t s_bits[D * D / 32];
   __shared__ float s_cent[16];
+  __shared__ __attribute__((aligned(16))) float s_res[KB * RS];
+  __shared__ __attribute__((aligned(16))) float4 s_sgn[16];
+  __shared__ uint32_t s_sw[KB * (D / 32)];
   build_sign_bits<D>(s_bits, k.qjl_seed);
-  if (threadIdx.x < 16) s_cent[threadIdx.x] = k.polar.cent[threadIdx.x & ((1 << PB) - 1)];
+  const int tid = threadIdx.x, kk = tid / LPK, rq = tid % LPK;
+  if (tid < 16) {
+    s_cent[tid] = k.polar.cent[tid & ((1 << PB) - 1)];
+    s_sgn[tid] = nibble_signs(tid);
+  }
+  for (int e = tid; e < KB * (D / 32); e += kBlock) s_sw[e] = 0u;
   __syncthreads();
-  const long long v = (long long)blockIdx.x * kBlock + threadIdx.x;
-  if (v >= n) return;
-  const float4 *xp = reinterpret_cast<const float4 *>(x + v * D);
-  float w[D];
+  const long long v = (long long)blockIdx.x * KB + kk;
+  const bool live = v < n;
+  if (rq == 0 && live) {
+    const float4 *xp = reinterpret_cast<const float4 *>(x + v * D);
+    float w[D];
 #pragma unroll
-  for (int q = 0; q < D / 4; q++) {
-    const float4 f = xp[q];
-    w[4 * q] = f.x; w[4 * q + 1] = f.y; w[4 * q + 2] = f.z; w[4 * q + 3] = f.w;
+    for (int q = 0; q < D / 4; q++) {
+      const float4 f = xp[q];
+      w[4 * q] = f.x; w[4 * q + 1] = f.y; w[4 * q + 2] = f.z; w[4 * q + 3] = f.w;
+    }
+    uint32_t pk[NW];
+    const float norm = quantize_lane<D, 1, PB>(w, 0, k.polar, pk);
+    const uint16_t sc = f32_to_f16(norm < kMinNorm ? 0.0f : norm);
+    // x_mse = dequantize_vec(polar block), residual r = x - x_mse (qjl.rs:362-368)
+    dequant_lane<D, 1, PB, true>(pk, f16_to_f32(sc), 0, s_cent, k.polar, w);
+#pragma unroll
+    for (int q = 0; q < D / 4; q++) {
+      const float4 f = xp[q];
+      w[4 * q] = f.x - w[4 * q]; w[4 * q + 1] = f.y - w[4 * q + 1];
+      w[4 * q + 2] = f.z - w[4 * q + 2]; w[4 * q + 3] = f.w - w[4 * q + 3];
+    }
+    float rs = -0.0f;
+#pragma unroll
+    for (int e = 0; e < D; e++) rs = rs + w[e] * w[e];
+#pragma unroll
+    for (int q = 0; q < D / 4; q++)
+      *reinterpret_cast<float4 *>(s_res + kk * RS + 4 * q) = make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    store_words<NW, U>(polar + v * (D * PB / 8), pk);
+    polar_scales[v] = sc;
+    residual_norms[v] = f32_to_f16(sqrtf(rs));
   }
-  uint32_t pk[NW];
-  const float norm = quantize_lane<D, 1, PB>(w, 0, k.polar, pk);
-  const uint16_t sc = f32_to_f16(norm < kMinNorm ? 0.0f : norm);
-  // x_mse = dequantize_vec(polar block), residual r = x - x_mse (qjl.rs:362-368)
-  dequant_lane<D, 1, PB, true>(pk, f16_to_f32(sc), 0, s_cent, k.polar, w);
-#pragma unroll
-  for (int q = 0; q < D / 4; q++) {
-    const float4 f = xp[q];
-    w[4 * q] = f.x - w[4 * q]; w[4 * q + 1] = f.y - w[4 * q + 1];
-    w[4 * q + 2] = f.z - w[4 * q + 2]; w[4 * q + 3] = f.w - w[4 * q + 3];
-  }
-  float rs = -0.0f;
-#pragma unroll
-  for (int e = 0; e < D; e++) rs = rs + w[e] * w[e];
-  const float rn = sqrtf(rs);
+  __syncthreads();
   // compute_qjl_signs + pack_sign_bits (qjl.rs:305-319, 245-256): bit j = p_j >= 0
-  uint32_t sw[D / 32];
+  if (live) {
+    const float4 *res = reinterpret_cast<const float4 *>(s_res + kk * RS);
+    uint32_t mine = 0u;  // bits of rows rq * RPL .. + RPL, at their place in the row's word
 #pragma unroll
-  for (int i = 0; i < D / 32; i++) sw[i] = 0u;
-  for (int j = 0; j < D; j++) {
-    const float p = row_product<D>(w, s_bits + j * (D / 32), k.inv_sqrt_d);
-    const uint32_t bit = (p >= 0.0f) ? 1u : 0u;
+    for (int r0 = 0; r0 < RPL; r0 += RI) {
+      const int j0 = rq * RPL + r0;
+      float sum[RI];
 #pragma unroll
-    for (int i = 0; i < D / 32; i++) sw[i] |= (i == (j >> 5)) ? (bit << (j & 31)) : 0u;
+      for (int i = 0; i < RI; i++) sum[i] = -0.0f;
+#pragma unroll
+      for (int w = 0; w < D / 32; w++) {
+        uint32_t bw[RI];
+#pragma unroll
+        for (int i = 0; i < RI; i++) bw[i] = s_bits[(j0 + i) * (D / 32) + w];
+#pragma unroll
+        for (int nb = 0; nb < 8; nb++) {
+          const float4 rv = res[8 * w + nb];
+#pragma unroll
+          for (int i = 0; i < RI; i++) {
+            const float4 sg = s_sgn[(bw[i] >> (4 * nb)) & 15u];
+            sum[i] = __builtin_fmaf(sg.x, rv.x, sum[i]);
+            sum[i] = __builtin_fmaf(sg.y, rv.y, sum[i]);
+            sum[i] = __builtin_fmaf(sg.z, rv.z, sum[i]);
+            sum[i] = __builtin_fmaf(sg.w, rv.w, sum[i]);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RI; i++) {
+        const float p = sum[i] * k.inv_sqrt_d;
+        mine |= (p >= 0.0f ? 1u : 0u) << ((j0 + i) & 31);
+      }
+    }
+    if (mine) atomicOr(&s_sw[kk * (D / 32) + (rq * RPL) / 32], mine);
   }
-  store_words<NW, U>(polar + v * (D * PB / 8), pk);
-  polar_scales[v] = sc;
-#pragma unroll
-  for (int i = 0; i < D / 32; i++) signs[v * (D / 32) + i] = sw[i];
-  residual_norms[v] = f32_to_f16(rn);
+  __syncthreads();
+  if (live && rq < D / 32) signs[v * (D / 32) + rq] = s_sw[kk * (D / 32) + rq];
 }
 
 // EstimationContext for a batch of queries (qjl.rs:488-492, 561-572):
 // ctx[q] = { qt[D] = forward rotation of q (no normalization), rq[D] = R q }.
+// A workgroup serves 8 queries x 32 projection rows, lane = (query, row): it
+// hashes only its rows' sign bits; each lane sums its row in column order
+// from -0.0 (rademacher_vector_product, qjl.rs:196-208).  The workgroups of
+// the first row block also rotate their queries (one lane per query).
 template <int D>
 __global__ __launch_bounds__(kBlock) void qjl_query_kernel(const float *__restrict__ queries, float *__restrict__ ctx,
                                                            long long nq, QjlConsts k) {
-  __shared__ uint32_t s_bits[D * D / 32];
-  build_sign_bits<D>(s_bits, k.qjl_seed);
+  constexpr int RB = 32, QB = kBlock / RB;
+  __shared__ uint32_t s_bits[RB * (D / 32)];
+  __shared__ __attribute__((aligned(16))) float s_q[QB * D];
+  __shared__ __attribute__((aligned(16))) float4 s_sgn[16];
+  const int tid = threadIdx.x, qq = tid / RB, jj = tid % RB;
+  if (tid < 16) s_sgn[tid] = nibble_signs(tid);
+  const int jb = blockIdx.x * RB;
+  const long long q0 = (long long)blockIdx.y * QB;
+  // one sign per lane, 64 consecutive (row, column) entries per wave and step,
+  // gathered into two words by a ballot
+  for (int base = (tid >> 6) * 64; base < RB * D; base += kBlock) {
+    const int f = base + (tid & 63), j = jb + f / D, col = f % D;
+    const uint64_t m = __ballot(sign_negative(mix_seed(k.qjl_seed, (uint64_t)j), (uint64_t)j, (uint64_t)col));
+    if ((tid & 63) == 0) {
+      s_bits[base / 32] = (uint32_t)m;
+      s_bits[base / 32 + 1] = (uint32_t)(m >> 32);
+    }
+  }
+  for (int e = tid; e < QB * D; e += kBlock) {
+    const long long qi = q0 + e / D;
+    s_q[e] = qi < nq ? queries[qi * D + e % D] : 0.0f;
+  }
   __syncthreads();
-  const long long qi = (long long)blockIdx.x * kBlock + threadIdx.x;
+  const long long qi = q0 + qq;
   if (qi >= nq) return;
-  float q[D];
-  const float4 *qp = reinterpret_cast<const float4 *>(queries + qi * D);
+  const float *qv = s_q + qq * D;
+  float s = -0.0f;
 #pragma unroll
-  for (int i = 0; i < D / 4; i++) {
-    const float4 f = qp[i];
-    q[4 * i] = f.x; q[4 * i + 1] = f.y; q[4 * i + 2] = f.z; q[4 * i + 3] = f.w;
+  for (int w = 0; w < D / 32; w++) {
+    const uint32_t bits = s_bits[jj * (D / 32) + w];
+#pragma unroll
+    for (int nb = 0; nb < 8; nb++) {  // the signs of four columns by one table read
+      const float4 sg = s_sgn[(bits >> (4 * nb)) & 15u];
+      const float4 v = *reinterpret_cast<const float4 *>(qv + 32 * w + 4 * nb);
+      s = __builtin_fmaf(sg.x, v.x, s);
+      s = __builtin_fmaf(sg.y, v.y, s);
+      s = __builtin_fmaf(sg.z, v.z, s);
+      s = __builtin_fmaf(sg.w, v.w, s);
+    }
   }
   float *out = ctx + qi * 2 * D;
-  for (int j = 0; j < D; j++) out[D + j] = row_product<D>(q, s_bits + j * (D / 32), k.inv_sqrt_d);
-  const float se = k.polar.sign_even, so = -k.polar.sign_even;
+  out[D + jb + jj] = s * k.inv_sqrt_d;
+  if (blockIdx.x == 0) {
+    // forward rotation, the query's 32 lanes holding E = D / 32 consecutive
+    // elements each: butterfly stages h < E inside a lane, h >= E with the
+    // lane jj ^ (h / E) (the lower element takes x + y, the upper x - y, in
+    // the stage order of butterfly<D>, so every value is the same)
+    constexpr int E = D / 32;
+    const float se = k.polar.sign_even, so = -k.polar.sign_even;
+    float q[E];
 #pragma unroll
-  for (int e = 0; e < D; e++) q[e] = q[e] * ((e & 1) ? so : se);
-  butterfly<D>(q);
+    for (int i = 0; i < E; i++) q[i] = qv[E * jj + i] * (((E * jj + i) & 1) ? so : se);
 #pragma unroll
-  for (int e = 0; e < D; e++) out[e] = q[e] * k.polar.wht_norm;
+    for (int h = 1; h < E; h *= 2)
+#pragma unroll
+      for (int i = 0; i < E; i += 2 * h)
+#pragma unroll
+        for (int t = i; t < i + h; t++) {
+          const float x = q[t], y = q[t + h];
+          q[t] = x + y;
+          q[t + h] = x - y;
+        }
+    auto cross = [&](auto xc) {
+      constexpr int X = decltype(xc)::value;
+      const bool upper = (jj & X) != 0;
+#pragma unroll
+      for (int i = 0; i < E; i++) {
+        const float o = tqm::lane_xor<X>(q[i]);
+        q[i] = upper ? o - q[i] : q[i] + o;
+      }
+    };
+    cross(std::integral_constant<int, 1>{});
+    cross(std::integral_constant<int, 2>{});
+    cross(std::integral_constant<int, 4>{});
+    cross(std::integral_constant<int, 8>{});
+    cross(std::integral_constant<int, 16>{});
+#pragma unroll
+    for (int i = 0; i < E; i++) out[E * jj + i] = q[i] * k.polar.wht_norm;
+  }
 }
 
 // Scores of QB queries x 256 keys per workgroup (lane = key):
@@ -220,29 +338,37 @@ __global__ __launch_bounds__(kBlock) void qjl_scores_kernel(const float *__restr
 
 // Row softmax: probs = exp(scale * (s - max)) / sum (textbook; the reference
 // returns raw scores, attention.rs:344-352).
-__global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const float *__restrict__ s, float *__restrict__ p,
-                                                              long long cols, float scale) {
-  __shared__ float red[kBlock / 64];
+constexpr int kSoftmaxBlock = 1024;
+// One workgroup per row: the max, then each exponential once (kept in the
+// output) and their sum, then the scaling in place.
+__global__ __launch_bounds__(kSoftmaxBlock) void softmax_rows_kernel(const float *__restrict__ s,
+                                                                     float *__restrict__ p, long long cols,
+                                                                     float scale) {
+  __shared__ float red[kSoftmaxBlock / 64];
   const float *row = s + (long long)blockIdx.x * cols;
   float *out = p + (long long)blockIdx.x * cols;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float m = -INFINITY;
-  for (long long c = threadIdx.x; c < cols; c += kBlock) m = fmaxf(m, row[c]);
+  for (long long c = threadIdx.x; c < cols; c += kSoftmaxBlock) m = fmaxf(m, row[c]);
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
   if (lane == 0) red[wave] = m;
   __syncthreads();
   m = red[0];
-  for (int w = 1; w < kBlock / 64; w++) m = fmaxf(m, red[w]);
+  for (int w = 1; w < kSoftmaxBlock / 64; w++) m = fmaxf(m, red[w]);
   __syncthreads();
   float sum = 0.0f;
-  for (long long c = threadIdx.x; c < cols; c += kBlock) sum += expf(scale * (row[c] - m));
+  for (long long c = threadIdx.x; c < cols; c += kSoftmaxBlock) {
+    const float e = expf(scale * (row[c] - m));
+    out[c] = e;
+    sum += e;
+  }
   for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
   if (lane == 0) red[wave] = sum;
   __syncthreads();
   sum = 0.0f;
-  for (int w = 0; w < kBlock / 64; w++) sum += red[w];
+  for (int w = 0; w < kSoftmaxBlock / 64; w++) sum += red[w];
   const float inv = 1.0f / sum;
-  for (long long c = threadIdx.x; c < cols; c += kBlock) out[c] = expf(scale * (row[c] - m)) * inv;
+  for (long long c = threadIdx.x; c < cols; c += kSoftmaxBlock) out[c] = out[c] * inv;
 }
 
 // weighted_values (attention.rs:371-408), rotated domain: a workgroup of D
@@ -251,53 +377,97 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_kernel(const float *__res
 // applies the inverse rotation once.
 constexpr int kWvChunk = 256;
 
+constexpr int kWvQueries = 4;  // queries per partial workgroup: each code decoded once for all of them
+
 template <int D, int PB>
 __global__ __launch_bounds__(D) void qjl_wv_partial_kernel(const uint8_t *__restrict__ polar,
                                                            const uint16_t *__restrict__ polar_scales, long long nv,
-                                                           const float *__restrict__ weights,
+                                                           long long nq, const float *__restrict__ weights,
                                                            float *__restrict__ partial, QjlConsts k) {
   constexpr int RWORDS = D * PB / 32;  // packed words per value
+  constexpr int QW = kWvQueries;
   __shared__ uint32_t s_codes[kWvChunk * RWORDS];
-  __shared__ float s_w[kWvChunk];
+  __shared__ float s_w[QW][kWvChunk];
   __shared__ float s_cent[16];
   if (threadIdx.x < 16) s_cent[threadIdx.x] = k.polar.cent[threadIdx.x & ((1 << PB) - 1)];
   const long long t0 = (long long)blockIdx.x * kWvChunk;
-  const long long qi = blockIdx.y;
+  const long long q0 = (long long)blockIdx.y * QW;
   const int cnt = (int)min<long long>(kWvChunk, nv - t0);
   for (int i = threadIdx.x; i < cnt * RWORDS; i += D)
     s_codes[i] = reinterpret_cast<const uint32_t *>(polar + t0 * (D * PB / 8))[i];
-  for (int i = threadIdx.x; i < cnt; i += D)
-    s_w[i] = weights[qi * nv + t0 + i] * f16_to_f32(polar_scales[t0 + i]);
+  for (int i = threadIdx.x; i < QW * cnt; i += D) {
+    const int qq = i / cnt, t = i % cnt;
+    const long long qi = q0 + qq;
+    s_w[qq][t] = qi < nq ? weights[qi * nv + t0 + t] * f16_to_f32(polar_scales[t0 + t]) : 0.0f;
+  }
   __syncthreads();
   const int e = threadIdx.x;
   const int bit = e * PB, wi = bit >> 5, sh = bit & 31;
-  float acc = 0.0f;
+  float acc[QW];
+#pragma unroll
+  for (int qq = 0; qq < QW; qq++) acc[qq] = 0.0f;
   for (int t = 0; t < cnt; t++) {
     const uint32_t *row = s_codes + t * RWORDS;
     uint32_t code = row[wi] >> sh;
     if (sh + PB > 32) code |= row[wi + 1] << (32 - sh);
-    acc = __builtin_fmaf(s_w[t], s_cent[code & ((1u << PB) - 1u)], acc);
+    const float c = s_cent[code & ((1u << PB) - 1u)];
+#pragma unroll
+    for (int qq = 0; qq < QW; qq++) acc[qq] = __builtin_fmaf(s_w[qq][t], c, acc[qq]);
   }
-  partial[(qi * gridDim.x + blockIdx.x) * D + e] = acc;
+#pragma unroll
+  for (int qq = 0; qq < QW; qq++)
+    if (q0 + qq < nq) partial[((q0 + qq) * gridDim.x + blockIdx.x) * D + e] = acc[qq];
 }
 
+// One workgroup of D lanes per query: lane e adds its element over the chunks
+// (chunk order, from 0); then 32 lanes of E = D / 32 consecutive elements
+// each apply the inverse rotation (butterfly<D>'s stages in its order: h < E
+// inside a lane, h >= E with lane ^ (h / E); then the norm and the signs).
 template <int D>
-__global__ __launch_bounds__(kBlock) void qjl_wv_finish_kernel(const float *__restrict__ partial, int nchunks,
-                                                               float *__restrict__ out, long long nq, QjlConsts k) {
-  const long long qi = (long long)blockIdx.x * kBlock + threadIdx.x;
-  if (qi >= nq) return;
-  float a[D];
+__global__ __launch_bounds__(D) void qjl_wv_finish_kernel(const float *__restrict__ partial, int nchunks,
+                                                          float *__restrict__ out, long long nq, QjlConsts k) {
+  constexpr int E = D / 32;
+  __shared__ float s_a[D];
+  const long long qi = blockIdx.x;
+  const int e = threadIdx.x;
+  float a = 0.0f;
+  for (int c = 0; c < nchunks; c++) a += partial[(qi * nchunks + c) * D + e];
+  s_a[e] = a;
+  __syncthreads();
+  if (e >= 32) return;
+  float q[E];
 #pragma unroll
-  for (int e = 0; e < D; e++) a[e] = 0.0f;
-  for (int c = 0; c < nchunks; c++) {
-    const float *p = partial + (qi * nchunks + c) * D;
+  for (int i = 0; i < E; i++) q[i] = s_a[E * e + i];
 #pragma unroll
-    for (int e = 0; e < D; e++) a[e] += p[e];
-  }
-  butterfly<D>(a);
+  for (int h = 1; h < E; h *= 2)
+#pragma unroll
+    for (int i = 0; i < E; i += 2 * h)
+#pragma unroll
+      for (int t = i; t < i + h; t++) {
+        const float x = q[t], y = q[t + h];
+        q[t] = x + y;
+        q[t + h] = x - y;
+      }
+  auto cross = [&](auto xc) {
+    constexpr int X = decltype(xc)::value;
+    const bool upper = (e & X) != 0;
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const float o = tqm::lane_xor<X>(q[i]);
+      q[i] = upper ? o - q[i] : q[i] + o;
+    }
+  };
+  cross(std::integral_constant<int, 1>{});
+  cross(std::integral_constant<int, 2>{});
+  cross(std::integral_constant<int, 4>{});
+  cross(std::integral_constant<int, 8>{});
+  cross(std::integral_constant<int, 16>{});
   const float se = k.polar.sign_even, so = -k.polar.sign_even;
 #pragma unroll
-  for (int e = 0; e < D; e++) out[qi * D + e] = (a[e] * k.polar.wht_norm) * ((e & 1) ? so : se);
+  for (int i = 0; i < E; i++) {
+    const int el = E * e + i;
+    out[qi * D + el] = (q[i] * k.polar.wht_norm) * ((el & 1) ? so : se);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -582,8 +752,8 @@ extern "C" int tq_qjl_quantize_batch(const float *data, uint8_t *polar_packed, u
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   const long long n = (long long)num_vectors;
   return by_dim_bits(dim, total_bits - 1, [&](auto d, auto pb) {
-    hipLaunchKernelGGL((qjl_quant_kernel<decltype(d)::value, decltype(pb)::value>), dim3(grid_for(n)), dim3(kBlock),
-                       0, stream, data, polar_packed, polar_scales, reinterpret_cast<uint32_t *>(signs),
+    hipLaunchKernelGGL((qjl_quant_kernel<decltype(d)::value, decltype(pb)::value>), dim3((unsigned)((n + 31) / 32)),
+                       dim3(kBlock), 0, stream, data, polar_packed, polar_scales, reinterpret_cast<uint32_t *>(signs),
                        residual_norms, n, k);
     return tqh::check_launch("qjl_quant_kernel");
   });
@@ -597,9 +767,11 @@ extern "C" int tq_qjl_query_context(const float *queries, float *ctx_out, size_t
   if (num_queries == 0) return TQ_OK;
   if (!queries || !ctx_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   const long long nq = (long long)num_queries;
+  if (nq > 8LL * 65535) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "too many queries (%lld > %d)", nq, 8 * 65535);
   return by_dim(dim, [&](auto d) {
-    hipLaunchKernelGGL((qjl_query_kernel<decltype(d)::value>), dim3(grid_for(nq)), dim3(kBlock), 0, stream, queries,
-                       ctx_out, nq, k);
+    constexpr int D = decltype(d)::value;
+    hipLaunchKernelGGL((qjl_query_kernel<D>), dim3(D / 32, (unsigned)((nq + 7) / 8)), dim3(kBlock), 0, stream,
+                       queries, ctx_out, nq, k);
     return tqh::check_launch("qjl_query_kernel");
   });
 }
@@ -630,7 +802,7 @@ extern "C" int tq_softmax_rows(const float *scores, float *probs, size_t rows, s
   if (rows == 0 || cols == 0) return TQ_OK;
   if (!scores || !probs) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   if (rows > 0x7fffffffu) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "too many rows");
-  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(kBlock), 0, stream, scores, probs,
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(kSoftmaxBlock), 0, stream, scores, probs,
                      (long long)cols, scale);
   return tqh::check_launch("softmax_rows_kernel");
 }
@@ -661,13 +833,12 @@ extern "C" int tq_qjl_weighted_values(const uint8_t *polar_packed, const uint16_
   return by_dim_bits(dim, polar_bits, [&](auto d, auto pb) {
     constexpr int D = decltype(d)::value, PB = decltype(pb)::value;
     if (nchunks > 0) {
-      hipLaunchKernelGGL((qjl_wv_partial_kernel<D, PB>), dim3((unsigned)nchunks, (unsigned)nq), dim3(D), 0, stream,
-                         polar_packed, polar_scales, nv, weights, partial, k);
+      hipLaunchKernelGGL((qjl_wv_partial_kernel<D, PB>), dim3((unsigned)nchunks, (unsigned)((nq + kWvQueries - 1) / kWvQueries)),
+                         dim3(D), 0, stream, polar_packed, polar_scales, nv, nq, weights, partial, k);
       int rc2 = tqh::check_launch("qjl_wv_partial_kernel");
       if (rc2) return rc2;
     }
-    hipLaunchKernelGGL((qjl_wv_finish_kernel<D>), dim3(grid_for(nq)), dim3(kBlock), 0, stream, partial, nchunks, out,
-                       nq, k);
+    hipLaunchKernelGGL((qjl_wv_finish_kernel<D>), dim3((unsigned)nq), dim3(D), 0, stream, partial, nchunks, out, nq, k);
     return tqh::check_launch("qjl_wv_finish_kernel");
   });
 }
