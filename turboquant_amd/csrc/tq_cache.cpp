@@ -39,6 +39,18 @@ struct CacheMode {
   bool qjl = false;
 };
 
+// Stream-ordered device memory from the device's default pool.
+template <class T>
+bool pool_alloc(T **p, size_t bytes, hipStream_t stream) {
+  void *q = nullptr;
+  if (hipMallocAsync(&q, bytes, stream) != hipSuccess) return false;
+  *p = static_cast<T *>(q);
+  return true;
+}
+inline void pool_free(void *p, hipStream_t stream) {
+  if (p) (void)hipFreeAsync(p, stream);
+}
+
 class CompressedStorage {
  public:
   CompressedStorage(int num_kv_heads, int head_dim, int bits, int num_layers, bool qjl)
@@ -65,11 +77,14 @@ class CompressedStorage {
     N.cap = cap;
     N.seq = L.seq;
     N.active = L.active;
-    bool ok = hipMalloc(&N.k_idx, ib) == hipSuccess && hipMalloc(&N.v_idx, ib) == hipSuccess &&
-              hipMalloc(&N.k_sc, sb) == hipSuccess && hipMalloc(&N.v_sc, sb) == hipSuccess;
-    if (ok && qjl_) ok = hipMalloc(&N.signs, gb) == hipSuccess && hipMalloc(&N.norms, nb) == hipSuccess;
+    // stream-ordered allocation and release (the device's memory pool): the
+    // old buffers go back to the pool after the work queued before them, so
+    // growth never waits on the host
+    bool ok = pool_alloc(&N.k_idx, ib, stream) && pool_alloc(&N.v_idx, ib, stream) && pool_alloc(&N.k_sc, sb, stream) &&
+              pool_alloc(&N.v_sc, sb, stream);
+    if (ok && qjl_) ok = pool_alloc(&N.signs, gb, stream) && pool_alloc(&N.norms, nb, stream);
     if (!ok) {
-      free_layer(N);
+      free_layer(N, stream);
       return tqh::fail(TQ_ERR_DEVICE, "cache allocation of %zu records per head failed", cap);
     }
     // new capacity starts zeroed, as Tensor::zeros
@@ -78,7 +93,7 @@ class CompressedStorage {
     if (ok && qjl_)
       ok = hipMemsetAsync(N.signs, 0, gb, stream) == hipSuccess && hipMemsetAsync(N.norms, 0, nb, stream) == hipSuccess;
     if (!ok) {
-      free_layer(N);
+      free_layer(N, stream);
       return tqh::fail(TQ_ERR_DEVICE, "cache clear failed");
     }
     if (L.seq > 0) {
@@ -91,13 +106,13 @@ class CompressedStorage {
            copy(N.v_sc, L.v_sc, ps);
       if (ok && qjl_) ok = copy(N.signs, L.signs, sign_bytes()) && copy(N.norms, L.norms, 2);
       if (!ok) {
-        free_layer(N);
+        free_layer(N, stream);
         return tqh::fail(TQ_ERR_DEVICE, "cache growth copy failed");
       }
     }
-    // the old buffers may still be read by queued work: wait before freeing
-    if (hipStreamSynchronize(stream) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "stream synchronize failed");
-    free_layer(L);
+    // queued work may still read the old buffers: they return to the pool in
+    // stream order, after it
+    free_layer(L, stream);
     L = N;
     return TQ_OK;
   }
@@ -107,7 +122,8 @@ class CompressedStorage {
     layers_[l].active = true;
   }
 
-  // storage.rs:175-186 (and the QJL buffers, tq.rs:303-312)
+  // storage.rs:175-186 (and the QJL buffers, tq.rs:303-312); the caller has
+  // synchronized the device
   void reset() { release_all(); }
 
   // storage.rs:188-202, plus the whole QJL tensors as tq.rs:314-323 counts them
@@ -124,13 +140,13 @@ class CompressedStorage {
   }
 
  private:
-  static void free_layer(LayerBuffers &L) {
+  static void free_layer(LayerBuffers &L, hipStream_t stream) {
     for (void *p : {(void *)L.k_idx, (void *)L.v_idx, (void *)L.k_sc, (void *)L.v_sc, (void *)L.signs, (void *)L.norms})
-      if (p) (void)hipFree(p);
+      pool_free(p, stream);
     L = LayerBuffers{};
   }
   void release_all() {
-    for (LayerBuffers &L : layers_) free_layer(L);
+    for (LayerBuffers &L : layers_) free_layer(L, nullptr);
   }
 
   int heads_, head_dim_, bits_;
@@ -145,8 +161,7 @@ class KvCache {
       : layers_(num_layers), heads_(num_kv_heads), head_dim_(head_dim), mode_(mode),
         storage_(num_kv_heads, head_dim, mode.bits, num_layers, mode.qjl) {}
   ~KvCache() {
-    for (void *p : {ws_, rmat_, rq_})
-      if (p) (void)hipFree(p);
+    for (void *p : {ws_, rmat_, rq_}) pool_free(p, nullptr);
   }
 
   int layers() const { return layers_; }
@@ -202,11 +217,10 @@ class KvCache {
   int rq_scratch(size_t num_rows, hipStream_t stream) {
     const size_t need = num_rows * (size_t)head_dim_ * sizeof(float);
     if (need <= rq_bytes_) return TQ_OK;
-    if (hipStreamSynchronize(stream) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "stream synchronize failed");
-    if (rq_) (void)hipFree(rq_);
+    pool_free(rq_, stream);  // after the queued work that reads it
     rq_ = nullptr;
     rq_bytes_ = 0;
-    if (hipMalloc(&rq_, need) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "rq allocation failed");
+    if (!pool_alloc(&rq_, need, stream)) return tqh::fail(TQ_ERR_DEVICE, "rq allocation failed");
     rq_bytes_ = need;
     return TQ_OK;
   }
@@ -241,11 +255,10 @@ class KvCache {
     const size_t need = tq_attention_workspace_size(1, num_q_heads, heads_, head_dim_, (int)L.cap);
     if (need == 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid attention shape");
     if (need > ws_bytes_) {
-      if (hipStreamSynchronize(stream) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "stream synchronize failed");
-      if (ws_) (void)hipFree(ws_);
+      pool_free(ws_, stream);  // after the queued decodes that use it
       ws_ = nullptr;
       ws_bytes_ = 0;
-      if (hipMalloc(&ws_, need) != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "workspace allocation failed");
+      if (!pool_alloc(&ws_, need, stream)) return tqh::fail(TQ_ERR_DEVICE, "workspace allocation failed");
       ws_bytes_ = need;
       rc = tq_attention_workspace_init(ws_, ws_bytes_, 1, num_q_heads, heads_, head_dim_, (int)L.cap, stream);
       if (rc) return rc;
@@ -283,7 +296,7 @@ class KvCache {
   int sign_matrix(hipStream_t stream) {
     if (rmat_) return TQ_OK;
     const size_t bytes = (size_t)head_dim_ * head_dim_ / 8;
-    if (hipMalloc(&rmat_, bytes) != hipSuccess) {
+    if (!pool_alloc(&rmat_, bytes, stream)) {
       rmat_ = nullptr;
       return tqh::fail(TQ_ERR_DEVICE, "sign matrix allocation failed");
     }
@@ -349,7 +362,13 @@ extern "C" int tq_cache_create(int num_layers, int num_kv_heads, int head_dim, i
   return TQ_OK;
 }
 
-extern "C" void tq_cache_destroy(void *cache) { delete as_cache(cache); }
+extern "C" void tq_cache_destroy(void *cache) {
+  KvCache *c = as_cache(cache);
+  if (!c) return;
+  (void)hipDeviceSynchronize();  // no queued work may still use its buffers
+  delete c;
+  (void)hipStreamSynchronize(nullptr);  // the pool releases, ordered on the null stream
+}
 
 extern "C" int tq_cache_is_tq(void *cache) {
   KvCache *c = as_cache(cache);

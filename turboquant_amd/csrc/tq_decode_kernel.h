@@ -408,12 +408,11 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   uint32_t sgw[NKT][C::SW4];
   uint32_t nrm[NKT];
   uint32_t vsr[C::TPL][(NQB + 1) / 2];
-  // The wave's loads form one stream of NG groups, consumed in order: K tile
-  // i (records, scales, QJL signs and norms) is group i, the V scales group
-  // NKT, V tile i group NKT + 1 + i.  LA groups stay in flight: group c + LA
-  // is issued as group c is consumed, so no load instruction waits at issue
-  // for the CU's memory queue while arithmetic could run.
-  constexpr int NG = 2 * NKT + 1;
+  // The wave's loads form one stream of groups, consumed in order: K tile i
+  // (records, scales, QJL signs and norms) is group i, the V scales group
+  // NKT, V tile i group NKT + 1 + i.  Only a few groups are in flight at a
+  // time (issued as earlier ones are consumed), so no load instruction waits
+  // at issue for the CU's memory queue while arithmetic could run.
   auto issue = [&](int grp) {
     if (grp < NKT) {
       const int i = grp;
@@ -445,16 +444,35 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
         if constexpr (NQB == 1) vsr[u][0] = __builtin_amdgcn_raw_buffer_load_b16(rvs, vso + u * 2, 0, 0);
         else buf_words<NQB / 2>(vsr[u], rvs, vso + u * NQB * 2, 0);
       }
-    } else if (grp < NG) {
+    } else {
       const int i = grp - NKT - 1;
       const auto rv = rec_rsrc(vbase, nrec * PACKED, (tw0 + 16u * i) * PACKED);
 #pragma unroll
       for (int qg = 0; qg < QG; qg++) buf_words<NW>(vw[i][qg], rv, vvo + qg * QPM * QW * 4, 0);
     }
   };
-  constexpr int LA = dmin(C::LOOKAHEAD, NG);
+  // Schedule: K tiles 0 .. LA-1 and the V scales (needed by the softmax)
+  // before the setup; K tile i + LA as K tile i is consumed; V tiles 0-3
+  // during the last two K tiles, so the first values are in flight before the
+  // softmax; then V tiles 2 vp + 4, 2 vp + 5 as V pair vp is consumed.
+  constexpr int LA = dmin(C::LOOKAHEAD, NKT);
 #pragma unroll
   for (int grp = 0; grp < LA; grp++) issue(grp);
+  issue(NKT);
+  auto issue_k = [&](int i) {  // K tile i is being consumed
+    if (i + LA < NKT) issue(i + LA);
+    if (i >= NKT - 2) {
+      const int t = 2 * (i - (NKT - 2));
+      issue(NKT + 1 + t);
+      issue(NKT + 2 + t);
+    }
+  };
+  auto issue_v = [&](int vp) {  // V pair vp is being consumed
+    if (2 * vp + 4 < NKT) {
+      issue(NKT + 1 + 2 * vp + 4);
+      issue(NKT + 2 + 2 * vp + 4);
+    }
+  };
   // ---- pair table (the caller's device codebook, L2Norm tables from the
   // arguments, or the PQO constants) ----
   static_assert(C::NPAIR <= 256, "one pair-table entry per lane");
@@ -610,7 +628,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   float sc[NKT][NS];
 #pragma unroll
   for (int i = 0; i < NKT; i++) {
-    issue(i + LA);
+    issue_k(i);
     f32x4 dk[QG];
 #pragma unroll
     for (int qg = 0; qg < QG; qg++) {
@@ -680,7 +698,6 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   }
 
   // ---- softmax over the wave's tokens (base 2): per head row max and sum ----
-  issue(NKT + LA);
   float* stage = lds + C::OFF_W + wave * C::WSTAGE;
   float *st_p = stage;                 // [HG][TPW]
   float *st_s = stage + C::WP;         // [NQB][TPW]
@@ -752,8 +769,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     for (int j = 0; j < PPL; j++) dv[vs][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int vp = 0; vp < NVP; vp++) {
-    issue(NKT + 1 + 2 * vp + LA);
-    issue(NKT + 2 + 2 * vp + LA);
+    issue_v(vp);
     u32x4 bw[QG];
 #pragma unroll
     for (int vs = 0; vs < QG; vs++) {
