@@ -857,7 +857,18 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   }
 
   // ---- split-K arrival: the last of the (sequence, KV head)'s chunks x
-  // head groups merges every head of the KV head ----
+  // head groups merges every head of the KV head.
+  // Ordering (gfx942/gfx950 memory model, as LLVM's AMDGPU backend implements
+  // it): the partials are agent-scope atomic stores (sc1: written through the
+  // XCD's L2 to the device-coherent level) and every wave waits for its own to
+  // be acknowledged (s_waitcnt 0) before the workgroup barrier; only then does
+  // one lane add to the agent-scope counter, which is performed at the
+  // coherent level.  The workgroup that reads the final count has every other
+  // workgroup's increment, and so every partial, complete at that level; its
+  // merge loads are agent-scope atomic loads (sc1: they read the coherent
+  // level, never a stale L2 line), issued after the counter's value has
+  // returned and a barrier.  An acq_rel counter would add an L2 writeback and
+  // invalidate per workgroup that this needs nowhere. ----
   if constexpr (!INLINE_MERGE) return;
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
