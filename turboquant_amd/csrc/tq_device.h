@@ -16,13 +16,19 @@ __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
 // bf16 <-> f32.  bf16 -> f32 is exact; f32 -> bf16 rounds to nearest-even
-// (the `half` crate's bf16::from_f32), NaN kept quiet.
+// (the `half` crate's bf16::from_f32: (u + 0x7fff + lsb) >> 16, a NaN kept as
+// (u >> 16) | 0x40).  gfx950's v_cvt_pk_bf16_f32 gives exactly that for every
+// one of the 2^32 f32 inputs (both halves, checked exhaustively on MI355X);
+// it is written in assembly because this toolchain's lowering of a
+// two-element vector conversion fed the first element to both halves.
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
-__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
-  uint32_t u = f2u(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+// bf16(lo) in the low half, bf16(hi) in the high half
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+  return r;
 }
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) { return (uint16_t)(pack_bf16x2(x, x) & 0xffffu); }
 
 // f32 -> f16 round-to-nearest-even through the hardware conversion
 // (v_cvt_f16_f32 in the default RNE mode, f16 denormals kept).

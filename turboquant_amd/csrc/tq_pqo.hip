@@ -324,7 +324,9 @@ __global__ __launch_bounds__(256) void pqo_quant_rotated_dev_kernel(
 struct DequantConsts {
   float cb[16];   // codebook values (f32); the outlier codebook when mixed
   float cbn[16];  // mixed: the standard codebook
-  float sg[32];   // sign factor per element (the reference passes fl(R_fwd[0][j] * sqrt(32)))
+  // the reference's sign factor of element j is fl(R_fwd[0][j] * sqrt(32)) =
+  // (pqo_neg(j) ? -sgm : sgm): one magnitude for every j
+  float sgm;
   int mixed;      // codebook per block by the scale's sign (quantize_tensor.rs:242-260)
   int nn;         // mixed: standard codebook size (codes are clamped into it)
 };
@@ -333,7 +335,12 @@ struct DequantConsts {
 // butterfly_wht_inverse_cpu (wht_tensor.rs:38-64) then the broadcast_mul by
 // |scale| (quantize_tensor.rs:203, 217-218).
 // MAP: inputs come from cache records (CacheMap); outputs in block order.
-template <int BITS, int OUT_DT, bool DEV_CONSTS, bool MAP = false>
+// MIXED: the codebook per block from the scale's sign (else one codebook).
+// With the library's constants the table holds fl(cb * |sg|) and element j
+// takes it negated where sg[j] < 0: fl(c * -m) = -fl(c * m), the same value
+// as the per-element product, one multiply per table entry instead of per
+// element.
+template <int BITS, int OUT_DT, bool DEV_CONSTS, bool MAP = false, bool MIXED = false>
 __global__ __launch_bounds__(256) void pqo_dequant_kernel(const uint8_t *__restrict__ packed,
                                                           const uint16_t *__restrict__ scales,
                                                           void *__restrict__ out, long long nblocks,
@@ -342,56 +349,89 @@ __global__ __launch_bounds__(256) void pqo_dequant_kernel(const uint8_t *__restr
                                                           const float *__restrict__ dev_sg, CacheMap map = {}) {
   __shared__ float lut[32];
   constexpr int NC = 1 << BITS;
-  if (threadIdx.x < NC) lut[threadIdx.x] = DEV_CONSTS ? dev_cb[threadIdx.x] : dc.cb[threadIdx.x];
-  if (!DEV_CONSTS && threadIdx.x >= 16 && threadIdx.x < 32) lut[threadIdx.x] = dc.cbn[threadIdx.x - 16];
+  if (threadIdx.x < NC) lut[threadIdx.x] = DEV_CONSTS ? dev_cb[threadIdx.x] : dc.cb[threadIdx.x] * dc.sgm;
+  if (MIXED && threadIdx.x >= 16 && threadIdx.x < 32) lut[threadIdx.x] = dc.cbn[threadIdx.x - 16] * dc.sgm;
   __syncthreads();
   const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (blk >= nblocks) return;
-  const long long ib = MAP ? cache_block((uint32_t)blk, map) : blk;
+  // lanes past the end still take part in the wave's output staging
+  const bool valid = blk < nblocks;
+  const long long ib = !valid ? 0 : (MAP ? cache_block((uint32_t)blk, map) : blk);
   uint32_t w[Packed<BITS>::kWords];
-  const uint32_t *p = reinterpret_cast<const uint32_t *>(packed + ib * Packed<BITS>::kBytes);
-  if constexpr (BITS == 4) {
-    uint4 v = *reinterpret_cast<const uint4 *>(p);
-    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-  } else if constexpr (BITS == 2) {
-    uint2 v = *reinterpret_cast<const uint2 *>(p);
-    w[0] = v.x; w[1] = v.y;
-  } else {
 #pragma unroll
-    for (int q = 0; q < 3; q++) w[q] = p[q];
+  for (int q = 0; q < Packed<BITS>::kWords; q++) w[q] = 0u;
+  uint16_t sbits = 0;
+  if (valid) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(packed + ib * Packed<BITS>::kBytes);
+    if constexpr (BITS == 4) {
+      uint4 v = *reinterpret_cast<const uint4 *>(p);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (BITS == 2) {
+      uint2 v = *reinterpret_cast<const uint2 *>(p);
+      w[0] = v.x; w[1] = v.y;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 3; q++) w[q] = p[q];
+    }
+    sbits = scales[ib];
   }
-  const float ssig = f16_to_f32(scales[ib]);
+  const float ssig = f16_to_f32(sbits);
   const float s = fabsf(ssig);
   // mixed: a non-negative scale selects the standard codebook, codes clamped
-  const bool std_cb = !DEV_CONSTS && dc.mixed && !(ssig < 0.0f);
-  const uint32_t base = std_cb ? 16u : 0u, cmax = std_cb ? (uint32_t)dc.nn - 1u : 15u;
   float z[32];
+  if constexpr (MIXED) {
+    const bool std_cb = !(ssig < 0.0f);
+    const uint32_t base = std_cb ? 16u : 0u, cmax = std_cb ? (uint32_t)dc.nn - 1u : 15u;
 #pragma unroll
-  for (int j = 0; j < 32; j++) {
-    const float sgn = DEV_CONSTS ? dev_sg[j] : dc.sg[j];
-    z[j] = lut[base + min(field<BITS>(w, j), cmax)] * sgn;
+    for (int j = 0; j < 32; j++) {
+      const float c = lut[base + min(field<BITS>(w, j), cmax)];
+      z[j] = pqo_neg(j) ? -c : c;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      const float c = lut[field<BITS>(w, j)];
+      if constexpr (DEV_CONSTS) z[j] = c * dev_sg[j];
+      else z[j] = pqo_neg(j) ? -c : c;
+    }
   }
   butterfly<32>(z);
 #pragma unroll
   for (int j = 0; j < 32; j++) z[j] = (z[j] * kInvSqrt32) * s;
+  // the block's output words
+  constexpr int NDW = OUT_DT == kF32 ? 32 : 16;
+  uint32_t v[NDW];
   if constexpr (OUT_DT == kF32) {
-    float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + blk * 32);
 #pragma unroll
-    for (int q = 0; q < 8; q++) o[q] = make_float4(z[4 * q], z[4 * q + 1], z[4 * q + 2], z[4 * q + 3]);
+    for (int j = 0; j < 32; j++) v[j] = f2u(z[j]);
   } else {
-    uint4 *o = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + blk * 32);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      uint32_t v[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float a = z[8 * q + 2 * k], b = z[8 * q + 2 * k + 1];
-        uint32_t ha = OUT_DT == kBF16 ? f32_to_bf16(a) : f32_to_f16(a);
-        uint32_t hb = OUT_DT == kBF16 ? f32_to_bf16(b) : f32_to_f16(b);
-        v[k] = ha | (hb << 16);
-      }
-      o[q] = make_uint4(v[0], v[1], v[2], v[3]);
+    for (int k = 0; k < 16; k++) {
+      const float a = z[2 * k], b = z[2 * k + 1];
+      if constexpr (OUT_DT == kBF16) v[k] = pack_bf16x2(a, b);
+      else v[k] = (uint32_t)f32_to_f16(a) | ((uint32_t)f32_to_f16(b) << 16);
     }
+  }
+  // A wave's 64 blocks are one contiguous run of 64 * NDW words: staged
+  // through LDS (rows padded to RS words), each store instruction writes
+  // 1 KB of it contiguously rather than 16 bytes into each of 64 lines.
+  constexpr int RS = NDW + 4;
+  __shared__ __attribute__((aligned(16))) uint32_t s_out[4][64 * RS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t *row = s_out[wave] + lane * RS;
+#pragma unroll
+  for (int k = 0; k < NDW / 4; k++)
+    *reinterpret_cast<uint4 *>(row + 4 * k) = make_uint4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const long long wb = (long long)blockIdx.x * 256 + wave * 64;  // the wave's first block
+  uint32_t *dst = static_cast<uint32_t *>(out) + wb * NDW;
+#pragma unroll
+  for (int q = 0; q < NDW / 4; q++) {
+    const int f = 256 * q + 4 * lane;  // word of the wave's run
+    const int r = f / NDW, c = f % NDW;
+    if (wb + r < nblocks)
+      *reinterpret_cast<uint4 *>(dst + f) = *reinterpret_cast<const uint4 *>(s_out[wave] + r * RS + c);
   }
 }
 
@@ -507,10 +547,8 @@ DequantConsts make_dequant_consts(const tqh::PqoCodebook &cb) {
   volatile float thirty_two = 32.0f;
   volatile float sq = sqrtf(thirty_two);  // fl(sqrt(32)), IEEE sqrt
   volatile float inv = 1.0f / sq;
-  for (int j = 0; j < 32; j++) {
-    volatile float rf = pqo_neg(j) ? -inv : inv;
-    dc.sg[j] = rf * sq;
-  }
+  volatile float m = inv * sq;  // fl(+-inv * sq) = +-fl(inv * sq)
+  dc.sgm = m;
   return dc;
 }
 
@@ -531,8 +569,15 @@ template <bool MAP>
 int launch_dequant(const uint8_t *packed, const uint16_t *scales, void *out, int out_dtype, long long nblocks,
                    int bits, const DequantConsts &dc, const CacheMap &m, hipStream_t stream) {
   const dim3 grid((unsigned)((nblocks + 255) / 256)), block(256);
-#define DL(B, D) hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false, MAP>), grid, block, 0, stream, packed, scales, \
-                                    out, nblocks, dc, nullptr, nullptr, m)
+#define DL(B, D)                                                                                                  \
+  do {                                                                                                            \
+    if (dc.mixed)                                                                                                 \
+      hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false, MAP, true>), grid, block, 0, stream, packed, scales, out, \
+                         nblocks, dc, nullptr, nullptr, m);                                                       \
+    else                                                                                                          \
+      hipLaunchKernelGGL((pqo_dequant_kernel<B, D, false, MAP, false>), grid, block, 0, stream, packed, scales,     \
+                         out, nblocks, dc, nullptr, nullptr, m);                                                  \
+  } while (0)
   if (bits == 3) {
     if (out_dtype == kF32) DL(3, kF32);
     else if (out_dtype == kBF16) DL(3, kBF16);
