@@ -110,6 +110,42 @@ def test_pqo_quantize_fused_bit_exact(tq, bits, dtype):
 
 
 @pytest.mark.parametrize("bits", [3, 4])
+def test_pqo_quantize_fused_boundary_ties(tq, bits):
+    """Fused quantize on blocks whose rotated values land on, and one or a
+    few ulps either side of, every boundary b_k: a block (1, beta, 0, ...)
+    rotates to +-(1 + beta) / sqrt(32) and +-(1 - beta) / sqrt(32), so
+    v = (1 - beta) / (1 + beta) * outer up to rounding; beta is stepped by
+    ulps around each tie point.  Bit-exact vs the oracle; some v equal a
+    boundary exactly (the ties that the 4-bit grid path must hand to the
+    exact thresholds)."""
+    c, b, outer = orc.pqo_codebook(bits)[:3]
+    rows = []
+    for bk in b:
+        if bk <= 0:
+            continue
+        beta0 = np.float32((outer - bk) / (outer + bk))
+        for n in range(-48, 49):
+            beta = np.float32(beta0 + np.float32(n) * np.spacing(beta0))
+            blk = np.zeros(32, np.float32)
+            blk[0], blk[1] = 1.0, beta
+            rows.append(blk)
+    x = np.stack(rows).reshape(-1, 32)
+    x = np.concatenate([x, np.zeros((len(x) % 4 and 4 - len(x) % 4, 32), np.float32)]).reshape(-1, 128)
+    # the reference arithmetic: r = fl(x f), s = fl(max |r| * fl(1 / outer)), v = fl(r / s)
+    f = np.float32(float.fromhex("0x1.6a09e6p-3"))
+    blocks = x.reshape(-1, 32)
+    r = np.stack([blocks[:, 0] + blocks[:, 1], blocks[:, 0] - blocks[:, 1]], 1).astype(np.float32) * f
+    s = np.maximum((np.abs(r).max(1) * np.float32(1.0 / float(outer))).astype(np.float32), np.float32(1e-10))
+    v = (r / s[:, None]).astype(np.float32)
+    assert np.isin(v, b).sum() >= 3
+    p_ref, s_ref = orc.pqo_quantize(bits, x, 128)
+    p, sc = tq.pqo_quantize(_dev(x), bits)
+    torch.cuda.synchronize()
+    assert np.array_equal(p.cpu().numpy(), p_ref)
+    assert np.array_equal(_u16(sc), s_ref)
+
+
+@pytest.mark.parametrize("bits", [3, 4])
 def test_pqo_dequantize_bit_exact(tq, bits):
     rng = np.random.default_rng(12)
     x = kv_outlier(rng, 2, 500, 128).reshape(-1, 128)

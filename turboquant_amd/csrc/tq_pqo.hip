@@ -16,6 +16,8 @@
 #include "tq_common.h"
 #include "tq_device.h"
 
+#include <algorithm>
+#include <cmath>
 #include <cstring>
 
 namespace {
@@ -34,7 +36,16 @@ struct QuantConsts {
   int mixed_sign;  // scale sign per block: -1 for block % nb < eo
   int nb, eo;
   long long blk0;  // first block of this launch
+  // Evenly spaced boundaries (the 4-bit MaxNorm codebook): b_k = b_0 + k D
+  // up to a few ulps, and grid_step = fl(D), grid_off = fl(1 - b_0 / D).
+  int grid;
+  float grid_step, grid_off;
 };
+
+// Half-width of the band around an integer of the grid coordinate inside
+// which the fast 4-bit path defers to the exact thresholds: 2^-16 = 256 u
+// (u = 2^-24).  The coordinate's error is below 70 u (see quantize_grid).
+constexpr float kGridBand = 0x1p-16f;
 
 enum NormMode : int { kMaxNorm = 0, kL2Norm = 1 };
 
@@ -208,6 +219,38 @@ __device__ __forceinline__ float quantize_block(const float (&r)[32], const Quan
   return s;
 }
 
+// Fast MaxNorm bucketize for evenly spaced boundaries, on the butterfly
+// outputs x_j before the sign and 1/sqrt(32) factor f_j = +-fl(1/sqrt(32)).
+// The reference code is q_j = #{k : fl(fl(x_j f_j) / s) > b_k}.  With
+// W = x_j f_j / s (real) and D the boundary spacing, boundary k sits at
+// T = (v - b_0) / D + 1 = k + 1 + d_k, |d_k| <= 11 u for this codebook
+// (checked on the host, which sets k.grid only below 16 u).  The lane
+// computes t = fma(x_j, +-fl(fl(1/sqrt(32)) / fl(s D)), fl(1 - b_0 / D)):
+// the scale carries <= 3 u, v's two roundings 2 u, |W / D| <= outer / D =
+// 7.5, the offset's rounding 8 u (|1 - b_0 / D| < 8.5) and t's own rounding
+// 8 u (t < 16 near a boundary), so |t - T| <= 7.5 * 5 u + 8 u + 8 u + 16 u
+// (d_k) < 70 u.  Where t is more than
+// kGridBand = 256 u from every integer, each comparison v > b_k equals
+// t > k + 1, so q_j = min(floor(t), 15) (0 for t < 1).  Returns false when
+// some element of the block falls inside the band (or t is NaN); the caller
+// then takes the exact path for the whole block.
+__device__ __forceinline__ bool quantize_grid(const float (&x)[32], float s, const QuantConsts &k,
+                                              uint32_t (&w)[4]) {
+  const float a = kInvSqrt32 / (s * k.grid_step);
+  bool clear = true;
+#pragma unroll
+  for (int q = 0; q < 4; q++) w[q] = 0;
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    const float t = __builtin_fmaf(x[j], pqo_neg(j) ? -a : a, k.grid_off);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_fmed3f(t, 0.0f, 15.5f);
+    const float f = __builtin_amdgcn_fractf(t);
+    clear = clear && (fabsf(f - 0.5f) < 0.5f - kGridBand);
+    w[j >> 3] |= c << (4 * (j & 7));
+  }
+  return clear;
+}
+
 template <int BITS>
 __device__ __forceinline__ void store_packed(uint8_t *__restrict__ packed, long long blk,
                                              const uint32_t (&w)[Packed<BITS>::kWords]) {
@@ -269,14 +312,29 @@ __global__ __launch_bounds__(256) void pqo_quant_kernel(const void *__restrict__
 #pragma unroll
     for (int j = 0; j < 32; j++) r[j] = r[j] / nrm;
   }
+  uint32_t w[Packed<BITS>::kWords];
+  float s = 0.0f;
+  bool done = false;
   if constexpr (ROTATE) {
     butterfly<32>(r);
+    if constexpr (NORM == kMaxNorm && BITS == 4 && CB == 4) {
+      if (k.grid) {
+        // max_j |fl(x_j f_j)| = fl(max_j |x_j| / sqrt(32)): rounding is monotone
+        float am = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; j++) r[j] = r[j] * (pqo_neg(j) ? -kInvSqrt32 : kInvSqrt32);
+        for (int j = 0; j < 32; j++) am = fmaxf(am, fabsf(r[j]));
+        s = (am * kInvSqrt32) * k.mul;
+        if (s < 1e-10f) s = 1e-10f;
+        done = __builtin_isfinite(s) && quantize_grid(r, s, k, w);
+      }
+    }
+    if (!done) {
+#pragma unroll
+      for (int j = 0; j < 32; j++) r[j] = r[j] * (pqo_neg(j) ? -kInvSqrt32 : kInvSqrt32);
+    }
   }
-  uint32_t w[Packed<BITS>::kWords];
-  float s;
-  if constexpr (NORM == kL2Norm) {
+  if (done) {
+  } else if constexpr (NORM == kL2Norm) {
     float U[(1 << CB) - 1];
 #pragma unroll
     for (int t = 0; t < (1 << CB) - 1; t++) U[t] = k.u[t];
@@ -496,6 +554,19 @@ QuantConsts make_quant_consts(const tqh::PqoCodebook &cb, float outer, float sca
   k.strict_mask = t.strict_mask;
   k.mul = t.mul;
   k.scale_sign = scale_sign;
+  // Evenly spaced 15 boundaries whose offsets from the grid stay below 16 u
+  // in grid units (11 u for the 4-bit MaxNorm codebook) and whose spacing
+  // keeps |W / D| <= outer / D near 7.5 (the error budget of quantize_grid).
+  if (cb.nc == 16) {
+    const double d = ((double)cb.b[14] - (double)cb.b[0]) / 14.0;
+    double dev = 0.0;
+    for (int i = 0; i < 15; i++) dev = std::max(dev, std::fabs(((double)cb.b[i] - (double)cb.b[0]) / d - i));
+    if (d > 0.0 && dev < 16.0 * 0x1p-24 && (double)outer / d < 7.6 && std::fabs(1.0 - (double)cb.b[0] / d) < 8.5) {
+      k.grid = 1;
+      k.grid_step = (float)d;
+      k.grid_off = (float)(1.0 - (double)cb.b[0] / d);
+    }
+  }
   return k;
 }
 
