@@ -35,16 +35,27 @@ constexpr int kCounterStride = 64;  // ints
 enum Mode : int { kModePqo = 0, kModePq = 1, kModeTq = 2 };
 
 struct AttnArgs {
+  // Read by every workgroup before its first record load, so kept together
+  // at the head of the block (the kernel reads them in one batch).
   const void *q;
+  // reference ABI (tq_fused_attention): the caller's device codebook
+  // (indexed by code, tq_attention_kernel.cu:129) and 32 decode signs
+  // (applied before the WHT, tq_attention_kernel.cu:45), or null
+  const float *cb_dev;
+  const float *sg_dev;
+  const int *ws_hdr;         // see cnt_top
+  const int *kv_lens;        // device lengths, or null -> single_len
+  const float *rq;           // TQ: see below
   int q_dtype;
+  int ngroups;               // head groups per KV head (grid.y = num_kv_heads * ngroups)
+  int nr;                    // query heads per KV head
+  int num_heads;
+  int max_len;               // host bound; device lengths are clamped to it
   const uint8_t *k_idx;
   const uint16_t *k_sc;
   const uint8_t *v_idx;
   const uint16_t *v_sc;
-  const int *kv_lens;        // device lengths, or null -> single_len
   int single_len;
-  int max_len;               // host bound; device lengths are clamped to it
-  int num_heads;
   int num_kv_heads;
   long long kv_head_stride;  // tokens
   long long seq_stride;      // tokens
@@ -61,19 +72,15 @@ struct AttnArgs {
   // its partials and cnt_top); otherwise it stores nothing and writes NaN
   // outputs.
   int *cnt_top;
-  const int *ws_hdr;
   int ws_pairs;
   int ws_room;
   int P;                     // chunk stride per (b, h) in the partial arrays
   int chunk;                 // tokens per workgroup (split-K chunk)
-  int nr;                    // query heads per KV head
-  int ngroups;               // head groups per KV head (grid.y = num_kv_heads * ngroups)
   void *out;
   int out_dtype;
   // TQ: rq [b][h][head_dim] f32 = R q (precompute_query_projections); per
   // record, signs [16] u8 of R r and the f16 residual norm |r|; qjl_c =
   // f32(sqrt(pi/2)) / sqrt(head_dim)
-  const float *rq;
   const uint32_t *qjl_signs;
   const uint16_t *qjl_norms;
   float qjl_c;
@@ -81,11 +88,6 @@ struct AttnArgs {
   // MaxNorm constants compiled in
   int cb_args;
   float cb[16];
-  // reference ABI (tq_fused_attention): the caller's device codebook
-  // (indexed by code, tq_attention_kernel.cu:129) and 32 decode signs
-  // (applied before the WHT, tq_attention_kernel.cu:45), or null
-  const float *cb_dev;
-  const float *sg_dev;
 };
 
 // Query element as stored (f32 bits or a 16-bit pattern), converted
@@ -657,6 +659,8 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
   if (P > num_partitions)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_partitions %d < the %d chunks of %d tokens", num_partitions, P,
                      chunk);
+  if (num_partitions > (1 << 20))  // the merge addresses a round's partials with 32-bit offsets
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_partitions %d exceeds 2^20", num_partitions);
   rc = launch_stream<false>(a, bits, qjl_enabled ? kModeTq : kModePqo, head_dim,
                             dim3((unsigned)P, (unsigned)num_kv_heads, 1u), stream);
   if (rc) return rc;

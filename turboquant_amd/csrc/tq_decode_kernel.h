@@ -217,15 +217,22 @@ __device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
     const bool active = oq < outs;
     const int r = active ? oq / HD : 0, d0 = oq - r * HD;
     const long long c0 = (bh0 + r) * a.P;
+    // one descriptor over the partial rows of the round's heads (uniform: a
+    // per-lane descriptor would cost a waterfall loop per load); the lane's
+    // head and chunk ride in the offset.  The round's heads hold hrn * HD <=
+    // 256 outputs per chunk, so the range is at most 1 KiB x P (P below
+    // 2^20, checked on the host).
+    const int hr0 = o0 / HD, hrn = min(a.nr - hr0, (256 + HD - 1) / HD);
     const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(a.po + c0 * HD, (short)0, a.P * HD * (int)sizeof(float), 0x00020000);
+        rec_rsrc(a.po + (bh0 + hr0) * a.P * HD, (uint32_t)(hrn * a.P * HD * (int)sizeof(float)));
+    const uint32_t lane_off = (uint32_t)(((r - hr0) * a.P * HD + d0) * (int)sizeof(float));
     float4 pv[MAXC];
     float pm[MAXC], pl[MAXC];
 #pragma unroll
     for (int k = 0; k < MAXC; k++) {
       const int cc = part + W * k;
       const bool ok = active && cc < nchunks;
-      pv[k] = ok ? ld_agent16(rsrc, (uint32_t)((cc * HD + d0) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+      pv[k] = ok ? ld_agent16(rsrc, lane_off + (uint32_t)(cc * HD * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
       pm[k] = ok ? ld_agent(&a.pm[c0 + cc]) : -INFINITY;
       pl[k] = ok ? ld_agent(&a.ps[c0 + cc]) : 0.f;
     }
@@ -245,7 +252,7 @@ __device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
     for (int k = 0; k < MAXC; k++) fold(pv[k], pl[k], pm[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[k] - M));
     for (int cc = part + W * MAXC; active && cc < nchunks; cc += W) {  // long contexts only
       const float m = ld_agent(&a.pm[c0 + cc]), l = ld_agent(&a.ps[c0 + cc]);
-      const float4 v = ld_agent16(rsrc, (uint32_t)((cc * HD + d0) * 4));
+      const float4 v = ld_agent16(rsrc, lane_off + (uint32_t)(cc * HD * 4));
       if (m == -INFINITY) continue;
       if (m > M) {
         const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - m);
@@ -330,9 +337,20 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the wave's scalar offsets
   const int l16 = lane & 15, lg = lane >> 4;
   const int c = blockIdx.x, b = blockIdx.z;
-  const int g = blockIdx.y / a.ngroups, gh = blockIdx.y - g * a.ngroups;
-  const int nh = min(HG, a.nr - gh * HG);                    // heads of this group
-  const long long hq0 = (long long)b * a.num_heads + (long long)g * a.nr + gh * HG;  // its first q head
+  // The argument fields that the first loads depend on, all requested
+  // before one wait (the empty asm makes them available together; left to
+  // itself the compiler requests each behind the branch that uses it, and
+  // each request after the first that misses the scalar cache costs a
+  // memory round trip before any record load goes out).
+  const void *const a_q = a.q;
+  const float *const a_sg = a.sg_dev, *const a_cb = a.cb_dev, *const a_rq = a.rq;
+  const int *const a_ws = a.ws_hdr, *const a_lens = a.kv_lens;
+  const int a_qdt = a.q_dtype, a_ngroups = a.ngroups, a_nr = a.nr, a_heads = a.num_heads, a_max = a.max_len;
+  asm volatile("" ::"s"(a_q), "s"(a_sg), "s"(a_cb), "s"(a_rq), "s"(a_ws), "s"(a_lens), "s"(a_qdt), "s"(a_ngroups),
+               "s"(a_nr), "s"(a_heads), "s"(a_max));
+  const int g = blockIdx.y / a_ngroups, gh = blockIdx.y - g * a_ngroups;
+  const int nh = min(HG, a_nr - gh * HG);                    // heads of this group
+  const long long hq0 = (long long)b * a_heads + (long long)g * a_nr + gh * HG;  // its first q head
   const int t0 = c * C::CHUNK, tw = t0 + wave * TPW;
 
   // ---- the query (and for TQ its projection) goes out first: later waits
@@ -348,29 +366,32 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     rqv[k] = 0.f;
     if (e < QE && hl < nh) {
       const long long qi = hq0 * HD + e;
-      if (a.q_dtype == kF32) qbits[k] = static_cast<const uint32_t *>(a.q)[qi];
-      else qbits[k] = static_cast<const uint16_t *>(a.q)[qi];
-      if constexpr (C::QJL) rqv[k] = a.rq[qi];
+      if (a_qdt == kF32) qbits[k] = static_cast<const uint32_t *>(a_q)[qi];
+      else qbits[k] = static_cast<const uint16_t *>(a_q)[qi];
+      if constexpr (C::QJL) rqv[k] = a_rq[qi];
     }
   }
   // the caller's decode sign for this lane (selected at its use: a select
   // here would make the constant path wait for the load before any record
   // load goes out)
   float sgl = 0.f;
-  if (a.sg_dev) sgl = a.sg_dev[tid & 31];
+  if (a_sg) sgl = a_sg[tid & 31];
   // the caller's codebook entries for this lane's pair-table entry, also
   // before any record load (a wait for them then waits for nothing else)
   constexpr int CM = (1 << C::CB) - 1;  // slot codes >= 2^CB never occur
   const int pi0 = tid & ((1 << BITS) - 1) & CM, pi1 = (tid >> BITS) & CM;
   float pc0 = 0.f, pc1 = 0.f;
-  if (a.cb_dev && tid < C::NPAIR) {
-    pc0 = a.cb_dev[pi0];
-    pc1 = a.cb_dev[pi1];
+  if (a_cb && tid < C::NPAIR) {
+    pc0 = a_cb[pi0];
+    pc1 = a_cb[pi1];
   }
+  // the workspace header, needed only at the split-K arrival: a vector load
+  // (a scalar one would be waited for here, before the record loads)
   int ws_hdr = 0;
-  if (INLINE_MERGE && tid == 0) ws_hdr = *a.ws_hdr;
+  if constexpr (INLINE_MERGE)
+    ws_hdr = (int)__builtin_amdgcn_raw_buffer_load_b32(rec_rsrc(a_ws, 4u), 0u, 0u, 0);
 
-  const int len = len_hint >= 0 ? len_hint : min(max(a.kv_lens[b], 0), a.max_len);
+  const int len = len_hint >= 0 ? len_hint : min(max(a_lens[b], 0), a_max);
   if (t0 >= len) {  // an empty chunk is not counted by the merge
     if (len == 0 && c == 0) {
       // an empty sequence attends to nothing: zero output (cuda/attention.rs:65-68)
