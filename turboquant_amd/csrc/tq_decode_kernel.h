@@ -391,7 +391,11 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   if constexpr (INLINE_MERGE)
     ws_hdr = (int)__builtin_amdgcn_raw_buffer_load_b32(rec_rsrc(a_ws, 4u), 0u, 0u, 0);
 
-  const int len = len_hint >= 0 ? len_hint : min(max(a_lens[b], 0), a_max);
+  // the sequence's length through the scalar cache (constant address space):
+  // a vector load would queue behind the records other workgroups on this
+  // compute unit have in flight, and every record load here waits for it
+  typedef __attribute__((address_space(4))) const int const_int;
+  const int len = len_hint >= 0 ? len_hint : min(max(((const_int *)a_lens)[b], 0), a_max);
   if (t0 >= len) {  // an empty chunk is not counted by the merge
     if (len == 0 && c == 0) {
       // an empty sequence attends to nothing: zero output (cuda/attention.rs:65-68)
