@@ -249,7 +249,16 @@ void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
   grid.x = (unsigned)((a.max_len + C::CHUNK - 1) / C::CHUNK);
   if (grid.x == 0) grid.x = 1;  // an empty batch still zeroes its outputs
   const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
-  hipLaunchKernelGGL((stream_decode_kernel<C, INLINE>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx, a.k_sc,
+  // 4-bit codes on the compiled-in MaxNorm codebook (evenly spaced) take the
+  // grid key pass; a caller's codebook or the L2Norm tables, the pair table
+  if constexpr (C::BITS == 4 && C::MODE == kModePqo) {
+    if (!a.cb_dev && !a.cb_args) {
+      hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, true>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx,
+                         a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, false>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx, a.k_sc,
                      a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
 }
 // The cache decode picks the workgroup size per launch: 8 waves while the

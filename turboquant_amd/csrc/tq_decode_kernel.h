@@ -80,7 +80,8 @@ struct DecCfg {
   static constexpr int OFF_QMAX = OFF_Q + HG * HD;                    // [HG][NQB] block max |qt|
   static constexpr int OFF_RQ = OFF_QMAX + HG * NQB;                  // QJL [HG][HD]
   static constexpr int OFF_RQMAX = OFF_RQ + (QJL ? HG * HD : 0);      // QJL [HG][NQB]
-  static constexpr int SETUP_END = OFF_RQMAX + (QJL ? HG * NQB : 0);
+  static constexpr int OFF_QSUM = OFF_RQMAX + (QJL ? HG * NQB : 0);   // [HG][NQB] block sums of the query
+  static constexpr int SETUP_END = OFF_QSUM + (BITS == 4 && MODE == kModePqo ? HG * NQB : 0);
   // register query operands are built once per workgroup, staged here
   static constexpr int OFF_QAS = (SETUP_END + 3) & ~3;               // u32x4 [QG*KJ][64]
   // per wave: weights p [HG][TPW] and |s_V| 2^-Ev [NQB][TPW] for the V pass;
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(256) void stream_merge_kernel(AttnArgs a) {
   merge_heads<HD, 4>(a, b, g, nchunks);
 }
 
-template <class C, bool INLINE_MERGE>
+template <class C, bool INLINE_MERGE, bool GRID>
 #ifndef TQ_DECODE_WPE
 #define TQ_DECODE_WPE 2
 #endif
@@ -323,6 +324,14 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   static_assert(C::LDS_FITS, "the workgroup's LDS (with the merge's scratch) fits 64 KiB");
   constexpr int QPM = C::QPM, HPM = C::HPM, QG = C::QG, ES = C::ES, KJ = C::KJ, PPL = C::PPL;
   constexpr int NKT = C::NKT, NVP = C::NVP, PACKED = C::PACKED;
+  // GRID: 4-bit codes on the evenly spaced MaxNorm codebook c_i = -R + i D.
+  // The key pass then contracts the query with the codes themselves (exact
+  // f16 subnormals i 2^-24, eight per word by masks) and applies
+  // q.c = D sum q_j i_j - R sum q_j after the product: no codebook reads,
+  // half the instructions of the two-part codebook operand.
+  static_assert(!GRID || (BITS == 4 && C::MODE == kModePqo), "the grid key pass takes 4-bit PQO codes");
+  constexpr int KJA = GRID ? QPM : KJ;                  // key-pass instructions per qblock group
+  constexpr bool QAR = GRID || C::QA_REGS;              // query operands in registers
   __shared__ __attribute__((aligned(16))) float lds[C::TOTAL];
   __shared__ int s_flag;
   uint2 *s_pair = reinterpret_cast<uint2 *>(lds + C::OFF_PAIR);
@@ -330,6 +339,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   float *s_qmax = lds + C::OFF_QMAX;
   float *s_rq = lds + C::OFF_RQ;
   float *s_rqmax = lds + C::OFF_RQMAX;
+  float *s_qsum = lds + C::OFF_QSUM;
   uint2 *s_nib = reinterpret_cast<uint2 *>(lds + C::OFF_NIB);
   u32x4 *s_qa = reinterpret_cast<u32x4 *>(lds + C::OFF_QA);
 
@@ -547,6 +557,15 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       m = fmaxf(m, lane_xor<8>(m));
       m = fmaxf(m, lane_xor<16>(m));
       if ((e & 31) == 0) s_qmax[e >> 5] = m;
+      if constexpr (GRID) {
+        float sm = qt;
+        sm += lane_xor<1>(sm);
+        sm += lane_xor<2>(sm);
+        sm += lane_xor<4>(sm);
+        sm += lane_xor<8>(sm);
+        sm += lane_xor<16>(sm);
+        if ((e & 31) == 0) s_qsum[e >> 5] = sm;
+      }
       if constexpr (C::QJL) {
         const float rsv = rqv[k] * (a.softmax_scale * kLog2e);
         s_rq[e] = rsv;
@@ -587,18 +606,41 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
     return val;
   };
-  u32x4 qa[C::QA_REGS ? QG * KJ : 1];
-  if constexpr (C::QA_REGS) {
+  // Grid key pass: word j of the lane's stream part holds elements
+  // 8 j + (0..7) as nibbles; B's register r carries nibbles r and r + 4
+  // (masks 0x000F000F after a shift by 4 r), so slot u = 2 r + h takes
+  // element 8 j + r + 4 h, and the query operand follows that order.
+  auto make_qa_grid = [&](int qg, int j, int m, int kg) -> u32x4 {
+    const int qbl = m / (2 * HPM), hl = (m >> 1) % HPM, part = m & 1;
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (kg / ES == qbl && hl < nh) {
+      const float sc = exp2i(-head_exp(s_qmax, hl));
+      const float *src = s_q + hl * HD + (qg * QPM + qbl) * 32 + (kg % ES) * (32 / ES) + 8 * j;
+      const float4 lo4 = *reinterpret_cast<const float4 *>(src), hi4 = *reinterpret_cast<const float4 *>(src + 4);
+      const float xa[4] = {lo4.x * sc, lo4.y * sc, lo4.z * sc, lo4.w * sc};
+      const float xb[4] = {hi4.x * sc, hi4.y * sc, hi4.z * sc, hi4.w * sc};
+      uint32_t w[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float ha = split_hi(xa[r]), hb = split_hi(xb[r]);
+        w[r] = part ? pack_f16(xa[r] - ha, xb[r] - hb) : pack_f16(ha, hb);
+      }
+      val = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    return val;
+  };
+  u32x4 qa[QAR ? QG * KJA : 1];
+  if constexpr (QAR) {
     // each operand is the same for every wave: the workgroup's lanes build
     // them once, each wave then reads its registers
     u32x4 *s_qas = reinterpret_cast<u32x4 *>(lds + C::OFF_QAS);
-    for (int e = tid; e < QG * KJ * 64; e += C::THREADS) {
+    for (int e = tid; e < QG * KJA * 64; e += C::THREADS) {
       const int sl = e >> 6, ln = e & 63;
-      s_qas[e] = make_qa(sl / KJ, sl % KJ, ln & 15, ln >> 4);
+      s_qas[e] = GRID ? make_qa_grid(sl / KJA, sl % KJA, ln & 15, ln >> 4) : make_qa(sl / KJA, sl % KJA, ln & 15, ln >> 4);
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < QG * KJ; k++) qa[k] = s_qas[k * 64 + lane];
+    for (int k = 0; k < QG * KJA; k++) qa[k] = s_qas[k * 64 + lane];
   } else {
     for (int e = tid; e < QG * KJ * 64; e += C::THREADS) {
       const int sl = e >> 6, ln = e & 63;
@@ -612,6 +654,20 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // hl0 and lanes 32-63 head hl0 + 1).
   const int hl0 = (2 * lg) % HPM, uh = lane >> 5;
   constexpr int NS = QPM == 1 ? 2 : 1;
+  // grid key pass: the lane's rows are qblock qg QPM + lg / ES of heads
+  // hl0 + u; their R sum_j Q_j (Q as in the operand, exact power-of-two scale)
+  float rqs[GRID ? QG : 1][2];
+  constexpr float kGridR = 2.1573f;                       // -c_0 of the 4-bit MaxNorm codebook
+  constexpr float kGridD24 = ((2.0f * kGridR) / 15.0f) * 16777216.0f;  // D 2^24 (codes enter as i 2^-24)
+  if constexpr (GRID) {
+#pragma unroll
+    for (int qg = 0; qg < QG; qg++)
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int hl = min(hl0 + u, HG - 1);
+        rqs[qg][u] = kGridR * s_qsum[hl * NQB + qg * QPM + lg / ES] * exp2i(-head_exp(s_qmax, hl));
+      }
+  }
   float escale[NS], erscale[NS];
 #pragma unroll
   for (int v = 0; v < NS; v++) {
@@ -660,6 +716,16 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       dk[qg] = f32x4{0.f, 0.f, 0.f, 0.f};
       align_part<C>(kw[i][qg], kes);
     }
+    if constexpr (GRID) {
+#pragma unroll
+      for (int qg = 0; qg < QG; qg++)
+#pragma unroll
+        for (int j = 0; j < KJA; j++) {
+          const uint32_t w = kw[i][qg][j];
+          const u32x4 bv = {w & 0x000F000Fu, (w >> 4) & 0x000F000Fu, (w >> 8) & 0x000F000Fu, (w >> 12) & 0x000F000Fu};
+          dk[qg] = mfma(qa[qg * KJA + j], bv, dk[qg]);
+        }
+    } else {
     // every pair-table read of the tile goes out before its first MFMA, so
     // the LDS latency is paid once per tile, not once per instruction
     uint2 e[QG][KJ][2];
@@ -674,9 +740,10 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     for (int qg = 0; qg < QG; qg++)
 #pragma unroll
       for (int j = 0; j < KJ; j++) {
-        const u32x4 qv = C::QA_REGS ? qa[C::QA_REGS ? qg * KJ + j : 0] : s_qa[(qg * KJ + j) * 64 + lane];
+        const u32x4 qv = QAR ? qa[QAR ? qg * KJ + j : 0] : s_qa[(qg * KJ + j) * 64 + lane];
         dk[qg] = mfma(qv, u32x4{e[qg][j][0].x, e[qg][j][0].y, e[qg][j][1].x, e[qg][j][1].y}, dk[qg]);
       }
+    }
     f32x4 dq = {0.f, 0.f, 0.f, 0.f};
     if constexpr (C::QJL) {
 #pragma unroll
@@ -694,7 +761,9 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
 #pragma unroll
       for (int qg = 0; qg < QG; qg++) {
         const float sk = fabsf(f16_to_f32((uint16_t)ksv[i][qg]));
-        x[u] = __builtin_fmaf(dk[qg][2 * u] + dk[qg][2 * u + 1], sk, x[u]);
+        float d = dk[qg][2 * u] + dk[qg][2 * u + 1];
+        if constexpr (GRID) d = __builtin_fmaf(d, kGridD24, -rqs[qg][u]);
+        x[u] = __builtin_fmaf(d, sk, x[u]);
       }
     }
     // sum over the qblocks of the instruction (row groups lg ^ 2 and, for
