@@ -183,3 +183,61 @@ def test_batched_ragged_grid_over_the_compute_units(tq, bits, nr):
     out = out.cpu().numpy()
     for b in range(bsz):
         assert np.abs(out[b] - refs[b]).max() <= TOL, b
+
+
+@pytest.mark.parametrize("bits,nr", [(3, 2), (4, 4)])
+def test_batched_ranges_of_chunks(tq, bits, nr):
+    """A batch whose single-chunk grid needs several rounds of resident
+    workgroups runs ranges of several chunks per workgroup (one online softmax
+    over the range, the value sums rescaled as the running max and V-scale
+    exponent move); ragged lengths: empty, one token, exactly a chunk
+    multiple, the capacity, and ranges left partly or wholly empty."""
+    bsz, hkv, d, cap = 12, 8, 128, 9000
+    rng = np.random.default_rng(90 + bits + nr)
+    lens = rng.integers(1, cap + 1, size=bsz)
+    lens[2], lens[5], lens[7], lens[9] = 0, 1, 4096, cap
+    h = hkv * nr
+    pd, nb = d * bits // 8, d // 32
+    kp = np.zeros((bsz, hkv, cap, pd), np.uint8)
+    ks = np.zeros((bsz, hkv, cap, nb), np.int16)
+    vp = np.zeros_like(kp)
+    vs = np.zeros_like(ks)
+    q = bf16_round(rng.standard_normal((bsz, h, d)).astype(np.float32) / np.float32(math.sqrt(d)))
+    refs = []
+    for b in range(bsz):
+        t = int(lens[b])
+        if t == 0:
+            refs.append(np.zeros((h, d), np.float32))
+            continue
+        k = kv_outlier(rng, hkv, t, d).reshape(-1, d)
+        v = kv_outlier(rng, hkv, t, d).reshape(-1, d)
+        # a late stretch of keys much larger than the rest: the running max
+        # moves up several chunks into a range
+        k[-min(t, 700) // 2:] *= 3.0
+        pk, sk = orc.polar_quantize(bits, orc.OUTLIER_ALL, k, d)
+        pv, sv = orc.polar_quantize(bits, orc.OUTLIER_ALL, v, d)
+        kd = orc.polar_dequantize(bits, orc.OUTLIER_ALL, pk, sk, d).reshape(hkv, t, d)
+        vd = orc.polar_dequantize(bits, orc.OUTLIER_ALL, pv, sv, d).reshape(hkv, t, d)
+        kp[b, :, :t] = pk.reshape(hkv, t, pd)
+        ks[b, :, :t] = sk.view(np.int16).reshape(hkv, t, nb)
+        vp[b, :, :t] = pv.reshape(hkv, t, pd)
+        vs[b, :, :t] = sv.view(np.int16).reshape(hkv, t, nb)
+        refs.append(orc.attention_dense(q[b], kd, vd, 1 / math.sqrt(d)))
+    # 4-wave chunks of 512 tokens: 18 per (sequence, KV head), 1,728 in all,
+    # beyond one round of 768 resident workgroups
+    assert bsz * hkv * -(-cap // 512) > 3 * 256
+    ws = tq.AttentionWorkspace(bsz, h, hkv, d, cap)
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    out = tq.cache_decode_attention(qd, _dev(kp), _dev(ks), _dev(vp), _dev(vs),
+                                    _dev(lens.astype(np.int32)), hkv, bits, cap, cap, hkv * cap,
+                                    1 / math.sqrt(d), ws, orc.OUTLIER_ALL)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for b in range(bsz):
+        assert np.abs(out[b] - refs[b]).max() <= TOL, (b, int(lens[b]))
+    # a second call re-arms every counter it used
+    out2 = tq.cache_decode_attention(qd, _dev(kp), _dev(ks), _dev(vp), _dev(vs),
+                                     _dev(lens.astype(np.int32)), hkv, bits, cap, cap, hkv * cap,
+                                     1 / math.sqrt(d), ws, orc.OUTLIER_ALL)
+    torch.cuda.synchronize()
+    assert np.array_equal(out2.cpu().numpy(), out)

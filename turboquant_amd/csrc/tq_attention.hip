@@ -75,7 +75,8 @@ struct AttnArgs {
   int ws_pairs;
   int ws_room;
   int P;                     // chunk stride per (b, h) in the partial arrays
-  int chunk;                 // tokens per workgroup (split-K chunk)
+  int chunk;                 // tokens per chunk (a wave pass per TPW tokens)
+  int cpr;                   // chunks per workgroup: workgroup c takes chunks [c cpr, (c + 1) cpr)
   void *out;
   int out_dtype;
   // TQ: rq [b][h][head_dim] f32 = R q (precompute_query_projections); per
@@ -228,6 +229,7 @@ WsLayout ws_layout(int batch, int num_heads, int num_kv_heads, int head_dim, int
 AttnArgs base_args() {
   AttnArgs a{};
   a.out_dtype = kF32;
+  a.cpr = 1;
   return a;
 }
 
@@ -243,23 +245,45 @@ int device_cus() {
   return cus[dev];
 }
 
-template <class C, bool INLINE>
-void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
-  a.chunk = C::CHUNK;
-  grid.x = (unsigned)((a.max_len + C::CHUNK - 1) / C::CHUNK);
-  if (grid.x == 0) grid.x = 1;  // an empty batch still zeroes its outputs
-  const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
-  // 4-bit codes on the compiled-in MaxNorm codebook (evenly spaced) take the
-  // grid key pass; a caller's codebook or the L2Norm tables, the pair table
+// 4-bit codes on the compiled-in MaxNorm codebook (evenly spaced) take the
+// grid key pass; a caller's codebook or the L2Norm tables, the pair table
+template <class C, bool INLINE, bool MULTI>
+void launch_stream_k(AttnArgs &a, dim3 grid, hipStream_t st, int len_hint) {
   if constexpr (C::BITS == 4 && C::MODE == kModePqo) {
     if (!a.cb_dev && !a.cb_args) {
-      hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, true>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx,
-                         a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+      hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, true, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx,
+                         a.v_idx, a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
       return;
     }
   }
-  hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, false>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx, a.k_sc,
-                     a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+  hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, false, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx,
+                     a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+}
+template <class C, bool INLINE>
+void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
+  a.chunk = C::CHUNK;
+  const int chunks = (a.max_len + C::CHUNK - 1) / C::CHUNK;
+  // Chunks per workgroup: one while the grid of single chunks fits one round
+  // of resident workgroups (three waves per SIMD); beyond that, ranges of cpr
+  // chunks sized for one round of the range kernel (two workgroups per
+  // compute unit), so that each workgroup pays its setup, combine and
+  // split-K arrival once per range and streams the next chunk's first tiles
+  // during the current chunk's value pass.  The reference ABI's separate
+  // merge launch takes single chunks.
+  a.cpr = 1;
+  if constexpr (INLINE) {
+    const long long tasks = (long long)chunks * grid.y * grid.z;
+    const long long cus = device_cus();
+    if (tasks > cus * (12 / C::WAVES))
+      a.cpr = (int)min((long long)max(chunks, 1), (tasks + 2 * cus - 1) / (2 * cus));
+  }
+  grid.x = (unsigned)((chunks + a.cpr - 1) / a.cpr);
+  if (grid.x == 0) grid.x = 1;  // an empty batch still zeroes its outputs
+  const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
+  if constexpr (INLINE) {
+    if (a.cpr > 1) return launch_stream_k<C, INLINE, true>(a, grid, st, len_hint);
+  }
+  launch_stream_k<C, INLINE, false>(a, grid, st, len_hint);
 }
 // The cache decode picks the workgroup size per launch: 8 waves while the
 // grid of 8-wave workgroups leaves compute units idle (one long sequence:

@@ -73,8 +73,10 @@ struct DecCfg {
   // LDS carve (32-bit words)
   static constexpr int OFF_PAIR = 0;                                  // uint2 [NPAIR]
   static constexpr int OFF_NIB = OFF_PAIR + 2 * NPAIR;                // QJL uint2 [16]
-  static constexpr int OFF_QA = (OFF_NIB + (QJL ? 32 : 0) + 3) & ~3;  // u32x4 [QG*KJ][64] (LDS operands)
-  static constexpr int OFF_W = OFF_QA + (QA_REGS ? 0 : QG * KJ * 64 * 4);
+  // the key-pass query operands, u32x4 [QG*KJ][64] (read per instruction,
+  // or by QA_REGS configurations into registers at each chunk's K pass)
+  static constexpr int OFF_QA = (OFF_NIB + (QJL ? 32 : 0) + 3) & ~3;
+  static constexpr int OFF_W = OFF_QA + QG * KJ * 64 * 4;
   // the query setup lives in the wave staging area until the K pass starts
   static constexpr int OFF_Q = OFF_W;                                 // [HG][HD] scaled rotated query
   static constexpr int OFF_QMAX = OFF_Q + HG * HD;                    // [HG][NQB] block max |qt|
@@ -82,24 +84,25 @@ struct DecCfg {
   static constexpr int OFF_RQMAX = OFF_RQ + (QJL ? HG * HD : 0);      // QJL [HG][NQB]
   static constexpr int OFF_QSUM = OFF_RQMAX + (QJL ? HG * NQB : 0);   // [HG][NQB] block sums of the query
   static constexpr int SETUP_END = OFF_QSUM + (BITS == 4 && MODE == kModePqo ? HG * NQB : 0);
-  // register query operands are built once per workgroup, staged here
-  static constexpr int OFF_QAS = (SETUP_END + 3) & ~3;               // u32x4 [QG*KJ][64]
-  // per wave: weights p [HG][TPW] and |s_V| 2^-Ev [NQB][TPW] for the V pass;
-  // after it, the wave's output acc [HG][HD] over them; then m [HG], l [HG], 2^Ev
+  // per wave: weights p [HG][TPW] and |s_V| 2^-Ev [NQB][TPW] of the current
+  // chunk for the V pass; the wave's value sums acc [HG][HD] over its chunks;
+  // then m [HG], l [HG], 2^Ev and the chunk's rescale factors [HG]
   static constexpr int WP = HG * TPW;
   static constexpr int WS = NQB * TPW;
-  static constexpr int WA = WP + WS > HG * HD ? WP + WS : HG * HD;
-  static constexpr int WSTAGE = (WA + 2 * HG + 1 + 3) & ~3;
+  static constexpr int WC = WP + WS;
+  static constexpr int WM = WC + HG * HD;
+  static constexpr int WSTAGE = (WM + 3 * HG + 1 + 3) & ~3;
   static constexpr int TOTAL = OFF_W + WAVES * WSTAGE;
   static constexpr int MERGE_LDS = merge_lds(WAVES);
   static_assert(SETUP_END <= TOTAL, "the query setup fits the staging area");
-  static_assert(!QA_REGS || OFF_QAS + QG * KJ * 64 * 4 <= TOTAL, "the operand staging fits the staging area");
   static_assert(HG >= 1 && HG <= 8, "heads per group");
   static_assert(TPW % 64 == 0, "whole V-scale loads per lane");
   static_assert(QPM * HPM == 8 && HPM >= HG, "one instruction serves every head");
   static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "waves per workgroup");
-  // does the workgroup's LDS (with the merge's scratch) fit 64 KiB?
+  // does the workgroup's LDS (with the merge's scratch) fit 64 KiB (the
+  // 8-wave form is taken only then), and gfx950's 160 KiB at all?
   static constexpr bool LDS_FITS = TOTAL * 4 + MERGE_LDS <= 64 * 1024;
+  static constexpr bool LDS_OK = TOTAL * 4 + MERGE_LDS <= 160 * 1024;
 };
 
 // A buffer resource over the bytes [off, total) of the records at base:
@@ -298,7 +301,9 @@ __device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
       else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(res);
       else static_cast<uint16_t *>(a.out)[oi] = f32_to_f16(res);
     }
-    __syncthreads();
+    // the next round reuses the LDS scratch (after the last, nothing does: no
+    // barrier, whose fence would wait for the output stores)
+    if (o0 + 256 < outs) __syncthreads();
   }
 }
 
@@ -309,10 +314,11 @@ __global__ __launch_bounds__(256) void stream_merge_kernel(AttnArgs a) {
   const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
   const int nchunks = (len + a.chunk - 1) / a.chunk;
   if (nchunks == 0) return;
-  merge_heads<HD, 4>(a, b, g, nchunks);
+  merge_heads<HD, 4>(a, b, g, (nchunks + a.cpr - 1) / a.cpr);
 }
 
-template <class C, bool INLINE_MERGE, bool GRID>
+// MULTI: the launch gives workgroups ranges of several chunks (cpr > 1)
+template <class C, bool INLINE_MERGE, bool GRID, bool MULTI>
 #ifndef TQ_DECODE_WPE
 #define TQ_DECODE_WPE 2
 #endif
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
                                                                long long seq_stride, long long kv_head_stride,
                                                                int len_hint, AttnArgs a) {
   constexpr int BITS = C::BITS, HD = C::HD, NQB = C::NQB, HG = C::HG, TPW = C::TPW, QW = C::QW, NW = C::NW;
-  static_assert(C::LDS_FITS, "the workgroup's LDS (with the merge's scratch) fits 64 KiB");
+  static_assert(C::LDS_OK, "the workgroup's LDS (with the merge's scratch) fits 160 KiB");
   constexpr int QPM = C::QPM, HPM = C::HPM, QG = C::QG, ES = C::ES, KJ = C::KJ, PPL = C::PPL;
   constexpr int NKT = C::NKT, NVP = C::NVP, PACKED = C::PACKED;
   // GRID: 4-bit codes on the evenly spaced MaxNorm codebook c_i = -R + i D.
@@ -356,12 +362,12 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   const float *const a_sg = a.sg_dev, *const a_cb = a.cb_dev, *const a_rq = a.rq;
   const int *const a_ws = a.ws_hdr, *const a_lens = a.kv_lens;
   const int a_qdt = a.q_dtype, a_ngroups = a.ngroups, a_nr = a.nr, a_heads = a.num_heads, a_max = a.max_len;
+  const int a_cpr = a.cpr;
   asm volatile("" ::"s"(a_q), "s"(a_sg), "s"(a_cb), "s"(a_rq), "s"(a_ws), "s"(a_lens), "s"(a_qdt), "s"(a_ngroups),
-               "s"(a_nr), "s"(a_heads), "s"(a_max));
+               "s"(a_nr), "s"(a_heads), "s"(a_max), "s"(a_cpr));
   const int g = blockIdx.y / a_ngroups, gh = blockIdx.y - g * a_ngroups;
   const int nh = min(HG, a_nr - gh * HG);                    // heads of this group
   const long long hq0 = (long long)b * a_heads + (long long)g * a_nr + gh * HG;  // its first q head
-  const int t0 = c * C::CHUNK, tw = t0 + wave * TPW;
 
   // ---- the query (and for TQ its projection) goes out first: later waits
   // for it count no record load ----
@@ -406,7 +412,13 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // compute unit have in flight, and every record load here waits for it
   typedef __attribute__((address_space(4))) const int const_int;
   const int len = len_hint >= 0 ? len_hint : min(max(((const_int *)a_lens)[b], 0), a_max);
-  if (t0 >= len) {  // an empty chunk is not counted by the merge
+  // Workgroup c takes the range of cpr consecutive chunks from chunk c cpr
+  // (the host picks cpr; the merge counts ranges): its waves keep one online
+  // softmax state over the range's chunks, so the setup, the combine and the
+  // split-K arrival are paid once per range.
+  const int nchunks = (len + C::CHUNK - 1) / C::CHUNK;
+  const int ck0 = c * a_cpr;
+  if (ck0 >= nchunks) {  // an empty range is not counted by the merge
     if (len == 0 && c == 0) {
       // an empty sequence attends to nothing: zero output (cuda/attention.rs:65-68)
       for (int e = tid; e < nh * HD; e += C::THREADS) {
@@ -418,9 +430,11 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     __builtin_amdgcn_s_waitcnt(0);
     return;
   }
-  const int nchunks = (len + C::CHUNK - 1) / C::CHUNK;
+  const int nck = MULTI ? min(a_cpr, nchunks - ck0) : 1;  // chunks of this range
+  const int nparts = (nchunks + a_cpr - 1) / a_cpr;    // ranges the merge folds
 
-  // ---- records.  K tile i, lane (l16, lg): token tw + 16 i + l16, for
+  // ---- records.  Wave w's tokens of a chunk start at tw = chunk CHUNK +
+  // w TPW.  K tile i, lane (l16, lg): token tw + 16 i + l16, for
   // group qg the stream part lg % ES of qblock qg * QPM + lg / ES; its key
   // scale.  V tile i, lane (l16, lg): token tw + 16 i + 4 lg + l16 / 4, row
   // set rs = l16 & 3 -> stream part rs % ES of qblock vs * QPM + rs / ES.
@@ -437,7 +451,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   const uint32_t kvo = (uint32_t)l16 * PACKED + (uint32_t)(kqb * QW + part_word<C>(kes)) * 4u;
   const uint32_t kso = ((uint32_t)l16 * NQB + kqb) * 2u;
   const uint32_t vvo = (uint32_t)(4 * lg + (l16 >> 2)) * PACKED + (uint32_t)(vqb * QW + part_word<C>(ves)) * 4u;
-  const uint32_t tw0 = (uint32_t)tw;
+  const uint32_t tw_first = (uint32_t)(ck0 * C::CHUNK + wave * TPW);
   uint32_t kw[NKT][QG][NW], vw[NKT][QG][NW];
   uint32_t ksv[NKT][QG];
   uint32_t sgw[NKT][C::SW4];
@@ -448,7 +462,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // NKT, V tile i group NKT + 1 + i.  Only a few groups are in flight at a
   // time (issued as earlier ones are consumed), so no load instruction waits
   // at issue for the CU's memory queue while arithmetic could run.
-  auto issue = [&](int grp) {
+  auto issue = [&](int grp, uint32_t tw0) {
     if (grp < NKT) {
       const int i = grp;
       const uint32_t t16 = tw0 + 16u * i;  // the tile's first token
@@ -487,25 +501,34 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
   };
   // Schedule: K tiles 0 .. LA-1 and the V scales (needed by the softmax)
-  // before the setup; K tile i + LA as K tile i is consumed; V tiles 0-3
-  // during the last two K tiles, so the first values are in flight before the
-  // softmax; then V tiles 2 vp + 4, 2 vp + 5 as V pair vp is consumed.
-  constexpr int LA = dmin(C::LOOKAHEAD, NKT);
+  // of the first chunk before the setup; K tile i + LA as K tile i is
+  // consumed; V tiles 0-3 during the last two K tiles, so the first values
+  // are in flight before the softmax; then V tiles 2 vp + 4, 2 vp + 5 as V
+  // pair vp is consumed, and the next chunk's first K tiles and V scales
+  // two pairs before the chunk's last.
+#ifndef TQ_DECODE_LOOKAHEAD_MULTI
+#define TQ_DECODE_LOOKAHEAD_MULTI 4
+#endif
+  constexpr int LA = dmin(MULTI ? TQ_DECODE_LOOKAHEAD_MULTI : C::LOOKAHEAD, NKT);
+  constexpr int VP_NEXT = NVP >= 2 ? NVP - 2 : 0;
+  auto issue_first = [&](uint32_t tw0) {
 #pragma unroll
-  for (int grp = 0; grp < LA; grp++) issue(grp);
-  issue(NKT);
-  auto issue_k = [&](int i) {  // K tile i is being consumed
-    if (i + LA < NKT) issue(i + LA);
+    for (int grp = 0; grp < LA; grp++) issue(grp, tw0);
+    issue(NKT, tw0);
+  };
+  issue_first(tw_first);
+  auto issue_k = [&](int i, uint32_t tw0) {  // K tile i is being consumed
+    if (i + LA < NKT) issue(i + LA, tw0);
     if (i >= NKT - 2) {
       const int t = 2 * (i - (NKT - 2));
-      issue(NKT + 1 + t);
-      issue(NKT + 2 + t);
+      issue(NKT + 1 + t, tw0);
+      issue(NKT + 2 + t, tw0);
     }
   };
-  auto issue_v = [&](int vp) {  // V pair vp is being consumed
+  auto issue_v = [&](int vp, uint32_t tw0) {  // V pair vp is being consumed
     if (2 * vp + 4 < NKT) {
-      issue(NKT + 1 + 2 * vp + 4);
-      issue(NKT + 2 + 2 * vp + 4);
+      issue(NKT + 1 + 2 * vp + 4, tw0);
+      issue(NKT + 2 + 2 * vp + 4, tw0);
     }
   };
   // ---- pair table (the caller's device codebook, L2Norm tables from the
@@ -629,23 +652,11 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
     return val;
   };
-  u32x4 qa[QAR ? QG * KJA : 1];
-  if constexpr (QAR) {
-    // each operand is the same for every wave: the workgroup's lanes build
-    // them once, each wave then reads its registers
-    u32x4 *s_qas = reinterpret_cast<u32x4 *>(lds + C::OFF_QAS);
-    for (int e = tid; e < QG * KJA * 64; e += C::THREADS) {
-      const int sl = e >> 6, ln = e & 63;
-      s_qas[e] = GRID ? make_qa_grid(sl / KJA, sl % KJA, ln & 15, ln >> 4) : make_qa(sl / KJA, sl % KJA, ln & 15, ln >> 4);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < QG * KJA; k++) qa[k] = s_qas[k * 64 + lane];
-  } else {
-    for (int e = tid; e < QG * KJ * 64; e += C::THREADS) {
-      const int sl = e >> 6, ln = e & 63;
-      s_qa[e] = make_qa(sl / KJ, sl % KJ, ln & 15, ln >> 4);
-    }
+  // each operand is the same for every wave: the workgroup's lanes build
+  // them once
+  for (int e = tid; e < QG * KJA * 64; e += C::THREADS) {
+    const int sl = e >> 6, ln = e & 63;
+    s_qa[e] = GRID ? make_qa_grid(sl / KJA, sl % KJA, ln & 15, ln >> 4) : make_qa(sl / KJA, sl % KJA, ln & 15, ln >> 4);
   }
   // score rows of this lane's MFMA outputs: heads hl0 + u (u = 0, 1) of
   // qblock row qbl.  After the cross-qblock sum a lane keeps NS scores: both
@@ -705,11 +716,51 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // the query setup is dead from here: the staging area it lives in is the waves' own
   __syncthreads();
 
+  // ---- the range's chunks: per chunk a K pass, an online softmax step and a
+  // V pass whose value sums are folded into the wave's running sums ----
+  float *stage = lds + C::OFF_W + wave * C::WSTAGE;
+  float *st_p = stage;                 // [HG][TPW]
+  float *st_s = stage + C::WP;         // [NQB][TPW]
+  float *comb = stage + C::WC;         // [HG][HD] value sums over the chunks
+  float *cml = stage + C::WM;          // m[HG], l[HG], 2^Ev, the chunk's rescale [HG]
+  // 16-lane rows holding the same head: R replicas (QPM 4: the row groups
+  // lg and lg ^ 1; else one), replica ri stores every R-th tile's weights
+  constexpr int R = QPM == 4 ? 2 : 1;
+  const int ri = QPM == 4 ? (lg & 1) : 0;
+  // V pass weight operand of lane (n, kg), column n = (qblock qsp of the
+  // set, head hv, weight part): the weights of tokens 4 kg .. 4 kg + 3 of
+  // both tiles
+  const int qsp = l16 / (2 * HPM), hv = (l16 >> 1) % HPM, wpart = l16 & 1;
+  const float kpart = wpart ? -1.f : 0.f;
+  if constexpr (MULTI)
+    for (int e = lane; e < HG * HD / 4; e += 64) reinterpret_cast<float4 *>(comb)[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+  // online softmax state of the lane's head rows (base 2) and the wave's
+  // V-scale exponent
+  float mrun[NS], lrun[NS];
+#pragma unroll
+  for (int v = 0; v < NS; v++) {
+    mrun[v] = -INFINITY;
+    lrun[v] = 0.f;
+  }
+  int evrun = 0;
+  for (int ck = 0; ck < nck; ck++) {
+  const int tw = (ck0 + ck) * C::CHUNK + wave * TPW;
+  const uint32_t tw0 = (uint32_t)tw;
   // ---- K pass, tile by tile as the records arrive ----
+  // QA_REGS: the operands come into registers for the pass (a reload per
+  // chunk through an opaque lane offset, so they do not occupy registers
+  // through the V pass)
+  u32x4 qa[QAR ? QG * KJA : 1];
+  if constexpr (QAR) {
+    int qoff = lane;
+    if constexpr (MULTI) asm volatile("" : "+v"(qoff));
+#pragma unroll
+    for (int k = 0; k < QG * KJA; k++) qa[k] = s_qa[k * 64 + qoff];
+  }
   float sc[NKT][NS];
 #pragma unroll
   for (int i = 0; i < NKT; i++) {
-    issue_k(i);
+    issue_k(i, tw0);
     f32x4 dk[QG];
 #pragma unroll
     for (int qg = 0; qg < QG; qg++) {
@@ -791,33 +842,27 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
   }
 
-  // ---- softmax over the wave's tokens (base 2): per head row max and sum ----
-  float* stage = lds + C::OFF_W + wave * C::WSTAGE;
-  float *st_p = stage;                 // [HG][TPW]
-  float *st_s = stage + C::WP;         // [NQB][TPW]
-  float *comb = stage;                 // [HG][HD] after the V pass
-  float *cml = stage + C::WA;          // m[HG], l[HG], 2^Ev
-  float mrow[NS], lrow[NS];
-  // 16-lane rows holding the same head: R replicas (QPM 4: the row groups
-  // lg and lg ^ 1; else one), replica ri stores every R-th tile's weights
-  constexpr int R = QPM == 4 ? 2 : 1;
-  const int ri = QPM == 4 ? (lg & 1) : 0;
+  // ---- online softmax step (base 2): the running row max of each head
+  // moves to mn, the chunk's weights are 2^(s - mn) and the sums so far are
+  // rescaled by 2^(m_old - mn) ----
+  float alpha[NS];
 #pragma unroll
   for (int v = 0; v < NS; v++) {
-    float m = -INFINITY;
+    float mc = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NKT; i++) m = fmaxf(m, sc[i][v]);
-    m = row_max16(m);
+    for (int i = 0; i < NKT; i++) mc = fmaxf(mc, sc[i][v]);
+    const float mn = fmaxf(mrun[v], row_max16(mc));
     float l = 0.f;
     const int hl = hl0 + (NS == 2 ? v : uh);
 #pragma unroll
     for (int i = 0; i < NKT; i++) {
-      const float p = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[i][v] - m);
+      const float p = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[i][v] - mn);
       l += p;
       if (hl < HG && i % R == ri) st_p[hl * TPW + 16 * i + l16] = p;
     }
-    mrow[v] = m;
-    lrow[v] = row_sum16(l);
+    alpha[v] = mrun[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrun[v] - mn);
+    lrun[v] = __builtin_fmaf(lrun[v], alpha[v], row_sum16(l));
+    mrun[v] = mn;
   }
   // V scales (lane: tokens TPL lane + u) as |s| 2^-Ev, Ev from the wave's largest
   float svv[C::TPL][NQB];
@@ -830,32 +875,29 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       svv[u][qb] = fabsf(f16_to_f32((uint16_t)(bits & 0xffffu)));
       smax = fmaxf(smax, svv[u][qb]);
     }
-  const int ev = pow2_exponent(wave_max(smax));
+  // the running exponent Ev is the largest of the range's chunks so far; the
+  // sums so far are rescaled by 2^(Ev_old - Ev) with the softmax factor
+  const int evc = pow2_exponent(wave_max(smax));
+  const int ev = ck == 0 ? evc : max(evrun, evc);
+  const float beta = ck == 0 ? 0.f : exp2i(evrun - ev);
+  evrun = ev;
   const float vinv = exp2i(-ev);
 #pragma unroll
   for (int u = 0; u < C::TPL; u++)
 #pragma unroll
     for (int qb = 0; qb < NQB; qb++) st_s[qb * TPW + C::TPL * lane + u] = svv[u][qb] * vinv;
-  if (l16 == 0) {
+  if (MULTI && l16 == 0) {
 #pragma unroll
     for (int v = 0; v < NS; v++) {
       const int hl = hl0 + (NS == 2 ? v : uh);
-      if (hl < HG && ri == 0) {
-        cml[hl] = mrow[v];
-        cml[HG + hl] = lrow[v];
-      }
+      if (hl < HG && ri == 0) cml[2 * HG + 1 + hl] = alpha[v] * beta;
     }
-    if (lane == 0) cml[2 * HG] = exp2i(ev);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- V pass, tile pair by tile pair.  Weight operand of lane (n, kg),
-  // column n = (qblock qsp of the set, head hv, weight part): the weights of
-  // tokens 4 kg .. 4 kg + 3 of both tiles ----
-  const int qsp = l16 / (2 * HPM), hv = (l16 >> 1) % HPM, wpart = l16 & 1;
-  const float kpart = wpart ? -1.f : 0.f;
+  // ---- V pass, tile pair by tile pair ----
   f32x4 dv[QG][PPL];
 #pragma unroll
   for (int vs = 0; vs < QG; vs++)
@@ -863,7 +905,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     for (int j = 0; j < PPL; j++) dv[vs][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int vp = 0; vp < NVP; vp++) {
-    issue_v(vp);
+    issue_v(vp, tw0);
+    if (MULTI && vp == VP_NEXT && ck + 1 < nck) issue_first(tw0 + C::CHUNK);
     u32x4 bw[QG];
 #pragma unroll
     for (int vs = 0; vs < QG; vs++) {
@@ -899,10 +942,12 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   }
   // useful outputs: lane (n, lg) holds rows (row set lg: qblock lg / ES, pair
   // part lg % ES; parts hi c0, hi c1, lo c0, lo c1) under column n; the two
-  // weight parts of a head sit in lanes n, n ^ 1
+  // weight parts of a head sit in lanes n, n ^ 1.  They are added to the
+  // wave's sums, rescaled for this chunk's max and exponent.
   {
     const int oqb = lg / ES, ops = lg % ES;
     const bool keep = qsp == oqb && wpart == 0 && hv < nh;
+    const float rf = MULTI ? cml[2 * HG + 1 + dmin(hv, HG - 1)] : 0.f;
 #pragma unroll
     for (int vs = 0; vs < QG; vs++)
 #pragma unroll
@@ -914,10 +959,28 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
           o[cc] = dpp_quad_xor1(xx) + xx;
           asm volatile("" : "+v"(o[cc]));  // keeps the add beside its DPP read
         }
-        if (keep)
-          *reinterpret_cast<float2 *>(comb + hv * HD + (vs * QPM + oqb) * 32 + 2 * (ops * PPL + j)) =
-              make_float2(o[0], o[1]);
+        if (keep) {
+          float2 *dst = reinterpret_cast<float2 *>(comb + hv * HD + (vs * QPM + oqb) * 32 + 2 * (ops * PPL + j));
+          if constexpr (MULTI) {
+            const float2 old = *dst;
+            *dst = make_float2(__builtin_fmaf(old.x, rf, o[0]), __builtin_fmaf(old.y, rf, o[1]));
+          } else {
+            *dst = make_float2(o[0], o[1]);
+          }
+        }
       }
+  }
+  }  // chunks
+  if (l16 == 0) {
+#pragma unroll
+    for (int v = 0; v < NS; v++) {
+      const int hl = hl0 + (NS == 2 ? v : uh);
+      if (hl < HG && ri == 0) {
+        cml[hl] = mrun[v];
+        cml[HG + hl] = lrun[v];
+      }
+    }
+    if (lane == 0) cml[2 * HG] = exp2i(evrun);
   }
 
   // ---- combine the waves' records; the workgroup's partial goes out ----
@@ -929,7 +992,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     float mw[C::WAVES], M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < C::WAVES; w++) {
-      mw[w] = lds[C::OFF_W + w * C::WSTAGE + C::WA + hl];
+      mw[w] = lds[C::OFF_W + w * C::WSTAGE + C::WM + hl];
       M = fmaxf(M, mw[w]);
     }
     float A = 0.f, L = 0.f;
@@ -937,8 +1000,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     for (int w = 0; w < C::WAVES; w++) {
       const float *cw = lds + C::OFF_W + w * C::WSTAGE;
       const float f = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
-      A = __builtin_fmaf(cw[hl * HD + d], f * cw[C::WA + 2 * HG], A);
-      L = __builtin_fmaf(cw[C::WA + HG + hl], f, L);
+      A = __builtin_fmaf(cw[C::WC + hl * HD + d], f * cw[C::WM + 2 * HG], A);
+      L = __builtin_fmaf(cw[C::WM + HG + hl], f, L);
     }
     if (ws_ok) {
       const long long bh = hq0 + hl;
@@ -970,7 +1033,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   int *counter = a.cnt_top - (1 + b * a.num_kv_heads + g) * kCounterStride;
   if (tid == 0 && ws_ok) {
     const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_flag = (prev == nchunks * a.ngroups - 1);
+    s_flag = (prev == nparts * a.ngroups - 1);
   }
   __syncthreads();
   if (!ws_ok) {
@@ -981,7 +1044,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
   } else if (s_flag) {
     if constexpr (INLINE_MERGE) {
-      merge_heads<HD, C::WAVES>(a, b, g, nchunks);
+      merge_heads<HD, C::WAVES>(a, b, g, nparts);
       if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
