@@ -509,15 +509,26 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
 #ifndef TQ_DECODE_LOOKAHEAD_MULTI
 #define TQ_DECODE_LOOKAHEAD_MULTI 4
 #endif
-  constexpr int LA = dmin(MULTI ? TQ_DECODE_LOOKAHEAD_MULTI : C::LOOKAHEAD, NKT);
+#ifndef TQ_DECODE_LOOKAHEAD_PASS
+#define TQ_DECODE_LOOKAHEAD_PASS TQ_DECODE_LOOKAHEAD
+#endif
+  // LA0 K tiles go out with the first chunk's prologue (more would hold the
+  // waves at issue before their setup), LA during the K passes
+  constexpr int LA = dmin(MULTI ? TQ_DECODE_LOOKAHEAD_MULTI : TQ_DECODE_LOOKAHEAD_PASS, NKT);
+  constexpr int LA0 = MULTI ? LA : dmin(C::LOOKAHEAD, LA);
   constexpr int VP_NEXT = NVP >= 2 ? NVP - 2 : 0;
-  auto issue_first = [&](uint32_t tw0) {
+  auto issue_first = [&](uint32_t tw0, int n) {
 #pragma unroll
-    for (int grp = 0; grp < LA; grp++) issue(grp, tw0);
+    for (int grp = 0; grp < NKT; grp++)
+      if (grp < n) issue(grp, tw0);
     issue(NKT, tw0);
   };
-  issue_first(tw_first);
+  issue_first(tw_first, LA0);
   auto issue_k = [&](int i, uint32_t tw0) {  // K tile i is being consumed
+    if (i == 0) {
+#pragma unroll
+      for (int t = LA0; t < LA; t++) issue(t, tw0);
+    }
     if (i + LA < NKT) issue(i + LA, tw0);
     if (i >= NKT - 2) {
       const int t = 2 * (i - (NKT - 2));
@@ -906,7 +917,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
 #pragma unroll
   for (int vp = 0; vp < NVP; vp++) {
     issue_v(vp, tw0);
-    if (MULTI && vp == VP_NEXT && ck + 1 < nck) issue_first(tw0 + C::CHUNK);
+    if (MULTI && vp == VP_NEXT && ck + 1 < nck) issue_first(tw0 + C::CHUNK, LA);
     u32x4 bw[QG];
 #pragma unroll
     for (int vs = 0; vs < QG; vs++) {

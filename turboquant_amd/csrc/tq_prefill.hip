@@ -103,8 +103,18 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   float mone = -1.f;
   asm volatile("" : "+v"(mone));
   const int l16 = lane & 15, lg = lane >> 4;
-  const int g = blockIdx.y;
-  const int i0 = blockIdx.x * QB;
+  // Workgroups start in the order of their linear index.  Causal blocks'
+  // work grows with the query block, so the linear index is mapped to the
+  // longest blocks first (every KV head's last query block, then the blocks
+  // before it): the short blocks fill in at the end instead of the long ones
+  // starting last.
+  int g = blockIdx.y, qblk = blockIdx.x;
+  if (a.causal) {
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+    g = lin % gridDim.y;
+    qblk = (int)gridDim.x - 1 - lin / (int)gridDim.y;
+  }
+  const int i0 = qblk * QB;
   const long long rec0 = (long long)g * a.kv_head_stride;
   const float lscale = a.softmax_scale * kLog2e;
 
