@@ -18,7 +18,11 @@
 // wave's tokens: no running rescale), and each V tile pair is accumulated as
 // it arrives, overlapping the values' transfer.  What remains after the last
 // byte is one tile pair's value products, the waves' combine and the split-K
-// arrival.
+// arrival.  When the launch has more chunks than one round of workgroups
+// holds, a workgroup takes a range of consecutive chunks instead: the
+// per-chunk step above repeats, the softmax state and the value sums are
+// carried across chunks with an online rescale, and the next chunk's first K
+// tiles are requested during the current chunk's last value tiles.
 //
 // Arithmetic (the same decomposition as the reference's per-qblock dequant,
 // tq_attention_kernel.cu:33-53, k_j = |s| inv (H (cb[idx] d))_j): keys are
@@ -352,7 +356,22 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the wave's scalar offsets
   const int l16 = lane & 15, lg = lane >> 4;
-  const int c = blockIdx.x, b = blockIdx.z;
+  // (range c, head group y, sequence b).  Ranges: workgroups start in the
+  // order of their linear index, so it is mapped range-major (range 0 of
+  // every (sequence, head group) first): the ranges that the batch's lengths
+  // leave empty come last instead of holding slots among the others (an
+  // empty workgroup still waits for its first loads, queued behind the
+  // records in flight), and consecutive workgroups, which go to different
+  // XCDs, take different (sequence, KV head) pairs.
+  int c = blockIdx.x, y = blockIdx.y, b = blockIdx.z;
+  if constexpr (MULTI) {
+    const int per = (int)(gridDim.y * gridDim.z);
+    const int lin = blockIdx.x + (int)gridDim.x * (blockIdx.y + (int)gridDim.y * blockIdx.z);
+    c = lin / per;
+    const int rest = lin - c * per;
+    b = rest / (int)gridDim.y;
+    y = rest - b * (int)gridDim.y;
+  }
   // The argument fields that the first loads depend on, all requested
   // before one wait (the empty asm makes them available together; left to
   // itself the compiler requests each behind the branch that uses it, and
@@ -365,7 +384,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   const int a_cpr = a.cpr;
   asm volatile("" ::"s"(a_q), "s"(a_sg), "s"(a_cb), "s"(a_rq), "s"(a_ws), "s"(a_lens), "s"(a_qdt), "s"(a_ngroups),
                "s"(a_nr), "s"(a_heads), "s"(a_max), "s"(a_cpr));
-  const int g = blockIdx.y / a_ngroups, gh = blockIdx.y - g * a_ngroups;
+  const int g = y / a_ngroups, gh = y - g * a_ngroups;
   const int nh = min(HG, a_nr - gh * HG);                    // heads of this group
   const long long hq0 = (long long)b * a_heads + (long long)g * a_nr + gh * HG;  // its first q head
 
@@ -417,7 +436,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // softmax state over the range's chunks, so the setup, the combine and the
   // split-K arrival are paid once per range.
   const int nchunks = (len + C::CHUNK - 1) / C::CHUNK;
-  const int ck0 = c * a_cpr;
+  const int cpr = a_cpr;
+  const int ck0 = c * cpr;
   if (ck0 >= nchunks) {  // an empty range is not counted by the merge
     if (len == 0 && c == 0) {
       // an empty sequence attends to nothing: zero output (cuda/attention.rs:65-68)
@@ -430,8 +450,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     __builtin_amdgcn_s_waitcnt(0);
     return;
   }
-  const int nck = MULTI ? min(a_cpr, nchunks - ck0) : 1;  // chunks of this range
-  const int nparts = (nchunks + a_cpr - 1) / a_cpr;    // ranges the merge folds
+  const int nck = MULTI ? min(cpr, nchunks - ck0) : 1;  // chunks of this range
+  const int nparts = (nchunks + cpr - 1) / cpr;       // ranges the merge folds
 
   // ---- records.  Wave w's tokens of a chunk start at tw = chunk CHUNK +
   // w TPW.  K tile i, lane (l16, lg): token tw + 16 i + l16, for
