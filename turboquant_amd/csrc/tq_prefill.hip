@@ -45,6 +45,24 @@ constexpr int kKStride = 66;  // uint2 per token row of the K tile (64 pairs + p
 constexpr int kVRow = 144;    // halves per token row of the V tiles (128 elements + pad: the
                               // transposing reads of 4 tokens x 4 element quads hit 32 distinct banks)
 
+// The K tile row's 16-byte chunk c (4 elements, hi and lo) sits at chunk
+// c ^ 2 ((c >> 3) & 3): the four lanes of a token, one per qblock (chunks 8
+// apart), write four distinct bank groups instead of one, and the S^T reads
+// (one chunk of 8 consecutive tokens, rows 33 chunks apart) stay distinct.
+__device__ __forceinline__ int kchunk(int c) { return c ^ (2 * ((c >> 3) & 3)); }
+// The V rows' 16-byte chunk c (8 elements of one plane) sits at chunk
+// c ^ ((c >> 3) & 1): rows are 18 chunks apart, and the 16-byte stores of
+// tokens t, t + 1 (qblocks 0-3 each: chunks 0, 4, 8, 12 from the row start)
+// then reach 8 distinct bank groups instead of 4; a transposing read (8
+// bytes of one chunk per lane, 4 rows x 2 chunks per 16 lanes) stays
+// distinct.
+__device__ __forceinline__ int vchunk(int c) { return c ^ ((c >> 3) & 1); }
+// Row strides of the staged query halves and the output floats, padded so
+// that consecutive rows start 4 banks apart (the per-row accesses of 16 rows
+// would otherwise all start in one bank)
+constexpr int kQRow = 128 + 8;  // halves
+constexpr int kORow = 128 + 4;  // floats
+
 enum PMode : int { kPPqo = 0, kPPq = 1, kPTq = 2 };
 constexpr int kPrefillModeTq = kPTq;
 
@@ -137,8 +155,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const int prow = tid >> 2, pq = tid & 3;
   const int qi = i0 + prow / NR, qh = g * NR + prow % NR;
   const bool row_ok = qi < a.q_len;
-  _Float16 *s_qh = reinterpret_cast<_Float16 *>(s_tile);  // [row][128] hi
-  _Float16 *s_ql = s_qh + kRows * HD;                 // [row][128] lo
+  _Float16 *s_qh = reinterpret_cast<_Float16 *>(s_tile);  // [row][kQRow] hi
+  _Float16 *s_ql = s_qh + kRows * kQRow;              // [row][kQRow] lo
   {
     float x[32];
     const long long base = ((long long)qh * a.q_len + (row_ok ? qi : 0)) * HD + 32 * pq;
@@ -164,13 +182,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     for (int j = 0; j < 32; j++) {
       const float v = row_ok ? x[j] * sc : 0.f;
       const float h = split_hi(v);
-      s_qh[prow * HD + 32 * pq + j] = (_Float16)h;
-      s_ql[prow * HD + 32 * pq + j] = (_Float16)(v - h);
+      s_qh[prow * kQRow + 32 * pq + j] = (_Float16)h;
+      s_ql[prow * kQRow + 32 * pq + j] = (_Float16)(v - h);
     }
   }
   // TQ: rq rows the same way (no rotation), into the K tile region
-  _Float16 *s_rh = reinterpret_cast<_Float16 *>(s_tile + kRows * HD);
-  _Float16 *s_rl = s_rh + kRows * HD;
+  _Float16 *s_rh = reinterpret_cast<_Float16 *>(s_tile + kRows * kQRow);
+  _Float16 *s_rl = s_rh + kRows * kQRow;
   if constexpr (QJL) {
     float x[32];
     const long long base = ((long long)qh * a.q_len + (row_ok ? qi : 0)) * HD + 32 * pq;
@@ -189,8 +207,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     for (int j = 0; j < 32; j++) {
       const float v = row_ok ? x[j] * sc : 0.f;
       const float h = split_hi(v);
-      s_rh[prow * HD + 32 * pq + j] = (_Float16)h;
-      s_rl[prow * HD + 32 * pq + j] = (_Float16)(v - h);
+      s_rh[prow * kQRow + 32 * pq + j] = (_Float16)h;
+      s_rl[prow * kQRow + 32 * pq + j] = (_Float16)(v - h);
     }
   }
   __syncthreads();
@@ -200,7 +218,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   u32x4 qop[8][2];
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    const int e = myrow * HD + 16 * j + 4 * lg;
+    const int e = myrow * kQRow + 16 * j + 4 * lg;
     const uint2 h = *reinterpret_cast<const uint2 *>(s_qh + e);
     const uint2 l = *reinterpret_cast<const uint2 *>(s_ql + e);
     qop[j][0] = u32x4{h.x, h.x, h.y, h.y};
@@ -210,7 +228,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   if constexpr (QJL) {
 #pragma unroll
     for (int sl = 0; sl < 4; sl++) {
-      const int e = myrow * HD + 32 * sl + 8 * lg;
+      const int e = myrow * kQRow + 32 * sl + 8 * lg;
       const uint4 h = *reinterpret_cast<const uint4 *>(s_rh + e);
       const uint4 l = *reinterpret_cast<const uint4 *>(s_rl + e);
       rop[sl][0] = u32x4{h.x, h.y, h.z, h.w};
@@ -262,8 +280,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   _Float16 *vth = reinterpret_cast<_Float16 *>(s_v);
   _Float16 *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
-  static_assert((QJL ? 2 : 1) * kRows * HD <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
-  static_assert(kRows * HD + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
+  static_assert((QJL ? 2 : 1) * kRows * kQRow <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
+  static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
 
   for (int tile = 0; tile < ntiles; tile++) {
     const int t0 = tile * kTile;
@@ -297,7 +315,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
           const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * kf;
           const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * kf;
           const uint32_t hi = pack_f16(x0, x1);
-          kt[ftok * kKStride + 16 * fqb + p] = make_uint2(hi, pack_rem(x0, x1, hi, mone));
+          kt[ftok * kKStride + 2 * kchunk(8 * fqb + (p >> 1)) + (p & 1)] = make_uint2(hi, pack_rem(x0, x1, hi, mone));
         }
         uint32_t hw[NP], lw[NP];
 #pragma unroll
@@ -309,12 +327,12 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
           lw[pp] = pack_rem(x0, x1, hw[pp], mone);
         }
         // token-major rows: this thread's 2 NP elements, 16-byte stores per plane
-        uint4 *vrh = reinterpret_cast<uint4 *>(vth + ftok * kVRow + 32 * fqb + 2 * P0);
-        uint4 *vrl = reinterpret_cast<uint4 *>(vtl + ftok * kVRow + 32 * fqb + 2 * P0);
+        _Float16 *vrh = vth + ftok * kVRow, *vrl = vtl + ftok * kVRow;
 #pragma unroll
         for (int i = 0; i < NP / 4; i++) {
-          vrh[i] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
-          vrl[i] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
+          const int c = 8 * vchunk(4 * fqb + P0 / 4 + i);
+          *reinterpret_cast<uint4 *>(vrh + c) = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
+          *reinterpret_cast<uint4 *>(vrl + c) = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
         }
       };
       if constexpr (SPLIT == 1) {
@@ -335,7 +353,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       const uint2 *krow = kt + (16 * tb + l16) * kKStride;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const uint4 kk = *reinterpret_cast<const uint4 *>(krow + 8 * j + 2 * lg);
+        const uint4 kk = *reinterpret_cast<const uint4 *>(krow + 2 * kchunk(4 * j + lg));
         const u32x4 ka = {kk.x, kk.y, kk.z, kk.w};
         d = mfma(ka, qop[j][0], d);
         d = mfma(ka, qop[j][1], d);
@@ -405,7 +423,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       f32x4 acc = o[eb] * rescale;
 #pragma unroll
       for (int tp = 0; tp < 2; tp++) {
-        const int r0 = (32 * tp + vrow) * kVRow + 16 * eb + vcol, r1 = r0 + 16 * kVRow;
+        const int r0 = (32 * tp + vrow) * kVRow + 8 * vchunk(2 * eb + (vcol >> 3)) + (vcol & 7),
+                  r1 = r0 + 16 * kVRow;
         const u32x2 h0 = lds_read_tr16(vth + r0), h1 = lds_read_tr16(vth + r1);
         const u32x2 q0 = lds_read_tr16(vtl + r0), q1 = lds_read_tr16(vtl + r1);
         const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {q0[0], q0[1], q1[0], q1[1]};
@@ -424,19 +443,19 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   float L = l_run;
   L += __shfl_xor(L, 16, 64);
   L += __shfl_xor(L, 32, 64);
-  float *s_o = reinterpret_cast<float *>(s_tile);  // [row][128] (rotated, in units of 2^ev_cur)
+  float *s_o = reinterpret_cast<float *>(s_tile);  // [row][kORow] (rotated, in units of 2^ev_cur)
   const float ofac = exp2i(max(min(ev_cur, 126), -126));
 #pragma unroll
   for (int eb = 0; eb < 8; eb++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) s_o[myrow * HD + 16 * eb + 4 * lg + i] = o[eb][i] * ofac;
-  float *s_rowl = s_o + kRows * HD;  // [rows] (the tiles are done)
+    for (int i = 0; i < 4; i++) s_o[myrow * kORow + 16 * eb + 4 * lg + i] = o[eb][i] * ofac;
+  float *s_rowl = s_o + kRows * kORow;  // [rows] (the tiles are done)
   if (lg == 0) s_rowl[myrow] = L;
   __syncthreads();
   {
     float v[32];
 #pragma unroll
-    for (int j = 0; j < 32; j++) v[j] = s_o[prow * HD + 32 * pq + j] * decode_sign(j);
+    for (int j = 0; j < 32; j++) v[j] = s_o[prow * kORow + 32 * pq + j] * decode_sign(j);
     butterfly<32>(v);
     const float Lr = s_rowl[prow];
     if (row_ok) {
