@@ -160,11 +160,24 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   {
     float x[32];
     const long long base = ((long long)qh * a.q_len + (row_ok ? qi : 0)) * HD + 32 * pq;
+    // one dtype branch around all 32 loads (a branch per element keeps each
+    // load behind its own test and wait)
+    if (a.q_dtype == kF32) {
+      const float *src = static_cast<const float *>(a.q) + base;
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-      if (a.q_dtype == kF32) x[j] = static_cast<const float *>(a.q)[base + j];
-      else if (a.q_dtype == kBF16) x[j] = bf16_to_f32(static_cast<const uint16_t *>(a.q)[base + j]);
-      else x[j] = f16_to_f32(static_cast<const uint16_t *>(a.q)[base + j]);
+      for (int j = 0; j < 32; j++) x[j] = src[j];
+    } else {
+      const uint16_t *src = static_cast<const uint16_t *>(a.q) + base;
+      uint16_t hb[32];
+#pragma unroll
+      for (int j = 0; j < 32; j++) hb[j] = src[j];
+      if (a.q_dtype == kBF16) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) x[j] = bf16_to_f32(hb[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) x[j] = f16_to_f32(hb[j]);
+      }
     }
     butterfly<32>(x);
     float m = 0.f;
@@ -461,11 +474,16 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     if (row_ok) {
       const long long ob = ((long long)qh * a.q_len + qi) * HD + 32 * pq;
 #pragma unroll
-      for (int j = 0; j < 32; j++) {
-        const float res = Lr > 0.f ? v[j] * kInvSqrt32 / Lr : 0.f;
-        if (a.out_dtype == kF32) static_cast<float *>(a.out)[ob + j] = res;
-        else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[ob + j] = f32_to_bf16(res);
-        else static_cast<uint16_t *>(a.out)[ob + j] = f32_to_f16(res);
+      for (int j = 0; j < 32; j++) v[j] = Lr > 0.f ? v[j] * kInvSqrt32 / Lr : 0.f;
+      if (a.out_dtype == kF32) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) static_cast<float *>(a.out)[ob + j] = v[j];
+      } else if (a.out_dtype == kBF16) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) static_cast<uint16_t *>(a.out)[ob + j] = f32_to_bf16(v[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) static_cast<uint16_t *>(a.out)[ob + j] = f32_to_f16(v[j]);
       }
     }
   }
