@@ -228,14 +228,16 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 
   // ---- per-wave operands for its 16 rows (lane column = row 16 wave + l16) ----
   const int myrow = 16 * wave + l16;
-  u32x4 qop[8][2];
+  // per 32-element slice s, lane (row, lg) holds elements 32 s + 8 lg .. + 7
+  // of its row, hi and lo
+  u32x4 qop[4][2];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int e = myrow * kQRow + 16 * j + 4 * lg;
-    const uint2 h = *reinterpret_cast<const uint2 *>(s_qh + e);
-    const uint2 l = *reinterpret_cast<const uint2 *>(s_ql + e);
-    qop[j][0] = u32x4{h.x, h.x, h.y, h.y};
-    qop[j][1] = u32x4{l.x, l.x, l.y, l.y};
+  for (int s = 0; s < 4; s++) {
+    const int e = myrow * kQRow + 32 * s + 8 * lg;
+    const uint4 h = *reinterpret_cast<const uint4 *>(s_qh + e);
+    const uint4 l = *reinterpret_cast<const uint4 *>(s_ql + e);
+    qop[s][0] = u32x4{h.x, h.y, h.z, h.w};
+    qop[s][1] = u32x4{l.x, l.y, l.z, l.w};
   }
   u32x4 rop[4][2];
   if constexpr (QJL) {
@@ -321,16 +323,24 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       // every pair index folds to a constant)
       auto decode_pairs = [&](auto p0c) {
         constexpr int P0 = decltype(p0c)::value;
+        uint32_t hw[NP], lw[NP];
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
-          const int p = P0 + pp;
-          const uint32_t code = pair_code<BITS>(kw, p);
+          const uint32_t code = pair_code<BITS>(kw, P0 + pp);
           const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * kf;
           const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * kf;
-          const uint32_t hi = pack_f16(x0, x1);
-          kt[ftok * kKStride + 2 * kchunk(8 * fqb + (p >> 1)) + (p & 1)] = make_uint2(hi, pack_rem(x0, x1, hi, mone));
+          hw[pp] = pack_f16(x0, x1);
+          lw[pp] = pack_rem(x0, x1, hw[pp], mone);
         }
-        uint32_t hw[NP], lw[NP];
+        // 8-element groups of qblock fqb: chunk 8 fqb + 2 g holds the hi
+        // halves, the next chunk the lo halves
+        uint4 *krow = reinterpret_cast<uint4 *>(kt + ftok * kKStride);
+#pragma unroll
+        for (int i = 0; i < NP / 4; i++) {
+          const int c = 8 * fqb + 2 * (P0 / 4 + i);
+          krow[kchunk(c)] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
+          krow[kchunk(c + 1)] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
+        }
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
           const uint32_t code = pair_code<BITS>(vw, P0 + pp);
@@ -363,13 +373,14 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) {
       f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-      const uint2 *krow = kt + (16 * tb + l16) * kKStride;
+      const uint4 *krow = reinterpret_cast<const uint4 *>(kt + (16 * tb + l16) * kKStride);
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const uint4 kk = *reinterpret_cast<const uint4 *>(krow + 2 * kchunk(4 * j + lg));
-        const u32x4 ka = {kk.x, kk.y, kk.z, kk.w};
-        d = mfma(ka, qop[j][0], d);
-        d = mfma(ka, qop[j][1], d);
+      for (int s = 0; s < 4; s++) {
+        const uint4 kh = krow[kchunk(8 * s + 2 * lg)], kl = krow[kchunk(8 * s + 2 * lg + 1)];
+        const u32x4 ah = {kh.x, kh.y, kh.z, kh.w}, al = {kl.x, kl.y, kl.z, kl.w};
+        d = mfma(ah, qop[s][0], d);
+        d = mfma(ah, qop[s][1], d);
+        d = mfma(al, qop[s][0], d);
       }
       f32x4 dc = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (QJL) {
