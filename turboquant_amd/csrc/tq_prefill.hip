@@ -8,15 +8,15 @@
 // t <= kv_len - q_len + i when causal), corr the QJL correction of a TQ
 // cache (tq.rs:185-253).
 //
-// One workgroup (4 waves) serves 64 rows = (query, head) pairs of one KV
-// head, query-major, so the NR query heads of a KV head share every decoded
-// tile.  Per 64-token tile the workgroup decodes K and V (token-major,
-// per-token exponents folded out) into LDS as two-part f16 values (hi = 11
-// significant bits, lo = the remainder), then each wave
-// (16 rows) runs
-//   S^T = K Q^T          16x16x32 MFMAs, K's hi/lo along k against a
-//                        duplicated query value, query hi and lo as two
-//                        operands (22-bit products, f32 accumulation)
+// One workgroup serves 128 rows = (query, head) pairs of one KV head (8
+// waves; 64 rows and 4 waves for a TQ cache), query-major, so the NR query
+// heads of a KV head share every decoded tile.  Per 64-token tile the
+// workgroup decodes K and V (token-major, per-token exponents folded out)
+// into LDS as two-part f16 values (hi = 11 significant bits, lo = the
+// remainder), then each wave (16 rows) runs
+//   S^T = K Q^T          16x16x32 MFMAs per 32-element slice: K hi x Q hi,
+//                        K hi x Q lo, K lo x Q hi (22-bit products, lo x lo
+//                        dropped, f32 accumulation)
 //   corr^T = Sg RQ^T     TQ: the keys' +-1 sign bits against rq hi/lo
 //   O^T += V^T P^T       16x16x32 MFMAs over two 16-token blocks whose B
 //                        operand is S^T's accumulator layout (4 tokens per
@@ -41,14 +41,15 @@ using namespace tqm;
 // the TQ mode, whose wave needs 256 registers, keeps 64 (4 waves)
 constexpr int prefill_rows(int mode) { return mode == 2 ? 64 : 128; }
 constexpr int kTile = 64;   // tokens per tile
-constexpr int kKStride = 66;  // uint2 per token row of the K tile (64 pairs + pad)
+constexpr int kKStride = 66;  // uint2 per token row of the K tile (32 chunks of 16 bytes + pad)
 constexpr int kVRow = 144;    // halves per token row of the V tiles (128 elements + pad: the
                               // transposing reads of 4 tokens x 4 element quads hit 32 distinct banks)
 
-// The K tile row's 16-byte chunk c (4 elements, hi and lo) sits at chunk
-// c ^ 2 ((c >> 3) & 3): the four lanes of a token, one per qblock (chunks 8
-// apart), write four distinct bank groups instead of one, and the S^T reads
-// (one chunk of 8 consecutive tokens, rows 33 chunks apart) stay distinct.
+// A K tile row holds, per 8-element group g, a 16-byte chunk of hi halves
+// (2 g) and one of lo halves (2 g + 1).  Chunk c sits at c ^ 2 ((c >> 3) & 3):
+// the four lanes of a token, one per qblock (chunks 8 apart), write four
+// distinct bank groups instead of one, and the S^T reads (one chunk of 8
+// consecutive tokens, rows 33 chunks apart) stay distinct.
 __device__ __forceinline__ int kchunk(int c) { return c ^ (2 * ((c >> 3) & 3)); }
 // The V rows' 16-byte chunk c (8 elements of one plane) sits at chunk
 // c ^ ((c >> 3) & 1): rows are 18 chunks apart, and the 16-byte stores of
