@@ -107,9 +107,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // them the output rows
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[K_WORDS + V_WORDS];
   uint32_t *s_k = s_tile, *s_v = s_tile + K_WORDS;
-  __shared__ float s_ek[kTile];       // 2^E_k per token (key exponent folded out)
-  __shared__ int s_ev[kTile];         // V exponent per token
-  __shared__ int s_evw[NW];           // max V exponent over each wave's 16 tokens
+  // per-token and per-wave scalars, read 4 at a time
+  __shared__ __attribute__((aligned(16))) float s_ek[kTile];  // 2^E_k per token (key exponent folded out)
+  __shared__ __attribute__((aligned(16))) int s_ev[kTile];    // V exponent per token
+  __shared__ __attribute__((aligned(16))) int s_evw[NW];      // max V exponent over each wave's 16 tokens
   __shared__ float s_cn[kTile];       // TQ: |r_t| * qjl_c
   __shared__ __attribute__((aligned(16))) uint32_t s_sg[kTile * 4];  // TQ: sign words
   __shared__ float s_cb[16];
@@ -416,9 +417,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     const float m_new = fmaxf(m_run, mt);
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
     // V exponent of the tile (each wave reads all 64)
-    int evt = s_evw[0];
+    static_assert(NW % 4 == 0, "the wave maxima are read 4 at a time");
+    int evt = -1000;
 #pragma unroll
-    for (int w = 1; w < NW; w++) evt = max(evt, s_evw[w]);
+    for (int w = 0; w < NW; w += 4) {
+      const int4 e4 = *reinterpret_cast<const int4 *>(s_evw + w);
+      evt = max(max(evt, max(e4.x, e4.y)), max(e4.z, e4.w));
+    }
     const int ev_new = max(ev_cur, evt);
     const float rescale = alpha * exp2i(max(ev_cur - ev_new, -126));
     ev_cur = ev_new;
@@ -427,12 +432,14 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     u32x2 pb[4][2];
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) {
+      const int4 e4 = *reinterpret_cast<const int4 *>(s_ev + 16 * tb + 4 * lg);
+      const int evk[4] = {e4.x, e4.y, e4.z, e4.w};
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const float e = (x[tb][i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[tb][i] - m_new);
         ls += e;
-        p[i] = e * exp2i(max(s_ev[16 * tb + 4 * lg + i] - ev_new, -126));
+        p[i] = e * exp2i(max(evk[i] - ev_new, -126));
       }
       pb[tb][0] = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
       pb[tb][1] = u32x2{pack_rem(p[0], p[1], pb[tb][0][0], mone), pack_rem(p[2], p[3], pb[tb][0][1], mone)};
