@@ -105,14 +105,16 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   constexpr int V_WORDS = V_HALVES;  // hi and lo planes, 2 halves per word each
   // K tile | V tiles; before the tiles the split query (and rq) rows, after
   // them the output rows
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[K_WORDS + V_WORDS];
-  uint32_t *s_k = s_tile, *s_v = s_tile + K_WORDS;
+  // two tile buffers: tile t + 1 is decoded into one while tile t is read
+  // from the other
+  constexpr int TILE_WORDS = K_WORDS + V_WORDS;
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[2 * TILE_WORDS];
   // per-token and per-wave scalars, read 4 at a time
-  __shared__ __attribute__((aligned(16))) float s_ek[kTile];  // 2^E_k per token (key exponent folded out)
-  __shared__ __attribute__((aligned(16))) int s_ev[kTile];    // V exponent per token
-  __shared__ __attribute__((aligned(16))) int s_evw[NW];      // max V exponent over each wave's 16 tokens
-  __shared__ float s_cn[kTile];       // TQ: |r_t| * qjl_c
-  __shared__ __attribute__((aligned(16))) uint32_t s_sg[kTile * 4];  // TQ: sign words
+  __shared__ __attribute__((aligned(16))) float s_ek[2][kTile];  // 2^E_k per token (key exponent folded out)
+  __shared__ __attribute__((aligned(16))) int s_ev[2][kTile];    // V exponent per token
+  __shared__ __attribute__((aligned(16))) int s_evw[2][NW];      // max V exponent over each wave's 16 tokens
+  __shared__ float s_cn[2][kTile];       // TQ: |r_t| * qjl_c
+  __shared__ __attribute__((aligned(16))) uint32_t s_sg[2][kTile * 4];  // TQ: sign words
   __shared__ float s_cb[16];
   __shared__ int s_eq[kRows], s_er[kRows];
   __shared__ uint2 s_nib[16];
@@ -293,16 +295,18 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
   for (int eb = 0; eb < 8; eb++) o[eb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  uint2 *kt = reinterpret_cast<uint2 *>(s_k);
-  _Float16 *vth = reinterpret_cast<_Float16 *>(s_v);
-  _Float16 *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
+  // buffer b: K tile at s_tile + b TILE_WORDS, V hi plane after it, lo plane
+  // after that
+  auto ktile = [&](int b) { return reinterpret_cast<uint2 *>(s_tile + b * TILE_WORDS); };
+  auto vhi = [&](int b) { return reinterpret_cast<_Float16 *>(s_tile + b * TILE_WORDS + K_WORDS); };
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
   static_assert((QJL ? 2 : 1) * kRows * kQRow <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
   static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
 
-  for (int tile = 0; tile < ntiles; tile++) {
-    const int t0 = tile * kTile;
-    // ---- decode this thread's record into the tiles ----
+  // ---- decode this thread's record into tile buffer b ----
+  auto decode_tile = [&](int b) {
+    uint2 *kt = ktile(b);
+    _Float16 *vth = vhi(b), *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
     {
       const float sk = fabsf(f16_to_f32(ks)), sv = fabsf(f16_to_f32(vs));
       float mk = fmaxf(sk, dpp_quad_xor1(sk));
@@ -312,15 +316,15 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       const int ek = pow2_exponent(mk), ev = pow2_exponent(mv);
       const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
       if (fqb == 0 && fpart == 0) {
-        s_ek[ftok] = exp2i(ek);
-        s_ev[ftok] = ev;
-        if constexpr (QJL) s_cn[ftok] = f16_to_f32(nm) * a.qjl_c;
+        s_ek[b][ftok] = exp2i(ek);
+        s_ev[b][ftok] = ev;
+        if constexpr (QJL) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
       }
       {
         const float wm = wave_max((float)ev);  // exact: |ev| <= 100
-        if (lane == 0) s_evw[wave] = (int)wm;
+        if (lane == 0) s_evw[b][wave] = (int)wm;
       }
-      if constexpr (QJL) s_sg[ftok * 4 + fqb] = sgw;
+      if constexpr (QJL) s_sg[b][ftok * 4 + fqb] = sgw;
       // this thread's code pairs P0 .. P0 + NP - 1 (a wave-uniform part, so
       // every pair index folds to a constant)
       auto decode_pairs = [&](auto p0c) {
@@ -367,8 +371,26 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         else decode_pairs(std::integral_constant<int, NP>{});
       }
     }
-    __syncthreads();
-    if (tile + 1 < ntiles) fetch(t0 + kTile);  // next tile's records arrive during the compute
+  };
+  if (ntiles > 0) {
+    decode_tile(0);
+    if (ntiles > 1) fetch(kTile);  // each tile's records arrive during the tile before
+  }
+  __syncthreads();
+  // One barrier per tile: tile + 1 is decoded into the other buffer in the
+  // same stretch as tile's products (the waves sharing a SIMD in opposite
+  // orders, so that one's decode overlaps the other's matrix products); the
+  // barrier then publishes tile + 1 and frees tile's buffer for tile + 2.
+  const bool decode_first = (wave >> 2) & 1;
+  for (int tile = 0; tile < ntiles; tile++) {
+    const int t0 = tile * kTile, cur = tile & 1;
+    const bool more = tile + 1 < ntiles;
+    if (decode_first && more) {
+      decode_tile(cur ^ 1);
+      if (tile + 2 < ntiles) fetch(t0 + 2 * kTile);
+    }
+    const uint2 *kt = ktile(cur);
+    const _Float16 *vth = vhi(cur), *vtl = vth + V_HALVES;
 
     // ---- S^T = K Q^T (+ corr), four 16-token blocks ----
     float x[4][4];
@@ -386,7 +408,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       }
       f32x4 dc = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (QJL) {
-        const uint32_t *sgrow = s_sg + (16 * tb + l16) * 4;
+        const uint32_t *sgrow = s_sg[cur] + (16 * tb + l16) * 4;
 #pragma unroll
         for (int sl = 0; sl < 4; sl++) {
           const uint32_t byte = (sgrow[sl] >> (8 * lg)) & 0xffu;
@@ -396,13 +418,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
           dc = mfma(sa, rop[sl][1], dc);
         }
       }
-      const float4 ekv = *reinterpret_cast<const float4 *>(s_ek + 16 * tb + 4 * lg);
+      const float4 ekv = *reinterpret_cast<const float4 *>(s_ek[cur] + 16 * tb + 4 * lg);
       const float ek4[4] = {ekv.x, ekv.y, ekv.z, ekv.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int tp = t0 + 16 * tb + 4 * lg + i;
         float v = d[i] * (ek4[i] * eq_scale);
-        if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[16 * tb + 4 * lg + i] * er_scale, v);
+        if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
         const bool ok = my_ok && tp < a.kv_len && (!a.causal || tp <= qpos);
         x[tb][i] = ok ? v : -INFINITY;
       }
@@ -421,7 +443,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     int evt = -1000;
 #pragma unroll
     for (int w = 0; w < NW; w += 4) {
-      const int4 e4 = *reinterpret_cast<const int4 *>(s_evw + w);
+      const int4 e4 = *reinterpret_cast<const int4 *>(s_evw[cur] + w);
       evt = max(max(evt, max(e4.x, e4.y)), max(e4.z, e4.w));
     }
     const int ev_new = max(ev_cur, evt);
@@ -432,7 +454,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     u32x2 pb[4][2];
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) {
-      const int4 e4 = *reinterpret_cast<const int4 *>(s_ev + 16 * tb + 4 * lg);
+      const int4 e4 = *reinterpret_cast<const int4 *>(s_ev[cur] + 16 * tb + 4 * lg);
       const int evk[4] = {e4.x, e4.y, e4.z, e4.w};
       float p[4];
 #pragma unroll
@@ -468,7 +490,11 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       }
       o[eb] = acc;
     }
-    __syncthreads();  // the next decode overwrites the tiles
+    if (!decode_first && more) {
+      decode_tile(cur ^ 1);
+      if (tile + 2 < ntiles) fetch(t0 + 2 * kTile);
+    }
+    __syncthreads();
   }
 
   // ---- finish: row sums, inverse rotation per 32-element block, store ----
