@@ -24,8 +24,9 @@
 //                        transposing LDS read, V hi/lo x P hi/lo (three
 //                        products, lo x lo dropped)
 // with an online base-2 softmax per row.  Values stay in the rotated
-// domain; each row is inverse-rotated once at the end.  The next tile's
-// records are fetched while the current one is computed.
+// domain; each row is inverse-rotated once at the end.  Two tile buffers:
+// tile t + 1 is decoded while tile t is computed (one barrier per tile), and
+// the records of tile t + 2 are fetched meanwhile.
 #include "tq_common.h"
 #include "tq_device.h"
 #include "tq_mfma.h"
