@@ -107,3 +107,31 @@ def test_pqo_cache_attend_prefill_full_layer(tq):
     ref = orc.attention_prefill(q, kd, vd, 1 / math.sqrt(D), True)
     err = np.abs(out[0].cpu().numpy() - ref).max()
     assert err <= TOL, err
+
+
+def test_prefill_bench_shape_sampled_rows(tq):
+    """The bench's prefill shape (16 q-heads over 8 KV heads, 4096 queries
+    over 4096 tokens, causal, PQO3, bf16 queries): every workgroup order and
+    tile buffer of the full launch runs; sampled query positions (first and
+    last query blocks, tile edges) are checked against the oracle.  A causal
+    query at position p sees tokens 0..p, which is the oracle's non-causal
+    single query over the first p + 1 records; K/V are the oracle's
+    dequantization of the GPU's own codes."""
+    h, hkv, t, bits = 16, 8, 4096, 3
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    x = torch.randn((2, hkv * t, D), generator=gen, device="cuda")
+    x[:, :, torch.tensor([3, 40, 77, 101], device="cuda")] *= 8.0
+    pk, sk = tq.pqo_quantize(x[0].to(torch.bfloat16), bits)
+    pv, sv = tq.pqo_quantize(x[1].to(torch.bfloat16), bits)
+    q = (torch.randn((h, t, D), generator=gen, device="cuda") / math.sqrt(D)).to(torch.bfloat16)
+    scale = 1 / math.sqrt(D)
+    out = tq.cache_prefill_attention(q, pk, sk, pv, sv, hkv, bits, t, t, scale, orc.OUTLIER_ALL, causal=True)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    kd = orc.pqo_dequantize(bits, pk.cpu().numpy(), sk.cpu().numpy().view(np.uint16), D).reshape(hkv, t, D)
+    vd = orc.pqo_dequantize(bits, pv.cpu().numpy(), sv.cpu().numpy().view(np.uint16), D).reshape(hkv, t, D)
+    qf = q.float().cpu().numpy()
+    for p in (0, 1, 63, 64, 1000, 2047, 2048 + 37, 4000, 4032, 4095):
+        ref = orc.attention_prefill(qf[:, p:p + 1], kd[:, :p + 1], vd[:, :p + 1], scale, False)
+        err = np.abs(out[:, p:p + 1] - ref).max()
+        assert err <= TOL, (p, err)
