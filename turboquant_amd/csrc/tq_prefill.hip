@@ -65,6 +65,26 @@ __device__ __forceinline__ int vchunk(int c) { return c ^ ((c >> 3) & 1); }
 constexpr int kQRow = 128 + 8;  // halves
 constexpr int kORow = 128 + 4;  // floats
 
+// Stores 32 values split into f16 hi (11 significant bits) and lo (the
+// exact remainder) at hi[0..31] and lo[0..31], 16 bytes per store.
+__device__ __forceinline__ void stage_split32(const float (&x)[32], _Float16 *hi, _Float16 *lo) {
+  uint32_t hw[16], lw[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    const float h0 = split_hi(x[2 * k]), h1 = split_hi(x[2 * k + 1]);
+    const _Float16 a0 = (_Float16)h0, a1 = (_Float16)h1;
+    const _Float16 b0 = (_Float16)(x[2 * k] - h0), b1 = (_Float16)(x[2 * k + 1] - h1);
+    hw[k] = (uint32_t)__builtin_bit_cast(uint16_t, a0) | ((uint32_t)__builtin_bit_cast(uint16_t, a1) << 16);
+    lw[k] = (uint32_t)__builtin_bit_cast(uint16_t, b0) | ((uint32_t)__builtin_bit_cast(uint16_t, b1) << 16);
+  }
+  uint4 *dh = reinterpret_cast<uint4 *>(hi), *dl = reinterpret_cast<uint4 *>(lo);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    dh[k] = make_uint4(hw[4 * k], hw[4 * k + 1], hw[4 * k + 2], hw[4 * k + 3]);
+    dl[k] = make_uint4(lw[4 * k], lw[4 * k + 1], lw[4 * k + 2], lw[4 * k + 3]);
+  }
+}
+
 enum PMode : int { kPPqo = 0, kPPq = 1, kPTq = 2 };
 constexpr int kPrefillModeTq = kPTq;
 
@@ -197,12 +217,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     const float sc = exp2i(-eq);
     if (pq == 0) s_eq[prow] = eq;
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-      const float v = row_ok ? x[j] * sc : 0.f;
-      const float h = split_hi(v);
-      s_qh[prow * kQRow + 32 * pq + j] = (_Float16)h;
-      s_ql[prow * kQRow + 32 * pq + j] = (_Float16)(v - h);
-    }
+    for (int j = 0; j < 32; j++) x[j] = row_ok ? x[j] * sc : 0.f;
+    stage_split32(x, s_qh + prow * kQRow + 32 * pq, s_ql + prow * kQRow + 32 * pq);
   }
   // TQ: rq rows the same way (no rotation), into the K tile region
   _Float16 *s_rh = reinterpret_cast<_Float16 *>(s_tile + kRows * kQRow);
@@ -222,12 +238,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     const float sc = exp2i(-er);
     if (pq == 0) s_er[prow] = er;
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-      const float v = row_ok ? x[j] * sc : 0.f;
-      const float h = split_hi(v);
-      s_rh[prow * kQRow + 32 * pq + j] = (_Float16)h;
-      s_rl[prow * kQRow + 32 * pq + j] = (_Float16)(v - h);
-    }
+    for (int j = 0; j < 32; j++) x[j] = row_ok ? x[j] * sc : 0.f;
+    stage_split32(x, s_rh + prow * kQRow + 32 * pq, s_rl + prow * kQRow + 32 * pq);
   }
   __syncthreads();
 
@@ -506,15 +518,21 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const float ofac = exp2i(max(min(ev_cur, 126), -126));
 #pragma unroll
   for (int eb = 0; eb < 8; eb++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) s_o[myrow * kORow + 16 * eb + 4 * lg + i] = o[eb][i] * ofac;
+    *reinterpret_cast<float4 *>(s_o + myrow * kORow + 16 * eb + 4 * lg) =
+        make_float4(o[eb][0] * ofac, o[eb][1] * ofac, o[eb][2] * ofac, o[eb][3] * ofac);
   float *s_rowl = s_o + kRows * kORow;  // [rows] (the tiles are done)
   if (lg == 0) s_rowl[myrow] = L;
   __syncthreads();
   {
     float v[32];
 #pragma unroll
-    for (int j = 0; j < 32; j++) v[j] = s_o[prow * kORow + 32 * pq + j] * decode_sign(j);
+    for (int k = 0; k < 8; k++) {
+      const float4 f = *reinterpret_cast<const float4 *>(s_o + prow * kORow + 32 * pq + 4 * k);
+      v[4 * k] = f.x * decode_sign(4 * k);
+      v[4 * k + 1] = f.y * decode_sign(4 * k + 1);
+      v[4 * k + 2] = f.z * decode_sign(4 * k + 2);
+      v[4 * k + 3] = f.w * decode_sign(4 * k + 3);
+    }
     butterfly<32>(v);
     const float Lr = s_rowl[prow];
     if (row_ok) {
