@@ -342,12 +342,26 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       // every pair index folds to a constant)
       auto decode_pairs = [&](auto p0c) {
         constexpr int P0 = decltype(p0c)::value;
-        uint32_t hw[NP], lw[NP];
+        // every codebook value of the K and V codes first (the reads go out
+        // together instead of in dependent groups), then the products
+        constexpr uint32_t SM = (1u << BITS) - 1u, CMk = (1u << CB) - 1u;
+        float ck[2 * NP], cv[2 * NP];
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
           const uint32_t code = pair_code<BITS>(kw, P0 + pp);
-          const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * kf;
-          const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * kf;
+          ck[2 * pp] = s_cb[code & SM & CMk];
+          ck[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
+        }
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+          const uint32_t code = pair_code<BITS>(vw, P0 + pp);
+          cv[2 * pp] = s_cb[code & SM & CMk];
+          cv[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
+        }
+        uint32_t hw[NP], lw[NP];
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+          const float x0 = ck[2 * pp] * kf, x1 = ck[2 * pp + 1] * kf;
           hw[pp] = pack_f16(x0, x1);
           lw[pp] = pack_rem(x0, x1, hw[pp], mone);
         }
@@ -362,9 +376,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         }
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
-          const uint32_t code = pair_code<BITS>(vw, P0 + pp);
-          const float x0 = s_cb[code & ((1u << BITS) - 1u) & ((1u << CB) - 1u)] * vf;
-          const float x1 = s_cb[(code >> BITS) & ((1u << CB) - 1u)] * vf;
+          const float x0 = cv[2 * pp] * vf, x1 = cv[2 * pp + 1] * vf;
           hw[pp] = pack_f16(x0, x1);
           lw[pp] = pack_rem(x0, x1, hw[pp], mone);
         }
