@@ -272,6 +272,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const float eq_scale = exp2i(s_eq[myrow]);
   const float er_scale = QJL ? exp2i(s_er[myrow]) : 0.f;
   const int qpos = a.kv_len - a.q_len + my_qi;  // causal limit of this row
+  const int qmin = a.kv_len - a.q_len + i0;     // the workgroup's first query position
   __syncthreads();  // operands built: the tiles may overwrite the query staging
 
   // ---- tiles ----
@@ -418,6 +419,9 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     const _Float16 *vth = vhi(cur), *vtl = vth + V_HALVES;
 
     // ---- S^T = K Q^T (+ corr), four 16-token blocks ----
+    // a tile wholly before the workgroup's first query position (and inside
+    // the sequence) is visible to every row: no per-element mask
+    const bool open = t0 + kTile <= a.kv_len && (!a.causal || t0 + kTile - 1 <= qmin);
     float x[4][4];
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) {
@@ -450,7 +454,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         const int tp = t0 + 16 * tb + 4 * lg + i;
         float v = d[i] * (ek4[i] * eq_scale);
         if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
-        const bool ok = my_ok && tp < a.kv_len && (!a.causal || tp <= qpos);
+        const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
         x[tb][i] = ok ? v : -INFINITY;
       }
     }
@@ -462,6 +466,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       for (int i = 0; i < 4; i++) mt = fmaxf(mt, x[tb][i]);
     mt = max_xor32(max_xor16(mt));
     const float m_new = fmaxf(m_run, mt);
+    const float m_exp = m_new == -INFINITY ? 0.f : m_new;  // a row with nothing visible yet
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
     // V exponent of the tile (each wave reads all 64)
     static_assert(NW % 4 == 0, "the wave maxima are read 4 at a time");
@@ -484,7 +489,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float e = (x[tb][i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[tb][i] - m_new);
+        const float e = __builtin_amdgcn_exp2f(x[tb][i] - m_exp);  // 2^-inf = 0 for masked tokens
         ls += e;
         p[i] = e * exp2i(max(evk[i] - ev_new, -126));
       }
