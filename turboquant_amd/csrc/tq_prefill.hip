@@ -269,6 +269,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   }
   const int my_qi = i0 + myrow / NR;
   const bool my_ok = my_qi < a.q_len;
+  const bool wave_rows_ok = __all(my_ok);  // every row of the wave is a query
   const float eq_scale = exp2i(s_eq[myrow]);
   const float er_scale = QJL ? exp2i(s_er[myrow]) : 0.f;
   const int qpos = a.kv_len - a.q_len + my_qi;  // causal limit of this row
@@ -449,14 +450,23 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       }
       const float4 ekv = *reinterpret_cast<const float4 *>(s_ek[cur] + 16 * tb + 4 * lg);
       const float ek4[4] = {ekv.x, ekv.y, ekv.z, ekv.w};
+      auto logits = [&](auto maskc) {
+        constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int tp = t0 + 16 * tb + 4 * lg + i;
-        float v = d[i] * (ek4[i] * eq_scale);
-        if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
-        const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
-        x[tb][i] = ok ? v : -INFINITY;
-      }
+        for (int i = 0; i < 4; i++) {
+          const int tp = t0 + 16 * tb + 4 * lg + i;
+          float v = d[i] * (ek4[i] * eq_scale);
+          if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
+          if constexpr (MASK) {
+            const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
+            x[tb][i] = ok ? v : -INFINITY;
+          } else {
+            x[tb][i] = v;
+          }
+        }
+      };
+      if (open && wave_rows_ok) logits(std::false_type{});
+      else logits(std::true_type{});
     }
     // ---- online softmax of this row (its 64 logits sit in the 4 lanes l16 + 16 k) ----
     float mt = -INFINITY;
@@ -502,9 +512,14 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     // of group lg receives element 16 eb + 4 a + b of tokens 16 tb + 4 lg ..
     // + 3 from the token-major rows addressed by lanes a + 4 j. ----
     const int vrow = 4 * lg + (l16 >> 2), vcol = 4 * (l16 & 3);
+    // the accumulators' rescale, skipped when every row's factor is 1
+    if (!__all(rescale == 1.f)) {
+#pragma unroll
+      for (int eb = 0; eb < 8; eb++) o[eb] = o[eb] * rescale;
+    }
 #pragma unroll
     for (int eb = 0; eb < 8; eb++) {
-      f32x4 acc = o[eb] * rescale;
+      f32x4 acc = o[eb];
 #pragma unroll
       for (int tp = 0; tp < 2; tp++) {
         const int r0 = (32 * tp + vrow) * kVRow + 8 * vchunk(2 * eb + (vcol >> 3)) + (vcol & 7),
