@@ -455,7 +455,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int tp = t0 + 16 * tb + 4 * lg + i;
-          float v = d[i] * (ek4[i] * eq_scale);
+          // without QJL the row's query scale 2^E_q is applied in the softmax
+          float v = d[i] * (QJL ? ek4[i] * eq_scale : ek4[i]);
           if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
           if constexpr (MASK) {
             const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
@@ -475,6 +476,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
       for (int i = 0; i < 4; i++) mt = fmaxf(mt, x[tb][i]);
     mt = max_xor32(max_xor16(mt));
+    const float xsc = QJL ? 1.f : eq_scale;  // logit = x xsc (a power of 2: exact)
+    mt *= xsc;
     const float m_new = fmaxf(m_run, mt);
     const float m_exp = m_new == -INFINITY ? 0.f : m_new;  // a row with nothing visible yet
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -499,7 +502,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float e = __builtin_amdgcn_exp2f(x[tb][i] - m_exp);  // 2^-inf = 0 for masked tokens
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[tb][i], xsc, -m_exp));  // 2^-inf = 0 for masked tokens
         ls += e;
         p[i] = e * exp2i(max(evk[i] - ev_new, -126));
       }
