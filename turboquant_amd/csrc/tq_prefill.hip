@@ -132,7 +132,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[2 * TILE_WORDS];
   // per-token and per-wave scalars, read 4 at a time
   __shared__ __attribute__((aligned(16))) float s_ek[2][kTile];  // 2^E_k per token (key exponent folded out)
-  __shared__ __attribute__((aligned(16))) int s_ev[2][kTile];    // V exponent per token
+  __shared__ __attribute__((aligned(16))) float s_ev[2][kTile];  // 2^E_v per token (V exponent folded out)
   __shared__ __attribute__((aligned(16))) int s_evw[2][NW];      // max V exponent over each wave's 16 tokens
   __shared__ float s_cn[2][kTile];       // TQ: |r_t| * qjl_c
   __shared__ __attribute__((aligned(16))) uint32_t s_sg[2][kTile * 4];  // TQ: sign words
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
       if (fqb == 0 && fpart == 0) {
         s_ek[b][ftok] = exp2i(ek);
-        s_ev[b][ftok] = ev;
+        s_ev[b][ftok] = exp2i(ev);
         if constexpr (QJL) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
       }
       {
@@ -491,20 +491,23 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     }
     const int ev_new = max(ev_cur, evt);
     const float rescale = alpha * exp2i(max(ev_cur - ev_new, -126));
+    const float evs = exp2i(-ev_new);
     ev_cur = ev_new;
     m_run = m_new;
     float ls = 0.f;
     u32x2 pb[4][2];
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) {
-      const int4 e4 = *reinterpret_cast<const int4 *>(s_ev[cur] + 16 * tb + 4 * lg);
-      const int evk[4] = {e4.x, e4.y, e4.z, e4.w};
+      // 2^(E_v,t - Ev) as 2^E_v,t 2^-Ev: exact (f16 scales keep both exponents
+      // within [-23, 16])
+      const float4 e4 = *reinterpret_cast<const float4 *>(s_ev[cur] + 16 * tb + 4 * lg);
+      const float evk[4] = {e4.x * evs, e4.y * evs, e4.z * evs, e4.w * evs};
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[tb][i], xsc, -m_exp));  // 2^-inf = 0 for masked tokens
         ls += e;
-        p[i] = e * exp2i(max(evk[i] - ev_new, -126));
+        p[i] = e * evk[i];
       }
       pb[tb][0] = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
       pb[tb][1] = u32x2{pack_rem(p[0], p[1], pb[tb][0][0], mone), pack_rem(p[2], p[3], pb[tb][0][1], mone)};
