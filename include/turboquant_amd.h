@@ -390,6 +390,12 @@ int tq_qjl_logit_bias(const float *rq, int num_q_heads, int q_len, const uint8_t
  * num_layers, norm_mode, outlier_blocks}). */
 int tq_cache_create(int num_layers, int num_kv_heads, int head_dim, int bits, int norm_mode,
                     size_t outlier_blocks, int qjl, void **cache);
+/* Frees the handle.  Its device buffers go back to the device's memory pool
+ * in the order of the stream of the cache's last call (stream-ordered, no
+ * host or device synchronization; work queued on that stream that reads them
+ * runs first), as the reference's tensors are released on their device's
+ * stream.  That stream must still exist; work on other streams that reads the
+ * cache must be ordered before it by the caller. */
 void tq_cache_destroy(void *cache);
 /* 1 for a TqCache handle. */
 int tq_cache_is_tq(void *cache);
@@ -431,7 +437,9 @@ int tq_cache_attend_prefill(void *cache, int layer, const void *q, int q_dtype, 
                             hipStream_t stream);
 
 /* seq_len / reset / memory_usage (pqo.rs:224-236, tq.rs:299-323,
- * storage.rs:175-202). */
+ * storage.rs:175-202).  reset releases every layer's buffers in the order of
+ * the cache's last stream, as tq_cache_destroy does (no synchronization); the
+ * next append allocates zeroed buffers afresh. */
 size_t tq_cache_seq_len(void *cache, int layer);
 int tq_cache_reset(void *cache);
 size_t tq_cache_memory_usage(void *cache);

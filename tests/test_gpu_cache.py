@@ -106,3 +106,70 @@ def test_errors(tq):
     k, v = _kv(2, 0.0)
     with pytest.raises(tq.TurboQuantError):
         cache.prefill(3, k, v)
+
+
+def _pqo_ref(bits, kall, vall, q):
+    """Dense attention of q [Hq, D] over the oracle-dequantized PQO records of
+    kall, vall [H, S, D]."""
+    s = kall.shape[1]
+    pk, sk = orc.pqo_quantize(bits, kall.reshape(-1, D), D)
+    pv, sv = orc.pqo_quantize(bits, vall.reshape(-1, D), D)
+    kd = orc.pqo_dequantize(bits, pk, sk, D).reshape(H, s, D)
+    vd = orc.pqo_dequantize(bits, pv, sv, D).reshape(H, s, D)
+    return orc.attention_dense(q, kd, vd, 1 / math.sqrt(D))
+
+
+def test_reset_and_destroy_are_stream_ordered(tq):
+    """reset and destroy release the buffers in the order of the cache's
+    stream with no synchronization (storage.rs:175-186 touches no device):
+    decodes still queued behind a long-running kernel when the cache is reset
+    (and refilled with other data), or destroyed (and another cache created on
+    the same pool), read the records they were queued against."""
+    bits, t = 3, 700
+    rng = np.random.default_rng(31)
+    k0 = rng.standard_normal((1, H, t, D)).astype(np.float32)
+    v0 = rng.standard_normal((1, H, t, D)).astype(np.float32)
+    k1 = rng.standard_normal((1, H, t, D)).astype(np.float32)
+    v1 = rng.standard_normal((1, H, t, D)).astype(np.float32)
+    kn = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+    vn = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+    q = rng.standard_normal((2 * H, D)).astype(np.float32) / np.float32(math.sqrt(D))
+    dev = lambda a: torch.from_numpy(a).cuda()
+    k0d, v0d, k1d, v1d, knd, vnd = map(dev, (k0, v0, k1, v1, kn, vn))
+    qd = dev(q).reshape(1, 2 * H, 1, D)
+    big = torch.randn((4096, 4096), device="cuda")
+    cfg = tq.AttendConfig(1 / math.sqrt(D), 2)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        cache = tq.PqoCache(1, H, D, bits)
+        cache.prefill(0, k0d, v0d)
+        for _ in range(8):  # the decodes wait behind this on the stream
+            big = big @ big
+            big = big / big.abs().max()
+        outs = [cache.decode(0, knd, vnd, qd, cfg) for _ in range(3)]
+        cache.reset()
+        assert cache.seq_len(0) == 0 and cache.memory_usage() == 0
+        cache.prefill(0, k1d, v1d)
+        after = cache.decode(0, knd, vnd, qd, cfg)
+        other = tq.PqoCache(1, H, D, bits)
+        other.prefill(0, k0d, v0d)
+        for _ in range(8):
+            big = big @ big
+            big = big / big.abs().max()
+        queued = other.decode(0, knd, vnd, qd, cfg)
+        del other  # destroyed while its decode is still queued
+        fresh = tq.PqoCache(1, H, D, bits)
+        fresh.prefill(0, k1d, v1d)
+        fresh_out = fresh.decode(0, knd, vnd, qd, cfg)
+    s.synchronize()
+    for i, o in enumerate(outs):
+        kall = np.concatenate([k0] + [kn] * (i + 1), 2)[0]
+        vall = np.concatenate([v0] + [vn] * (i + 1), 2)[0]
+        ref = _pqo_ref(bits, kall, vall, q)
+        assert np.abs(o.float().cpu().numpy().reshape(2 * H, D) - ref).max() <= 1e-3, i
+    ref1 = _pqo_ref(bits, np.concatenate([k1, kn], 2)[0], np.concatenate([v1, vn], 2)[0], q)
+    assert np.abs(after.float().cpu().numpy().reshape(2 * H, D) - ref1).max() <= 1e-3
+    assert np.abs(fresh_out.float().cpu().numpy().reshape(2 * H, D) - ref1).max() <= 1e-3
+    ref0 = _pqo_ref(bits, np.concatenate([k0, kn], 2)[0], np.concatenate([v0, vn], 2)[0], q)
+    assert np.abs(queued.float().cpu().numpy().reshape(2 * H, D) - ref0).max() <= 1e-3

@@ -241,3 +241,56 @@ def test_batched_ranges_of_chunks(tq, bits, nr):
                                      1 / math.sqrt(d), ws, orc.OUTLIER_ALL)
     torch.cuda.synchronize()
     assert np.array_equal(out2.cpu().numpy(), out)
+
+
+@pytest.mark.parametrize("kv_len", [1000, 4097])
+@pytest.mark.parametrize("d,nr,qjl", [(256, 4, False), (256, 8, False), (128, 8, True), (256, 4, True)],
+                         ids=["d256-gqa4", "d256-gqa8", "d128-gqa8-qjl", "d256-gqa4-qjl"])
+def test_reference_abi_partition_contract(tq, d, nr, qjl, kv_len):
+    """tq_fused_attention with exactly the reference caller's partial buffers,
+    ceil(kv_len / 512) partitions (cuda/attention.rs:70-77), at shapes whose
+    operands only fit 4-wave workgroups of 64 tokens per wave (256-token
+    chunks, taken in 512-token ranges): the output matches the oracle and no
+    byte past the caller's partials is written (a NaN guard after each
+    buffer)."""
+    hkv, bits = 2, 3
+    cap = kv_len + 7
+    rng = np.random.default_rng(1200 + d + nr + kv_len + 7 * qjl)
+    ob = 0 if qjl else orc.OUTLIER_ALL
+    recs, k, kd, vd = _records(rng, hkv, kv_len, cap, d, bits, outlier_blocks=ob)
+    h = hkv * nr
+    q = rng.standard_normal((h, d)).astype(np.float32) / np.float32(math.sqrt(d))
+    if qjl:
+        sg, nm = orc.tq_signs_norms(k.reshape(-1, d), kd.reshape(-1, d))
+        rq = np.stack([orc.query_projections(q[i], 12345) for i in range(h)])
+        bias = orc.tq_logit_bias(q[:, None, :], sg.reshape(hkv, kv_len, -1), nm.reshape(hkv, kv_len))[:, 0, :]
+        ref = orc.attention_dense_bias(q, kd, vd, bias, 1 / math.sqrt(d))
+        sgb = np.zeros((hkv, cap, d // 8), np.uint8)
+        sgb[:, :kv_len] = sg.reshape(hkv, kv_len, -1)
+        nmb = np.zeros((hkv, cap), np.int16)
+        nmb[:, :kv_len] = nm.view(np.int16).reshape(hkv, kv_len)
+        c, _, _ = orc.pqo_codebook(bits - 1)
+        c = np.concatenate([c, np.zeros((1 << bits) - c.size, np.float32)])
+        sgd, nmd, rqd = _dev(sgb), _dev(nmb), _dev(rq)
+    else:
+        ref = orc.attention_dense(q, kd, vd, 1 / math.sqrt(d))
+        c, _, _ = orc.pqo_codebook(bits)
+        sgd = nmd = rqd = None
+    p = (kv_len + 511) // 512
+    guard = 64
+    po = torch.full((h * p * d + guard,), float("nan"), dtype=torch.float32, device="cuda")
+    pm = torch.full((h * p + guard,), float("nan"), dtype=torch.float32, device="cuda")
+    ps = torch.full((h * p + guard,), float("nan"), dtype=torch.float32, device="cuda")
+    out = torch.zeros((h * d + guard,), dtype=torch.float32, device="cuda")
+    qd, cb, sgp = _dev(q), _dev(c), _dev(orc.pqo_decode_signs())
+    ptr = lambda t: None if t is None else t.data_ptr()
+    tq.check(tq.lib.tq_fused_attention(qd.data_ptr(), *(r.data_ptr() for r in recs), cb.data_ptr(), sgp.data_ptr(),
+                                       out.data_ptr(), po.data_ptr(), pm.data_ptr(), ps.data_ptr(), ptr(sgd),
+                                       ptr(nmd), ptr(rqd), int(qjl), h, hkv, d, kv_len, cap, d * bits // 8, d // 32,
+                                       bits, float(1 / math.sqrt(d)), p, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.abs(o[:h * d].reshape(h, d) - ref).max() <= TOL
+    assert np.all(o[h * d:] == 0)
+    for t, n in ((po, h * p * d), (pm, h * p), (ps, h * p)):
+        assert np.isnan(t[n:].cpu().numpy()).all(), "write past the caller's partials"

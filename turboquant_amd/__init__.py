@@ -128,8 +128,11 @@ def pack_indices(indices: torch.Tensor, bits: int, bytes_per_block: int | None =
 
 
 def fused_attention(q, k_idx, k_sc, v_idx, v_sc, codebook, sign_pattern, num_kv_heads, kv_len, kv_stride, bits,
-                    softmax_scale):
-    """Reference-ABI fused decode attention (single sequence, f32 q/out)."""
+                    softmax_scale, qjl=None):
+    """Reference-ABI fused decode attention (single sequence, f32 q/out), with
+    the caller's partials sized as cuda/attention.rs:70-77 sizes them:
+    ceil(kv_len / 512) partitions.  qjl = (rq, signs, residual_norms) attends
+    TQ records with the QJL correction (qjl_enabled = 1)."""
     h, hd = q.shape
     p = (kv_len + 511) // 512
     dev = q.device
@@ -137,8 +140,10 @@ def fused_attention(q, k_idx, k_sc, v_idx, v_sc, codebook, sign_pattern, num_kv_
     po = torch.zeros((h * max(p, 1), hd), dtype=torch.float32, device=dev)
     pm = torch.zeros((h * max(p, 1),), dtype=torch.float32, device=dev)
     ps = torch.zeros((h * max(p, 1),), dtype=torch.float32, device=dev)
+    rq, sg, nm = qjl if qjl is not None else (None, None, None)
     check(lib.tq_fused_attention(_ptr(q), _ptr(k_idx), _ptr(k_sc), _ptr(v_idx), _ptr(v_sc), _ptr(codebook),
-                                 _ptr(sign_pattern), _ptr(out), _ptr(po), _ptr(pm), _ptr(ps), None, None, None, 0,
+                                 _ptr(sign_pattern), _ptr(out), _ptr(po), _ptr(pm), _ptr(ps),
+                                 _ptr(sg), _ptr(nm), _ptr(rq), int(qjl is not None),
                                  h, num_kv_heads, hd, kv_len, kv_stride, hd * bits // 8, hd // 32, bits,
                                  float(softmax_scale), p, _stream()))
     return out

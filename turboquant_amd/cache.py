@@ -115,8 +115,7 @@ class _DeviceCache:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:
-            torch.cuda.synchronize()
-            lib.tq_cache_destroy(h)
+            lib.tq_cache_destroy(h)  # stream-ordered release: no synchronization
             self._h = None
 
     def _layer_out(self, k: torch.Tensor, s: int):

@@ -12,100 +12,39 @@
 // workgroup of a (sequence, KV head) to arrive (device-scope counter) merges
 // them, inverse-rotates and writes the output, then re-arms the counter, so
 // one launch does the whole decode.
-#include "tq_common.h"
-#include "tq_device.h"
-#include "tq_mfma.h"
+#include "tq_attention.h"
 
 #include <mutex>
-#include <type_traits>
+
+namespace tqa {
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
+}  // namespace tqa
 
 namespace {
 
-using namespace tqd;
-using namespace tqm;
+using namespace tqa;
 
-// One split-K counter per (sequence, KV head), each on its own 256-byte line
-// so the tiles' arrivals at different counters do not queue on one line.
-constexpr int kCounterStride = 64;  // ints
-
-// Cache codec of the attended records: PQO (outlier codebook, CB = BITS),
-// PQ (standard (BITS - 1)-bit codebook in BITS-wide slots) and TQ (PQ plus
-// the QJL correction of the keys' residuals, tq.rs:185-253 and the QJL
-// branch of tq_attention_kernel.cu:192-231).
-enum Mode : int { kModePqo = 0, kModePq = 1, kModeTq = 2 };
-
-struct AttnArgs {
-  // Read by every workgroup before its first record load, so kept together
-  // at the head of the block (the kernel reads them in one batch).
-  const void *q;
-  // reference ABI (tq_fused_attention): the caller's device codebook
-  // (indexed by code, tq_attention_kernel.cu:129) and 32 decode signs
-  // (applied before the WHT, tq_attention_kernel.cu:45), or null
-  const float *cb_dev;
-  const float *sg_dev;
-  const int *ws_hdr;         // see cnt_top
-  const int *kv_lens;        // device lengths, or null -> single_len
-  const float *rq;           // TQ: see below
-  int q_dtype;
-  int ngroups;               // head groups per KV head (grid.y = num_kv_heads * ngroups)
-  int nr;                    // query heads per KV head
-  int num_heads;
-  int max_len;               // host bound; device lengths are clamped to it
-  const uint8_t *k_idx;
-  const uint16_t *k_sc;
-  const uint8_t *v_idx;
-  const uint16_t *v_sc;
-  int single_len;
-  int num_kv_heads;
-  long long kv_head_stride;  // tokens
-  long long seq_stride;      // tokens
-  float softmax_scale;
-  float *po;                 // partial acc  [(b*H + h) * P + c][head_dim]
-  float *pm;                 // partial max  [(b*H + h) * P + c]   (base-2 logits)
-  float *ps;                 // partial sum  [(b*H + h) * P + c]
-  // Split-K arrival counters, one 256-byte line per (sequence, KV head),
-  // zero between launches: counter i = b * Hkv + g sits at
-  // cnt_top - (i + 1) * kCounterStride; *ws_hdr = the number of counters
-  // below cnt_top that were zeroed.  A launch merges only if its ws_pairs =
-  // batch * num_kv_heads counters were zeroed (ws_pairs <= *ws_hdr) and its
-  // partials end below them (*ws_hdr <= ws_room, the counter lines between
-  // its partials and cnt_top); otherwise it stores nothing and writes NaN
-  // outputs.
-  int *cnt_top;
-  int ws_pairs;
-  int ws_room;
-  int P;                     // chunk stride per (b, h) in the partial arrays
-  int chunk;                 // tokens per chunk (a wave pass per TPW tokens)
-  int cpr;                   // chunks per workgroup: workgroup c takes chunks [c cpr, (c + 1) cpr)
-  void *out;
-  int out_dtype;
-  // TQ: rq [b][h][head_dim] f32 = R q (precompute_query_projections); per
-  // record, signs [16] u8 of R r and the f16 residual norm |r|; qjl_c =
-  // f32(sqrt(pi/2)) / sqrt(head_dim)
-  const uint32_t *qjl_signs;
-  const uint16_t *qjl_norms;
-  float qjl_c;
-  // cb_args: the codebook comes from cb (L2Norm tables) instead of the
-  // MaxNorm constants compiled in
-  int cb_args;
-  float cb[16];
-};
-
-// Query element as stored (f32 bits or a 16-bit pattern), converted
-// separately so that the wait for the load lands at the first use.
-__device__ __forceinline__ float q_value(uint32_t bits, int qt) {
-  if (qt == kF32) return u2f(bits);
-  if (qt == kBF16) return bf16_to_f32((uint16_t)bits);
-  return f16_to_f32((uint16_t)bits);
+// The reference ABI's second launch: the split-K merge alone.
+template <int HD>
+__global__ __launch_bounds__(256) void stream_merge_kernel(AttnArgs a) {
+  const int g = blockIdx.x, b = blockIdx.y;
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
+  const int nchunks = (len + a.chunk - 1) / a.chunk;
+  if (nchunks == 0) return;
+  merge_heads<HD, 4>(a, b, g, (nchunks + a.cpr - 1) / a.cpr);
 }
-
-// 16-byte load with the coherence of an agent-scope atomic load (SC1): the
-// partials were written by other workgroups, possibly on other dies.
-__device__ __forceinline__ float4 ld_agent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
-}
-
-#include "tq_decode_kernel.h"
 
 __global__ void fill_zero_kernel(int *p, long long n) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
@@ -130,37 +69,6 @@ __global__ void fill_header_kernel(int *p, long long n, int hdr) {
   if (i < n) p[i] = i == n - kCounterStride ? hdr : 0;
 }
 
-// ---- streaming decode: configuration and dispatch ----
-// Heads per group: the MFMA layouts take 2, 4 or 8 heads per instruction
-// (fewer heads leave rows zero); more than 8 query heads per KV head run in
-// several groups (each reading the KV head's records once).
-int stream_hg(int nr) { return nr <= 2 ? 2 : (nr <= 4 ? 4 : 8); }
-// Tokens per wave: 128, or 64 where 128 tokens' records and the wider
-// operand sets would not fit the registers of two waves per SIMD (head_dim
-// 256 with 4 or 8 heads per group; the QJL correction at head_dim 256 or 8
-// heads) or the LDS staging of two workgroups per CU.
-#ifndef TQ_DECODE_TPW
-#define TQ_DECODE_TPW 128
-#endif
-constexpr int stream_tpw_c(int nqb, int hg, bool qjl) {
-  return (nqb == 8 && hg >= 4) || (qjl && (nqb == 8 || hg == 8)) ? 64 : TQ_DECODE_TPW;
-}
-// Waves per workgroup: 8 where their LDS staging fits (a chunk of 8 TPW
-// tokens halves the split-K partials of a long sequence, and the merge has
-// twice the lanes to fetch them), else 4.
-#ifndef TQ_DECODE_WAVES
-#define TQ_DECODE_WAVES 8
-#endif
-template <int BITS, int MODE, int NQB, int HG>
-constexpr int stream_waves_c() {
-  return TQ_DECODE_WAVES == 16 && DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), 16>::LDS_FITS
-             ? 16
-             : (TQ_DECODE_WAVES >= 8 && DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), 8>::LDS_FITS ? 8 : 4);
-}
-template <int BITS, int MODE, int NQB, int HG>
-using StreamCfg = DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), stream_waves_c<BITS, MODE, NQB, HG>()>;
-template <int BITS, int MODE, int NQB, int HG>
-using StreamCfg4 = DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), 4>;
 // The workspace layout is fixed by the shape alone: its chunk is the
 // smallest any bit width, mode or workgroup size uses (the 4-wave form), so
 // every launch's chunks fit its partial rows.
@@ -233,92 +141,6 @@ AttnArgs base_args() {
   return a;
 }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
-  }
-  return cus[dev];
-}
-
-// 4-bit codes on the compiled-in MaxNorm codebook (evenly spaced) take the
-// grid key pass; a caller's codebook or the L2Norm tables, the pair table
-template <class C, bool INLINE, bool MULTI>
-void launch_stream_k(AttnArgs &a, dim3 grid, hipStream_t st, int len_hint) {
-  if constexpr (C::BITS == 4 && C::MODE == kModePqo) {
-    if (!a.cb_dev && !a.cb_args) {
-      hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, true, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx,
-                         a.v_idx, a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
-      return;
-    }
-  }
-  hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, false, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx,
-                     a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
-}
-template <class C, bool INLINE>
-void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
-  a.chunk = C::CHUNK;
-  const int chunks = (a.max_len + C::CHUNK - 1) / C::CHUNK;
-  // Chunks per workgroup: one while the grid of single chunks fits one round
-  // of resident workgroups (three waves per SIMD); beyond that, ranges of
-  // several chunks, so that each workgroup pays its setup, combine and
-  // split-K arrival once per range and streams the next chunk's first tiles
-  // during the current chunk's value pass.  The range length is sized for
-  // one round of the range kernel (two workgroups per compute unit) with
-  // every sequence at max_len.  Measured at C4 (16 sequences of 4096-16384
-  // tokens, capacity 16384): 8 chunks per range 69.5 us; 7, 10, 12 and 16
-  // chunks 79.0, 82.1, 81.4 and 93.7 us, so the batch's actual lengths do
-  // not pick a shorter range.  The reference ABI's separate merge launch
-  // takes single chunks.
-  a.cpr = 1;
-  if constexpr (INLINE) {
-    const long long tasks = (long long)chunks * grid.y * grid.z;
-    const long long cus = device_cus();
-    if (tasks > cus * (12 / C::WAVES))
-      a.cpr = (int)min((long long)max(chunks, 1), (tasks + 2 * cus - 1) / (2 * cus));
-  }
-  grid.x = (unsigned)((chunks + a.cpr - 1) / a.cpr);
-  if (grid.x == 0) grid.x = 1;  // an empty batch still zeroes its outputs
-  const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
-  if constexpr (INLINE) {
-    if (a.cpr > 1) return launch_stream_k<C, INLINE, true>(a, grid, st, len_hint);
-  }
-  launch_stream_k<C, INLINE, false>(a, grid, st, len_hint);
-}
-// The cache decode picks the workgroup size per launch: 8 waves while the
-// grid of 8-wave workgroups leaves compute units idle (one long sequence:
-// the halved split-K merge is on the critical path), else 4 waves (several
-// workgroups per compute unit keep more waves per SIMD in flight).  The
-// reference ABI (a separate merge launch) always takes the 8-wave form.
-template <int BITS, int MODE, int NQB, int HG, bool INLINE>
-void launch_stream_cfg(AttnArgs &a, dim3 grid, hipStream_t st) {
-  using C = StreamCfg<BITS, MODE, NQB, HG>;
-  using C4 = StreamCfg4<BITS, MODE, NQB, HG>;
-  if constexpr (INLINE && C::WAVES != 4) {
-    const long long wgs = (long long)((a.max_len + C::CHUNK - 1) / C::CHUNK) * grid.y * grid.z;
-    if (wgs > device_cus()) return launch_stream_c<C4, INLINE>(a, grid, st);
-  }
-  launch_stream_c<C, INLINE>(a, grid, st);
-}
-template <int BITS, int MODE, int NQB, bool INLINE>
-void launch_stream_hg(AttnArgs &a, int hg, dim3 grid, hipStream_t st) {
-  if (hg == 2) launch_stream_cfg<BITS, MODE, NQB, 2, INLINE>(a, grid, st);
-  else if (hg == 4) launch_stream_cfg<BITS, MODE, NQB, 4, INLINE>(a, grid, st);
-  else launch_stream_cfg<BITS, MODE, NQB, 8, INLINE>(a, grid, st);
-}
-template <int BITS, int MODE, bool INLINE>
-void launch_stream_nqb(AttnArgs &a, int nqb, int hg, dim3 grid, hipStream_t st) {
-  if constexpr (MODE != kModeTq) {
-    if (nqb == 1) return launch_stream_hg<BITS, MODE, 1, INLINE>(a, hg, grid, st);
-  }
-  if (nqb == 2) launch_stream_hg<BITS, MODE, 2, INLINE>(a, hg, grid, st);
-  else if (nqb == 4) launch_stream_hg<BITS, MODE, 4, INLINE>(a, hg, grid, st);
-  else launch_stream_hg<BITS, MODE, 8, INLINE>(a, hg, grid, st);
-}
 // grid: (-, num_kv_heads, batch); the chunk count (grid.x), a.nr / a.ngroups
 // and a.chunk are set here from the launched configuration
 template <bool INLINE>
@@ -328,13 +150,13 @@ int launch_stream(AttnArgs &a, int bits, int mode, int head_dim, dim3 grid, hipS
   grid.y *= (unsigned)a.ngroups;
   const int nqb = head_dim / 32;
   if (bits == 3) {
-    if (mode == kModePqo) launch_stream_nqb<3, kModePqo, INLINE>(a, nqb, hg, grid, st);
-    else if (mode == kModePq) launch_stream_nqb<3, kModePq, INLINE>(a, nqb, hg, grid, st);
-    else launch_stream_nqb<3, kModeTq, INLINE>(a, nqb, hg, grid, st);
+    if (mode == kModePqo) launch_stream_bm<3, kModePqo, INLINE>(a, nqb, hg, grid, st);
+    else if (mode == kModePq) launch_stream_bm<3, kModePq, INLINE>(a, nqb, hg, grid, st);
+    else launch_stream_bm<3, kModeTq, INLINE>(a, nqb, hg, grid, st);
   } else {
-    if (mode == kModePqo) launch_stream_nqb<4, kModePqo, INLINE>(a, nqb, hg, grid, st);
-    else if (mode == kModePq) launch_stream_nqb<4, kModePq, INLINE>(a, nqb, hg, grid, st);
-    else launch_stream_nqb<4, kModeTq, INLINE>(a, nqb, hg, grid, st);
+    if (mode == kModePqo) launch_stream_bm<4, kModePqo, INLINE>(a, nqb, hg, grid, st);
+    else if (mode == kModePq) launch_stream_bm<4, kModePq, INLINE>(a, nqb, hg, grid, st);
+    else launch_stream_bm<4, kModeTq, INLINE>(a, nqb, hg, grid, st);
   }
   return tqh::check_launch("stream_decode_kernel");
 }
@@ -657,8 +479,11 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
   // passes pre.outlier_centroids, so an L2Norm cache brings its Beta tables);
   // with qjl_enabled the records are TQ records (standard (bits-1)-bit
   // codebook, the QJL branch of tq_attention_kernel.cu:192-231).  The
-  // caller's partial buffers (sized for 512-token partitions) hold this
-  // entry's 1024-token partials.
+  // caller's partial buffers are sized for 512-token partitions
+  // (cuda/attention.rs:70-77): every partial of this entry covers at least
+  // 512 tokens (1024-token chunks, 512-token chunks, or ranges of two
+  // 256-token chunks where a shape's operands only fit 4-wave workgroups of
+  // 64 tokens per wave), so ceil(kv_len / 512) partitions always suffice.
   AttnArgs a = base_args();
   a.cb_dev = codebook;
   a.sg_dev = sign_pattern;
@@ -692,10 +517,11 @@ extern "C" int tq_fused_attention(const float *q, const uint8_t *k_indices, cons
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "the QJL-corrected decode takes head_dim 64, 128 or 256");
   a.nr = num_attention_heads / num_kv_heads;
   const int chunk = stream_cfg_chunk(bits, qjl_enabled ? kModeTq : kModePqo, head_dim, a.nr);
-  const int P = (kv_len + chunk - 1) / chunk;
-  if (P > num_partitions)
-    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_partitions %d < the %d chunks of %d tokens", num_partitions, P,
-                     chunk);
+  const int span = chunk < kRefPartition ? kRefPartition : chunk;  // tokens per partial
+  const int P = (kv_len + span - 1) / span;
+  if (P > num_partitions)  // unreachable after the ceil(kv_len / 512) check: kept as the launch's own bound
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_partitions %d < the %d partials of %d tokens", num_partitions, P,
+                     span);
   if (num_partitions > (1 << 20))  // the merge addresses a round's partials with 32-bit offsets
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "num_partitions %d exceeds 2^20", num_partitions);
   rc = launch_stream<false>(a, bits, qjl_enabled ? kModeTq : kModePqo, head_dim,

@@ -1,0 +1,11 @@
+// tq_attention_k3_pqo.hip -- the fused decode kernels for 3-bit
+// PQO (outlier codebook) records: every head_dim, head-group and
+// workgroup shape, with the inline split-K merge and for the reference
+// ABI's separate merge launch.  One unit per bit width and cache mode, so
+// that the kernels build in parallel.
+#include "tq_decode_kernel.h"
+
+namespace tqa {
+template void launch_stream_bm<3, kModePqo, true>(AttnArgs &, int, int, dim3, hipStream_t);
+template void launch_stream_bm<3, kModePqo, false>(AttnArgs &, int, int, dim3, hipStream_t);
+}  // namespace tqa

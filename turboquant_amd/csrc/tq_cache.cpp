@@ -55,7 +55,7 @@ class CompressedStorage {
  public:
   CompressedStorage(int num_kv_heads, int head_dim, int bits, int num_layers, bool qjl)
       : heads_(num_kv_heads), head_dim_(head_dim), bits_(bits), qjl_(qjl), layers_(num_layers) {}
-  ~CompressedStorage() { release_all(); }
+  ~CompressedStorage() { release_all(nullptr); }
 
   int packed_dim() const { return head_dim_ * bits_ / 8; }
   int num_blocks() const { return head_dim_ / 32; }
@@ -122,9 +122,9 @@ class CompressedStorage {
     layers_[l].active = true;
   }
 
-  // storage.rs:175-186 (and the QJL buffers, tq.rs:303-312); the caller has
-  // synchronized the device
-  void reset() { release_all(); }
+  // storage.rs:175-186 (and the QJL buffers, tq.rs:303-312): the buffers go
+  // back to the pool in the order of `stream`, after the work queued on it
+  void reset(hipStream_t stream) { release_all(stream); }
 
   // storage.rs:188-202, plus the whole QJL tensors as tq.rs:314-323 counts them
   size_t memory_usage() const {
@@ -145,8 +145,8 @@ class CompressedStorage {
       pool_free(p, stream);
     L = LayerBuffers{};
   }
-  void release_all() {
-    for (LayerBuffers &L : layers_) free_layer(L, nullptr);
+  void release_all(hipStream_t stream) {
+    for (LayerBuffers &L : layers_) free_layer(L, stream);
   }
 
   int heads_, head_dim_, bits_;
@@ -160,9 +160,16 @@ class KvCache {
   KvCache(int num_layers, int num_kv_heads, int head_dim, const CacheMode &mode)
       : layers_(num_layers), heads_(num_kv_heads), head_dim_(head_dim), mode_(mode),
         storage_(num_kv_heads, head_dim, mode.bits, num_layers, mode.qjl) {}
+  // Every buffer is released in the order of the stream of the cache's last
+  // call (as the reference's tensors are freed on their device's stream): no
+  // host synchronization, and queued work that reads them runs first.
   ~KvCache() {
-    for (void *p : {ws_, rmat_, rq_}) pool_free(p, nullptr);
+    storage_.reset(stream_);
+    for (void *p : {ws_, rmat_, rq_}) pool_free(p, stream_);
   }
+  // the stream of the cache's latest call
+  void use_stream(hipStream_t stream) { stream_ = stream; }
+  hipStream_t last_stream() const { return stream_; }
 
   int layers() const { return layers_; }
   int num_kv_heads() const { return heads_; }
@@ -308,6 +315,7 @@ class KvCache {
   int layers_, heads_, head_dim_;
   CacheMode mode_;
   CompressedStorage storage_;
+  hipStream_t stream_ = nullptr;
   void *ws_ = nullptr;
   size_t ws_bytes_ = 0;
   void *rmat_ = nullptr;
@@ -365,9 +373,7 @@ extern "C" int tq_cache_create(int num_layers, int num_kv_heads, int head_dim, i
 extern "C" void tq_cache_destroy(void *cache) {
   KvCache *c = as_cache(cache);
   if (!c) return;
-  (void)hipDeviceSynchronize();  // no queued work may still use its buffers
-  delete c;
-  (void)hipStreamSynchronize(nullptr);  // the pool releases, ordered on the null stream
+  delete c;  // every buffer released in the order of the cache's last stream
 }
 
 extern "C" int tq_cache_is_tq(void *cache) {
@@ -391,6 +397,7 @@ extern "C" int tq_cache_prefill(void *cache, int layer, const void *k, const voi
       return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "TqCache prefill needs q_len >= 0 and a logit bias output");
   }
   size_t old = 0;
+  c->use_stream(stream);
   rc = c->append(layer, k, v, dtype, tokens, &old, stream);
   if (rc) return rc;
   // pqo.rs:184-200, tq.rs:258-273: the first prefill returns the caller's own K/V
@@ -421,6 +428,7 @@ extern "C" int tq_cache_decode(void *cache, int layer, const void *k, const void
                      "fused decode takes outlier_blocks 0 or all (mixed configs: tq_cache_decode_dequantized)");
   size_t old = 0;
   const bool fuse_rq = m.qjl && tokens > 0;  // the sketch launch projects q too
+  c->use_stream(stream);
   rc = c->append(layer, k, v, kv_dtype, tokens, &old, stream, fuse_rq ? q : nullptr, q_dtype,
                  fuse_rq ? (size_t)num_q_heads : 0);
   if (rc) return rc;
@@ -443,6 +451,7 @@ extern "C" int tq_cache_decode_dequantized(void *cache, int layer, const void *k
     if (q_len <= 0 || !logit_bias_out) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "TqCache decode needs a logit bias output");
   }
   size_t old = 0;
+  c->use_stream(stream);
   rc = c->append(layer, k, v, dtype, tokens, &old, stream);
   if (rc) return rc;
   rc = c->dequantize_full(layer, k_out, v_out, dtype, stream);  // pqo.rs:219-221, tq.rs:284-289
@@ -459,6 +468,7 @@ extern "C" int tq_cache_attend_prefill(void *cache, int layer, const void *q, in
   rc = check_q(c, q, q_dtype, num_q_heads);
   if (rc) return rc;
   if (!out || !tqh::valid_dtype(out_dtype) || q_len < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "invalid arguments");
+  c->use_stream(stream);
   return c->attend_prefill(layer, q, q_dtype, num_q_heads, q_len, causal, softmax_scale, out, out_dtype, stream);
 }
 
@@ -475,8 +485,10 @@ extern "C" size_t tq_cache_capacity(void *cache, int layer) {
 extern "C" int tq_cache_reset(void *cache) {
   KvCache *c = as_cache(cache);
   if (!c) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null cache");
-  if (hipDeviceSynchronize() != hipSuccess) return tqh::fail(TQ_ERR_DEVICE, "device synchronize failed");
-  c->storage().reset();
+  // storage.rs:175-186 touches no device: the buffers return to the pool in
+  // the order of the cache's last stream, after the work queued on it, and
+  // the next append allocates afresh (zeroed) on its own stream
+  c->storage().reset(c->last_stream());
   return TQ_OK;
 }
 
@@ -509,6 +521,7 @@ extern "C" int tq_cache_read_layer(void *cache, int layer, uint8_t *k_indices, u
   if (L.seq == 0) return TQ_OK;
   if (!k_indices || !k_scales || !v_indices || !v_scales) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   const size_t h = (size_t)c->num_kv_heads();
+  c->use_stream(stream);
   auto copy = [&](void *dst, const void *src, size_t rec_bytes) {
     return hipMemcpy2DAsync(dst, L.seq * rec_bytes, src, L.cap * rec_bytes, L.seq * rec_bytes, h,
                             hipMemcpyDeviceToDevice, stream) == hipSuccess;

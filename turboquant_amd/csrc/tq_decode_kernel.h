@@ -1,6 +1,8 @@
-// tq_decode_kernel.h -- the streaming fused decode kernel; included by
-// tq_attention.hip inside its anonymous namespace (after AttnArgs and the
-// split-K helpers).
+#pragma once
+
+// tq_decode_kernel.h -- the streaming fused decode kernel and its launchers;
+// included by the tq_attention_k<bits>_<mode>.hip units, each of which
+// instantiates launch_stream_bm for its bit width and cache mode.
 //
 // One workgroup of WAVES waves (4 or 8) owns a chunk of CHUNK = WAVES * TPW tokens of
 // one (sequence b, KV head g) for a group of HG query heads of that KV head;
@@ -44,108 +46,10 @@
 //      row set's qblock part.  Accumulated over the wave's tiles in MFMA
 //      registers; the useful (block-diagonal) outputs are extracted once.
 
-constexpr int dmin(int x, int y) { return x < y ? x : y; }
-// LDS of the split-K merge (merge_heads) for a workgroup of `waves` waves
-constexpr int merge_lds(int waves) { return waves * 256 * 4 + waves * 8 * 2 * 4; }
+#include "tq_attention.h"
 
-template <int BITS_, int MODE_, int NQB_, int HG_, int TPW_, int WAVES_>
-struct DecCfg {
-  static constexpr int BITS = BITS_, MODE = MODE_, NQB = NQB_, HG = HG_, TPW = TPW_, WAVES = WAVES_;
-  static constexpr int CB = MODE == kModePqo ? BITS : BITS - 1;  // codebook bits
-  static constexpr bool QJL = MODE == kModeTq;
-  static constexpr int HD = 32 * NQB;
-  static constexpr int QW = BITS;                // 32-bit words per qblock record
-  static constexpr int PACKED = NQB * QW * 4;    // bytes per token record
-  // qblocks per instruction (K and V) and heads per instruction
-  static constexpr int QPM = dmin(NQB, HG <= 2 ? 4 : (HG <= 4 ? 2 : 1));
-  static constexpr int HPM = 8 / QPM;
-  static constexpr int QG = NQB / QPM;           // qblock groups (K) / sets (V)
-  static constexpr int ES = 4 / QPM;             // parts of a qblock stream (lanes per qblock)
-  static constexpr int KJ = 2 * QPM;             // K slices (4 elements each) per group
-  static constexpr int PPL = 16 / ES;            // pairs per lane part (= V slices per set)
-  static constexpr int NW = ES == 1 ? QW : 2;    // record words a lane holds per group
-  static constexpr int NKT = TPW / 16, NVP = TPW / 32;
-#ifndef TQ_DECODE_LOOKAHEAD
-#define TQ_DECODE_LOOKAHEAD 2
-#endif
-  static constexpr int LOOKAHEAD = TQ_DECODE_LOOKAHEAD;  // load groups in flight per wave
-  static constexpr int THREADS = 64 * WAVES, CHUNK = WAVES * TPW;
-  static constexpr int NPAIR = 1 << (2 * BITS);
-  static constexpr int SW4 = (NQB + 3) / 4;      // QJL: sign words per lane and tile
-  static constexpr int TPL = TPW / 64;           // V-scale tokens per lane
-  static constexpr bool QA_REGS = QG * KJ <= 8;  // query operands in registers (else LDS)
-  // LDS carve (32-bit words)
-  static constexpr int OFF_PAIR = 0;                                  // uint2 [NPAIR]
-  static constexpr int OFF_NIB = OFF_PAIR + 2 * NPAIR;                // QJL uint2 [16]
-  // the key-pass query operands, u32x4 [QG*KJ][64] (read per instruction,
-  // or by QA_REGS configurations into registers at each chunk's K pass)
-  static constexpr int OFF_QA = (OFF_NIB + (QJL ? 32 : 0) + 3) & ~3;
-  static constexpr int OFF_W = OFF_QA + QG * KJ * 64 * 4;
-  // the query setup lives in the wave staging area until the K pass starts
-  static constexpr int OFF_Q = OFF_W;                                 // [HG][HD] scaled rotated query
-  static constexpr int OFF_QMAX = OFF_Q + HG * HD;                    // [HG][NQB] block max |qt|
-  static constexpr int OFF_RQ = OFF_QMAX + HG * NQB;                  // QJL [HG][HD]
-  static constexpr int OFF_RQMAX = OFF_RQ + (QJL ? HG * HD : 0);      // QJL [HG][NQB]
-  static constexpr int OFF_QSUM = OFF_RQMAX + (QJL ? HG * NQB : 0);   // [HG][NQB] block sums of the query
-  static constexpr int SETUP_END = OFF_QSUM + (BITS == 4 && MODE == kModePqo ? HG * NQB : 0);
-  // per wave: weights p [HG][TPW] and |s_V| 2^-Ev [NQB][TPW] of the current
-  // chunk for the V pass; the wave's value sums acc [HG][HD] over its chunks;
-  // then m [HG], l [HG], 2^Ev and the chunk's rescale factors [HG]
-  static constexpr int WP = HG * TPW;
-  static constexpr int WS = NQB * TPW;
-  static constexpr int WC = WP + WS;
-  static constexpr int WM = WC + HG * HD;
-  static constexpr int WSTAGE = (WM + 3 * HG + 1 + 3) & ~3;
-  static constexpr int TOTAL = OFF_W + WAVES * WSTAGE;
-  static constexpr int MERGE_LDS = merge_lds(WAVES);
-  static_assert(SETUP_END <= TOTAL, "the query setup fits the staging area");
-  static_assert(HG >= 1 && HG <= 8, "heads per group");
-  static_assert(TPW % 64 == 0, "whole V-scale loads per lane");
-  static_assert(QPM * HPM == 8 && HPM >= HG, "one instruction serves every head");
-  static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "waves per workgroup");
-  // does the workgroup's LDS (with the merge's scratch) fit 64 KiB (the
-  // 8-wave form is taken only then), and gfx950's 160 KiB at all?
-  static constexpr bool LDS_FITS = TOTAL * 4 + MERGE_LDS <= 64 * 1024;
-  static constexpr bool LDS_OK = TOTAL * 4 + MERGE_LDS <= 160 * 1024;
-};
-
-// A buffer resource over the bytes [off, total) of the records at base:
-// loads past the end return zeros.  The tile offset moves the base (scalar
-// arithmetic) rather than riding in the instruction's scalar offset, so
-// every byte a load touches is inside the range check.
-// (The arguments are wave-uniform; readfirstlane keeps the descriptor in
-// scalar registers, where a buffer instruction takes it.)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rec_rsrc(const void *base, uint32_t total, uint32_t off = 0) {
-  const int d = (int)(total - off);  // both below 2^31 (the host bounds a sequence's records)
-  const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane(d > 0 ? d : 0);
-  const uint64_t p = reinterpret_cast<uint64_t>(base) + off;
-  const uint64_t ps = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) << 32) |
-                      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p);
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(ps), (short)0, (int)n, 0x00020000);
-}
-// N consecutive 32-bit words at voff + soff of a buffer
-template <int N>
-__device__ __forceinline__ void buf_words(uint32_t (&w)[N], __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  if constexpr (N == 1) {
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
-  } else if constexpr (N == 2) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
-    w[0] = v[0];
-    w[1] = v[1];
-  } else if constexpr (N == 3) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
-    w[0] = v[0];
-    w[1] = v[1];
-    w[2] = v[2];
-  } else {
-    static_assert(N == 4, "1 to 4 words");
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    w[0] = v[0];
-    w[1] = v[1];
-    w[2] = v[2];
-    w[3] = v[3];
-  }
-}
+namespace tqa {
+namespace {
 
 // BITS-bit code pair p of a lane's stream w (little-endian words), as the
 // byte offset of its pair-table entry (code * 8): two VALU per pair.
@@ -200,125 +104,6 @@ __device__ __forceinline__ float sum_xor16(float v) {
   float a, b;
   swap_pair16(v, a, b);
   return a + b;
-}
-
-// ---------------------------------------------------------------------------
-// Split-K merge and inverse rotation of the nr query heads of (b, g):
-//   o = inv * H(sg * sum_c 2^(m_c - M) acc_c) / sum_c 2^(m_c - M) l_c
-// (tq_attention_kernel.cu:299-332; 0 when the sum is 0).  Outputs go in
-// rounds of 256; in a round each of the W waves is one lane set folding every
-// W-th chunk of four consecutive outputs per lane (one 16-byte device-coherent
-// load per chunk, MAXC chunks per lane in one latency round, an online
-// update beyond); the W sets meet once in LDS.
-// ---------------------------------------------------------------------------
-template <int HD, int W>
-__device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
-  constexpr int MAXC = 64 / W;
-  __shared__ __attribute__((aligned(16))) float s_ma[W * 256];
-  __shared__ float s_mml[W * 8 * 2];
-  static_assert(sizeof(s_ma) + sizeof(s_mml) == merge_lds(W), "merge scratch");
-  const int tid = threadIdx.x, part = tid >> 6, quad = tid & 63;
-  const long long bh0 = (long long)b * a.num_heads + (long long)g * a.nr;
-  const int outs = a.nr * HD;
-  for (int o0 = 0; o0 < outs; o0 += 256) {
-    const int oq = o0 + 4 * quad;  // this lane's first output
-    const bool active = oq < outs;
-    const int r = active ? oq / HD : 0, d0 = oq - r * HD;
-    const long long c0 = (bh0 + r) * a.P;
-    // one descriptor over the partial rows of the round's heads (uniform: a
-    // per-lane descriptor would cost a waterfall loop per load); the lane's
-    // head and chunk ride in the offset.  The round's heads hold hrn * HD <=
-    // 256 outputs per chunk, so the range is at most 1 KiB x P (P below
-    // 2^20, checked on the host).
-    const int hr0 = o0 / HD, hrn = min(a.nr - hr0, (256 + HD - 1) / HD);
-    const __amdgpu_buffer_rsrc_t rsrc =
-        rec_rsrc(a.po + (bh0 + hr0) * a.P * HD, (uint32_t)(hrn * a.P * HD * (int)sizeof(float)));
-    const uint32_t lane_off = (uint32_t)(((r - hr0) * a.P * HD + d0) * (int)sizeof(float));
-    float4 pv[MAXC];
-    float pm[MAXC], pl[MAXC];
-#pragma unroll
-    for (int k = 0; k < MAXC; k++) {
-      const int cc = part + W * k;
-      const bool ok = active && cc < nchunks;
-      pv[k] = ok ? ld_agent16(rsrc, lane_off + (uint32_t)(cc * HD * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
-      pm[k] = ok ? ld_agent(&a.pm[c0 + cc]) : -INFINITY;
-      pl[k] = ok ? ld_agent(&a.ps[c0 + cc]) : 0.f;
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < MAXC; k++) M = fmaxf(M, pm[k]);
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    float L = 0.f;
-    auto fold = [&](const float4 &v, float l, float w) {
-      A.x = __builtin_fmaf(v.x, w, A.x);
-      A.y = __builtin_fmaf(v.y, w, A.y);
-      A.z = __builtin_fmaf(v.z, w, A.z);
-      A.w = __builtin_fmaf(v.w, w, A.w);
-      L = __builtin_fmaf(l, w, L);
-    };
-#pragma unroll
-    for (int k = 0; k < MAXC; k++) fold(pv[k], pl[k], pm[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[k] - M));
-    for (int cc = part + W * MAXC; active && cc < nchunks; cc += W) {  // long contexts only
-      const float m = ld_agent(&a.pm[c0 + cc]), l = ld_agent(&a.ps[c0 + cc]);
-      const float4 v = ld_agent16(rsrc, lane_off + (uint32_t)(cc * HD * 4));
-      if (m == -INFINITY) continue;
-      if (m > M) {
-        const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - m);
-        A.x *= f;
-        A.y *= f;
-        A.z *= f;
-        A.w *= f;
-        L *= f;
-        M = m;
-      }
-      fold(v, l, __builtin_amdgcn_exp2f(m - M));
-    }
-    if (active) {
-      *reinterpret_cast<float4 *>(s_ma + part * 256 + 4 * quad) = A;
-      if (d0 == 0) {
-        const int rl = (oq - o0) / HD;
-        s_mml[2 * (part * 8 + rl)] = M;
-        s_mml[2 * (part * 8 + rl) + 1] = L;
-      }
-    }
-    __syncthreads();
-    const int o = o0 + tid;
-    if (tid < 256 && o < outs) {  // whole 32-lane blocks
-      const int rl = tid / HD, d = o - (o / HD) * HD;
-      float Mx = -INFINITY;
-#pragma unroll
-      for (int p = 0; p < W; p++) Mx = fmaxf(Mx, s_mml[2 * (p * 8 + rl)]);
-      float At = 0.f, Lt = 0.f;
-#pragma unroll
-      for (int p = 0; p < W; p++) {
-        const float mp = s_mml[2 * (p * 8 + rl)];
-        const float f = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - Mx);
-        At = __builtin_fmaf(s_ma[p * 256 + tid], f, At);
-        Lt = __builtin_fmaf(s_mml[2 * (p * 8 + rl) + 1], f, Lt);
-      }
-      const int i = d & 31;
-      const float sg = a.sg_dev ? a.sg_dev[i] : decode_sign(i);
-      const float v = wht32_lanes(At * sg, i);
-      const float res = (Lt > 0.f) ? v * kInvSqrt32 / Lt : 0.f;
-      const long long oi = bh0 * HD + o;
-      if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = res;
-      else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(res);
-      else static_cast<uint16_t *>(a.out)[oi] = f32_to_f16(res);
-    }
-    // the next round reuses the LDS scratch (after the last, nothing does: no
-    // barrier, whose fence would wait for the output stores)
-    if (o0 + 256 < outs) __syncthreads();
-  }
-}
-
-// The reference ABI's second launch: the split-K merge alone.
-template <int HD>
-__global__ __launch_bounds__(256) void stream_merge_kernel(AttnArgs a) {
-  const int g = blockIdx.x, b = blockIdx.y;
-  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.max_len) : a.single_len;
-  const int nchunks = (len + a.chunk - 1) / a.chunk;
-  if (nchunks == 0) return;
-  merge_heads<HD, 4>(a, b, g, (nchunks + a.cpr - 1) / a.cpr);
 }
 
 // MULTI: the launch gives workgroups ranges of several chunks (cpr > 1)
@@ -1080,3 +865,92 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
   }
 }
+
+// 4-bit codes on the compiled-in MaxNorm codebook (evenly spaced) take the
+// grid key pass; a caller's codebook or the L2Norm tables, the pair table
+template <class C, bool INLINE, bool MULTI>
+void launch_stream_k(AttnArgs &a, dim3 grid, hipStream_t st, int len_hint) {
+  if constexpr (C::BITS == 4 && C::MODE == kModePqo) {
+    if (!a.cb_dev && !a.cb_args) {
+      hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, true, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx,
+                         a.v_idx, a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, false, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx,
+                     a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+}
+template <class C, bool INLINE>
+void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
+  a.chunk = C::CHUNK;
+  const int chunks = (a.max_len + C::CHUNK - 1) / C::CHUNK;
+  // Chunks per workgroup: one while the grid of single chunks fits one round
+  // of resident workgroups (three waves per SIMD); beyond that, ranges of
+  // several chunks, so that each workgroup pays its setup, combine and
+  // split-K arrival once per range and streams the next chunk's first tiles
+  // during the current chunk's value pass.  The range length is sized for
+  // one round of the range kernel (two workgroups per compute unit) with
+  // every sequence at max_len.  Measured at C4 (16 sequences of 4096-16384
+  // tokens, capacity 16384): 8 chunks per range 69.5 us; 7, 10, 12 and 16
+  // chunks 79.0, 82.1, 81.4 and 93.7 us, so the batch's actual lengths do
+  // not pick a shorter range.  The reference ABI's separate merge launch
+  // takes single chunks.
+  a.cpr = 1;
+  if constexpr (INLINE) {
+    const long long tasks = (long long)chunks * grid.y * grid.z;
+    const long long cus = device_cus();
+    if (tasks > cus * (12 / C::WAVES))
+      a.cpr = (int)min((long long)max(chunks, 1), (tasks + 2 * cus - 1) / (2 * cus));
+  } else if constexpr (C::CHUNK < kRefPartition) {
+    // The reference ABI's caller sizes its partials for 512-token partitions
+    // (cuda/attention.rs:70-77): a configuration with shorter chunks takes
+    // ranges of 512 tokens, one partial per range.
+    static_assert(kRefPartition % C::CHUNK == 0, "whole chunks per reference partition");
+    a.cpr = kRefPartition / C::CHUNK;
+  }
+  grid.x = (unsigned)((chunks + a.cpr - 1) / a.cpr);
+  if (grid.x == 0) grid.x = 1;  // an empty batch still zeroes its outputs
+  const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
+  if constexpr (INLINE || C::CHUNK < kRefPartition) {
+    if (a.cpr > 1) return launch_stream_k<C, INLINE, true>(a, grid, st, len_hint);
+  }
+  launch_stream_k<C, INLINE, false>(a, grid, st, len_hint);
+}
+// The cache decode picks the workgroup size per launch: 8 waves while the
+// grid of 8-wave workgroups leaves compute units idle (one long sequence:
+// the halved split-K merge is on the critical path), else 4 waves (several
+// workgroups per compute unit keep more waves per SIMD in flight).  The
+// reference ABI (a separate merge launch) always takes the 8-wave form.
+template <int BITS, int MODE, int NQB, int HG, bool INLINE>
+void launch_stream_cfg(AttnArgs &a, dim3 grid, hipStream_t st) {
+  using C = StreamCfg<BITS, MODE, NQB, HG>;
+  using C4 = StreamCfg4<BITS, MODE, NQB, HG>;
+  if constexpr (INLINE && C::WAVES != 4) {
+    const long long wgs = (long long)((a.max_len + C::CHUNK - 1) / C::CHUNK) * grid.y * grid.z;
+    if (wgs > device_cus()) return launch_stream_c<C4, INLINE>(a, grid, st);
+  }
+  launch_stream_c<C, INLINE>(a, grid, st);
+}
+template <int BITS, int MODE, int NQB, bool INLINE>
+void launch_stream_hg(AttnArgs &a, int hg, dim3 grid, hipStream_t st) {
+  if (hg == 2) launch_stream_cfg<BITS, MODE, NQB, 2, INLINE>(a, grid, st);
+  else if (hg == 4) launch_stream_cfg<BITS, MODE, NQB, 4, INLINE>(a, grid, st);
+  else launch_stream_cfg<BITS, MODE, NQB, 8, INLINE>(a, grid, st);
+}
+template <int BITS, int MODE, bool INLINE>
+void launch_stream_nqb(AttnArgs &a, int nqb, int hg, dim3 grid, hipStream_t st) {
+  if constexpr (MODE != kModeTq) {
+    if (nqb == 1) return launch_stream_hg<BITS, MODE, 1, INLINE>(a, hg, grid, st);
+  }
+  if (nqb == 2) launch_stream_hg<BITS, MODE, 2, INLINE>(a, hg, grid, st);
+  else if (nqb == 4) launch_stream_hg<BITS, MODE, 4, INLINE>(a, hg, grid, st);
+  else launch_stream_hg<BITS, MODE, 8, INLINE>(a, hg, grid, st);
+}
+}  // namespace
+
+template <int BITS, int MODE, bool INLINE>
+void launch_stream_bm(AttnArgs &a, int nqb, int hg, dim3 grid, hipStream_t st) {
+  launch_stream_nqb<BITS, MODE, INLINE>(a, nqb, hg, grid, st);
+}
+
+}  // namespace tqa
