@@ -208,8 +208,10 @@ int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices
  * and merge counters live in the library's file-scope device array of 8 MiB
  * per device (held until the process ends; room for 1,024 (sequence, KV
  * head) pairs and 7.75 MiB of partials = batch * num_heads *
- * ceil(max_kv_len / 1024) * (head_dim + 2) * 4 bytes, each part rounded up
- * to 256); larger shapes are rejected with TQ_ERR_INVALID_ARGUMENT.  No
+ * ceil(max_kv_len / chunk) * (head_dim + 2) * 4 bytes, each part rounded up
+ * to 256, with chunk = 512 tokens, or 256 at head_dim 256 or with more than
+ * 4 query heads per KV head); larger shapes are rejected with
+ * TQ_ERR_INVALID_ARGUMENT.  No
  * hipMalloc, hipFree or other allocation.  Every call on a device shares that
  * device's array: calls that overlap in time on one device race. */
 int tq_pqo_decode_attention_noalloc(const void *q, int q_dtype, const uint8_t *k_indices,
