@@ -110,11 +110,14 @@ def time_steps(torch, fn, steps: int, warmup: int, graph: bool = False):
 TRIALS, LAUNCHES = 5, 100
 
 
-def time_median(torch, fn, warmup: int = 10, launches: int = LAUNCHES, trials: int = TRIALS, graph: bool = False):
+def time_median(torch, fn, warmup: int = 10, launches: int = None, trials: int = None, graph: bool = False):
     """Median ms per launch over `trials` trials of `launches` launches each
-    (HIP events on the launch stream around each trial), after `warmup`
-    untimed launches; also the spread (min, max) of the trials."""
+    (HIP events on the launch stream around each trial; TRIALS x LAUNCHES by
+    default), after `warmup` untimed launches; also the spread (min, max) of
+    the trials."""
     import statistics
+    launches = LAUNCHES if launches is None else launches
+    trials = TRIALS if trials is None else trials
     per = []
     for t in range(trials):
         ms, _ = time_steps(torch, fn, launches, warmup if t == 0 else 0, graph=graph)
@@ -564,6 +567,7 @@ def read_ceiling(torch, nbytes: int, steps: int, warmup: int):
 
 
 def main():
+    global LAUNCHES, TRIALS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -572,10 +576,18 @@ def main():
     # and the clock has come up from idle after the host-side setup
     ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--records", default="all",
+                    help="secondary records to run besides the C3 headline, comma separated from "
+                         "read,c2,c4,tq3,prefill,c1,c5 (default all); the others are reported as null")
+    ap.add_argument("--launches", type=int, default=LAUNCHES,
+                    help="launches per timed trial of the secondary records (profiling runs pass fewer)")
+    ap.add_argument("--trials", type=int, default=TRIALS, help="timed trials of the secondary records")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
+    LAUNCHES, TRIALS = max(1, args.launches), max(1, args.trials)
+    want = set(["read", "c2", "c4", "tq3", "prefill", "c1", "c5"] if args.records == "all" else args.records.split(","))
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the decode path shards by KV head with no exchange, see DESIGN.md", file=sys.stderr)
@@ -616,8 +628,10 @@ def main():
     ms_devlen, _ = time_steps(torch, lambda i: attn_step(i, lens), args.steps, args.warmup)
     gbs = c3_bytes() / (ms * 1e-3) / 1e9
     del caches
-    ceiling = read_ceiling(torch, c3_bytes(), args.steps, args.warmup)
-    ceiling["decode_frac_of_read"] = round(gbs / ceiling["gbs"], 4)
+    ceiling = None
+    if "read" in want:
+        ceiling = read_ceiling(torch, c3_bytes(), args.steps, args.warmup)
+        ceiling["decode_frac_of_read"] = round(gbs / ceiling["gbs"], 4)
 
     # ---- config 2: PQO3/PQO4 quantize (fused rotation, bf16 in) and
     # dequantize (bf16 out); the headline's quantize figure is the PQO3
@@ -627,27 +641,31 @@ def main():
     x = torch.randn((n_vec, C2["head_dim"]), generator=gen, device="cuda", dtype=torch.float32)
     x[:, torch.tensor([3, 40, 77, 101], device="cuda")] *= 8.0
     x = x.to(torch.bfloat16)
-    c2 = {f"pqo{b}": bench_c2_codec(torch, tq, args, x, b) for b in (3, 4)}
+    c2 = {f"pqo{b}": bench_c2_codec(torch, tq, args, x, b) for b in (3, 4)} if "c2" in want else None
     del x
-    q3 = c2["pqo3"]["quantize"]
-    c4 = bench_c4(torch, tq, args)
-    tq_c3 = bench_tq_c3(torch, tq, args)
-    pf = bench_prefill(torch, tq, args)
-    c1 = bench_c1(torch, tq, args)
-    c5 = bench_c5(torch, tq, args)
+    q3 = c2["pqo3"]["quantize"] if c2 else None
+    c4 = bench_c4(torch, tq, args) if "c4" in want else None
+    tq_c3 = bench_tq_c3(torch, tq, args) if "tq3" in want else None
+    pf = bench_prefill(torch, tq, args) if "prefill" in want else None
+    c1 = bench_c1(torch, tq, args) if "c1" in want else None
+    c5 = bench_c5(torch, tq, args) if "c5" in want else None
 
     cpu = None
     qcpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_c3()
-        for b in (3, 4):
-            cq, cd = cpu_baseline_c2(b)
-            c2[f"pqo{b}"]["quantize"]["cpu_baseline"] = cq
-            c2[f"pqo{b}"]["dequantize"]["cpu_baseline"] = cd
-        qcpu = q3["cpu_baseline"]
-        c4["cpu_baseline"] = cpu_baseline_c4(c4["contexts"])
-        c1["cpu_baseline"] = cpu_baseline_c1()
-        c5["cpu_baseline"] = cpu_baseline_c5()
+        if c2:
+            for b in (3, 4):
+                cq, cd = cpu_baseline_c2(b)
+                c2[f"pqo{b}"]["quantize"]["cpu_baseline"] = cq
+                c2[f"pqo{b}"]["dequantize"]["cpu_baseline"] = cd
+            qcpu = q3["cpu_baseline"]
+        if c4:
+            c4["cpu_baseline"] = cpu_baseline_c4(c4["contexts"])
+        if c1:
+            c1["cpu_baseline"] = cpu_baseline_c1()
+        if c5:
+            c5["cpu_baseline"] = cpu_baseline_c5()
 
     rec = {
         "metric": "PQO3 fused decode attn GB/s (%HBM peak) @32K ctx; quantize Mvec/s at d=128",
@@ -672,11 +690,12 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic("stream_decode_kernel_c3")},
         "cpu_baseline": cpu,
         "read_ceiling": ceiling,
-        "quantize": {"metric": "PQO3 quantize Mvec/s at d=128 (C2, bf16 in, fused rotation)",
-                     "value": q3["mvec_s"], "unit": "Mvec/s", "ms_per_step": q3["ms_per_step"],
-                     "source": "c2_codec.pqo3.quantize (the same measurement)",
-                     "vectors_per_step": n_vec, "algorithmic_bytes_per_step": q3["algorithmic_bytes_per_step"],
-                     "roofline": q3["roofline"], "cpu_baseline": qcpu},
+        "quantize": None if q3 is None else {
+            "metric": "PQO3 quantize Mvec/s at d=128 (C2, bf16 in, fused rotation)",
+            "value": q3["mvec_s"], "unit": "Mvec/s", "ms_per_step": q3["ms_per_step"],
+            "source": "c2_codec.pqo3.quantize (the same measurement)",
+            "vectors_per_step": n_vec, "algorithmic_bytes_per_step": q3["algorithmic_bytes_per_step"],
+            "roofline": q3["roofline"], "cpu_baseline": qcpu},
         "c2_codec": c2,
         "c4_batched_decode": c4,
         "tq_decode_c3": tq_c3,

@@ -97,10 +97,15 @@ __device__ __forceinline__ float q_value(uint32_t bits, int qt) {
   return f16_to_f32((uint16_t)bits);
 }
 
-// 16-byte load with the coherence of an agent-scope atomic load (SC1): the
-// partials were written by other workgroups, possibly on other dies.
+// Loads with the coherence of an agent-scope atomic load (SC1: read at the
+// device-coherent level): the partials were written by other workgroups,
+// possibly on other dies.  Buffer loads over a uniform descriptor, so a
+// round's loads go out together with no per-lane address arithmetic.
 __device__ __forceinline__ float4 ld_agent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+}
+__device__ __forceinline__ float ld_agent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 16));
 }
 
 
@@ -125,6 +130,9 @@ struct DecCfg {
   static constexpr int PPL = 16 / ES;            // pairs per lane part (= V slices per set)
   static constexpr int NW = ES == 1 ? QW : 2;    // record words a lane holds per group
   static constexpr int NKT = TPW / 16, NVP = TPW / 32;
+  // grid V pass: the row stride (bytes) of a staged V record, padded by 8 so
+  // that the 16 rows a transposing read addresses fall in distinct banks
+  static constexpr int VRS = PACKED + 8;
 #ifndef TQ_DECODE_LOOKAHEAD
 #define TQ_DECODE_LOOKAHEAD 2
 #endif
@@ -151,8 +159,12 @@ struct DecCfg {
   // per wave: weights p [HG][TPW] and |s_V| 2^-Ev [NQB][TPW] of the current
   // chunk for the V pass; the wave's value sums acc [HG][HD] over its chunks;
   // then m [HG], l [HG], 2^Ev and the chunk's rescale factors [HG]
-  static constexpr int WP = HG * TPW;
-  static constexpr int WS = NQB * TPW;
+  // (rows PSTR words apart, padded by 16 bytes, so that the rows of
+  // different heads and qblocks that one V-pass read touches sit in
+  // different banks)
+  static constexpr int PSTR = TPW + 4;
+  static constexpr int WP = HG * PSTR;
+  static constexpr int WS = NQB * PSTR;
   static constexpr int WC = WP + WS;
   static constexpr int WM = WC + HG * HD;
   static constexpr int WSTAGE = (WM + 3 * HG + 1 + 3) & ~3;
@@ -167,6 +179,15 @@ struct DecCfg {
   // 8-wave form is taken only then), and gfx950's 160 KiB at all?
   static constexpr bool LDS_FITS = TOTAL * 4 + MERGE_LDS <= 64 * 1024;
   static constexpr bool LDS_OK = TOTAL * 4 + MERGE_LDS <= 160 * 1024;
+  // The grid passes (4-bit codes on the MaxNorm codebook) read no codebook
+  // table and take one query operand per qblock instead of per slice pair:
+  // their layout starts the query operands at 0 and everything from OFF_W
+  // on G_SHIFT words lower; each wave also stages a 64-token block of V
+  // records (VSTAGE bytes for the workgroup, a separate array).
+  static constexpr int G_OFF_W = QG * QPM * 64 * 4;
+  static constexpr int G_SHIFT = OFF_W - G_OFF_W;
+  static constexpr int VSTAGE = WAVES * 64 * VRS;
+  static constexpr bool G_LDS_OK = (TOTAL - G_SHIFT) * 4 + MERGE_LDS + VSTAGE <= 160 * 1024;
 };
 
 // A buffer resource over the bytes [off, total) of the records at base:
@@ -229,7 +250,6 @@ __device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
     const int oq = o0 + 4 * quad;  // this lane's first output
     const bool active = oq < outs;
     const int r = active ? oq / HD : 0, d0 = oq - r * HD;
-    const long long c0 = (bh0 + r) * a.P;
     // one descriptor over the partial rows of the round's heads (uniform: a
     // per-lane descriptor would cost a waterfall loop per load); the lane's
     // head and chunk ride in the offset.  The round's heads hold hrn * HD <=
@@ -239,6 +259,9 @@ __device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
     const __amdgpu_buffer_rsrc_t rsrc =
         rec_rsrc(a.po + (bh0 + hr0) * a.P * HD, (uint32_t)(hrn * a.P * HD * (int)sizeof(float)));
     const uint32_t lane_off = (uint32_t)(((r - hr0) * a.P * HD + d0) * (int)sizeof(float));
+    const __amdgpu_buffer_rsrc_t rm = rec_rsrc(a.pm + (bh0 + hr0) * a.P, (uint32_t)(hrn * a.P * (int)sizeof(float)));
+    const __amdgpu_buffer_rsrc_t rl = rec_rsrc(a.ps + (bh0 + hr0) * a.P, (uint32_t)(hrn * a.P * (int)sizeof(float)));
+    const uint32_t ml_off = (uint32_t)((r - hr0) * a.P * (int)sizeof(float));
     float4 pv[MAXC];
     float pm[MAXC], pl[MAXC];
 #pragma unroll
@@ -246,8 +269,8 @@ __device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
       const int cc = part + W * k;
       const bool ok = active && cc < nchunks;
       pv[k] = ok ? ld_agent16(rsrc, lane_off + (uint32_t)(cc * HD * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
-      pm[k] = ok ? ld_agent(&a.pm[c0 + cc]) : -INFINITY;
-      pl[k] = ok ? ld_agent(&a.ps[c0 + cc]) : 0.f;
+      pm[k] = ok ? ld_agent4(rm, ml_off + (uint32_t)cc * 4u) : -INFINITY;
+      pl[k] = ok ? ld_agent4(rl, ml_off + (uint32_t)cc * 4u) : 0.f;
     }
     float M = -INFINITY;
 #pragma unroll
@@ -264,7 +287,7 @@ __device__ void merge_heads(const AttnArgs &a, int b, int g, int nchunks) {
 #pragma unroll
     for (int k = 0; k < MAXC; k++) fold(pv[k], pl[k], pm[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[k] - M));
     for (int cc = part + W * MAXC; active && cc < nchunks; cc += W) {  // long contexts only
-      const float m = ld_agent(&a.pm[c0 + cc]), l = ld_agent(&a.ps[c0 + cc]);
+      const float m = ld_agent4(rm, ml_off + (uint32_t)cc * 4u), l = ld_agent4(rl, ml_off + (uint32_t)cc * 4u);
       const float4 v = ld_agent16(rsrc, lane_off + (uint32_t)(cc * HD * 4));
       if (m == -INFINITY) continue;
       if (m > M) {

@@ -51,6 +51,54 @@
 namespace tqa {
 namespace {
 
+// N (1, 2, 4 or 8) consecutive 32-bit words at voff of a buffer, and their
+// store into LDS at p (4 N-byte aligned)
+template <int N>
+__device__ __forceinline__ void load_words(uint32_t (&w)[N], __amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  if constexpr (N == 8) {
+    uint32_t a[4], b[4];
+    buf_words<4>(a, r, voff, 0);
+    buf_words<4>(b, r, voff + 16, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      w[i] = a[i];
+      w[i + 4] = b[i];
+    }
+  } else {
+    buf_words<N>(w, r, voff, 0);
+  }
+}
+template <int N>
+__device__ __forceinline__ void stage_words(uint8_t *p, const uint32_t (&w)[N]) {
+  if constexpr (N == 1) {
+    *reinterpret_cast<uint32_t *>(p) = w[0];
+  } else if constexpr (N == 2) {
+    *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) *reinterpret_cast<uint4 *>(p + 4 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+  }
+}
+// Transposing 4-bit LDS read (ds_read_b64_tr_b4): inside each group of 16
+// lanes, lane i receives 4-bit item i of the 8-byte rows addressed by lanes
+// 0 .. 15 of its group, the row of lane j in bits 4 j .. 4 j + 3 (checked on
+// MI355X).  p must point into LDS.
+__device__ __forceinline__ u32x2 lds_read_tr4(const void *p) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_v2i *)p));
+}
+
+// The 8 nibbles of w (4-bit codes, LSB first) as an f16 MFMA operand of
+// exact subnormals, code r and r + 4 in register r: registers 0 and 2 hold
+// i 2^-24 (the low nibble of each half), registers 1 and 3 i 2^-20 (the
+// nibble left at bits 4..7 of its half), so the other operand's registers 0
+// and 2 carry a factor 16 and every product is x i 2^-20.
+__device__ __forceinline__ u32x4 nib_operand(uint32_t w) {
+  const uint32_t h = w >> 8;
+  return u32x4{w & 0x000F000Fu, w & 0x00F000F0u, h & 0x000F000Fu, h & 0x00F000F0u};
+}
+
 // BITS-bit code pair p of a lane's stream w (little-endian words), as the
 // byte offset of its pair-table entry (code * 8): two VALU per pair.
 template <int BITS, int NWD>
@@ -116,27 +164,33 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
                                                                long long seq_stride, long long kv_head_stride,
                                                                int len_hint, AttnArgs a) {
   constexpr int BITS = C::BITS, HD = C::HD, NQB = C::NQB, HG = C::HG, TPW = C::TPW, QW = C::QW, NW = C::NW;
-  static_assert(C::LDS_OK, "the workgroup's LDS (with the merge's scratch) fits 160 KiB");
+  static_assert(GRID ? C::G_LDS_OK : C::LDS_OK, "the workgroup's LDS (with the merge's scratch) fits 160 KiB");
+  // word offset of the layout from OFF_W on (the grid passes need no
+  // codebook table and fewer query operands)
+  constexpr int LSH = GRID ? C::G_SHIFT : 0;
   constexpr int QPM = C::QPM, HPM = C::HPM, QG = C::QG, ES = C::ES, KJ = C::KJ, PPL = C::PPL;
   constexpr int NKT = C::NKT, NVP = C::NVP, PACKED = C::PACKED;
   // GRID: 4-bit codes on the evenly spaced MaxNorm codebook c_i = -R + i D.
-  // The key pass then contracts the query with the codes themselves (exact
-  // f16 subnormals i 2^-24, eight per word by masks) and applies
-  // q.c = D sum q_j i_j - R sum q_j after the product: no codebook reads,
-  // half the instructions of the two-part codebook operand.
-  static_assert(!GRID || (BITS == 4 && C::MODE == kModePqo), "the grid key pass takes 4-bit PQO codes");
+  // Both passes then contract with the codes themselves (exact f16
+  // subnormals, eight per word by masks: nib_operand) and apply
+  // q.c = D sum q_j i_j - R sum q_j (and its value-pass counterpart) after
+  // the product: no codebook reads, half the instructions of the two-part
+  // codebook operand.
+  static_assert(!GRID || (BITS == 4 && C::MODE == kModePqo), "the grid passes take 4-bit PQO codes");
   constexpr int KJA = GRID ? QPM : KJ;                  // key-pass instructions per qblock group
   constexpr bool QAR = GRID || C::QA_REGS;              // query operands in registers
-  __shared__ __attribute__((aligned(16))) float lds[C::TOTAL];
+  __shared__ __attribute__((aligned(16))) float lds[C::TOTAL - LSH];
   __shared__ int s_flag;
+  // grid V pass: each wave's 64-token block of V records, token-major
+  __shared__ __attribute__((aligned(16))) uint8_t vstage[GRID ? C::VSTAGE : 16];
   uint2 *s_pair = reinterpret_cast<uint2 *>(lds + C::OFF_PAIR);
-  float *s_q = lds + C::OFF_Q;
-  float *s_qmax = lds + C::OFF_QMAX;
-  float *s_rq = lds + C::OFF_RQ;
-  float *s_rqmax = lds + C::OFF_RQMAX;
-  float *s_qsum = lds + C::OFF_QSUM;
+  float *s_q = lds + C::OFF_Q - LSH;
+  float *s_qmax = lds + C::OFF_QMAX - LSH;
+  float *s_rq = lds + C::OFF_RQ - LSH;
+  float *s_rqmax = lds + C::OFF_RQMAX - LSH;
+  float *s_qsum = lds + C::OFF_QSUM - LSH;
   uint2 *s_nib = reinterpret_cast<uint2 *>(lds + C::OFF_NIB);
-  u32x4 *s_qa = reinterpret_cast<u32x4 *>(lds + C::OFF_QA);
+  u32x4 *s_qa = reinterpret_cast<u32x4 *>(lds + (GRID ? 0 : C::OFF_QA));
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the wave's scalar offsets
@@ -257,7 +311,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   const uint32_t kso = ((uint32_t)l16 * NQB + kqb) * 2u;
   const uint32_t vvo = (uint32_t)(4 * lg + (l16 >> 2)) * PACKED + (uint32_t)(vqb * QW + part_word<C>(ves)) * 4u;
   const uint32_t tw_first = (uint32_t)(ck0 * C::CHUNK + wave * TPW);
-  uint32_t kw[NKT][QG][NW], vw[NKT][QG][NW];
+  uint32_t kw[NKT][QG][NW], vw[GRID ? 1 : NKT][QG][NW];
+  uint32_t vg[GRID ? NKT : 1][NQB];  // grid V pass: lane l's 4 NQB bytes of its tile
   uint32_t ksv[NKT][QG];
   uint32_t sgw[NKT][C::SW4];
   uint32_t nrm[NKT];
@@ -301,8 +356,12 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     } else {
       const int i = grp - NKT - 1;
       const auto rv = rec_rsrc(vbase, nrec * PACKED, (tw0 + 16u * i) * PACKED);
+      if constexpr (GRID) {
+        load_words<NQB>(vg[i], rv, (uint32_t)lane * (4u * NQB));
+      } else {
 #pragma unroll
-      for (int qg = 0; qg < QG; qg++) buf_words<NW>(vw[i][qg], rv, vvo + qg * QPM * QW * 4, 0);
+        for (int qg = 0; qg < QG; qg++) buf_words<NW>(vw[i][qg], rv, vvo + qg * QPM * QW * 4, 0);
+      }
     }
   };
   // Schedule: K tiles 0 .. LA-1 and the V scales (needed by the softmax)
@@ -350,7 +409,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // ---- pair table (the caller's device codebook, L2Norm tables from the
   // arguments, or the PQO constants) ----
   static_assert(C::NPAIR <= 256, "one pair-table entry per lane");
-  if (tid < C::NPAIR) {
+  if (!GRID && tid < C::NPAIR) {  // the grid passes read no table (its words hold the query operands)
     const int e = tid, i0 = pi0, i1 = pi1;
     float c0, c1;
     if (a.cb_dev) {
@@ -447,8 +506,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   };
   // Grid key pass: word j of the lane's stream part holds elements
   // 8 j + (0..7) as nibbles; B's register r carries nibbles r and r + 4
-  // (masks 0x000F000F after a shift by 4 r), so slot u = 2 r + h takes
-  // element 8 j + r + 4 h, and the query operand follows that order.
+  // (nib_operand), so slot u = 2 r + h takes element 8 j + r + 4 h, and the
+  // query operand follows that order.
   auto make_qa_grid = [&](int qg, int j, int m, int kg) -> u32x4 {
     const int qbl = m / (2 * HPM), hl = (m >> 1) % HPM, part = m & 1;
     u32x4 val = {0u, 0u, 0u, 0u};
@@ -456,8 +515,11 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       const float sc = exp2i(-head_exp(s_qmax, hl));
       const float *src = s_q + hl * HD + (qg * QPM + qbl) * 32 + (kg % ES) * (32 / ES) + 8 * j;
       const float4 lo4 = *reinterpret_cast<const float4 *>(src), hi4 = *reinterpret_cast<const float4 *>(src + 4);
-      const float xa[4] = {lo4.x * sc, lo4.y * sc, lo4.z * sc, lo4.w * sc};
-      const float xb[4] = {hi4.x * sc, hi4.y * sc, hi4.z * sc, hi4.w * sc};
+      // registers 0 and 2 meet codes i 2^-24, 1 and 3 codes i 2^-20
+      // (nib_operand): the former take the factor 16 (exact)
+      const float sc16 = sc * 16.f;
+      const float xa[4] = {lo4.x * sc16, lo4.y * sc, lo4.z * sc16, lo4.w * sc};
+      const float xb[4] = {hi4.x * sc16, hi4.y * sc, hi4.z * sc16, hi4.w * sc};
       uint32_t w[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
@@ -485,7 +547,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // hl0 + u; their R sum_j Q_j (Q as in the operand, exact power-of-two scale)
   float rqs[GRID ? QG : 1][2];
   constexpr float kGridR = 2.1573f;                       // -c_0 of the 4-bit MaxNorm codebook
-  constexpr float kGridD24 = ((2.0f * kGridR) / 15.0f) * 16777216.0f;  // D 2^24 (codes enter as i 2^-24)
+  constexpr float kGridD20 = ((2.0f * kGridR) / 15.0f) * 1048576.0f;  // D 2^20 (products enter as x i 2^-20)
+  constexpr float kGridR20 = kGridR * 1048576.0f;                     // R 2^20
   if constexpr (GRID) {
 #pragma unroll
     for (int qg = 0; qg < QG; qg++)
@@ -534,9 +597,9 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
 
   // ---- the range's chunks: per chunk a K pass, an online softmax step and a
   // V pass whose value sums are folded into the wave's running sums ----
-  float *stage = lds + C::OFF_W + wave * C::WSTAGE;
-  float *st_p = stage;                 // [HG][TPW]
-  float *st_s = stage + C::WP;         // [NQB][TPW]
+  float *stage = lds + C::OFF_W - LSH + wave * C::WSTAGE;
+  float *st_p = stage;                 // [HG][PSTR]
+  float *st_s = stage + C::WP;         // [NQB][PSTR]
   float *comb = stage + C::WC;         // [HG][HD] value sums over the chunks
   float *cml = stage + C::WM;          // m[HG], l[HG], 2^Ev, the chunk's rescale [HG]
   // 16-lane rows holding the same head: R replicas (QPM 4: the row groups
@@ -588,9 +651,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       for (int qg = 0; qg < QG; qg++)
 #pragma unroll
         for (int j = 0; j < KJA; j++) {
-          const uint32_t w = kw[i][qg][j];
-          const u32x4 bv = {w & 0x000F000Fu, (w >> 4) & 0x000F000Fu, (w >> 8) & 0x000F000Fu, (w >> 12) & 0x000F000Fu};
-          dk[qg] = mfma(qa[qg * KJA + j], bv, dk[qg]);
+          dk[qg] = mfma(qa[qg * KJA + j], nib_operand(kw[i][qg][j]), dk[qg]);
         }
     } else {
     // every pair-table read of the tile goes out before its first MFMA, so
@@ -629,7 +690,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       for (int qg = 0; qg < QG; qg++) {
         const float sk = fabsf(f16_to_f32((uint16_t)ksv[i][qg]));
         float d = dk[qg][2 * u] + dk[qg][2 * u + 1];
-        if constexpr (GRID) d = __builtin_fmaf(d, kGridD24, -rqs[qg][u]);
+        if constexpr (GRID) d = __builtin_fmaf(d, kGridD20, -rqs[qg][u]);
         x[u] = __builtin_fmaf(d, sk, x[u]);
       }
     }
@@ -674,7 +735,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     for (int i = 0; i < NKT; i++) {
       const float p = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[i][v] - mn);
       l += p;
-      if (hl < HG && i % R == ri) st_p[hl * TPW + 16 * i + l16] = p;
+      if (hl < HG && i % R == ri) st_p[hl * C::PSTR + 16 * i + l16] = p;
     }
     alpha[v] = mrun[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrun[v] - mn);
     lrun[v] = __builtin_fmaf(lrun[v], alpha[v], row_sum16(l));
@@ -701,7 +762,11 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
 #pragma unroll
   for (int u = 0; u < C::TPL; u++)
 #pragma unroll
-    for (int qb = 0; qb < NQB; qb++) st_s[qb * TPW + C::TPL * lane + u] = svv[u][qb] * vinv;
+    for (int qb = 0; qb < NQB; qb++) {
+      // the grid V pass: even tokens' weights meet codes i 2^-24 (nib_operand), so they take the factor 16
+      const float f = GRID && ((C::TPL * lane + u) & 1) == 0 ? vinv * 16.f : vinv;
+      st_s[qb * C::PSTR + C::TPL * lane + u] = svv[u][qb] * f;
+    }
   if (MULTI && l16 == 0) {
 #pragma unroll
     for (int v = 0; v < NS; v++) {
@@ -713,6 +778,115 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+  if constexpr (GRID) {
+  // ---- V pass on the grid, 64-token block by block: the block's records
+  // are staged token-major in LDS; a transposing 4-bit read hands lane
+  // (m, kg) code m of a 16-code chunk for 16 tokens, which become the A
+  // operand as exact f16 subnormals (nib_operand; the weight operand takes
+  // the same token order), so
+  // sum_t W_t c_i = D 2^20 sum_t W_t (i 2^-20) - R 2^20 sum_t W_t 2^-20, the
+  // last sum from one MFMA per weight operand over a constant code of 1
+  // (nib_operand's scales: the weights of even tokens carry the factor 16). ----
+  constexpr int NB = TPW / 64, NCH = 2 * NQB, RS = C::VRS;
+  uint8_t *stg = vstage + wave * 64 * RS;
+  f32x4 acc[NCH], acc1[QG];
+#pragma unroll
+  for (int cc = 0; cc < NCH; cc++) acc[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int vs = 0; vs < QG; vs++) acc1[vs] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int bk = 0; bk < NB; bk++) {
+    // tiles 4 bk + 4 .. 4 bk + 7 go out as this block's are consumed; the
+    // next chunk's first K tiles and V scales with the last block
+    if (4 * bk + 4 < NKT) {
+#pragma unroll
+      for (int u = 4; u < 8; u++)
+        if (4 * bk + u < NKT) issue(NKT + 1 + 4 * bk + u, tw0);
+    }
+    if (MULTI && bk == NB - 1 && ck + 1 < nck) issue_first(tw0 + C::CHUNK, LA);
+    // stage the block's four tiles: lane l holds token l / 4 of its tile,
+    // bytes 4 NQB (l % 4) .. of the record
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      stage_words<NQB>(stg + (16 * u + (lane >> 2)) * RS + 4 * NQB * (lane & 3), vg[4 * bk + u]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // per qblock group: the weight operands for k = 8 kg + 2 r + e <-> token
+    // 16 kg + 8 h + r + 4 e of the block (h: which half of the lane group's
+    // 16 tokens), then the group's chunks (transposing reads ahead of the
+    // MFMAs), so only one group's operands are live at a time
+#pragma unroll
+    for (int vs = 0; vs < QG; vs++) {
+      u32x4 bw[2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (hv < nh) {
+          const int t = 64 * bk + 16 * lg + 8 * h;
+          const float4 pa = *reinterpret_cast<const float4 *>(st_p + hv * C::PSTR + t);
+          const float4 pb = *reinterpret_cast<const float4 *>(st_p + hv * C::PSTR + t + 4);
+          const float4 sa = *reinterpret_cast<const float4 *>(st_s + (vs * QPM + qsp) * C::PSTR + t);
+          const float4 sb = *reinterpret_cast<const float4 *>(st_s + (vs * QPM + qsp) * C::PSTR + t + 4);
+          const float xa[4] = {pa.x * sa.x, pa.y * sa.y, pa.z * sa.z, pa.w * sa.w};
+          const float xb[4] = {pb.x * sb.x, pb.y * sb.y, pb.z * sb.z, pb.w * sb.w};
+#pragma unroll
+          for (int r = 0; r < 4; r++) w[r] = pack_rem(xa[r], xb[r], pack_f16(xa[r], xb[r]), kpart);
+        }
+        bw[h] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+      constexpr int GC = 2 * QPM;  // 16-code chunks of a qblock group
+      u32x2 cw[GC];
+#pragma unroll
+      for (int j = 0; j < GC; j++) cw[j] = lds_read_tr4(stg + (16 * lg + l16) * RS + 8 * (vs * GC + j));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < GC; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          acc[vs * GC + j] = mfma(nib_operand(cw[j][h]), bw[h], acc[vs * GC + j]);
+        }
+      // a code of 1 in nib_operand's scales: 2^-24 in registers 0 and 2, 2^-20 in 1 and 3
+      constexpr uint32_t kOne = 0x00010001u, kOne16 = 0x00100010u;
+#pragma unroll
+      for (int h = 0; h < 2; h++) acc1[vs] = mfma(u32x4{kOne, kOne16, kOne, kOne16}, bw[h], acc1[vs]);
+    }
+  }
+  // lane (n, lg) holds codes' dims 16 cc + 4 lg + (0..3) under column n; the
+  // two weight parts of a head sit in lanes n, n ^ 1
+  {
+    const float rf = MULTI ? cml[2 * HG + 1 + dmin(hv, HG - 1)] : 0.f;
+    float one[QG];
+#pragma unroll
+    for (int vs = 0; vs < QG; vs++) {
+      const float xx = acc1[vs][0];
+      one[vs] = dpp_quad_xor1(xx) + xx;
+      asm volatile("" : "+v"(one[vs]));
+    }
+#pragma unroll
+    for (int cc = 0; cc < NCH; cc++) {
+      const int qb = cc >> 1, vs = qb / QPM;
+      float o[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        const float xx = acc[cc][jj];
+        float t = dpp_quad_xor1(xx) + xx;
+        asm volatile("" : "+v"(t));
+        o[jj] = __builtin_fmaf(t, kGridD20, -kGridR20 * one[vs]);
+      }
+      if (qsp == qb % QPM && wpart == 0 && hv < nh) {
+        float4 *dst = reinterpret_cast<float4 *>(comb + hv * HD + 16 * cc + 4 * lg);
+        if constexpr (MULTI) {
+          const float4 old = *dst;
+          *dst = make_float4(__builtin_fmaf(old.x, rf, o[0]), __builtin_fmaf(old.y, rf, o[1]),
+                             __builtin_fmaf(old.z, rf, o[2]), __builtin_fmaf(old.w, rf, o[3]));
+        } else {
+          *dst = make_float4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    }
+  }
+  } else {
   // ---- V pass, tile pair by tile pair ----
   f32x4 dv[QG][PPL];
 #pragma unroll
@@ -731,8 +905,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
 #pragma unroll
         for (int u = 0; u < 2; u++) {
           const int t = 32 * vp + 16 * u + 4 * lg;
-          const float4 p4 = *reinterpret_cast<const float4 *>(st_p + hv * TPW + t);
-          const float4 s4 = *reinterpret_cast<const float4 *>(st_s + (vs * QPM + qsp) * TPW + t);
+          const float4 p4 = *reinterpret_cast<const float4 *>(st_p + hv * C::PSTR + t);
+          const float4 s4 = *reinterpret_cast<const float4 *>(st_s + (vs * QPM + qsp) * C::PSTR + t);
           const float x0 = p4.x * s4.x, x1 = p4.y * s4.y, x2 = p4.z * s4.z, x3 = p4.w * s4.w;
           w[2 * u] = pack_rem(x0, x1, pack_f16(x0, x1), kpart);
           w[2 * u + 1] = pack_rem(x2, x3, pack_f16(x2, x3), kpart);
@@ -786,6 +960,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
         }
       }
   }
+  }  // V pass
   }  // chunks
   if (l16 == 0) {
 #pragma unroll
@@ -808,13 +983,13 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     float mw[C::WAVES], M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < C::WAVES; w++) {
-      mw[w] = lds[C::OFF_W + w * C::WSTAGE + C::WM + hl];
+      mw[w] = lds[C::OFF_W - LSH + w * C::WSTAGE + C::WM + hl];
       M = fmaxf(M, mw[w]);
     }
     float A = 0.f, L = 0.f;
 #pragma unroll
     for (int w = 0; w < C::WAVES; w++) {
-      const float *cw = lds + C::OFF_W + w * C::WSTAGE;
+      const float *cw = lds + C::OFF_W - LSH + w * C::WSTAGE;
       const float f = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
       A = __builtin_fmaf(cw[C::WC + hl * HD + d], f * cw[C::WM + 2 * HG], A);
       L = __builtin_fmaf(cw[C::WM + HG + hl], f, L);
@@ -899,8 +1074,11 @@ void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
   if constexpr (INLINE) {
     const long long tasks = (long long)chunks * grid.y * grid.z;
     const long long cus = device_cus();
+#ifndef TQ_RANGE_WGS
+#define TQ_RANGE_WGS 2
+#endif
     if (tasks > cus * (12 / C::WAVES))
-      a.cpr = (int)min((long long)max(chunks, 1), (tasks + 2 * cus - 1) / (2 * cus));
+      a.cpr = (int)min((long long)max(chunks, 1), (tasks + TQ_RANGE_WGS * cus - 1) / (TQ_RANGE_WGS * cus));
   } else if constexpr (C::CHUNK < kRefPartition) {
     // The reference ABI's caller sizes its partials for 512-token partitions
     // (cuda/attention.rs:70-77): a configuration with shorter chunks takes
