@@ -294,3 +294,92 @@ def test_reference_abi_partition_contract(tq, d, nr, qjl, kv_len):
     assert np.all(o[h * d:] == 0)
     for t, n in ((po, h * p * d), (pm, h * p), (ps, h * p)):
         assert np.isnan(t[n:].cpu().numpy()).all(), "write past the caller's partials"
+
+
+def _ragged_batch(tq, bsz, hkv, d, cap, bits, nr, lens, seed, qjl=False):
+    """Batched decode of ragged sequences through tq_cache_decode_attention,
+    each sequence checked against dense attention over the oracle's records
+    (with the QJL logit bias for TQ records)."""
+    rng = np.random.default_rng(seed)
+    h = hkv * nr
+    pd, nb = d * bits // 8, d // 32
+    ob = 0 if qjl else orc.OUTLIER_ALL
+    kp = np.zeros((bsz, hkv, cap, pd), np.uint8)
+    ks = np.zeros((bsz, hkv, cap, nb), np.int16)
+    vp = np.zeros_like(kp)
+    vs = np.zeros_like(ks)
+    sgb = np.zeros((bsz, hkv, cap, d // 8), np.uint8)
+    nmb = np.zeros((bsz, hkv, cap), np.int16)
+    q = bf16_round(rng.standard_normal((bsz, h, d)).astype(np.float32) / np.float32(math.sqrt(d)))
+    rq = np.stack([[orc.query_projections(q[b, i], 12345) for i in range(h)] for b in range(bsz)]) if qjl else None
+    refs = []
+    for b in range(bsz):
+        t = int(lens[b])
+        if t == 0:
+            refs.append(np.zeros((h, d), np.float32))
+            continue
+        k = kv_outlier(rng, hkv, t, d).reshape(-1, d)
+        v = kv_outlier(rng, hkv, t, d).reshape(-1, d)
+        pk, sk = orc.polar_quantize(bits, ob, k, d)
+        pv, sv = orc.polar_quantize(bits, ob, v, d)
+        kd = orc.polar_dequantize(bits, ob, pk, sk, d).reshape(hkv, t, d)
+        vd = orc.polar_dequantize(bits, ob, pv, sv, d).reshape(hkv, t, d)
+        kp[b, :, :t] = pk.reshape(hkv, t, pd)
+        ks[b, :, :t] = sk.view(np.int16).reshape(hkv, t, nb)
+        vp[b, :, :t] = pv.reshape(hkv, t, pd)
+        vs[b, :, :t] = sv.view(np.int16).reshape(hkv, t, nb)
+        if qjl:
+            sg, nm = orc.tq_signs_norms(k, kd.reshape(-1, d))
+            sgb[b, :, :t] = sg.reshape(hkv, t, -1)
+            nmb[b, :, :t] = nm.view(np.int16).reshape(hkv, t)
+            bias = orc.tq_logit_bias(q[b][:, None, :], sg.reshape(hkv, t, -1), nm.reshape(hkv, t))[:, 0, :]
+            refs.append(orc.attention_dense_bias(q[b], kd, vd, bias, 1 / math.sqrt(d)))
+        else:
+            refs.append(orc.attention_dense(q[b], kd, vd, 1 / math.sqrt(d)))
+    ws = tq.AttentionWorkspace(bsz, h, hkv, d, cap)
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    kw = {} if not qjl else dict(rq=_dev(rq.astype(np.float32)), qjl_signs=_dev(sgb), qjl_norms=_dev(nmb))
+    out = tq.cache_decode_attention(qd, _dev(kp), _dev(ks), _dev(vp), _dev(vs),
+                                    _dev(np.asarray(lens, np.int32)), hkv, bits, cap, cap, hkv * cap,
+                                    1 / math.sqrt(d), ws, ob, **kw)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for b in range(bsz):
+        assert np.abs(out[b] - refs[b]).max() <= TOL, b
+
+
+@pytest.mark.parametrize("bits,nr,d", [(3, 2, 128), (4, 4, 128), (4, 8, 64), (3, 1, 256), (4, 4, 256)])
+def test_balanced_split_ragged_batch(tq, bits, nr, d):
+    """A batch whose chunks exceed one round of resident workgroups, at most
+    64 sequences and one head group per KV head: the balanced split (each
+    sequence's chunks cut into near-equal ranges so that every workgroup
+    gets at most the same number), with empty, single-token and near-capacity
+    sequences."""
+    bsz, hkv, cap = 40, 8, 3000
+    rng = np.random.default_rng(300 + bits + nr + d)
+    lens = rng.integers(0, cap + 1, size=bsz)
+    lens[[2, 9, 17]] = 0
+    lens[[5, 23]] = 1
+    lens[11] = cap
+    assert -(-cap // 512) * hkv * bsz > 3 * 256  # more tasks than one round holds
+    _ragged_batch(tq, bsz, hkv, d, cap, bits, nr, lens, 301 + d)
+
+
+@pytest.mark.parametrize("case", ["batch70", "gqa16", "all_empty", "tq"])
+def test_range_split_cases(tq, case):
+    """Range launches outside the balanced split (more than 64 sequences; two
+    head groups per KV head), a batch of empty sequences under a large
+    capacity, and TQ records with the QJL correction under the balanced
+    split."""
+    if case == "batch70":
+        lens = np.random.default_rng(7).integers(0, 2001, size=70)
+        _ragged_batch(tq, 70, 4, 64, 2000, 4, 2, lens, 71)
+    elif case == "gqa16":
+        lens = np.random.default_rng(8).integers(1, 4001, size=12)
+        _ragged_batch(tq, 12, 4, 128, 4000, 3, 16, lens, 72)
+    elif case == "all_empty":
+        _ragged_batch(tq, 30, 8, 128, 5000, 3, 2, np.zeros(30, np.int64), 73)
+    else:
+        lens = np.random.default_rng(9).integers(0, 2501, size=36)
+        lens[4] = 0
+        _ragged_batch(tq, 36, 8, 128, 2500, 3, 2, lens, 74, qjl=True)

@@ -75,6 +75,11 @@ struct AttnArgs {
   int P;                     // chunk stride per (b, h) in the partial arrays
   int chunk;                 // tokens per chunk (a wave pass per TPW tokens)
   int cpr;                   // chunks per workgroup: workgroup c takes chunks [c cpr, (c + 1) cpr)
+  // balanced split of a range launch (0: off): workgroups, sequences and
+  // (KV head x head group) pairs per sequence; the grid is (bal_nwg, 1, 1)
+  int bal_nwg;
+  int bal_batch;
+  int bal_ny;
   void *out;
   int out_dtype;
   // TQ: rq [b][h][head_dim] f32 = R q (precompute_query_projections); per

@@ -223,6 +223,64 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   const int a_cpr = a.cpr;
   asm volatile("" ::"s"(a_q), "s"(a_sg), "s"(a_cb), "s"(a_rq), "s"(a_ws), "s"(a_lens), "s"(a_qdt), "s"(a_ngroups),
                "s"(a_nr), "s"(a_heads), "s"(a_max), "s"(a_cpr));
+  // ---- balanced split (range launches with a.bal_nwg > 0, one head group
+  // per KV head, at most 64 sequences): the ranges' length S (in chunks) is
+  // the smallest whose ranges, sequence b's chunks split into
+  // R_b = ceil(n_b / S) near-equal ranges per KV head, number at most
+  // bal_nwg.  Ragged batches then give every workgroup at most S chunks;
+  // ranges of one fixed length would leave the compute units that hold the
+  // long sequences' ranges setting the time.  A wave holds the batch's chunk
+  // counts (one sequence per lane), so the split costs a few reductions and
+  // a ballot, no LDS and no barrier before the first loads. ----
+  int bal_ck0 = 0, bal_nck = 0, bal_nparts = 0;
+  const bool bal = MULTI && a.bal_nwg > 0;
+  if constexpr (MULTI) {
+    if (bal) {
+      const int nwg = a.bal_nwg, ny = a.bal_ny, nb = a.bal_batch;
+      int n = 0;
+      if (lane < nb) {
+        const int lb = len_hint >= 0 ? len_hint : min(max(a_lens[lane], 0), a_max);
+        n = (lb + C::CHUNK - 1) / C::CHUNK;
+      }
+      // S: the closed form ceil(ny T / (nwg - ny nb)) (feasible: sum_b
+      // ceil(n_b / S) <= T / S + nb), or one less when that still fits
+      const int T = wave_sum_i(n);
+      int S = nwg > ny * nb ? (int)(((long long)T * ny + (nwg - ny * nb) - 1) / (nwg - ny * nb)) : wave_max_i(n);
+      S = max(S, 1);
+      if (S > 1 && (long long)wave_sum_i((n + S - 2) / (S - 1)) * ny <= nwg) S--;
+      S = __builtin_amdgcn_readfirstlane(S);
+      const int rb = (n + S - 1) / S;  // ranges per KV head of the lane's sequence
+      const int incl = wave_incl_scan_i(rb);
+      const int pre = incl - rb;  // ranges before the lane's sequence, per KV head
+      const int wi = blockIdx.x;
+      const int total = __builtin_amdgcn_readlane(incl, 63) * ny;
+      // empty sequences attend to nothing: zero output (cuda/attention.rs:65-68)
+      for (int bb = wi; bb < nb; bb += nwg)
+        if (__builtin_amdgcn_readlane(n, bb) == 0)
+          for (int e = tid; e < a_heads * HD; e += C::THREADS) {
+            const long long oi = (long long)bb * a_heads * HD + e;
+            if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = 0.f;
+            else static_cast<uint16_t *>(a.out)[oi] = 0;
+          }
+      if (wi >= total) {
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
+      }
+      // workgroup wi: sequence b (the last whose ranges start at or before
+      // it), KV head y, range r of its R_b
+      const unsigned long long le = __ballot(lane < nb && pre * ny <= wi);
+      b = __builtin_amdgcn_readfirstlane(63 - __builtin_clzll(le));
+      const int pre_b = __builtin_amdgcn_readlane(pre, b), r_b = __builtin_amdgcn_readlane(rb, b);
+      const int n_b = __builtin_amdgcn_readlane(n, b);
+      const int k = wi - pre_b * ny;
+      y = k / r_b;
+      const int r = k - y * r_b;
+      bal_ck0 = (int)((long long)r * n_b / r_b);
+      bal_nck = (int)((long long)(r + 1) * n_b / r_b) - bal_ck0;
+      bal_nparts = r_b;
+      c = r;
+    }
+  }
   const int g = y / a_ngroups, gh = y - g * a_ngroups;
   const int nh = min(HG, a_nr - gh * HG);                    // heads of this group
   const long long hq0 = (long long)b * a_heads + (long long)g * a_nr + gh * HG;  // its first q head
@@ -276,7 +334,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // split-K arrival are paid once per range.
   const int nchunks = (len + C::CHUNK - 1) / C::CHUNK;
   const int cpr = a_cpr;
-  const int ck0 = c * cpr;
+  const int ck0 = bal ? bal_ck0 : c * cpr;
   if (ck0 >= nchunks) {  // an empty range is not counted by the merge
     if (len == 0 && c == 0) {
       // an empty sequence attends to nothing: zero output (cuda/attention.rs:65-68)
@@ -289,8 +347,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     __builtin_amdgcn_s_waitcnt(0);
     return;
   }
-  const int nck = MULTI ? min(cpr, nchunks - ck0) : 1;  // chunks of this range
-  const int nparts = (nchunks + cpr - 1) / cpr;       // ranges the merge folds
+  const int nck = bal ? bal_nck : (MULTI ? min(cpr, nchunks - ck0) : 1);  // chunks of this range
+  const int nparts = bal ? bal_nparts : (nchunks + cpr - 1) / cpr;      // ranges the merge folds
 
   // ---- records.  Wave w's tokens of a chunk start at tw = chunk CHUNK +
   // w TPW.  K tile i, lane (l16, lg): token tw + 16 i + l16, for
@@ -1013,8 +1071,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // one lane add to the agent-scope counter, which is performed at the
   // coherent level.  The workgroup that reads the final count has every other
   // workgroup's increment, and so every partial, complete at that level; its
-  // merge loads are agent-scope atomic loads (sc1: they read the coherent
-  // level, never a stale L2 line), issued after the counter's value has
+  // merge loads are agent-scope loads (sc1: they read the coherent level,
+  // never a stale L2 line), issued after the counter's value has
   // returned and a barrier.  An acq_rel counter would add an L2 writeback and
   // invalidate per workgroup that this needs nowhere. ----
   if constexpr (!INLINE_MERGE) return;
@@ -1041,19 +1099,41 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   }
 }
 
+#ifndef TQ_BALANCE
+#define TQ_BALANCE 1
+#endif
+#ifndef TQ_BAL_WGS
+#define TQ_BAL_WGS 3  // at most this many balanced workgroups per compute unit
+#endif
+
 // 4-bit codes on the compiled-in MaxNorm codebook (evenly spaced) take the
 // grid key pass; a caller's codebook or the L2Norm tables, the pair table
 template <class C, bool INLINE, bool MULTI>
 void launch_stream_k(AttnArgs &a, dim3 grid, hipStream_t st, int len_hint) {
-  if constexpr (C::BITS == 4 && C::MODE == kModePqo) {
-    if (!a.cb_dev && !a.cb_args) {
-      hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, true, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx,
-                         a.v_idx, a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
-      return;
+  auto go = [&](auto kernel) {
+    if (a.bal_nwg < 0) {
+      // balanced split: as many workgroups as the compute units hold at once
+      // (this kernel's occupancy, cached per device), at most one per task
+      static int occ[64] = {};
+      int dev = 0;
+      (void)hipGetDevice(&dev);
+      dev = dev >= 0 && dev < 64 ? dev : 0;
+      if (occ[dev] == 0) {
+        int n = 0;
+        occ[dev] = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, C::THREADS, 0) == hipSuccess && n > 0
+                       ? min(n, TQ_BAL_WGS)
+                       : 2;
+      }
+      a.bal_nwg = (int)min((long long)-a.bal_nwg, (long long)occ[dev] * device_cus());
+      grid = dim3((unsigned)a.bal_nwg, 1u, 1u);
     }
+    hipLaunchKernelGGL(kernel, grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx, a.k_sc, a.v_sc, a.seq_stride,
+                       a.kv_head_stride, len_hint, a);
+  };
+  if constexpr (C::BITS == 4 && C::MODE == kModePqo) {
+    if (!a.cb_dev && !a.cb_args) return go(stream_decode_kernel<C, INLINE, true, MULTI>);
   }
-  hipLaunchKernelGGL((stream_decode_kernel<C, INLINE, false, MULTI>), grid, dim3(C::THREADS), 0, st, a.k_idx, a.v_idx,
-                     a.k_sc, a.v_sc, a.seq_stride, a.kv_head_stride, len_hint, a);
+  go(stream_decode_kernel<C, INLINE, false, MULTI>);
 }
 template <class C, bool INLINE>
 void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
@@ -1077,8 +1157,23 @@ void launch_stream_c(AttnArgs &a, dim3 grid, hipStream_t st) {
 #ifndef TQ_RANGE_WGS
 #define TQ_RANGE_WGS 2
 #endif
-    if (tasks > cus * (12 / C::WAVES))
+    if (tasks > cus * (12 / C::WAVES)) {
       a.cpr = (int)min((long long)max(chunks, 1), (tasks + TQ_RANGE_WGS * cus - 1) / (TQ_RANGE_WGS * cus));
+      // Balanced split: as many near-equal ranges as the compute units hold
+      // at once (up to TQ_BAL_WGS per unit), for one head group per KV head
+      // and at most 64 sequences (a wave holds their chunk counts).  Ragged
+      // batches then load every compute unit alike; with ranges of a fixed
+      // length, a unit that holds two full ranges of long sequences sets the
+      // time.  Measured at C4: 64.3 -> 58.6 us; 16 sequences all at 16,384
+      // tokens 66.6 -> 67.2 us.
+      if (TQ_BALANCE && a.ngroups == 1 && grid.z <= 64u) {
+        a.bal_nwg = (int)-min(tasks, (long long)1 << 30);  // negative: sized by launch_stream_k
+        a.bal_batch = (int)grid.z;
+        a.bal_ny = (int)grid.y;
+        const int len_hint = a.kv_lens ? -1 : max(a.single_len, 0);
+        return launch_stream_k<C, INLINE, true>(a, grid, st, len_hint);
+      }
+    }
   } else if constexpr (C::CHUNK < kRefPartition) {
     // The reference ABI's caller sizes its partials for 512-token partitions
     // (cuda/attention.rs:70-77): a configuration with shorter chunks takes

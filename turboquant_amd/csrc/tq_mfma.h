@@ -143,6 +143,36 @@ __device__ __forceinline__ float wave_max(float v) {
   k = max(k, dpp_i<0x143, 0xc>(k, kMin));
   return __builtin_bit_cast(float, order_key(__builtin_amdgcn_readlane(k, 63)));
 }
+// Whole-wave integer sum and max (DPP row steps, two row broadcasts, lane
+// 63 read back as a uniform), and the inclusive prefix sum over the lanes.
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += dpp_i<0x111>(v, 0);
+  v += dpp_i<0x112>(v, 0);
+  v += dpp_i<0x114>(v, 0);
+  v += dpp_i<0x118>(v, 0);
+  v += dpp_i<0x142, 0xa>(v, 0);
+  v += dpp_i<0x143, 0xc>(v, 0);
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+  constexpr int kMin = -2147483647 - 1;
+  v = max(v, dpp_i<0x111>(v, kMin));
+  v = max(v, dpp_i<0x112>(v, kMin));
+  v = max(v, dpp_i<0x114>(v, kMin));
+  v = max(v, dpp_i<0x118>(v, kMin));
+  v = max(v, dpp_i<0x142, 0xa>(v, kMin));
+  v = max(v, dpp_i<0x143, 0xc>(v, kMin));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_incl_scan_i(int v) {
+  v += dpp_i<0x111>(v, 0);  // row_shr:1 .. 8: inclusive sums inside each row of 16
+  v += dpp_i<0x112>(v, 0);
+  v += dpp_i<0x114>(v, 0);
+  v += dpp_i<0x118>(v, 0);
+  v += dpp_i<0x142, 0xa>(v, 0);  // row 15's total into rows 1 and 3
+  v += dpp_i<0x143, 0xc>(v, 0);  // lane 31's total into rows 2 and 3
+  return v;
+}
 __device__ __forceinline__ float wave_sum(float v) {
   return wave_allreduce(v, 0.f, [](float x, float y) { return x + y; });
 }
