@@ -231,6 +231,25 @@ int tq_pqo_decode_attention_noalloc(const void *q, int q_dtype, const uint8_t *k
  * qjl_signs [..records..][head_dim/8] and qjl_norms [..records..] f16 laid
  * out by record like the codes.  Replaces TqCache::decode's dequantize +
  * logit bias + SDPA (tq.rs:275-297). */
+/* tq_cache_decode_attention for TQ records (outlier_blocks 0) with the query
+ * projection rq = R q computed inside the decode launch from the sign
+ * matrix (tq_qjl_sign_matrix: row j = head_dim / 32 words, bit c set = -1)
+ * instead of a separate tq_qjl_project launch.  rq is summed in column order
+ * exactly as tq_qjl_project sums it (precompute_query_projections,
+ * qjl.rs:196-208), so the outputs are bit-identical to
+ * tq_qjl_project + tq_cache_decode_attention.  No reference counterpart as
+ * one call: replaces the projection and TqCache::decode's attention
+ * (tq.rs:185-297). */
+int tq_tq_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
+                           const uint16_t *k_scales, const uint8_t *v_indices,
+                           const uint16_t *v_scales, const uint8_t *qjl_signs,
+                           const uint16_t *qjl_norms, const uint32_t *qjl_sign_matrix,
+                           const int *kv_lens, int batch, int num_heads, int num_kv_heads,
+                           int head_dim, int bits, int norm_mode, int max_kv_len,
+                           long long kv_head_stride, long long seq_stride, float softmax_scale,
+                           void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
 int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                               const uint16_t *k_scales, const uint8_t *v_indices,
                               const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,

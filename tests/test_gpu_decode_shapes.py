@@ -383,3 +383,44 @@ def test_range_split_cases(tq, case):
         lens = np.random.default_rng(9).integers(0, 2501, size=36)
         lens[4] = 0
         _ragged_batch(tq, 36, 8, 128, 2500, 3, 2, lens, 74, qjl=True)
+
+
+def _f16_bits(x):
+    return np.asarray(x, np.float16).view(np.int16)
+
+
+@pytest.mark.parametrize("d,nr,bsz", [(64, 2, 1), (128, 8, 1), (256, 4, 1), (128, 2, 24), (256, 2, 40)])
+def test_in_launch_query_projection_bit_identical(tq, d, nr, bsz):
+    """tq_tq_decode_attention (rq = R q computed inside the decode launch from
+    the sign matrix) against tq_qjl_project + tq_cache_decode_attention: the
+    projection is summed in the same column order, so the outputs agree bit
+    for bit (single sequences and ragged batches on the balanced split)."""
+    hkv, cap, bits = 4 if bsz == 1 else 8, 1800, 3
+    h = hkv * nr
+    rng = np.random.default_rng(d * 7 + nr + bsz)
+    pd, nb = d * bits // 8, d // 32
+    # TQ records: 2-bit codes in 3-bit slots (top bit of every slot zero)
+    codes = rng.integers(0, 4, size=(2, bsz, hkv, cap, d))
+    packed = []
+    for c in codes:
+        bitsarr = np.zeros(c.shape[:-1] + (d * bits,), np.uint8)
+        for b in range(2):
+            bitsarr[..., b::bits] = (c >> b) & 1
+        packed.append(np.packbits(bitsarr, axis=-1, bitorder="little"))
+    sc = [_f16_bits(np.abs(rng.standard_normal((bsz, hkv, cap, nb))) + 0.05) for _ in range(2)]
+    sg = rng.integers(0, 256, size=(bsz, hkv, cap, d // 8), dtype=np.uint8)
+    nm = _f16_bits(np.abs(rng.standard_normal((bsz, hkv, cap))) * 0.3)
+    lens = rng.integers(0, cap + 1, size=bsz).astype(np.int32) if bsz > 1 else np.array([cap - 5], np.int32)
+    q = rng.standard_normal((bsz, h, d)).astype(np.float32) / np.float32(math.sqrt(d))
+    qd = _dev(bf16_bits(bf16_round(q))).view(torch.bfloat16)
+    rmat = tq.qjl_sign_matrix(d, 12345)
+    rq = tq.qjl_project(qd.reshape(-1, d), rmat).reshape(bsz, h, d)
+    ws = tq.AttentionWorkspace(bsz, h, hkv, d, cap)
+    args = (qd, _dev(packed[0]), _dev(sc[0]), _dev(packed[1]), _dev(sc[1]), _dev(lens), hkv, bits, cap, cap,
+            hkv * cap, 1 / math.sqrt(d), ws, 0)
+    a = tq.cache_decode_attention(*args, rq=rq, qjl_signs=_dev(sg), qjl_norms=_dev(nm))
+    b = tq.cache_decode_attention(*args, qjl_signs=_dev(sg), qjl_norms=_dev(nm), qjl_sign_matrix=rmat)
+    torch.cuda.synchronize()
+    a, b = a.cpu().numpy(), b.cpu().numpy()
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -291,3 +291,30 @@ def test_mixed_cache_dequantized_paths(tq):
         cache.decode(0, _dev(k3[None]), _dev(v3[None]), q, tq.AttendConfig(1 / math.sqrt(D), 2))
     out = cache.decode_output(0, _dev(k3[None]), _dev(v3[None]), q, tq.AttendConfig(1 / math.sqrt(D), 2))
     assert isinstance(out, tq.Dequantized) and out.result.k.shape == (1, hkv, 40, D)
+
+
+def test_tq_cache_decode_without_new_tokens_projects_in_launch(tq):
+    """A TqCache decode that appends no token (the append has no sketch
+    launch to project q in): the decode launch projects q from the sign
+    matrix itself; checked against dense attention with the QJL bias."""
+    bits, hq, hkv, t = 3, 16, 8, 900
+    rng = np.random.default_rng(91)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    cache = tq.TqCache(tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1, outlier_blocks=0))
+    qp = rng.standard_normal((hq, 1, D)).astype(np.float32)
+    cache.prefill(0, _dev(k[None]), _dev(v[None]), _dev(qp[None]))
+    q = bf16_round(rng.standard_normal((hq, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16).reshape(1, hq, 1, D)
+    scale = 1 / math.sqrt(D)
+    empty = torch.zeros((1, hkv, 0, D), dtype=torch.float32, device="cuda")
+    out = cache.decode(0, empty, empty, qd, tq.AttendConfig(scale, hq // hkv))
+    torch.cuda.synchronize()
+    assert cache.seq_len(0) == t
+    _, _, kd, rsg, rnm = _tq_cache_ref(k, bits)
+    pv, sv = orc.polar_quantize(bits, 0, v.reshape(-1, D), D)
+    vd = orc.polar_dequantize(bits, 0, pv, sv, D).reshape(hkv, t, D)
+    bias = orc.tq_logit_bias(q[:, None, :], rsg, rnm)[:, 0, :]
+    ref = orc.attention_dense_bias(q, kd, vd, bias, scale)
+    err = np.abs(_host(out.float()).reshape(hq, D) - ref).max()
+    assert err <= TOL, err

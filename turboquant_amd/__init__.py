@@ -180,11 +180,20 @@ def pqo_decode_attention(q, k_idx, k_sc, v_idx, v_sc, kv_lens, num_kv_heads, bit
 def cache_decode_attention(q, k_idx, k_sc, v_idx, v_sc, kv_lens, num_kv_heads, bits, max_kv_len, kv_head_stride,
                            seq_stride, softmax_scale, workspace: AttentionWorkspace, outlier_blocks: int,
                            rq: torch.Tensor | None = None, qjl_signs: torch.Tensor | None = None,
-                           qjl_norms: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32):
+                           qjl_norms: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
+                           qjl_sign_matrix: torch.Tensor | None = None):
     """Fused decode attention over PQO / PQ records, or TQ records with the QJL
-    correction when qjl_signs is given (rq [B, H, D] f32 = R q)."""
+    correction when qjl_signs is given (rq [B, H, D] f32 = R q; or rq None and
+    qjl_sign_matrix given: the decode launch projects the query itself)."""
     b, h, hd = q.shape
     out = torch.empty((b, h, hd), dtype=out_dtype, device=q.device)
+    if rq is None and qjl_sign_matrix is not None:
+        check(lib.tq_tq_decode_attention(_ptr(q), _DT[q.dtype], _ptr(k_idx), _ptr(k_sc), _ptr(v_idx), _ptr(v_sc),
+                                         _ptr(qjl_signs), _ptr(qjl_norms), _ptr(qjl_sign_matrix), _ptr(kv_lens), b,
+                                         h, num_kv_heads, hd, bits, TQ_NORM_MAXNORM, max_kv_len, kv_head_stride,
+                                         seq_stride, float(softmax_scale), _ptr(out), _DT[out.dtype],
+                                         _ptr(workspace.buf), workspace.nbytes, _stream()))
+        return out
     check(lib.tq_cache_decode_attention(_ptr(q), _DT[q.dtype], _ptr(k_idx), _ptr(k_sc), _ptr(v_idx), _ptr(v_sc),
                                         _ptr(rq), _ptr(qjl_signs), _ptr(qjl_norms), _ptr(kv_lens), b, h,
                                         num_kv_heads, hd, bits, int(outlier_blocks), TQ_NORM_MAXNORM, max_kv_len,

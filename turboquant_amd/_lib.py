@@ -65,6 +65,8 @@ SIGNATURES = {
     "tq_polar_dequantize_from_cache": (_i, [_p, _p, _ll, _i, _i, _p, _i, _i, _i, _sz, _i, _p]),
     "tq_cache_decode_attention": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _sz, _i, _i,
                                        _ll, _ll, _f, _p, _i, _p, _sz, _p]),
+    "tq_tq_decode_attention": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _ll, _ll,
+                                    _f, _p, _i, _p, _sz, _p]),
     "tq_qjl_sign_matrix": (_i, [_p, _i, _u64, _p]),
     "tq_cache_prefill_attention": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _sz, _i, _i, _ll, _i,
                                         _f, _p, _i, _p]),

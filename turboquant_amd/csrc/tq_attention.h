@@ -88,6 +88,11 @@ struct AttnArgs {
   const uint32_t *qjl_signs;
   const uint16_t *qjl_norms;
   float qjl_c;
+  // TQ without rq: the sign matrix (row j: head_dim / 32 words, bit c set =
+  // -1, tq_qjl_sign_matrix) and 1 / sqrt(head_dim); the decode computes rq
+  // = R q itself, summed in column order as tq_qjl_project (qjl.rs:196-208)
+  const uint32_t *rmat;
+  float qjl_inv;
   // cb_args: the codebook comes from cb (L2Norm tables) instead of the
   // MaxNorm constants compiled in
   int cb_args;

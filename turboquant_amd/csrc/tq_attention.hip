@@ -242,7 +242,8 @@ int decode_attention_ws(const void *q, int q_dtype, const uint8_t *k_indices, co
                         const uint16_t *qjl_norms, const int *kv_lens, int host_len, int batch, int num_heads,
                         int num_kv_heads, int head_dim, int bits, size_t outlier_blocks, int norm_mode,
                         int max_kv_len, long long kv_head_stride, long long seq_stride, float softmax_scale, void *out,
-                        int out_dtype, const DecodeWs *wsd, size_t workspace_bytes, hipStream_t stream);
+                        int out_dtype, const DecodeWs *wsd, size_t workspace_bytes, hipStream_t stream,
+                        const uint32_t *rmat = nullptr);
 
 }  // namespace
 
@@ -254,12 +255,12 @@ int tqh::decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, 
                           int batch, int num_heads, int num_kv_heads, int head_dim, int bits, size_t outlier_blocks,
                           int norm_mode, int max_kv_len, long long kv_head_stride, long long seq_stride,
                           float softmax_scale, void *out, int out_dtype, void *workspace, size_t workspace_bytes,
-                          hipStream_t stream) {
+                          hipStream_t stream, const uint32_t *rmat) {
   const DecodeWs d = caller_ws(workspace, workspace_bytes);
   return decode_attention_ws(q, q_dtype, k_indices, k_scales, v_indices, v_scales, rq, qjl_signs, qjl_norms, kv_lens,
                              host_len, batch, num_heads, num_kv_heads, head_dim, bits, outlier_blocks, norm_mode,
                              max_kv_len, kv_head_stride, seq_stride, softmax_scale, out, out_dtype,
-                             workspace ? &d : nullptr, workspace_bytes, stream);
+                             workspace ? &d : nullptr, workspace_bytes, stream, rmat);
 }
 
 namespace {
@@ -269,7 +270,8 @@ int decode_attention_ws(const void *q, int q_dtype, const uint8_t *k_indices, co
                         const uint16_t *qjl_norms, const int *kv_lens, int host_len, int batch, int num_heads,
                         int num_kv_heads, int head_dim, int bits, size_t outlier_blocks, int norm_mode,
                         int max_kv_len, long long kv_head_stride, long long seq_stride, float softmax_scale, void *out,
-                        int out_dtype, const DecodeWs *wsd, size_t workspace_bytes, hipStream_t stream) {
+                        int out_dtype, const DecodeWs *wsd, size_t workspace_bytes, hipStream_t stream,
+                        const uint32_t *rmat) {
   int rc = check_common(num_heads, num_kv_heads, head_dim, bits, max_kv_len);
   if (rc) return rc;
   tqh::PolarCodec codec;
@@ -292,7 +294,8 @@ int decode_attention_ws(const void *q, int q_dtype, const uint8_t *k_indices, co
   if (!q || !k_indices || !k_scales || !v_indices || !v_scales || !out)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null pointer");
   if (!kv_lens && host_len < 0) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "null kv_lens");
-  if (qjl && (!rq || !qjl_norms)) return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL needs rq, signs and norms");
+  if (qjl && ((!rq && !rmat) || !qjl_norms))
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "QJL needs rq (or the sign matrix), signs and norms");
   if (kv_head_stride < max_kv_len)
     return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "kv_head_stride %lld < max_kv_len %d", kv_head_stride, max_kv_len);
   if (batch > 1 && seq_stride < (long long)num_kv_heads * kv_head_stride)
@@ -336,6 +339,8 @@ int decode_attention_ws(const void *q, int q_dtype, const uint8_t *k_indices, co
   a.out = out;
   a.out_dtype = out_dtype;
   a.rq = rq;
+  a.rmat = rq ? nullptr : rmat;
+  a.qjl_inv = tqh::inv_sqrt_dim(head_dim);
   a.qjl_signs = reinterpret_cast<const uint32_t *>(qjl_signs);
   a.qjl_norms = qjl_norms;
   a.qjl_c = tq_qjl_bias_scale(head_dim);
@@ -365,6 +370,21 @@ extern "C" int tq_cache_decode_attention(const void *q, int q_dtype, const uint8
                                max_kv_len, batch, num_heads, num_kv_heads, head_dim, bits, outlier_blocks, norm_mode,
                                max_kv_len, kv_head_stride, seq_stride, softmax_scale, out, out_dtype, workspace,
                                workspace_bytes, stream);
+}
+
+extern "C" int tq_tq_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,
+                                      const uint8_t *v_indices, const uint16_t *v_scales, const uint8_t *qjl_signs,
+                                      const uint16_t *qjl_norms, const uint32_t *qjl_sign_matrix, const int *kv_lens,
+                                      int batch, int num_heads, int num_kv_heads, int head_dim, int bits,
+                                      int norm_mode, int max_kv_len, long long kv_head_stride, long long seq_stride,
+                                      float softmax_scale, void *out, int out_dtype, void *workspace,
+                                      size_t workspace_bytes, hipStream_t stream) {
+  if (!qjl_signs || !qjl_sign_matrix)
+    return tqh::fail(TQ_ERR_INVALID_ARGUMENT, "TQ decode needs the QJL signs and the sign matrix");
+  return tqh::decode_attention(q, q_dtype, k_indices, k_scales, v_indices, v_scales, nullptr, qjl_signs, qjl_norms,
+                               kv_lens, max_kv_len, batch, num_heads, num_kv_heads, head_dim, bits, 0, norm_mode,
+                               max_kv_len, kv_head_stride, seq_stride, softmax_scale, out, out_dtype, workspace,
+                               workspace_bytes, stream, qjl_sign_matrix);
 }
 
 extern "C" int tq_pqo_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const uint16_t *k_scales,

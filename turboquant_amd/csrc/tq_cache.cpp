@@ -270,16 +270,20 @@ class KvCache {
       rc = tq_attention_workspace_init(ws_, ws_bytes_, 1, num_q_heads, heads_, head_dim_, (int)L.cap, stream);
       if (rc) return rc;
     }
-    if (mode_.qjl && !rq_ready) {
-      rc = project(q, q_dtype, (size_t)num_q_heads, stream);
+    // a TqCache whose append did not project q (no token appended): the
+    // decode launch projects it from the sign matrix
+    const bool in_launch = mode_.qjl && !rq_ready;
+    if (in_launch) {
+      rc = sign_matrix(stream);
       if (rc) return rc;
     }
     // the length is known here: the kernel reads none from memory
     return tqh::decode_attention(q, q_dtype, L.k_idx, L.k_sc, L.v_idx, L.v_sc,
-                                 mode_.qjl ? static_cast<const float *>(rq_) : nullptr,
+                                 mode_.qjl && !in_launch ? static_cast<const float *>(rq_) : nullptr,
                                  mode_.qjl ? L.signs : nullptr, mode_.qjl ? L.norms : nullptr, nullptr, (int)L.seq, 1,
                                  num_q_heads, heads_, head_dim_, mode_.bits, mode_.outlier_blocks, mode_.norm_mode,
-                                 (int)L.cap, (long long)L.cap, 0, scale, out, out_dtype, ws_, ws_bytes_, stream);
+                                 (int)L.cap, (long long)L.cap, 0, scale, out, out_dtype, ws_, ws_bytes_, stream,
+                                 in_launch ? static_cast<const uint32_t *>(rmat_) : nullptr);
   }
 
   // multi-query attention of q [num_q_heads][q_len][head_dim] over the whole

@@ -131,4 +131,10 @@ DivThresholds div_thresholds(const float *b, int nb, float outer) {
   return t;
 }
 
+float inv_sqrt_dim(int dim) {
+  volatile float fd = (float)dim;  // each step rounded to f32, as the reference's f32 arithmetic
+  volatile float sq = sqrtf(fd);
+  return 1.0f / sq;
+}
+
 }  // namespace tqh

@@ -68,7 +68,11 @@ int decode_attention(const void *q, int q_dtype, const uint8_t *k_indices, const
                      const uint16_t *qjl_norms, const int *kv_lens, int host_len, int batch, int num_heads,
                      int num_kv_heads, int head_dim, int bits, size_t outlier_blocks, int norm_mode, int max_kv_len,
                      long long kv_head_stride, long long seq_stride, float softmax_scale, void *out, int out_dtype,
-                     void *workspace, size_t workspace_bytes, hipStream_t stream);
+                     void *workspace, size_t workspace_bytes, hipStream_t stream, const uint32_t *rmat = nullptr);
+
+// fl(1 / fl(sqrt(dim))): the QJL projection's scale (1 / sqrt(d), qjl.rs),
+// each step rounded to f32.
+float inv_sqrt_dim(int dim);
 
 // Per-boundary constants of the exact division threshold (see
 // tqd::div_threshold): mu = midpoint of b and nextup(b), strict = b even.

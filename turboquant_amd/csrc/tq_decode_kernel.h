@@ -291,6 +291,8 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   constexpr int QIT = (QE + C::THREADS - 1) / C::THREADS;
   uint32_t qbits[QIT];
   float rqv[QIT];
+  // TQ without rq: the sign words of R's row for each of the lane's elements
+  uint32_t rsw[C::QJL ? QIT : 1][C::QJL ? NQB : 1];
 #pragma unroll
   for (int k = 0; k < QIT; k++) {
     const int e = tid + C::THREADS * k, hl = e / HD;
@@ -300,7 +302,16 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       const long long qi = hq0 * HD + e;
       if (a_qdt == kF32) qbits[k] = static_cast<const uint32_t *>(a_q)[qi];
       else qbits[k] = static_cast<const uint16_t *>(a_q)[qi];
-      if constexpr (C::QJL) rqv[k] = a_rq[qi];
+      if constexpr (C::QJL) {
+        if (a_rq) rqv[k] = a_rq[qi];
+      }
+    }
+    if constexpr (C::QJL) {
+      if (!a_rq) {
+        const uint32_t *row = a.rmat + (e % HD) * NQB;
+#pragma unroll
+        for (int w = 0; w < NQB; w++) rsw[k][w] = e < QE ? row[w] : 0u;
+      }
     }
   }
   // the caller's decode sign for this lane (selected at its use: a select
@@ -493,6 +504,40 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     if (tid < 16) {
       auto pm1 = [&](int bit) { return ((tid >> bit) & 1) ? 0x3C00u : 0xBC00u; };
       s_nib[tid] = make_uint2(pm1(0) | (pm1(1) << 16), pm1(2) | (pm1(3) << 16));
+    }
+  }
+  if constexpr (C::QJL) {
+    if (!a_rq) {
+      // rq = R q (precompute_query_projections, qjl.rs:196-208) in the
+      // launch: the raw query staged in s_rq (free until the scaled rq is
+      // written below), each element's row summed in column order from -0.0
+      // with exact +-1 products, as tq_qjl_project sums it (bit-identical)
+#pragma unroll
+      for (int k = 0; k < QIT; k++) {
+        const int e = tid + C::THREADS * k;
+        if (e < QE) s_rq[e] = q_value(qbits[k], a_qdt);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < QIT; k++) {
+        const int e = tid + C::THREADS * k;
+        if (e < QE) {
+          const float4 *row = reinterpret_cast<const float4 *>(s_rq + (e / HD) * HD);
+          float acc = -0.0f;
+#pragma unroll
+          for (int c4 = 0; c4 < HD / 4; c4++) {
+            const float4 v = row[c4];
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const int col = 4 * c4 + i;
+              acc = __builtin_fmaf(((rsw[k][col >> 5] >> (col & 31)) & 1u) ? -1.0f : 1.0f, vv[i], acc);
+            }
+          }
+          rqv[k] = acc * a.qjl_inv;
+        }
+      }
+      __syncthreads();  // s_rq is rewritten below
     }
   }
   // ---- rotated, scaled query: 32-lane butterflies (elements of a qblock sit

@@ -848,11 +848,7 @@ extern "C" int tq_qjl_weighted_values(const uint8_t *polar_packed, const uint16_
 // ---------------------------------------------------------------------------
 
 namespace {
-float inv_sqrt_dim(int dim) {
-  volatile float fd = (float)dim;
-  volatile float sq = sqrtf(fd);
-  return 1.0f / sq;
-}
+float inv_sqrt_dim(int dim) { return tqh::inv_sqrt_dim(dim); }
 int check_sketch_dim(int dim) {
   if (dim != 64 && dim != 128 && dim != 256)
     return tqh::fail(TQ_ERR_INVALID_DIMENSION, "cache QJL kernels take head_dim 64, 128 or 256 (got %d)", dim);
