@@ -135,3 +135,37 @@ def test_prefill_bench_shape_sampled_rows(tq):
         ref = orc.attention_prefill(qf[:, p:p + 1], kd[:, :p + 1], vd[:, :p + 1], scale, False)
         err = np.abs(out[:, p:p + 1] - ref).max()
         assert err <= TOL, (p, err)
+
+
+@pytest.mark.parametrize("bits,outlier,hq,hkv,ql,t,causal", [
+    (3, orc.OUTLIER_ALL, 16, 8, 300, 300, True),
+    (4, orc.OUTLIER_ALL, 32, 8, 270, 333, True),
+    (3, 0, 16, 16, 260, 260, False),
+    (4, 0, 8, 2, 400, 1000, True),
+    (3, orc.OUTLIER_ALL, 16, 4, 513, 577, False),
+])
+def test_staged_tiles_bit_identical(tq, monkeypatch, bits, outlier, hq, hkv, ql, t, causal):
+    """Tiles decoded once by the staging pass and copied into each
+    workgroup's LDS give the same bits as tiles decoded in every workgroup
+    (TQ_PREFILL_STAGING forces either path); both within TOL of the oracle.
+    Shapes: GQA 1, 2, 4 and 8, 3 and 4 bits, PQ and PQO codes, token counts
+    that end inside a tile, queries after earlier tokens."""
+    rng = np.random.default_rng(1700 + t + ql)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    cap = t + 3
+    ki, ks, kd = _records(bits, outlier, k, cap)
+    vi, vs, vd = _records(bits, outlier, v, cap)
+    q = bf16_round(rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    scale = 1 / math.sqrt(D)
+    outs = []
+    for mode in ("0", "1"):
+        monkeypatch.setenv("TQ_PREFILL_STAGING", mode)
+        outs.append(tq.cache_prefill_attention(qd, ki, ks, vi, vs, hkv, bits, t, cap, scale, outlier,
+                                               causal=causal))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = orc.attention_prefill(q, kd, vd, scale, causal)
+    err = np.abs(outs[1].cpu().numpy() - ref).max()
+    assert err <= TOL, err

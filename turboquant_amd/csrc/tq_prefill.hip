@@ -23,10 +23,22 @@
 //                        lane and block), the V operand read through the
 //                        transposing LDS read, V hi/lo x P hi/lo (three
 //                        products, lo x lo dropped)
-// with an online base-2 softmax per row.  Values stay in the rotated
-// domain; each row is inverse-rotated once at the end.  Two tile buffers:
-// tile t + 1 is decoded while tile t is computed (one barrier per tile), and
-// the records of tile t + 2 are fetched meanwhile.
+// with an online base-2 softmax per row.  The four 16-token blocks of the
+// key pass and pairs of 16-element blocks of the value pass run as
+// independent accumulator chains, interleaved (each accumulator still sums
+// its products in the same order).  Values stay in the rotated domain; each
+// row is inverse-rotated once at the end.  Two tile buffers: tile t + 1 is
+// decoded while tile t is computed (one barrier per tile), and the records of
+// tile t + 2 are fetched meanwhile.
+//
+// Staged tiles (PQ/PQO codes, 4 or more query blocks per KV head): the query
+// blocks of a KV head would each decode every tile again, so a staging pass
+// (the same kernel, one workgroup per tile and KV head) decodes each tile
+// once and stores the tile buffer's LDS image, and the attention workgroups
+// copy the images into LDS in place of decoding; the LDS contents, and so the
+// outputs, are bit-identical.  The workgroup order puts every query block of
+// KV head g on one XCD (g = linear index mod 8), so a head's images are read
+// from one L2.
 #include "tq_common.h"
 #include "tq_device.h"
 #include "tq_mfma.h"
@@ -64,6 +76,14 @@ __device__ __forceinline__ int vchunk(int c) { return c ^ ((c >> 3) & 1); }
 // would otherwise all start in one bank)
 constexpr int kQRow = 128 + 8;  // halves
 constexpr int kORow = 128 + 4;  // floats
+
+// Query blocks per KV head from which the tiles are decoded once, in a
+// staging pass, instead of in every workgroup
+constexpr int kStagingMinQueryBlocks = 4;
+// A staged tile image: the tile buffer's K rows and V planes, the per-token
+// 2^E_k and 2^E_v factors, and the 8 waves' V exponent maxima, in 16-byte chunks
+constexpr int kTileChunks = (kTile * kKStride * 2 + kTile * kVRow) / 4;
+constexpr int kImgChunks = kTileChunks + kTile / 2 + 2;
 
 // Stores 32 values split into f16 hi (11 significant bits) and lo (the
 // exact remainder) at hi[0..31] and lo[0..31], 16 bytes per store.
@@ -107,9 +127,18 @@ struct PrefillArgs {
   int out_dtype;
   int cb_args;               // codebook from cb (L2Norm) instead of the MaxNorm constants
   float cb[16];
+  // staged decode: per KV head, stage_tiles tile images of kImgChunks 16-byte
+  // chunks (the LDS contents of one decoded tile)
+  const uint4 *stage;
+  uint4 *stage_out;
+  int stage_tiles;
 };
 
-template <int BITS, int MODE, int NR>
+// Kernel phases: decode every tile in the workgroup (kDecode); read the tiles
+// as images that kStage wrote, one per tile and KV head (kStaged)
+enum PPhase : int { kDecode = 0, kStaged = 1, kStage = 2 };
+
+template <int BITS, int MODE, int NR, int PH>
 __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(PrefillArgs a) {
   constexpr int CB = MODE == kPPqo ? BITS : BITS - 1;
   constexpr bool QJL = MODE == kPTq;
@@ -129,7 +158,11 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // two tile buffers: tile t + 1 is decoded into one while tile t is read
   // from the other
   constexpr int TILE_WORDS = K_WORDS + V_WORDS;
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[2 * TILE_WORDS];
+  static_assert(PH == kDecode || (!QJL && NW == 8), "staged tiles: PQ/PQO codes, 8 waves");
+  static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kTile / 2 + NW / 4 == kImgChunks - kTileChunks),
+                "the tile image is the LDS tile buffer plus its exponent arrays");
+  // the staging pass decodes into one buffer
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[(PH == kStage ? 1 : 2) * TILE_WORDS];
   // per-token and per-wave scalars, read 4 at a time
   __shared__ __attribute__((aligned(16))) float s_ek[2][kTile];  // 2^E_k per token (key exponent folded out)
   __shared__ __attribute__((aligned(16))) float s_ev[2][kTile];  // 2^E_v per token (V exponent folded out)
@@ -152,7 +185,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // before it): the short blocks fill in at the end instead of the long ones
   // starting last.
   int g = blockIdx.y, qblk = blockIdx.x;
-  if (a.causal) {
+  if (PH != kStage && a.causal) {
     const int lin = blockIdx.y * gridDim.x + blockIdx.x;
     g = lin % gridDim.y;
     qblk = (int)gridDim.x - 1 - lin / (int)gridDim.y;
@@ -161,7 +194,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const long long rec0 = (long long)g * a.kv_head_stride;
   const float lscale = a.softmax_scale * kLog2e;
 
-  if (tid < 16) {
+  if (PH != kStaged && tid < 16) {
     constexpr int CM = (1 << CB) - 1;
     float c = a.cb[0];
     if (a.cb_args) {
@@ -173,6 +206,164 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     s_cb[tid] = c;
     auto pm1 = [&](int bit) { return ((tid >> bit) & 1) ? 0x3C00u : 0xBC00u; };
     s_nib[tid] = make_uint2(pm1(0) | (pm1(1) << 16), pm1(2) | (pm1(3) << 16));
+  }
+
+  // thread (token, qblock) fetches one record of K and V per tile
+  // thread (token, qblock, part): wave w decodes tokens 16 (w / SPLIT) ..
+  // + 15, code pairs NP (w % SPLIT) .. + NP - 1 of every qblock
+  const int ftok = 16 * (wave / SPLIT) + (lane >> 2), fqb = lane & 3, fpart = wave % SPLIT;
+  uint32_t kw[QW], vw[QW], sgw = 0;
+  uint16_t ks = 0, vs = 0, nm = 0;
+  // staged: thread tid moves chunks tid + 4 kRows r of a tile image
+  constexpr int IMG_ROUNDS = (kImgChunks + 4 * kRows - 1) / (4 * kRows);
+  // (native vectors: an array of uint4 structs stays in scratch memory)
+  u32x4 img[PH == kStaged ? IMG_ROUNDS : 1];
+  auto fetch = [&](int t0) {
+    if constexpr (PH == kStaged) {
+      const u32x4 *src =
+          reinterpret_cast<const u32x4 *>(a.stage) + ((long long)g * a.stage_tiles + t0 / kTile) * kImgChunks + tid;
+#pragma unroll
+      for (int r = 0; r < IMG_ROUNDS; r++)
+        if (r + 1 < IMG_ROUNDS || tid + 4 * kRows * r < kImgChunks) img[r] = src[4 * kRows * r];
+      return;
+    }
+    const int t = min(t0 + ftok, a.kv_len - 1);
+    const long long rec = rec0 + t;
+#pragma unroll
+    for (int w = 0; w < QW; w++) {
+      kw[w] = reinterpret_cast<const uint32_t *>(a.k_idx + rec * PACKED + fqb * 4 * QW)[w];
+      vw[w] = reinterpret_cast<const uint32_t *>(a.v_idx + rec * PACKED + fqb * 4 * QW)[w];
+    }
+    ks = a.k_sc[rec * 4 + fqb];
+    vs = a.v_sc[rec * 4 + fqb];
+    if constexpr (QJL) {
+      sgw = a.signs[rec * 4 + fqb];
+      nm = a.norms[rec];
+    }
+  };
+  // buffer b: K tile at s_tile + b TILE_WORDS, V hi plane after it, lo plane
+  // after that
+  auto ktile = [&](int b) { return reinterpret_cast<uint2 *>(s_tile + b * TILE_WORDS); };
+  auto vhi = [&](int b) { return reinterpret_cast<_Float16 *>(s_tile + b * TILE_WORDS + K_WORDS); };
+  static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
+  static_assert((QJL ? 2 : 1) * kRows * kQRow <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
+  static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
+
+  // chunk c of tile buffer b's image: the K tile and V planes, then the
+  // per-token K and V exponent factors, then the waves' V exponent maxima
+  auto img_chunk = [&](int b, int c) -> uint4 * {
+    if (c < kTileChunks) return reinterpret_cast<uint4 *>(s_tile + b * TILE_WORDS) + c;
+    if (c < kTileChunks + kTile / 4) return reinterpret_cast<uint4 *>(s_ek[b]) + (c - kTileChunks);
+    if (c < kTileChunks + kTile / 2) return reinterpret_cast<uint4 *>(s_ev[b]) + (c - kTileChunks - kTile / 4);
+    return reinterpret_cast<uint4 *>(s_evw[b]) + (c - kTileChunks - kTile / 2);
+  };
+
+  // ---- decode this thread's record into tile buffer b (staged: store the
+  // fetched image chunks) ----
+  auto decode_tile = [&](int b) {
+    if constexpr (PH == kStaged) {
+#pragma unroll
+      for (int r = 0; r < IMG_ROUNDS; r++) {
+        const int c = tid + 4 * kRows * r;
+        if (r + 1 < IMG_ROUNDS || c < kImgChunks) *reinterpret_cast<u32x4 *>(img_chunk(b, c)) = img[r];
+      }
+      return;
+    }
+    uint2 *kt = ktile(b);
+    _Float16 *vth = vhi(b), *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
+    {
+      const float sk = fabsf(f16_to_f32(ks)), sv = fabsf(f16_to_f32(vs));
+      float mk = fmaxf(sk, dpp_quad_xor1(sk));
+      mk = fmaxf(mk, dpp_quad_xor2(mk));
+      float mv = fmaxf(sv, dpp_quad_xor1(sv));
+      mv = fmaxf(mv, dpp_quad_xor2(mv));
+      const int ek = pow2_exponent(mk), ev = pow2_exponent(mv);
+      const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
+      if (fqb == 0 && fpart == 0) {
+        s_ek[b][ftok] = exp2i(ek);
+        s_ev[b][ftok] = exp2i(ev);
+        if constexpr (QJL) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
+      }
+      {
+        const float wm = wave_max((float)ev);  // exact: |ev| <= 100
+        if (lane == 0) s_evw[b][wave] = (int)wm;
+      }
+      if constexpr (QJL) s_sg[b][ftok * 4 + fqb] = sgw;
+      // this thread's code pairs P0 .. P0 + NP - 1 (a wave-uniform part, so
+      // every pair index folds to a constant)
+      auto decode_pairs = [&](auto p0c) {
+        constexpr int P0 = decltype(p0c)::value;
+        // every codebook value of the K and V codes first (the reads go out
+        // together instead of in dependent groups), then the products
+        constexpr uint32_t SM = (1u << BITS) - 1u, CMk = (1u << CB) - 1u;
+        float ck[2 * NP], cv[2 * NP];
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+          const uint32_t code = pair_code<BITS>(kw, P0 + pp);
+          ck[2 * pp] = s_cb[code & SM & CMk];
+          ck[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
+        }
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+          const uint32_t code = pair_code<BITS>(vw, P0 + pp);
+          cv[2 * pp] = s_cb[code & SM & CMk];
+          cv[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
+        }
+        uint32_t hw[NP], lw[NP];
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+          const float x0 = ck[2 * pp] * kf, x1 = ck[2 * pp + 1] * kf;
+          hw[pp] = pack_f16(x0, x1);
+          lw[pp] = pack_rem(x0, x1, hw[pp], mone);
+        }
+        // 8-element groups of qblock fqb: chunk 8 fqb + 2 g holds the hi
+        // halves, the next chunk the lo halves
+        uint4 *krow = reinterpret_cast<uint4 *>(kt + ftok * kKStride);
+#pragma unroll
+        for (int i = 0; i < NP / 4; i++) {
+          const int c = 8 * fqb + 2 * (P0 / 4 + i);
+          krow[kchunk(c)] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
+          krow[kchunk(c + 1)] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
+        }
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+          const float x0 = cv[2 * pp] * vf, x1 = cv[2 * pp + 1] * vf;
+          hw[pp] = pack_f16(x0, x1);
+          lw[pp] = pack_rem(x0, x1, hw[pp], mone);
+        }
+        // token-major rows: this thread's 2 NP elements, 16-byte stores per plane
+        _Float16 *vrh = vth + ftok * kVRow, *vrl = vtl + ftok * kVRow;
+#pragma unroll
+        for (int i = 0; i < NP / 4; i++) {
+          const int c = 8 * vchunk(4 * fqb + P0 / 4 + i);
+          *reinterpret_cast<uint4 *>(vrh + c) = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
+          *reinterpret_cast<uint4 *>(vrl + c) = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
+        }
+      };
+      if constexpr (SPLIT == 1) {
+        decode_pairs(std::integral_constant<int, 0>{});
+      } else {
+        if (fpart == 0) decode_pairs(std::integral_constant<int, 0>{});
+        else decode_pairs(std::integral_constant<int, NP>{});
+      }
+    }
+  };
+
+  // ---- staging pass: decode tile blockIdx.x of KV head g once and store the
+  // buffer's image for the attention workgroups of every query block ----
+  if constexpr (PH == kStage) {
+    const int t0 = (int)blockIdx.x * kTile;
+    fetch(t0);
+    __syncthreads();  // codebook staged
+    decode_tile(0);
+    __syncthreads();
+    u32x4 *dst = reinterpret_cast<u32x4 *>(a.stage_out) + ((long long)g * a.stage_tiles + blockIdx.x) * kImgChunks;
+#pragma unroll
+    for (int r = 0; r < IMG_ROUNDS; r++) {
+      const int c = tid + 4 * kRows * r;
+      if (c < kImgChunks) dst[c] = *reinterpret_cast<const u32x4 *>(img_chunk(0, c));
+    }
+    return;
   }
 
   // ---- query rows: thread (row, quarter) rotates one 32-element block ----
@@ -281,27 +472,6 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const int kv_end = a.causal ? min(a.kv_len, a.kv_len - a.q_len + last_q + 1) : a.kv_len;
   const int ntiles = (kv_end + kTile - 1) / kTile;
 
-  // thread (token, qblock) fetches one record of K and V per tile
-  // thread (token, qblock, part): wave w decodes tokens 16 (w / SPLIT) ..
-  // + 15, code pairs NP (w % SPLIT) .. + NP - 1 of every qblock
-  const int ftok = 16 * (wave / SPLIT) + (lane >> 2), fqb = lane & 3, fpart = wave % SPLIT;
-  uint32_t kw[QW], vw[QW], sgw = 0;
-  uint16_t ks = 0, vs = 0, nm = 0;
-  auto fetch = [&](int t0) {
-    const int t = min(t0 + ftok, a.kv_len - 1);
-    const long long rec = rec0 + t;
-#pragma unroll
-    for (int w = 0; w < QW; w++) {
-      kw[w] = reinterpret_cast<const uint32_t *>(a.k_idx + rec * PACKED + fqb * 4 * QW)[w];
-      vw[w] = reinterpret_cast<const uint32_t *>(a.v_idx + rec * PACKED + fqb * 4 * QW)[w];
-    }
-    ks = a.k_sc[rec * 4 + fqb];
-    vs = a.v_sc[rec * 4 + fqb];
-    if constexpr (QJL) {
-      sgw = a.signs[rec * 4 + fqb];
-      nm = a.norms[rec];
-    }
-  };
   if (ntiles > 0) fetch(0);
 
   float m_run = -INFINITY, l_run = 0.f;
@@ -310,95 +480,6 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
   for (int eb = 0; eb < 8; eb++) o[eb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // buffer b: K tile at s_tile + b TILE_WORDS, V hi plane after it, lo plane
-  // after that
-  auto ktile = [&](int b) { return reinterpret_cast<uint2 *>(s_tile + b * TILE_WORDS); };
-  auto vhi = [&](int b) { return reinterpret_cast<_Float16 *>(s_tile + b * TILE_WORDS + K_WORDS); };
-  static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
-  static_assert((QJL ? 2 : 1) * kRows * kQRow <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
-  static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
-
-  // ---- decode this thread's record into tile buffer b ----
-  auto decode_tile = [&](int b) {
-    uint2 *kt = ktile(b);
-    _Float16 *vth = vhi(b), *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
-    {
-      const float sk = fabsf(f16_to_f32(ks)), sv = fabsf(f16_to_f32(vs));
-      float mk = fmaxf(sk, dpp_quad_xor1(sk));
-      mk = fmaxf(mk, dpp_quad_xor2(mk));
-      float mv = fmaxf(sv, dpp_quad_xor1(sv));
-      mv = fmaxf(mv, dpp_quad_xor2(mv));
-      const int ek = pow2_exponent(mk), ev = pow2_exponent(mv);
-      const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
-      if (fqb == 0 && fpart == 0) {
-        s_ek[b][ftok] = exp2i(ek);
-        s_ev[b][ftok] = exp2i(ev);
-        if constexpr (QJL) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
-      }
-      {
-        const float wm = wave_max((float)ev);  // exact: |ev| <= 100
-        if (lane == 0) s_evw[b][wave] = (int)wm;
-      }
-      if constexpr (QJL) s_sg[b][ftok * 4 + fqb] = sgw;
-      // this thread's code pairs P0 .. P0 + NP - 1 (a wave-uniform part, so
-      // every pair index folds to a constant)
-      auto decode_pairs = [&](auto p0c) {
-        constexpr int P0 = decltype(p0c)::value;
-        // every codebook value of the K and V codes first (the reads go out
-        // together instead of in dependent groups), then the products
-        constexpr uint32_t SM = (1u << BITS) - 1u, CMk = (1u << CB) - 1u;
-        float ck[2 * NP], cv[2 * NP];
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++) {
-          const uint32_t code = pair_code<BITS>(kw, P0 + pp);
-          ck[2 * pp] = s_cb[code & SM & CMk];
-          ck[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
-        }
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++) {
-          const uint32_t code = pair_code<BITS>(vw, P0 + pp);
-          cv[2 * pp] = s_cb[code & SM & CMk];
-          cv[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
-        }
-        uint32_t hw[NP], lw[NP];
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++) {
-          const float x0 = ck[2 * pp] * kf, x1 = ck[2 * pp + 1] * kf;
-          hw[pp] = pack_f16(x0, x1);
-          lw[pp] = pack_rem(x0, x1, hw[pp], mone);
-        }
-        // 8-element groups of qblock fqb: chunk 8 fqb + 2 g holds the hi
-        // halves, the next chunk the lo halves
-        uint4 *krow = reinterpret_cast<uint4 *>(kt + ftok * kKStride);
-#pragma unroll
-        for (int i = 0; i < NP / 4; i++) {
-          const int c = 8 * fqb + 2 * (P0 / 4 + i);
-          krow[kchunk(c)] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
-          krow[kchunk(c + 1)] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
-        }
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++) {
-          const float x0 = cv[2 * pp] * vf, x1 = cv[2 * pp + 1] * vf;
-          hw[pp] = pack_f16(x0, x1);
-          lw[pp] = pack_rem(x0, x1, hw[pp], mone);
-        }
-        // token-major rows: this thread's 2 NP elements, 16-byte stores per plane
-        _Float16 *vrh = vth + ftok * kVRow, *vrl = vtl + ftok * kVRow;
-#pragma unroll
-        for (int i = 0; i < NP / 4; i++) {
-          const int c = 8 * vchunk(4 * fqb + P0 / 4 + i);
-          *reinterpret_cast<uint4 *>(vrh + c) = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
-          *reinterpret_cast<uint4 *>(vrl + c) = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
-        }
-      };
-      if constexpr (SPLIT == 1) {
-        decode_pairs(std::integral_constant<int, 0>{});
-      } else {
-        if (fpart == 0) decode_pairs(std::integral_constant<int, 0>{});
-        else decode_pairs(std::integral_constant<int, NP>{});
-      }
-    }
-  };
   if (ntiles > 0) {
     decode_tile(0);
     if (ntiles > 1) fetch(kTile);  // each tile's records arrive during the tile before
@@ -424,18 +505,29 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     // the sequence) is visible to every row: no per-element mask
     const bool open = t0 + kTile <= a.kv_len && (!a.causal || t0 + kTile - 1 <= qmin);
     float x[4][4];
+    f32x4 dk[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) dk[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      u32x4 ah[4], al[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) {
+        const uint4 *krow = reinterpret_cast<const uint4 *>(kt + (16 * tb + l16) * kKStride);
+        const uint4 kh = krow[kchunk(8 * s + 2 * lg)], kl = krow[kchunk(8 * s + 2 * lg + 1)];
+        ah[tb] = u32x4{kh.x, kh.y, kh.z, kh.w};
+        al[tb] = u32x4{kl.x, kl.y, kl.z, kl.w};
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) dk[tb] = mfma(ah[tb], qop[s][0], dk[tb]);
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) dk[tb] = mfma(ah[tb], qop[s][1], dk[tb]);
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) dk[tb] = mfma(al[tb], qop[s][0], dk[tb]);
+    }
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) {
-      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-      const uint4 *krow = reinterpret_cast<const uint4 *>(kt + (16 * tb + l16) * kKStride);
-#pragma unroll
-      for (int s = 0; s < 4; s++) {
-        const uint4 kh = krow[kchunk(8 * s + 2 * lg)], kl = krow[kchunk(8 * s + 2 * lg + 1)];
-        const u32x4 ah = {kh.x, kh.y, kh.z, kh.w}, al = {kl.x, kl.y, kl.z, kl.w};
-        d = mfma(ah, qop[s][0], d);
-        d = mfma(ah, qop[s][1], d);
-        d = mfma(al, qop[s][0], d);
-      }
+      const f32x4 d = dk[tb];
       f32x4 dc = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (QJL) {
         const uint32_t *sgrow = s_sg[cur] + (16 * tb + l16) * 4;
@@ -524,22 +616,29 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       for (int eb = 0; eb < 8; eb++) o[eb] = o[eb] * rescale;
     }
 #pragma unroll
-    for (int eb = 0; eb < 8; eb++) {
-      f32x4 acc = o[eb];
+    for (int e2 = 0; e2 < 8; e2 += 2) {
 #pragma unroll
       for (int tp = 0; tp < 2; tp++) {
-        const int r0 = (32 * tp + vrow) * kVRow + 8 * vchunk(2 * eb + (vcol >> 3)) + (vcol & 7),
-                  r1 = r0 + 16 * kVRow;
-        const u32x2 h0 = lds_read_tr16(vth + r0), h1 = lds_read_tr16(vth + r1);
-        const u32x2 q0 = lds_read_tr16(vtl + r0), q1 = lds_read_tr16(vtl + r1);
-        const u32x4 ah = {h0[0], h0[1], h1[0], h1[1]}, al = {q0[0], q0[1], q1[0], q1[1]};
         const u32x4 bh = {pb[2 * tp][0][0], pb[2 * tp][0][1], pb[2 * tp + 1][0][0], pb[2 * tp + 1][0][1]};
         const u32x4 bl = {pb[2 * tp][1][0], pb[2 * tp][1][1], pb[2 * tp + 1][1][0], pb[2 * tp + 1][1][1]};
-        acc = mfma(ah, bh, acc);
-        acc = mfma(ah, bl, acc);
-        acc = mfma(al, bh, acc);
+        u32x4 ah[2], al[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const int eb = e2 + j;
+          const int r0 = (32 * tp + vrow) * kVRow + 8 * vchunk(2 * eb + (vcol >> 3)) + (vcol & 7),
+                    r1 = r0 + 16 * kVRow;
+          const u32x2 h0 = lds_read_tr16(vth + r0), h1 = lds_read_tr16(vth + r1);
+          const u32x2 q0 = lds_read_tr16(vtl + r0), q1 = lds_read_tr16(vtl + r1);
+          ah[j] = u32x4{h0[0], h0[1], h1[0], h1[1]};
+          al[j] = u32x4{q0[0], q0[1], q1[0], q1[1]};
+        }
+        o[e2] = mfma(ah[0], bh, o[e2]);
+        o[e2 + 1] = mfma(ah[1], bh, o[e2 + 1]);
+        o[e2] = mfma(ah[0], bl, o[e2]);
+        o[e2 + 1] = mfma(ah[1], bl, o[e2 + 1]);
+        o[e2] = mfma(al[0], bh, o[e2]);
+        o[e2 + 1] = mfma(al[1], bh, o[e2 + 1]);
       }
-      o[eb] = acc;
     }
     if (!decode_first && more) {
       decode_tile(cur ^ 1);
@@ -591,14 +690,50 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   }
 }
 
+// Whether to decode each tile once into a staging buffer: with q_blocks query
+// blocks per KV head, the workgroups would otherwise decode a tile up to
+// q_blocks times (causal: about half of that on average).  TQ_PREFILL_STAGING
+// = 0 / 1 forces either path.
+bool use_staging(int q_blocks) {
+  if (const char *e = getenv("TQ_PREFILL_STAGING")) {
+    if (e[0] == '0') return false;
+    if (e[0] == '1') return true;
+  }
+  return q_blocks >= kStagingMinQueryBlocks;
+}
+
+template <int BITS, int MODE, int PH>
+void launch_attn(const PrefillArgs &a, int nr, dim3 grid, dim3 block, hipStream_t st) {
+  if (nr == 1) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, PH>), grid, block, 0, st, a);
+  else if (nr == 2) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 2, PH>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 4, PH>), grid, block, 0, st, a);
+}
+
 template <int BITS, int MODE>
-int launch_prefill_m(const PrefillArgs &a, int nr, hipStream_t st) {
+int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   const int qb = prefill_rows(MODE) / nr;
   const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
-  if (nr == 1) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1>), grid, block, 0, st, a);
-  else if (nr == 2) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 2>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 4>), grid, block, 0, st, a);
+  if constexpr (MODE != kPTq) {
+    if (a.kv_len > 0 && use_staging((int)grid.x)) {
+      // staging pass then the attention launch, in stream order; the buffer
+      // is released in stream order after the attention launch
+      a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
+      const size_t bytes = (size_t)a.num_kv_heads * (size_t)a.stage_tiles * kImgChunks * sizeof(uint4);
+      void *buf = nullptr;
+      if (hipMallocAsync(&buf, bytes, st) != hipSuccess)
+        return tqh::fail(TQ_ERR_DEVICE, "prefill staging buffer of %zu bytes not allocated", bytes);
+      a.stage = static_cast<const uint4 *>(buf);
+      a.stage_out = static_cast<uint4 *>(buf);
+      hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles, grid.y), block,
+                         0, st, a);
+      launch_attn<BITS, MODE, kStaged>(a, nr, grid, block, st);
+      const int rc = tqh::check_launch("prefill_attn_kernel (staged)");
+      (void)hipFreeAsync(buf, st);
+      return rc;
+    }
+  }
+  launch_attn<BITS, MODE, kDecode>(a, nr, grid, block, st);
   return tqh::check_launch("prefill_attn_kernel");
 }
 
