@@ -80,10 +80,11 @@ constexpr int kORow = 128 + 4;  // floats
 // Query blocks per KV head from which the tiles are decoded once, in a
 // staging pass, instead of in every workgroup
 constexpr int kStagingMinQueryBlocks = 4;
-// A staged tile image: the tile buffer's K rows and V planes, the per-token
-// 2^E_k and 2^E_v factors, and the 8 waves' V exponent maxima, in 16-byte chunks
+// A staged tile image: the tile buffer's K rows and V planes, then its
+// exponent words (the slices' K exponents, the waves' V exponents), in
+// 16-byte chunks
 constexpr int kTileChunks = (kTile * kKStride * 2 + kTile * kVRow) / 4;
-constexpr int kImgChunks = kTileChunks + kTile / 2 + 2;
+constexpr int kImgChunks = kTileChunks + 3;
 
 // Stores 32 values split into f16 hi (11 significant bits) and lo (the
 // exact remainder) at hi[0..31] and lo[0..31], 16 bytes per store.
@@ -159,14 +160,16 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // from the other
   constexpr int TILE_WORDS = K_WORDS + V_WORDS;
   static_assert(PH == kDecode || (!QJL && NW == 8), "staged tiles: PQ/PQO codes, 8 waves");
-  static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kTile / 2 + NW / 4 == kImgChunks - kTileChunks),
-                "the tile image is the LDS tile buffer plus its exponent arrays");
+  static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kImgChunks == kTileChunks + 3),
+                "the tile image is the LDS tile buffer plus its 12 exponent words");
   // the staging pass decodes into one buffer
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[(PH == kStage ? 1 : 2) * TILE_WORDS];
   // per-token and per-wave scalars, read 4 at a time
-  __shared__ __attribute__((aligned(16))) float s_ek[2][kTile];  // 2^E_k per token (key exponent folded out)
-  __shared__ __attribute__((aligned(16))) float s_ev[2][kTile];  // 2^E_v per token (V exponent folded out)
-  __shared__ __attribute__((aligned(16))) int s_evw[2][NW];      // max V exponent over each wave's 16 tokens
+  // per tile: [0..3] the K exponent E_k of each 16-token slice, [4 + w] the V
+  // exponent E_v of decoding wave w's slice (the exponents folded out of the
+  // decoded values)
+  static_assert(NW <= 8 && kTile == 64, "4 slices, at most 8 decoding waves");
+  __shared__ __attribute__((aligned(16))) int s_xe[2][12];
   __shared__ float s_cn[2][kTile];       // TQ: |r_t| * qjl_c
   __shared__ __attribute__((aligned(16))) uint32_t s_sg[2][kTile * 4];  // TQ: sign words
   __shared__ float s_cb[16];
@@ -250,12 +253,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
 
   // chunk c of tile buffer b's image: the K tile and V planes, then the
-  // per-token K and V exponent factors, then the waves' V exponent maxima
+  // exponent words
   auto img_chunk = [&](int b, int c) -> uint4 * {
     if (c < kTileChunks) return reinterpret_cast<uint4 *>(s_tile + b * TILE_WORDS) + c;
-    if (c < kTileChunks + kTile / 4) return reinterpret_cast<uint4 *>(s_ek[b]) + (c - kTileChunks);
-    if (c < kTileChunks + kTile / 2) return reinterpret_cast<uint4 *>(s_ev[b]) + (c - kTileChunks - kTile / 4);
-    return reinterpret_cast<uint4 *>(s_evw[b]) + (c - kTileChunks - kTile / 2);
+    return reinterpret_cast<uint4 *>(s_xe[b]) + (c - kTileChunks);
   };
 
   // ---- decode this thread's record into tile buffer b (staged: store the
@@ -272,21 +273,19 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     uint2 *kt = ktile(b);
     _Float16 *vth = vhi(b), *vtl = vth + V_HALVES;  // the lo plane follows the hi plane
     {
+      // one exponent per 16-token slice for K and one for V: the wave's 64
+      // lanes hold the slice's 16 tokens x 4 qblock scales (the SPLIT waves of
+      // a slice reduce the same scales), so the softmax applies 4 factors per
+      // tile instead of one per token
       const float sk = fabsf(f16_to_f32(ks)), sv = fabsf(f16_to_f32(vs));
-      float mk = fmaxf(sk, dpp_quad_xor1(sk));
-      mk = fmaxf(mk, dpp_quad_xor2(mk));
-      float mv = fmaxf(sv, dpp_quad_xor1(sv));
-      mv = fmaxf(mv, dpp_quad_xor2(mv));
-      const int ek = pow2_exponent(mk), ev = pow2_exponent(mv);
+      const int ek = pow2_exponent(wave_max(sk)), ev = pow2_exponent(wave_max(sv));
       const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
-      if (fqb == 0 && fpart == 0) {
-        s_ek[b][ftok] = exp2i(ek);
-        s_ev[b][ftok] = exp2i(ev);
-        if constexpr (QJL) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
+      if (lane == 0) {
+        if (fpart == 0) s_xe[b][wave / SPLIT] = ek;
+        s_xe[b][4 + wave] = ev;
       }
-      {
-        const float wm = wave_max((float)ev);  // exact: |ev| <= 100
-        if (lane == 0) s_evw[b][wave] = (int)wm;
+      if constexpr (QJL) {
+        if (fqb == 0) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
       }
       if constexpr (QJL) s_sg[b][ftok * 4 + fqb] = sgw;
       // this thread's code pairs P0 .. P0 + NP - 1 (a wave-uniform part, so
@@ -505,6 +504,15 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     // the sequence) is visible to every row: no per-element mask
     const bool open = t0 + kTile <= a.kv_len && (!a.causal || t0 + kTile - 1 <= qmin);
     float x[4][4];
+    // the tile's slice exponents (wave-uniform)
+    int ekt[4];
+    {
+      const int4 e4 = *reinterpret_cast<const int4 *>(s_xe[cur]);
+      ekt[0] = __builtin_amdgcn_readfirstlane(e4.x);
+      ekt[1] = __builtin_amdgcn_readfirstlane(e4.y);
+      ekt[2] = __builtin_amdgcn_readfirstlane(e4.z);
+      ekt[3] = __builtin_amdgcn_readfirstlane(e4.w);
+    }
     f32x4 dk[4];
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) dk[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -540,15 +548,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
           dc = mfma(sa, rop[sl][1], dc);
         }
       }
-      const float4 ekv = *reinterpret_cast<const float4 *>(s_ek[cur] + 16 * tb + 4 * lg);
-      const float ek4[4] = {ekv.x, ekv.y, ekv.z, ekv.w};
       auto logits = [&](auto maskc) {
         constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int tp = t0 + 16 * tb + 4 * lg + i;
-          // without QJL the row's query scale 2^E_q is applied in the softmax
-          float v = d[i] * (QJL ? ek4[i] * eq_scale : ek4[i]);
+          // without QJL the slice's 2^E_k and the row's 2^E_q are applied in the softmax
+          float v = QJL ? d[i] * (exp2i(ekt[tb]) * eq_scale) : d[i];
           if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
           if constexpr (MASK) {
             const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
@@ -562,44 +568,50 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       else logits(std::true_type{});
     }
     // ---- online softmax of this row (its 64 logits sit in the 4 lanes l16 + 16 k) ----
+    // logit = x z_tb, z_tb a power of 2 (exact): 2^E_k,tb 2^E_q (QJL: 1)
+    float zt[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) zt[tb] = QJL ? 1.f : exp2i(ekt[tb]) * eq_scale;
     float mt = -INFINITY;
 #pragma unroll
     for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) mt = fmaxf(mt, x[tb][i]);
+      mt = fmaxf(mt, fmaxf(fmaxf(x[tb][0], x[tb][1]), fmaxf(x[tb][2], x[tb][3])) * zt[tb]);
     mt = max_xor32(max_xor16(mt));
-    const float xsc = QJL ? 1.f : eq_scale;  // logit = x xsc (a power of 2: exact)
-    mt *= xsc;
     const float m_new = fmaxf(m_run, mt);
     const float m_exp = m_new == -INFINITY ? 0.f : m_new;  // a row with nothing visible yet
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
     // V exponent of the tile (each wave reads all 64)
-    static_assert(NW % 4 == 0, "the wave maxima are read 4 at a time");
-    int evt = -1000;
+    static_assert(NW % 4 == 0, "the wave exponents are read 4 at a time");
+    int evw[NW];
 #pragma unroll
     for (int w = 0; w < NW; w += 4) {
-      const int4 e4 = *reinterpret_cast<const int4 *>(s_evw[cur] + w);
-      evt = max(max(evt, max(e4.x, e4.y)), max(e4.z, e4.w));
+      const int4 e4 = *reinterpret_cast<const int4 *>(s_xe[cur] + 4 + w);
+      evw[w] = __builtin_amdgcn_readfirstlane(e4.x);
+      evw[w + 1] = __builtin_amdgcn_readfirstlane(e4.y);
+      evw[w + 2] = __builtin_amdgcn_readfirstlane(e4.z);
+      evw[w + 3] = __builtin_amdgcn_readfirstlane(e4.w);
     }
+    int evt = -1000;
+#pragma unroll
+    for (int w = 0; w < NW; w++) evt = max(evt, evw[w]);
     const int ev_new = max(ev_cur, evt);
     const float rescale = alpha * exp2i(max(ev_cur - ev_new, -126));
-    const float evs = exp2i(-ev_new);
     ev_cur = ev_new;
     m_run = m_new;
     float ls = 0.f;
     u32x2 pb[4][2];
 #pragma unroll
     for (int tb = 0; tb < 4; tb++) {
-      // 2^(E_v,t - Ev) as 2^E_v,t 2^-Ev: exact (f16 scales keep both exponents
-      // within [-23, 16])
-      const float4 e4 = *reinterpret_cast<const float4 *>(s_ev[cur] + 16 * tb + 4 * lg);
-      const float evk[4] = {e4.x * evs, e4.y * evs, e4.z * evs, e4.w * evs};
+      // p = e 2^(E_v,tb - Ev) with e = 2^(logit - m): the slice's V factor is
+      // a shift of exp2's argument (E_v,tb - Ev in [-40, 0]: p stays normal
+      // for every e above 2^-80), and e = p 2^(Ev - E_v,tb) for the row sum
+      const int dv = evw[SPLIT * tb] - ev_new;
+      const float cb = (float)dv - m_exp, gb = exp2i(-dv);
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[tb][i], xsc, -m_exp));  // 2^-inf = 0 for masked tokens
-        ls += e;
-        p[i] = e * evk[i];
+        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[tb][i], zt[tb], cb));  // 2^-inf = 0 for masked tokens
+        ls = __builtin_fmaf(p[i], gb, ls);
       }
       pb[tb][0] = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
       pb[tb][1] = u32x2{pack_rem(p[0], p[1], pb[tb][0][0], mone), pack_rem(p[2], p[3], pb[tb][0][1], mone)};
