@@ -163,7 +163,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kImgChunks == kTileChunks + 3),
                 "the tile image is the LDS tile buffer plus its 12 exponent words");
   // the staging pass decodes into one buffer
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[(PH == kStage ? 1 : 2) * TILE_WORDS];
+  // (the staging pass decodes straight into the global image)
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[PH == kStage ? 4 : 2 * TILE_WORDS];
   // per-token and per-wave scalars, read 4 at a time
   // per tile: [0..3] the K exponent E_k of each 16-token slice, [4 + w] the V
   // exponent E_v of decoding wave w's slice (the exponents folded out of the
@@ -246,8 +247,21 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   };
   // buffer b: K tile at s_tile + b TILE_WORDS, V hi plane after it, lo plane
   // after that
-  auto ktile = [&](int b) { return reinterpret_cast<uint2 *>(s_tile + b * TILE_WORDS); };
-  auto vhi = [&](int b) { return reinterpret_cast<_Float16 *>(s_tile + b * TILE_WORDS + K_WORDS); };
+  // (staging pass: the tile's image in the staging buffer)
+  auto tile_base = [&](int b) -> uint32_t * {
+    if constexpr (PH == kStage)
+      return reinterpret_cast<uint32_t *>(a.stage_out + ((long long)g * a.stage_tiles + blockIdx.x) * kImgChunks);
+    else
+      return s_tile + b * TILE_WORDS;
+  };
+  auto ktile = [&](int b) { return reinterpret_cast<uint2 *>(tile_base(b)); };
+  auto vhi = [&](int b) { return reinterpret_cast<_Float16 *>(tile_base(b) + K_WORDS); };
+  auto xe = [&](int b) -> int * {
+    if constexpr (PH == kStage)
+      return reinterpret_cast<int *>(tile_base(b) + TILE_WORDS);
+    else
+      return s_xe[b];
+  };
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
   static_assert((QJL ? 2 : 1) * kRows * kQRow <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
   static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
@@ -281,8 +295,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       const int ek = pow2_exponent(wave_max(sk)), ev = pow2_exponent(wave_max(sv));
       const float kf = sk * exp2i(-ek), vf = sv * exp2i(-ev);
       if (lane == 0) {
-        if (fpart == 0) s_xe[b][wave / SPLIT] = ek;
-        s_xe[b][4 + wave] = ev;
+        if (fpart == 0) xe(b)[wave / SPLIT] = ek;
+        xe(b)[4 + wave] = ev;
       }
       if constexpr (QJL) {
         if (fqb == 0) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
@@ -348,20 +362,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     }
   };
 
-  // ---- staging pass: decode tile blockIdx.x of KV head g once and store the
-  // buffer's image for the attention workgroups of every query block ----
+  // ---- staging pass: decode tile blockIdx.x of KV head g once, straight
+  // into its image (the K rows' padding words stay unwritten: nothing reads
+  // them), for the attention workgroups of every query block ----
   if constexpr (PH == kStage) {
-    const int t0 = (int)blockIdx.x * kTile;
-    fetch(t0);
+    fetch((int)blockIdx.x * kTile);
     __syncthreads();  // codebook staged
     decode_tile(0);
-    __syncthreads();
-    u32x4 *dst = reinterpret_cast<u32x4 *>(a.stage_out) + ((long long)g * a.stage_tiles + blockIdx.x) * kImgChunks;
-#pragma unroll
-    for (int r = 0; r < IMG_ROUNDS; r++) {
-      const int c = tid + 4 * kRows * r;
-      if (c < kImgChunks) dst[c] = *reinterpret_cast<const u32x4 *>(img_chunk(0, c));
-    }
     return;
   }
 
