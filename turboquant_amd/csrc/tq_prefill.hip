@@ -31,12 +31,12 @@
 // decoded while tile t is computed (one barrier per tile), and the records of
 // tile t + 2 are fetched meanwhile.
 //
-// Staged tiles (PQ/PQO codes, 4 or more query blocks per KV head): the query
-// blocks of a KV head would each decode every tile again, so a staging pass
-// (the same kernel, one workgroup per tile and KV head) decodes each tile
-// once and stores the tile buffer's LDS image, and the attention workgroups
-// copy the images into LDS in place of decoding; the LDS contents, and so the
-// outputs, are bit-identical.  The workgroup order puts every query block of
+// Staged tiles (PQ/PQO codes, 4 or more query blocks per KV head over 2048 or
+// more tokens): the query blocks of a KV head would each decode every tile
+// again, so a staging pass (the same kernel, one workgroup per tile and KV
+// head) decodes each tile once into an image of the tile buffer's LDS
+// contents, and the attention workgroups copy the images into LDS in place of
+// decoding; the LDS contents, and so the outputs, are bit-identical.  The workgroup order puts every query block of
 // KV head g on one XCD (g = linear index mod 8), so a head's images are read
 // from one L2.
 #include "tq_common.h"
@@ -77,9 +77,12 @@ __device__ __forceinline__ int vchunk(int c) { return c ^ ((c >> 3) & 1); }
 constexpr int kQRow = 128 + 8;  // halves
 constexpr int kORow = 128 + 4;  // floats
 
-// Query blocks per KV head from which the tiles are decoded once, in a
-// staging pass, instead of in every workgroup
+// Shapes whose tiles are decoded once, in a staging pass, instead of in every
+// workgroup: at least this many query blocks per KV head and tokens (the
+// pass and its buffer cost about 20 us, the decode it saves about a fifth of
+// each workgroup's time; measured crossover near 2048 x 2048 causal)
 constexpr int kStagingMinQueryBlocks = 4;
+constexpr int kStagingMinTokens = 2048;
 // A staged tile image: the tile buffer's K rows and V planes, then its
 // exponent words (the slices' K exponents, the waves' V exponents), in
 // 16-byte chunks
@@ -713,12 +716,12 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 // blocks per KV head, the workgroups would otherwise decode a tile up to
 // q_blocks times (causal: about half of that on average).  TQ_PREFILL_STAGING
 // = 0 / 1 forces either path.
-bool use_staging(int q_blocks) {
+bool use_staging(int q_blocks, int kv_len) {
   if (const char *e = getenv("TQ_PREFILL_STAGING")) {
     if (e[0] == '0') return false;
     if (e[0] == '1') return true;
   }
-  return q_blocks >= kStagingMinQueryBlocks;
+  return q_blocks >= kStagingMinQueryBlocks && kv_len >= kStagingMinTokens;
 }
 
 template <int BITS, int MODE, int PH>
@@ -734,7 +737,7 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
   if constexpr (MODE != kPTq) {
-    if (a.kv_len > 0 && use_staging((int)grid.x)) {
+    if (a.kv_len > 0 && use_staging((int)grid.x, a.kv_len)) {
       // staging pass then the attention launch, in stream order; the buffer
       // is released in stream order after the attention launch
       a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
