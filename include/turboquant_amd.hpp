@@ -470,41 +470,6 @@ class QuantizedKVCache {
     return dequantize_range(values_[layer], start, end, stream);
   }
 
-  // export_packed_range (attention.rs:663-675): (packed bytes, f16 scales)
-  std::pair<std::vector<uint8_t>, std::vector<uint16_t>> export_packed_range(size_t layer, size_t start, size_t end,
-                                                                             bool is_keys,
-                                                                             hipStream_t stream = nullptr) const {
-    check_layer(layer);
-    const Blocks &b = is_keys ? keys_[layer] : values_[layer];
-    check_range(start, end, b.count);
-    const size_t pb = polar_bytes(), n = end - start;
-    std::pair<std::vector<uint8_t>, std::vector<uint16_t>> out;
-    out.first.resize(n * pb);
-    out.second.resize(n);
-    detail::to_host(out.first.data(), b.polar.as<uint8_t>() + start * pb, n * pb, stream);
-    detail::to_host(out.second.data(), b.scales.as<uint16_t>() + start, n * 2, stream);
-    return out;
-  }
-
-  // import_packed_range (attention.rs:684-696; PackedImport :147-166)
-  void import_packed_range(size_t layer, const std::vector<uint8_t> &packed_bytes, const std::vector<uint16_t> &scales,
-                           const std::vector<uint8_t> &qjl_signs_flat, const std::vector<uint16_t> &residual_norms,
-                           bool is_keys, hipStream_t stream = nullptr) {
-    check_layer(layer);
-    Blocks &b = is_keys ? keys_[layer] : values_[layer];
-    const size_t n = scales.size(), pb = polar_bytes(), sb = config_.dim / 8;
-    check_values_match(packed_bytes.size(), n * pb);
-    check_values_match(qjl_signs_flat.size(), n * sb);
-    check_values_match(residual_norms.size(), n);
-    reserve(b, b.count + n, stream);
-    detail::to_device(b.polar.as<uint8_t>() + b.count * pb, packed_bytes.data(), n * pb, stream);
-    detail::to_device(b.scales.as<uint16_t>() + b.count, scales.data(), n * 2, stream);
-    detail::to_device(b.signs.as<uint8_t>() + b.count * sb, qjl_signs_flat.data(), n * sb, stream);
-    detail::to_device(b.norms.as<uint16_t>() + b.count, residual_norms.data(), n * 2, stream);
-    detail::DeviceBuffer::sync(stream);
-    b.count += n;
-  }
-
  private:
   struct Blocks {
     detail::DeviceBuffer polar, scales, signs, norms;

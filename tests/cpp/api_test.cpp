@@ -122,7 +122,6 @@ int run_gpu(const char *path) {
     c.attention_scores(3, std::vector<float>(64));
   });
   const tq::QjlBlock kb = cache.key_block(1, 2);
-  const auto exp = cache.export_packed_range(1, 1, 3, false);
   std::printf("{\"kv_cache\": {\"entries\": %zu, \"empty_layer\": %zu, \"memory\": %zu, \"fp16\": %zu, "
               "\"layer_error\": %d, \"key2_scale\": %u, ",
               cache.entry_count(1), cache.entry_count(0), cache.memory_usage(), cache.fp16_equivalent_memory(),
@@ -134,8 +133,6 @@ int run_gpu(const char *path) {
   print_floats("weighted", wv);
   std::printf(", ");
   print_floats("key1", cache.dequantize_keys_range(1, 1, 2)[0]);
-  std::printf(", ");
-  print_bytes("export_v_packed", exp.first);
   std::printf("}}\n");
 
   // PqoCache / TqCache through the CompressedKVCache trait (device buffers)
