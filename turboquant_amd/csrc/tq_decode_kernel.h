@@ -881,6 +881,10 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+  // the V pass at raised wave priority: the other waves of the SIMD, in
+  // their K passes or softmax, fill the gaps between its matrix products
+  // instead of delaying them (C4 58.8 -> 56.7 us; C3 unchanged)
+  __builtin_amdgcn_s_setprio(1);
   if constexpr (GRID) {
   // ---- V pass on the grid, 64-token block by block: the block's records
   // are staged token-major in LDS; a transposing 4-bit read hands lane
@@ -1064,6 +1068,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       }
   }
   }  // V pass
+  __builtin_amdgcn_s_setprio(0);
   }  // chunks
   if (l16 == 0) {
 #pragma unroll
