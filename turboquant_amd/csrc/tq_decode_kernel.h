@@ -728,6 +728,10 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   for (int ck = 0; ck < nck; ck++) {
   const int tw = (ck0 + ck) * C::CHUNK + wave * TPW;
   const uint32_t tw0 = (uint32_t)tw;
+  // range launches: the K pass above the softmax in wave priority, the V
+  // pass above both (C4 56.7 -> 55.5 us; single-chunk launches measured
+  // no gain from the K-pass step)
+  if constexpr (MULTI) __builtin_amdgcn_s_setprio(1);
   // ---- K pass, tile by tile as the records arrive ----
   // QA_REGS: the operands come into registers for the pass (a reload per
   // chunk through an opaque lane offset, so they do not occupy registers
@@ -822,6 +826,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
   }
 
+  if constexpr (MULTI) __builtin_amdgcn_s_setprio(0);
   // ---- online softmax step (base 2): the running row max of each head
   // moves to mn, the chunk's weights are 2^(s - mn) and the sums so far are
   // rescaled by 2^(m_old - mn) ----
@@ -884,7 +889,7 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // the V pass at raised wave priority: the other waves of the SIMD, in
   // their K passes or softmax, fill the gaps between its matrix products
   // instead of delaying them (C4 58.8 -> 56.7 us; C3 unchanged)
-  __builtin_amdgcn_s_setprio(1);
+  __builtin_amdgcn_s_setprio(MULTI ? 3 : 1);
   if constexpr (GRID) {
   // ---- V pass on the grid, 64-token block by block: the block's records
   // are staged token-major in LDS; a transposing 4-bit read hands lane
