@@ -36,9 +36,10 @@
 // again, so a staging pass (the same kernel, one workgroup per tile and KV
 // head) decodes each tile once into an image of the tile buffer's LDS
 // contents, and the attention workgroups copy the images into LDS in place of
-// decoding; the LDS contents, and so the outputs, are bit-identical.  The workgroup order puts every query block of
-// KV head g on one XCD (g = linear index mod 8), so a head's images are read
-// from one L2.
+// decoding; the LDS contents, and so the outputs, are bit-identical.  Both
+// launches put KV head g on one XCD (g = linear index mod 8, workgroups being
+// dealt to the 8 XCDs in turn): a head's images are written and read through
+// one L2.
 #include "tq_common.h"
 #include "tq_device.h"
 #include "tq_mfma.h"
@@ -192,6 +193,14 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // before it): the short blocks fill in at the end instead of the long ones
   // starting last.
   int g = blockIdx.y, qblk = blockIdx.x;
+  if (PH == kStage) {
+    // staging pass, a 1-D grid: KV head g = linear index mod num_kv_heads,
+    // so (with 8 heads) each head's tiles are decoded on the XCD whose
+    // attention workgroups read them (-3.3 % at the bench shape); qblk is
+    // the tile
+    g = (int)blockIdx.x % a.num_kv_heads;
+    qblk = (int)blockIdx.x / a.num_kv_heads;
+  }
   if (PH != kStage && a.causal) {
     const int lin = blockIdx.y * gridDim.x + blockIdx.x;
     g = lin % gridDim.y;
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // (staging pass: the tile's image in the staging buffer)
   auto tile_base = [&](int b) -> uint32_t * {
     if constexpr (PH == kStage)
-      return reinterpret_cast<uint32_t *>(a.stage_out + ((long long)g * a.stage_tiles + blockIdx.x) * kImgChunks);
+      return reinterpret_cast<uint32_t *>(a.stage_out + ((long long)g * a.stage_tiles + qblk) * kImgChunks);
     else
       return s_tile + b * TILE_WORDS;
   };
@@ -365,11 +374,11 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     }
   };
 
-  // ---- staging pass: decode tile blockIdx.x of KV head g once, straight
+  // ---- staging pass: decode tile qblk of KV head g once, straight
   // into its image (the K rows' padding words stay unwritten: nothing reads
   // them), for the attention workgroups of every query block ----
   if constexpr (PH == kStage) {
-    fetch((int)blockIdx.x * kTile);
+    fetch(qblk * kTile);
     __syncthreads();  // codebook staged
     decode_tile(0);
     return;
@@ -752,7 +761,7 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
         return tqh::fail(TQ_ERR_DEVICE, "prefill staging buffer of %zu bytes not allocated", bytes);
       a.stage = static_cast<const uint4 *>(buf);
       a.stage_out = static_cast<uint4 *>(buf);
-      hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles, grid.y), block,
+      hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles * grid.y), block,
                          0, st, a);
       launch_attn<BITS, MODE, kStaged>(a, nr, grid, block, st);
       const int rc = tqh::check_launch("prefill_attn_kernel (staged)");
