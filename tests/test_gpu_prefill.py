@@ -169,3 +169,34 @@ def test_staged_tiles_bit_identical(tq, monkeypatch, bits, outlier, hq, hkv, ql,
     ref = orc.attention_prefill(q, kd, vd, scale, causal)
     err = np.abs(outs[1].cpu().numpy() - ref).max()
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("outlier", [orc.OUTLIER_ALL, 0])
+def test_l2norm_cache_prefill_staged_and_in_workgroup(tq, monkeypatch, outlier):
+    """A PqoCache on the L2Norm codebooks (PQO codes, and PQ codes in 3-bit
+    slots): the staging pass and the in-workgroup decode read the caller's
+    codebook from the launch arguments; both paths give the same bits and
+    match the oracle's L2Norm dequantization within TOL."""
+    bits, hkv, hq, t, ql = 3, 4, 8, 700, 300
+    rng = np.random.default_rng(1900 + (1 if outlier else 0))
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    cfg = tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1,
+                         norm_mode=tq.QuantNormMode.L2Norm, outlier_blocks=outlier)
+    cache = tq.PqoCache(cfg)
+    cache.prefill(0, _dev(k[None]), _dev(v[None]))
+    q = bf16_round(rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    scale = 1 / math.sqrt(D)
+    outs = []
+    for mode in ("0", "1"):
+        monkeypatch.setenv("TQ_PREFILL_STAGING", mode)
+        outs.append(cache.attend_prefill(0, _dev(q[None]), scale, out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    pk, sk = orc.polar_quantize(bits, outlier, k.reshape(-1, D), D, norm_mode=1)
+    pv, sv = orc.polar_quantize(bits, outlier, v.reshape(-1, D), D, norm_mode=1)
+    kd = orc.polar_dequantize(bits, outlier, pk, sk, D, norm_mode=1).reshape(hkv, t, D)
+    vd = orc.polar_dequantize(bits, outlier, pv, sv, D, norm_mode=1).reshape(hkv, t, D)
+    ref = orc.attention_prefill(q, kd, vd, scale, True)
+    err = np.abs(outs[1][0].cpu().numpy() - ref).max()
+    assert err <= TOL, err
