@@ -31,7 +31,7 @@
 // decoded while tile t is computed (one barrier per tile), and the records of
 // tile t + 2 are fetched meanwhile.
 //
-// Staged tiles (PQ/PQO codes, 4 or more query blocks per KV head over 2048 or
+// Staged tiles (PQ/PQO codes, 2 or more query blocks per KV head over 1024 or
 // more tokens): the query blocks of a KV head would each decode every tile
 // again, so a staging pass (the same kernel, one workgroup per tile and KV
 // head) decodes each tile once into an image of the tile buffer's LDS
@@ -80,10 +80,12 @@ constexpr int kORow = 128 + 4;  // floats
 
 // Shapes whose tiles are decoded once, in a staging pass, instead of in every
 // workgroup: at least this many query blocks per KV head and tokens (the
-// pass and its buffer cost about 20 us, the decode it saves about a fifth of
-// each workgroup's time; measured crossover near 2048 x 2048 causal)
-constexpr int kStagingMinQueryBlocks = 4;
-constexpr int kStagingMinTokens = 2048;
+// pass and its buffer cost 15-20 us, the decode it saves about a fifth of
+// each workgroup's time; 16/8 heads, in-workgroup vs staged, us: 512 x 512
+// causal 36.5 vs 40.2, 1024 x 1024 64.6 vs 62.2, 2048 x 2048 119.9 vs 106.7,
+// 128 queries x 2048 tokens full 115.3 vs 110.6)
+constexpr int kStagingMinQueryBlocks = 2;
+constexpr int kStagingMinTokens = 1024;
 // A staged tile image: the tile buffer's K rows and V planes, then its
 // exponent words (the slices' K exponents, the waves' V exponents), in
 // 16-byte chunks
