@@ -200,3 +200,35 @@ def test_l2norm_cache_prefill_staged_and_in_workgroup(tq, monkeypatch, outlier):
     ref = orc.attention_prefill(q, kd, vd, scale, True)
     err = np.abs(outs[1][0].cpu().numpy() - ref).max()
     assert err <= TOL, err
+
+
+def test_staged_prefill_repeats_across_synchronizations(tq, monkeypatch):
+    """The staging buffer comes from the library's own memory pool, which keeps
+    its memory across synchronizations: staged launches separated by device
+    synchronizations, on the default stream and on a second stream, give the
+    same bits as the first."""
+    monkeypatch.setenv("TQ_PREFILL_STAGING", "1")
+    bits, hkv, hq, t = 3, 4, 8, 1100
+    rng = np.random.default_rng(2100)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    ki, ks, _ = _records(bits, orc.OUTLIER_ALL, k, t)
+    vi, vs, _ = _records(bits, orc.OUTLIER_ALL, v, t)
+    q = bf16_round(rng.standard_normal((hq, 300, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    scale = 1 / math.sqrt(D)
+
+    def run():
+        return tq.cache_prefill_attention(qd, ki, ks, vi, vs, hkv, bits, t, t, scale, orc.OUTLIER_ALL, causal=True)
+
+    first = run()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        again = run()
+        torch.cuda.synchronize()
+        assert torch.equal(first, again)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        other = run()
+    side.synchronize()
+    assert torch.equal(first, other)

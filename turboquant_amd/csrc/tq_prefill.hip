@@ -44,6 +44,7 @@
 #include "tq_device.h"
 #include "tq_mfma.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -740,6 +741,37 @@ bool use_staging(int q_blocks, int kv_len) {
   return q_blocks >= kStagingMinQueryBlocks && kv_len >= kStagingMinTokens;
 }
 
+// The staging buffers come from a memory pool of the library's own per
+// device, which keeps up to kStagingPoolKeep bytes across synchronizations
+// (the device's default pool, release threshold 0, would hand its memory
+// back to the driver at each synchronization, and the next prefill would
+// allocate it again).  nullptr: the pool could not be made; the caller then
+// takes the device's default pool.
+constexpr uint64_t kStagingPoolKeep = 1ull << 30;
+hipMemPool_t staging_pool(int dev) {
+  static std::mutex mu;
+  static hipMemPool_t pools[64] = {};
+  static bool tried[64] = {};
+  if (dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!tried[dev]) {
+    tried[dev] = true;
+    hipMemPoolProps props{};
+    props.allocType = hipMemAllocationTypePinned;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t pool = nullptr;
+    if (hipMemPoolCreate(&pool, &props) == hipSuccess) {
+      uint64_t keep = kStagingPoolKeep;
+      (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+      pools[dev] = pool;
+    } else {
+      (void)hipGetLastError();
+    }
+  }
+  return pools[dev];
+}
+
 template <int BITS, int MODE, int PH>
 void launch_attn(const PrefillArgs &a, int nr, dim3 grid, dim3 block, hipStream_t st) {
   if (nr == 1) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, PH>), grid, block, 0, st, a);
@@ -759,8 +791,14 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
       a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
       const size_t bytes = (size_t)a.num_kv_heads * (size_t)a.stage_tiles * kImgChunks * sizeof(uint4);
       void *buf = nullptr;
-      if (hipMallocAsync(&buf, bytes, st) != hipSuccess)
+      int dev = 0;
+      (void)hipGetDevice(&dev);
+      hipMemPool_t pool = staging_pool(dev);
+      const hipError_t ae = pool ? hipMallocFromPoolAsync(&buf, bytes, pool, st) : hipMallocAsync(&buf, bytes, st);
+      if (ae != hipSuccess) {
+        (void)hipGetLastError();
         return tqh::fail(TQ_ERR_DEVICE, "prefill staging buffer of %zu bytes not allocated", bytes);
+      }
       a.stage = static_cast<const uint4 *>(buf);
       a.stage_out = static_cast<uint4 *>(buf);
       hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles * grid.y), block,
