@@ -11,9 +11,9 @@
 // One workgroup serves 128 rows = (query, head) pairs of one KV head (8
 // waves; 64 rows and 4 waves for a TQ cache), query-major, so the NR query
 // heads of a KV head share every decoded tile.  Per 64-token tile the
-// workgroup decodes K and V (token-major, per-token exponents folded out)
-// into LDS as two-part f16 values (hi = 11 significant bits, lo = the
-// remainder), then each wave (16 rows) runs
+// workgroup decodes K and V (token-major, one K and one V exponent per
+// 16-token slice folded out) into LDS as two-part f16 values (hi = 11
+// significant bits, lo = the remainder), then each wave (16 rows) runs
 //   S^T = K Q^T          16x16x32 MFMAs per 32-element slice: K hi x Q hi,
 //                        K hi x Q lo, K lo x Q hi (22-bit products, lo x lo
 //                        dropped, f32 accumulation)
@@ -26,7 +26,8 @@
 // with an online base-2 softmax per row.  The four 16-token blocks of the
 // key pass and pairs of 16-element blocks of the value pass run as
 // independent accumulator chains, interleaved (each accumulator still sums
-// its products in the same order).  Values stay in the rotated domain; each
+// its products in the same order); the value pass runs at raised wave
+// priority.  Values stay in the rotated domain; each
 // row is inverse-rotated once at the end.  Two tile buffers: tile t + 1 is
 // decoded while tile t is computed (one barrier per tile), and the records of
 // tile t + 2 are fetched meanwhile.
@@ -157,7 +158,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   constexpr int NP = 16 / SPLIT;            // code pairs per decoding thread
   constexpr int QB = kRows / NR;  // queries per workgroup
   static_assert(kPrefillModeTq == 2, "prefill_rows keys on the TQ mode");
-  // LDS: K tile | V tiles (hi, lo) | per-token and per-row scalars
+  // LDS: K tile | V tiles (hi, lo) per buffer; slice exponents, TQ sign
+  // words and norms, and per-row scalars beside them
   constexpr int K_WORDS = kTile * kKStride * 2;
   constexpr int V_HALVES = kTile * kVRow;
   constexpr int V_WORDS = V_HALVES;  // hi and lo planes, 2 halves per word each
@@ -169,11 +171,9 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   static_assert(PH == kDecode || (!QJL && NW == 8), "staged tiles: PQ/PQO codes, 8 waves");
   static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kImgChunks == kTileChunks + 3),
                 "the tile image is the LDS tile buffer plus its 12 exponent words");
-  // the staging pass decodes into one buffer
   // (the staging pass decodes straight into the global image)
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[PH == kStage ? 4 : 2 * TILE_WORDS];
-  // per-token and per-wave scalars, read 4 at a time
-  // per tile: [0..3] the K exponent E_k of each 16-token slice, [4 + w] the V
+  // per tile, read 4 at a time: [0..3] the K exponent E_k of each 16-token slice, [4 + w] the V
   // exponent E_v of decoding wave w's slice (the exponents folded out of the
   // decoded values)
   static_assert(NW <= 8 && kTile == 64, "4 slices, at most 8 decoding waves");
