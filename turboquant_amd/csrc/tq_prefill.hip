@@ -9,8 +9,8 @@
 // cache (tq.rs:185-253).
 //
 // One workgroup serves 128 rows = (query, head) pairs of one KV head (8
-// waves; 64 rows and 4 waves for a TQ cache), query-major, so the NR query
-// heads of a KV head share every decoded tile.  Per 64-token tile the
+// waves), query-major, so the NR query heads of a KV head share every
+// decoded tile.  Per 64-token tile the
 // workgroup decodes K and V (token-major, one K and one V exponent per
 // 16-token slice folded out) into LDS as two-part f16 values (hi = 11
 // significant bits, lo = the remainder), then each wave (16 rows) runs
@@ -53,9 +53,9 @@ namespace {
 using namespace tqd;
 using namespace tqm;
 
-// (query, head) rows per workgroup: 128 (8 waves) share each decoded tile;
-// the TQ mode, whose wave needs 256 registers, keeps 64 (4 waves)
-constexpr int prefill_rows(int mode) { return mode == 2 ? 64 : 128; }
+// (query, head) rows per workgroup: 128 (8 waves) share each decoded tile,
+// the TQ mode too (its waves fit 244 registers at 8 waves per workgroup)
+constexpr int prefill_rows(int) { return 128; }
 constexpr int kTile = 64;   // tokens per tile
 constexpr int kKStride = 66;  // uint2 per token row of the K tile (32 chunks of 16 bytes + pad)
 constexpr int kVRow = 144;    // halves per token row of the V tiles (128 elements + pad: the
@@ -115,7 +115,6 @@ __device__ __forceinline__ void stage_split32(const float (&x)[32], _Float16 *hi
 }
 
 enum PMode : int { kPPqo = 0, kPPq = 1, kPTq = 2 };
-constexpr int kPrefillModeTq = kPTq;
 
 struct PrefillArgs {
   const void *q;
@@ -157,7 +156,6 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   constexpr int SPLIT = NW / 4;             // waves per 16-token slice of a tile's decode
   constexpr int NP = 16 / SPLIT;            // code pairs per decoding thread
   constexpr int QB = kRows / NR;  // queries per workgroup
-  static_assert(kPrefillModeTq == 2, "prefill_rows keys on the TQ mode");
   // LDS: K tile | V tiles (hi, lo) per buffer; slice exponents, TQ sign
   // words and norms, and per-row scalars beside them
   constexpr int K_WORDS = kTile * kKStride * 2;
@@ -278,7 +276,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       return s_xe[b];
   };
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
-  static_assert((QJL ? 2 : 1) * kRows * kQRow <= K_WORDS + V_WORDS, "the split query (and rq) fit the tile region");
+  // (the query and rq staging precedes the tiles and may span both buffers)
+  static_assert((QJL ? 2 : 1) * kRows * kQRow <= 2 * (K_WORDS + V_WORDS), "the split query (and rq) fit the tile region");
   static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
 
   // chunk c of tile buffer b's image: the K tile and V planes, then the
