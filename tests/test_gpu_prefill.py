@@ -239,18 +239,25 @@ def test_staged_prefill_repeats_across_synchronizations(tq, monkeypatch):
     (4, 8, 8, 200, 333, False),
     (3, 16, 8, 257, 257, True),
 ])
-def test_tq_prefill_several_query_blocks(tq, bits, hq, hkv, ql, t, causal):
+def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, causal):
     """TQ-cache prefill attention (QJL correction inside the key pass) over
-    several 128-row workgroups per KV head, GQA 4, 1 and 2, causal and full,
-    against the oracle's dequantized keys and values plus its logit bias."""
+    several 128-row workgroups per KV head, GQA 4, 1 and 2, causal and full:
+    staged tiles (signs and norms in the image) and in-workgroup decode give
+    the same bits, within TOL of the oracle's dequantized keys and values
+    plus its logit bias."""
     rng = np.random.default_rng(2300 + t + ql)
     k = kv_outlier(rng, hkv, t)
     v = kv_outlier(rng, hkv, t)
     cache = tq.TqCache(tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1, outlier_blocks=0))
     q = rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D))
     cache.prefill(0, _dev(k[None]), _dev(v[None]), _dev(q[None]))
-    out = cache.attend_prefill(0, _dev(q[None]), 1 / math.sqrt(D), causal=causal, out_dtype=torch.float32)
+    outs = []
+    for mode in ("0", "1"):
+        monkeypatch.setenv("TQ_PREFILL_STAGING", mode)
+        outs.append(cache.attend_prefill(0, _dev(q[None]), 1 / math.sqrt(D), causal=causal, out_dtype=torch.float32))
     torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    out = outs[1]
     pk, sk = orc.polar_quantize(bits, 0, k.reshape(-1, D), D)
     pv, sv = orc.polar_quantize(bits, 0, v.reshape(-1, D), D)
     kd = orc.polar_dequantize(bits, 0, pk, sk, D)

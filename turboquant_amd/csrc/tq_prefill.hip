@@ -32,12 +32,13 @@
 // decoded while tile t is computed (one barrier per tile), and the records of
 // tile t + 2 are fetched meanwhile.
 //
-// Staged tiles (PQ/PQO codes, 2 or more query blocks per KV head over 1024 or
-// more tokens): the query blocks of a KV head would each decode every tile
-// again, so a staging pass (the same kernel, one workgroup per tile and KV
-// head) decodes each tile once into an image of the tile buffer's LDS
-// contents, and the attention workgroups copy the images into LDS in place of
-// decoding; the LDS contents, and so the outputs, are bit-identical.  Both
+// Staged tiles (2 or more query blocks per KV head over 1024 or more
+// tokens): the query blocks of a KV head would each decode every tile again,
+// so a staging pass (the same kernel, one workgroup per tile and KV head)
+// decodes each tile once into an image of the tile buffer's LDS contents (TQ:
+// with the sign words and scaled norms), and the attention workgroups copy
+// the images into LDS in place of decoding; the LDS contents, and so the
+// outputs, are bit-identical.  Both
 // launches put KV head g on one XCD (g = linear index mod 8, workgroups being
 // dealt to the 8 XCDs in turn): a head's images are written and read through
 // one L2.
@@ -89,10 +90,13 @@ constexpr int kORow = 128 + 4;  // floats
 constexpr int kStagingMinQueryBlocks = 2;
 constexpr int kStagingMinTokens = 1024;
 // A staged tile image: the tile buffer's K rows and V planes, then its
-// exponent words (the slices' K exponents, the waves' V exponents), in
-// 16-byte chunks
+// exponent words (the slices' K exponents, the waves' V exponents), for a TQ
+// cache then the sign words and the scaled residual norms, in 16-byte chunks
 constexpr int kTileChunks = (kTile * kKStride * 2 + kTile * kVRow) / 4;
-constexpr int kImgChunks = kTileChunks + 3;
+constexpr int kImgChunksPq = kTileChunks + 3;
+// a TQ tile adds its tokens' sign words (64 x 4) and scaled norms (64)
+constexpr int kImgChunksTq = kImgChunksPq + kTile + kTile / 4;
+constexpr int img_chunks(int mode) { return mode == 2 ? kImgChunksTq : kImgChunksPq; }
 
 // Stores 32 values split into f16 hi (11 significant bits) and lo (the
 // exact remainder) at hi[0..31] and lo[0..31], 16 bytes per store.
@@ -135,7 +139,7 @@ struct PrefillArgs {
   int out_dtype;
   int cb_args;               // codebook from cb (L2Norm) instead of the MaxNorm constants
   float cb[16];
-  // staged decode: per KV head, stage_tiles tile images of kImgChunks 16-byte
+  // staged decode: per KV head, stage_tiles tile images of img_chunks(mode) 16-byte
   // chunks (the LDS contents of one decoded tile)
   const uint4 *stage;
   uint4 *stage_out;
@@ -166,9 +170,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // two tile buffers: tile t + 1 is decoded into one while tile t is read
   // from the other
   constexpr int TILE_WORDS = K_WORDS + V_WORDS;
-  static_assert(PH == kDecode || (!QJL && NW == 8), "staged tiles: PQ/PQO codes, 8 waves");
-  static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kImgChunks == kTileChunks + 3),
-                "the tile image is the LDS tile buffer plus its 12 exponent words");
+  constexpr int IMG = img_chunks(MODE);
+  static_assert(PH == kDecode || NW == 8, "staged tiles: 8 waves");
+  static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kImgChunksPq == kTileChunks + 3),
+                "the tile image is the LDS tile buffer plus its 12 exponent words (and the TQ arrays)");
   // (the staging pass decodes straight into the global image)
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[PH == kStage ? 4 : 2 * TILE_WORDS];
   // per tile, read 4 at a time: [0..3] the K exponent E_k of each 16-token slice, [4 + w] the V
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // decoded values)
   static_assert(NW <= 8 && kTile == 64, "4 slices, at most 8 decoding waves");
   __shared__ __attribute__((aligned(16))) int s_xe[2][12];
-  __shared__ float s_cn[2][kTile];       // TQ: |r_t| * qjl_c
+  __shared__ __attribute__((aligned(16))) float s_cn[2][kTile];       // TQ: |r_t| * qjl_c
   __shared__ __attribute__((aligned(16))) uint32_t s_sg[2][kTile * 4];  // TQ: sign words
   __shared__ float s_cb[16];
   __shared__ int s_eq[kRows], s_er[kRows];
@@ -211,16 +216,19 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const long long rec0 = (long long)g * a.kv_head_stride;
   const float lscale = a.softmax_scale * kLog2e;
 
-  if (PH != kStaged && tid < 16) {
-    constexpr int CM = (1 << CB) - 1;
-    float c = a.cb[0];
-    if (a.cb_args) {
+  // the codebook (for decoding) and the sign-nibble table (QJL correction)
+  if (tid < 16) {
+    if (PH != kStaged) {
+      constexpr int CM = (1 << CB) - 1;
+      float c = a.cb[0];
+      if (a.cb_args) {
 #pragma unroll
-      for (int kk = 1; kk <= CM; kk++) c = (tid == kk) ? a.cb[kk] : c;
-    } else {
-      c = pqo_centroid<CB>(tid & CM);
+        for (int kk = 1; kk <= CM; kk++) c = (tid == kk) ? a.cb[kk] : c;
+      } else {
+        c = pqo_centroid<CB>(tid & CM);
+      }
+      s_cb[tid] = c;
     }
-    s_cb[tid] = c;
     auto pm1 = [&](int bit) { return ((tid >> bit) & 1) ? 0x3C00u : 0xBC00u; };
     s_nib[tid] = make_uint2(pm1(0) | (pm1(1) << 16), pm1(2) | (pm1(3) << 16));
   }
@@ -232,16 +240,16 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   uint32_t kw[QW], vw[QW], sgw = 0;
   uint16_t ks = 0, vs = 0, nm = 0;
   // staged: thread tid moves chunks tid + 4 kRows r of a tile image
-  constexpr int IMG_ROUNDS = (kImgChunks + 4 * kRows - 1) / (4 * kRows);
+  constexpr int IMG_ROUNDS = (IMG + 4 * kRows - 1) / (4 * kRows);
   // (native vectors: an array of uint4 structs stays in scratch memory)
   u32x4 img[PH == kStaged ? IMG_ROUNDS : 1];
   auto fetch = [&](int t0) {
     if constexpr (PH == kStaged) {
       const u32x4 *src =
-          reinterpret_cast<const u32x4 *>(a.stage) + ((long long)g * a.stage_tiles + t0 / kTile) * kImgChunks + tid;
+          reinterpret_cast<const u32x4 *>(a.stage) + ((long long)g * a.stage_tiles + t0 / kTile) * IMG + tid;
 #pragma unroll
       for (int r = 0; r < IMG_ROUNDS; r++)
-        if (r + 1 < IMG_ROUNDS || tid + 4 * kRows * r < kImgChunks) img[r] = src[4 * kRows * r];
+        if (r + 1 < IMG_ROUNDS || tid + 4 * kRows * r < IMG) img[r] = src[4 * kRows * r];
       return;
     }
     const int t = min(t0 + ftok, a.kv_len - 1);
@@ -263,7 +271,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // (staging pass: the tile's image in the staging buffer)
   auto tile_base = [&](int b) -> uint32_t * {
     if constexpr (PH == kStage)
-      return reinterpret_cast<uint32_t *>(a.stage_out + ((long long)g * a.stage_tiles + qblk) * kImgChunks);
+      return reinterpret_cast<uint32_t *>(a.stage_out + ((long long)g * a.stage_tiles + qblk) * IMG);
     else
       return s_tile + b * TILE_WORDS;
   };
@@ -275,16 +283,32 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     else
       return s_xe[b];
   };
+  // TQ: the tile's sign words and scaled norms (after the exponent words in
+  // the image)
+  auto sgp = [&](int b) -> uint32_t * {
+    if constexpr (PH == kStage)
+      return tile_base(b) + TILE_WORDS + 12;
+    else
+      return s_sg[b];
+  };
+  auto cnp = [&](int b) -> float * {
+    if constexpr (PH == kStage)
+      return reinterpret_cast<float *>(tile_base(b) + TILE_WORDS + 12 + 4 * kTile);
+    else
+      return s_cn[b];
+  };
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
   // (the query and rq staging precedes the tiles and may span both buffers)
   static_assert((QJL ? 2 : 1) * kRows * kQRow <= 2 * (K_WORDS + V_WORDS), "the split query (and rq) fit the tile region");
   static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
 
   // chunk c of tile buffer b's image: the K tile and V planes, then the
-  // exponent words
+  // exponent words, then (TQ) the sign words and the scaled norms
   auto img_chunk = [&](int b, int c) -> uint4 * {
     if (c < kTileChunks) return reinterpret_cast<uint4 *>(s_tile + b * TILE_WORDS) + c;
-    return reinterpret_cast<uint4 *>(s_xe[b]) + (c - kTileChunks);
+    if (!QJL || c < kImgChunksPq) return reinterpret_cast<uint4 *>(s_xe[b]) + (c - kTileChunks);
+    if (c < kImgChunksPq + kTile) return reinterpret_cast<uint4 *>(s_sg[b]) + (c - kImgChunksPq);
+    return reinterpret_cast<uint4 *>(s_cn[b]) + (c - kImgChunksPq - kTile);
   };
 
   // ---- decode this thread's record into tile buffer b (staged: store the
@@ -294,7 +318,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
       for (int r = 0; r < IMG_ROUNDS; r++) {
         const int c = tid + 4 * kRows * r;
-        if (r + 1 < IMG_ROUNDS || c < kImgChunks) *reinterpret_cast<u32x4 *>(img_chunk(b, c)) = img[r];
+        if (r + 1 < IMG_ROUNDS || c < IMG) *reinterpret_cast<u32x4 *>(img_chunk(b, c)) = img[r];
       }
       return;
     }
@@ -313,9 +337,9 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         xe(b)[4 + wave] = ev;
       }
       if constexpr (QJL) {
-        if (fqb == 0) s_cn[b][ftok] = f16_to_f32(nm) * a.qjl_c;
+        if (fqb == 0) cnp(b)[ftok] = f16_to_f32(nm) * a.qjl_c;
       }
-      if constexpr (QJL) s_sg[b][ftok * 4 + fqb] = sgw;
+      if constexpr (QJL) sgp(b)[ftok * 4 + fqb] = sgw;
       // this thread's code pairs P0 .. P0 + NP - 1 (a wave-uniform part, so
       // every pair index folds to a constant)
       auto decode_pairs = [&](auto p0c) {
@@ -783,30 +807,28 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   const int qb = prefill_rows(MODE) / nr;
   const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
-  if constexpr (MODE != kPTq) {
-    if (a.kv_len > 0 && use_staging((int)grid.x, a.kv_len)) {
-      // staging pass then the attention launch, in stream order; the buffer
-      // is released in stream order after the attention launch
-      a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
-      const size_t bytes = (size_t)a.num_kv_heads * (size_t)a.stage_tiles * kImgChunks * sizeof(uint4);
-      void *buf = nullptr;
-      int dev = 0;
-      (void)hipGetDevice(&dev);
-      hipMemPool_t pool = staging_pool(dev);
-      const hipError_t ae = pool ? hipMallocFromPoolAsync(&buf, bytes, pool, st) : hipMallocAsync(&buf, bytes, st);
-      if (ae != hipSuccess) {
-        (void)hipGetLastError();
-        return tqh::fail(TQ_ERR_DEVICE, "prefill staging buffer of %zu bytes not allocated", bytes);
-      }
-      a.stage = static_cast<const uint4 *>(buf);
-      a.stage_out = static_cast<uint4 *>(buf);
-      hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles * grid.y), block,
-                         0, st, a);
-      launch_attn<BITS, MODE, kStaged>(a, nr, grid, block, st);
-      const int rc = tqh::check_launch("prefill_attn_kernel (staged)");
-      (void)hipFreeAsync(buf, st);
-      return rc;
+  if (a.kv_len > 0 && use_staging((int)grid.x, a.kv_len)) {
+    // staging pass then the attention launch, in stream order; the buffer
+    // is released in stream order after the attention launch
+    a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
+    const size_t bytes = (size_t)a.num_kv_heads * (size_t)a.stage_tiles * img_chunks(MODE) * sizeof(uint4);
+    void *buf = nullptr;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    hipMemPool_t pool = staging_pool(dev);
+    const hipError_t ae = pool ? hipMallocFromPoolAsync(&buf, bytes, pool, st) : hipMallocAsync(&buf, bytes, st);
+    if (ae != hipSuccess) {
+      (void)hipGetLastError();
+      return tqh::fail(TQ_ERR_DEVICE, "prefill staging buffer of %zu bytes not allocated", bytes);
     }
+    a.stage = static_cast<const uint4 *>(buf);
+    a.stage_out = static_cast<uint4 *>(buf);
+    hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles * grid.y), block,
+                       0, st, a);
+    launch_attn<BITS, MODE, kStaged>(a, nr, grid, block, st);
+    const int rc = tqh::check_launch("prefill_attn_kernel (staged)");
+    (void)hipFreeAsync(buf, st);
+    return rc;
   }
   launch_attn<BITS, MODE, kDecode>(a, nr, grid, block, st);
   return tqh::check_launch("prefill_attn_kernel");
