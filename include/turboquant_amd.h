@@ -275,7 +275,8 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
  * that keeps up to 1 GiB between calls; about 71 KB per tile and KV head,
  * 72 KB for TQ);
  * the environment variable
- * TQ_PREFILL_STAGING=0 or 1 forces either path (same results, bit for bit). */
+ * TQ_PREFILL_STAGING=0 or 1 forces either path (both within the tolerance;
+ * staged tiles hold K inverse-rotated, so the two differ by rounding). */
 int tq_cache_prefill_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                                const uint16_t *k_scales, const uint8_t *v_indices,
                                const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,

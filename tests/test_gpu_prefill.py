@@ -16,6 +16,10 @@ torch = pytest.importorskip("torch")
 
 D = 128
 TOL = 1e-3
+# staged tiles (K inverse-rotated once by the staging pass, the query taken
+# unrotated) against tiles decoded in the workgroup (K rotated, the query
+# rotated): the same products rounded in two domains
+PATHS_TOL = 1e-4
 
 
 @pytest.fixture(scope="module")
@@ -137,46 +141,56 @@ def test_prefill_bench_shape_sampled_rows(tq):
         assert err <= TOL, (p, err)
 
 
-@pytest.mark.parametrize("bits,outlier,hq,hkv,ql,t,causal", [
-    (3, orc.OUTLIER_ALL, 16, 8, 300, 300, True),
-    (4, orc.OUTLIER_ALL, 32, 8, 270, 333, True),
-    (3, 0, 16, 16, 260, 260, False),
-    (4, 0, 8, 2, 400, 1000, True),
-    (3, orc.OUTLIER_ALL, 16, 4, 513, 577, False),
+@pytest.mark.parametrize("bits,outlier,hq,hkv,ql,t,causal,qdt", [
+    (3, orc.OUTLIER_ALL, 16, 8, 300, 300, True, "bf16"),
+    (4, orc.OUTLIER_ALL, 32, 8, 270, 333, True, "bf16"),
+    (3, 0, 16, 16, 260, 260, False, "f16"),
+    (4, 0, 8, 2, 400, 1000, True, "bf16"),
+    (3, orc.OUTLIER_ALL, 16, 4, 513, 577, False, "f32"),
+    (3, orc.OUTLIER_ALL, 16, 8, 300, 1100, True, "f16"),
 ])
-def test_staged_tiles_bit_identical(tq, monkeypatch, bits, outlier, hq, hkv, ql, t, causal):
-    """Tiles decoded once by the staging pass and copied into each
-    workgroup's LDS give the same bits as tiles decoded in every workgroup
-    (TQ_PREFILL_STAGING forces either path); both within TOL of the oracle.
-    Shapes: GQA 1, 2, 4 and 8, 3 and 4 bits, PQ and PQO codes, token counts
-    that end inside a tile, queries after earlier tokens."""
+def test_staged_and_in_workgroup_tiles(tq, monkeypatch, bits, outlier, hq, hkv, ql, t, causal, qdt):
+    """Tiles decoded once by the staging pass (K inverse-rotated, the query
+    unrotated: two products per key slice for bf16 and f16 queries, three
+    for f32) and tiles decoded in every workgroup (TQ_PREFILL_STAGING forces
+    either path): both within TOL of the oracle, within PATHS_TOL of each
+    other.  Shapes: GQA 1, 2, 4 and 8, 3 and 4 bits, PQ and PQO codes, token
+    counts that end inside a tile, queries after earlier tokens."""
     rng = np.random.default_rng(1700 + t + ql)
     k = kv_outlier(rng, hkv, t)
     v = kv_outlier(rng, hkv, t)
     cap = t + 3
     ki, ks, kd = _records(bits, outlier, k, cap)
     vi, vs, vd = _records(bits, outlier, v, cap)
-    q = bf16_round(rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D)))
-    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    q = rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D))
+    if qdt == "bf16":
+        q = bf16_round(q)
+        qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    elif qdt == "f16":
+        q = q.astype(np.float16).astype(np.float32)
+        qd = _dev(q).to(torch.float16)
+    else:
+        qd = _dev(q)
     scale = 1 / math.sqrt(D)
     outs = []
     for mode in ("0", "1"):
         monkeypatch.setenv("TQ_PREFILL_STAGING", mode)
         outs.append(tq.cache_prefill_attention(qd, ki, ks, vi, vs, hkv, bits, t, cap, scale, outlier,
-                                               causal=causal))
+                                               causal=causal, out_dtype=torch.float32))
     torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1])
+    assert float((outs[0] - outs[1]).abs().max()) <= PATHS_TOL
     ref = orc.attention_prefill(q, kd, vd, scale, causal)
-    err = np.abs(outs[1].cpu().numpy() - ref).max()
-    assert err <= TOL, err
+    for o in outs:
+        err = np.abs(o.cpu().numpy() - ref).max()
+        assert err <= TOL, err
 
 
 @pytest.mark.parametrize("outlier", [orc.OUTLIER_ALL, 0])
 def test_l2norm_cache_prefill_staged_and_in_workgroup(tq, monkeypatch, outlier):
     """A PqoCache on the L2Norm codebooks (PQO codes, and PQ codes in 3-bit
     slots): the staging pass and the in-workgroup decode read the caller's
-    codebook from the launch arguments; both paths give the same bits and
-    match the oracle's L2Norm dequantization within TOL."""
+    codebook from the launch arguments; both paths agree within PATHS_TOL
+    and match the oracle's L2Norm dequantization within TOL."""
     bits, hkv, hq, t, ql = 3, 4, 8, 700, 300
     rng = np.random.default_rng(1900 + (1 if outlier else 0))
     k = kv_outlier(rng, hkv, t)
@@ -192,14 +206,15 @@ def test_l2norm_cache_prefill_staged_and_in_workgroup(tq, monkeypatch, outlier):
         monkeypatch.setenv("TQ_PREFILL_STAGING", mode)
         outs.append(cache.attend_prefill(0, _dev(q[None]), scale, out_dtype=torch.float32))
     torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1])
+    assert float((outs[0] - outs[1]).abs().max()) <= PATHS_TOL
     pk, sk = orc.polar_quantize(bits, outlier, k.reshape(-1, D), D, norm_mode=1)
     pv, sv = orc.polar_quantize(bits, outlier, v.reshape(-1, D), D, norm_mode=1)
     kd = orc.polar_dequantize(bits, outlier, pk, sk, D, norm_mode=1).reshape(hkv, t, D)
     vd = orc.polar_dequantize(bits, outlier, pv, sv, D, norm_mode=1).reshape(hkv, t, D)
     ref = orc.attention_prefill(q, kd, vd, scale, True)
-    err = np.abs(outs[1][0].cpu().numpy() - ref).max()
-    assert err <= TOL, err
+    for o in outs:
+        err = np.abs(o[0].cpu().numpy() - ref).max()
+        assert err <= TOL, err
 
 
 def test_staged_prefill_repeats_across_synchronizations(tq, monkeypatch):
@@ -242,9 +257,9 @@ def test_staged_prefill_repeats_across_synchronizations(tq, monkeypatch):
 def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, causal):
     """TQ-cache prefill attention (QJL correction inside the key pass) over
     several 128-row workgroups per KV head, GQA 4, 1 and 2, causal and full:
-    staged tiles (signs and norms in the image) and in-workgroup decode give
-    the same bits, within TOL of the oracle's dequantized keys and values
-    plus its logit bias."""
+    staged tiles (signs and norms in the image) and in-workgroup decode agree
+    within PATHS_TOL and lie within TOL of the oracle's dequantized keys and
+    values plus its logit bias."""
     rng = np.random.default_rng(2300 + t + ql)
     k = kv_outlier(rng, hkv, t)
     v = kv_outlier(rng, hkv, t)
@@ -256,8 +271,7 @@ def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, 
         monkeypatch.setenv("TQ_PREFILL_STAGING", mode)
         outs.append(cache.attend_prefill(0, _dev(q[None]), 1 / math.sqrt(D), causal=causal, out_dtype=torch.float32))
     torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1])
-    out = outs[1]
+    assert float((outs[0] - outs[1]).abs().max()) <= PATHS_TOL
     pk, sk = orc.polar_quantize(bits, 0, k.reshape(-1, D), D)
     pv, sv = orc.polar_quantize(bits, 0, v.reshape(-1, D), D)
     kd = orc.polar_dequantize(bits, 0, pk, sk, D)
@@ -265,5 +279,6 @@ def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, 
     sg, nm = orc.tq_signs_norms(k.reshape(-1, D), kd)
     bias = orc.tq_logit_bias(q, sg.reshape(hkv, t, -1), nm.reshape(hkv, t))
     ref = orc.attention_prefill(q, kd.reshape(hkv, t, D), vd, 1 / math.sqrt(D), causal, bias)
-    err = np.abs(out[0].cpu().numpy() - ref).max()
-    assert err <= TOL, err
+    for o in outs:
+        err = np.abs(o[0].cpu().numpy() - ref).max()
+        assert err <= TOL, err

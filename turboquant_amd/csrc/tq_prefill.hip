@@ -16,7 +16,8 @@
 // significant bits, lo = the remainder), then each wave (16 rows) runs
 //   S^T = K Q^T          16x16x32 MFMAs per 32-element slice: K hi x Q hi,
 //                        K hi x Q lo, K lo x Q hi (22-bit products, lo x lo
-//                        dropped, f32 accumulation)
+//                        dropped, f32 accumulation; staged tiles with a bf16
+//                        or f16 query: K hi x Q, K lo x Q)
 //   corr^T = Sg RQ^T     TQ: the keys' +-1 sign bits against rq hi/lo
 //   O^T += V^T P^T       16x16x32 MFMAs over two 16-token blocks whose B
 //                        operand is S^T's accumulator layout (4 tokens per
@@ -37,11 +38,12 @@
 // so a staging pass (the same kernel, one workgroup per tile and KV head)
 // decodes each tile once into an image of the tile buffer's LDS contents (TQ:
 // with the sign words and scaled norms), and the attention workgroups copy
-// the images into LDS in place of decoding; the LDS contents, and so the
-// outputs, are bit-identical.  Both
-// launches put KV head g on one XCD (g = linear index mod 8, workgroups being
-// dealt to the 8 XCDs in turn): a head's images are written and read through
-// one L2.
+// the images into LDS in place of decoding.  The staging pass inverse-rotates
+// K (original domain) and the attention takes the query unrotated, so a bf16
+// or f16 query is exact in f16 and each key slice takes two products (K hi Q,
+// K lo Q) instead of three; V stays rotated.  Both launches put KV head g on
+// one XCD (g = linear index mod 8, workgroups being dealt to the 8 XCDs in
+// turn): a head's images are written and read through one L2.
 #include "tq_common.h"
 #include "tq_device.h"
 #include "tq_mfma.h"
@@ -154,6 +156,10 @@ template <int BITS, int MODE, int NR, int PH>
 __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(PrefillArgs a) {
   constexpr int CB = MODE == kPPqo ? BITS : BITS - 1;
   constexpr bool QJL = MODE == kPTq;
+  // staged tiles hold K in the original domain (the staging pass inverse-
+  // rotates it) and the query is taken as it is: a bf16 or f16 query is then
+  // exact in f16 and the key pass needs no product with its lo part
+  constexpr bool ORIG = PH != kDecode;
   constexpr int HD = 128, QW = BITS, PACKED = 16 * QW;
   constexpr int kRows = prefill_rows(MODE);
   constexpr int NW = kRows / 16;            // waves
@@ -236,7 +242,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // thread (token, qblock) fetches one record of K and V per tile
   // thread (token, qblock, part): wave w decodes tokens 16 (w / SPLIT) ..
   // + 15, code pairs NP (w % SPLIT) .. + NP - 1 of every qblock
-  const int ftok = 16 * (wave / SPLIT) + (lane >> 2), fqb = lane & 3, fpart = wave % SPLIT;
+  // (staging pass: waves 0-3 take the K records of slices 0-3, waves 4-7 the
+  // V records, whole qblocks)
+  const int ftok = 16 * (PH == kStage ? (wave & 3) : wave / SPLIT) + (lane >> 2), fqb = lane & 3,
+            fpart = wave % SPLIT;
   uint32_t kw[QW], vw[QW], sgw = 0;
   uint16_t ks = 0, vs = 0, nm = 0;
   // staged: thread tid moves chunks tid + 4 kRows r of a tile image
@@ -250,6 +259,23 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
       for (int r = 0; r < IMG_ROUNDS; r++)
         if (r + 1 < IMG_ROUNDS || tid + 4 * kRows * r < IMG) img[r] = src[4 * kRows * r];
+      return;
+    }
+    if constexpr (PH == kStage) {
+      // one K (waves 0-3) or V (waves 4-7) record, into kw and ks
+      const long long rec = rec0 + min(t0 + ftok, a.kv_len - 1);
+      const bool kwave = wave < 4;
+      const uint32_t *src =
+          reinterpret_cast<const uint32_t *>((kwave ? a.k_idx : a.v_idx) + rec * PACKED + fqb * 4 * QW);
+#pragma unroll
+      for (int w = 0; w < QW; w++) kw[w] = src[w];
+      ks = (kwave ? a.k_sc : a.v_sc)[rec * 4 + fqb];
+      if constexpr (QJL) {
+        if (kwave) {
+          sgw = a.signs[rec * 4 + fqb];
+          nm = a.norms[rec];
+        }
+      }
       return;
     }
     const int t = min(t0 + ftok, a.kv_len - 1);
@@ -402,11 +428,73 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 
   // ---- staging pass: decode tile qblk of KV head g once, straight
   // into its image (the K rows' padding words stay unwritten: nothing reads
-  // them), for the attention workgroups of every query block ----
+  // them), for the attention workgroups of every query block.  Thread
+  // (token, qblock) of waves 0-3 decodes a K record and inverse-rotates it,
+  // k = H (d . c s) / sqrt 32 per 32-element block with d the decode signs
+  // (the transpose of the query's rotation); waves 4-7 decode a V record,
+  // which stays rotated.  One K and one V exponent per 16-token slice. ----
   if constexpr (PH == kStage) {
     fetch(qblk * kTile);
     __syncthreads();  // codebook staged
-    decode_tile(0);
+    const bool kwave = wave < 4;
+    const int slice = wave & 3;
+    const float sc = fabsf(f16_to_f32(ks));
+    const int e = pow2_exponent(wave_max(sc));
+    const float f = sc * exp2i(-e);
+    if (lane == 0) {
+      if (kwave) {
+        xe(0)[slice] = e;
+      } else {
+        xe(0)[4 + 2 * slice] = e;
+        xe(0)[5 + 2 * slice] = e;
+      }
+    }
+    if constexpr (QJL) {
+      if (kwave) {
+        if (fqb == 0) cnp(0)[ftok] = f16_to_f32(nm) * a.qjl_c;
+        sgp(0)[ftok * 4 + fqb] = sgw;
+      }
+    }
+    constexpr uint32_t SM = (1u << BITS) - 1u, CMk = (1u << CB) - 1u;
+    float y[32];
+#pragma unroll
+    for (int pp = 0; pp < 16; pp++) {
+      const uint32_t code = pair_code<BITS>(kw, pp);
+      y[2 * pp] = s_cb[code & SM & CMk];
+      y[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
+    }
+    uint32_t hw[16], lw[16];
+    if (kwave) {
+#pragma unroll
+      for (int j = 0; j < 32; j++) y[j] = (y[j] * f) * decode_sign(j);
+      butterfly<32>(y);
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const float x0 = y[2 * j] * kInvSqrt32, x1 = y[2 * j + 1] * kInvSqrt32;
+        hw[j] = pack_f16(x0, x1);
+        lw[j] = pack_rem(x0, x1, hw[j], mone);
+      }
+      uint4 *krow = reinterpret_cast<uint4 *>(ktile(0) + ftok * kKStride);
+#pragma unroll
+      for (int gq = 0; gq < 4; gq++) {
+        krow[kchunk(8 * fqb + 2 * gq)] = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
+        krow[kchunk(8 * fqb + 2 * gq + 1)] = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const float x0 = y[2 * j] * f, x1 = y[2 * j + 1] * f;
+        hw[j] = pack_f16(x0, x1);
+        lw[j] = pack_rem(x0, x1, hw[j], mone);
+      }
+      _Float16 *vrh = vhi(0) + ftok * kVRow, *vrl = vrh + V_HALVES;
+#pragma unroll
+      for (int gq = 0; gq < 4; gq++) {
+        const int c = 8 * vchunk(4 * fqb + gq);
+        *reinterpret_cast<uint4 *>(vrh + c) = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
+        *reinterpret_cast<uint4 *>(vrl + c) = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
+      }
+    }
     return;
   }
 
@@ -439,11 +527,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         for (int j = 0; j < 32; j++) x[j] = f16_to_f32(hb[j]);
       }
     }
-    butterfly<32>(x);
+    // (staged tiles: the query as it is; the softmax scale joins the row's
+    // exponent factor)
+    if constexpr (!ORIG) butterfly<32>(x);
     float m = 0.f;
 #pragma unroll
     for (int j = 0; j < 32; j++) {
-      x[j] = x[j] * (decode_sign(j) * (kInvSqrt32 * lscale));
+      if constexpr (!ORIG) x[j] = x[j] * (decode_sign(j) * (kInvSqrt32 * lscale));
       m = fmaxf(m, fabsf(x[j]));
     }
     m = fmaxf(m, dpp_quad_xor1(m));
@@ -506,6 +596,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const bool my_ok = my_qi < a.q_len;
   const bool wave_rows_ok = __all(my_ok);  // every row of the wave is a query
   const float eq_scale = exp2i(s_eq[myrow]);
+  // the row's factor on the key products: 2^E_q (staged: times the softmax
+  // scale, which the unrotated query does not carry)
+  const float eqz = ORIG ? eq_scale * lscale : eq_scale;
+  // the product with the query's lo part: every query in the workgroup's
+  // decode, f32 queries on staged tiles (a bf16 or f16 query scaled by 2^-E_q
+  // is exact in f16 down to 2^-24 of the row's maximum)
+  const bool q_lo = !ORIG || a.q_dtype == kF32;
   const float er_scale = QJL ? exp2i(s_er[myrow]) : 0.f;
   const int qpos = a.kv_len - a.q_len + my_qi;  // causal limit of this row
   const int qmin = a.kv_len - a.q_len + i0;     // the workgroup's first query position
@@ -573,8 +670,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       }
 #pragma unroll
       for (int tb = 0; tb < 4; tb++) dk[tb] = mfma(ah[tb], qop[s][0], dk[tb]);
+      if (q_lo) {
 #pragma unroll
-      for (int tb = 0; tb < 4; tb++) dk[tb] = mfma(ah[tb], qop[s][1], dk[tb]);
+        for (int tb = 0; tb < 4; tb++) dk[tb] = mfma(ah[tb], qop[s][1], dk[tb]);
+      }
 #pragma unroll
       for (int tb = 0; tb < 4; tb++) dk[tb] = mfma(al[tb], qop[s][0], dk[tb]);
     }
@@ -599,7 +698,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         for (int i = 0; i < 4; i++) {
           const int tp = t0 + 16 * tb + 4 * lg + i;
           // without QJL the slice's 2^E_k and the row's 2^E_q are applied in the softmax
-          float v = QJL ? d[i] * (exp2i(ekt[tb]) * eq_scale) : d[i];
+          float v = QJL ? d[i] * (exp2i(ekt[tb]) * eqz) : d[i];
           if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
           if constexpr (MASK) {
             const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
@@ -613,10 +712,11 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       else logits(std::true_type{});
     }
     // ---- online softmax of this row (its 64 logits sit in the 4 lanes l16 + 16 k) ----
-    // logit = x z_tb, z_tb a power of 2 (exact): 2^E_k,tb 2^E_q (QJL: 1)
+    // logit = x z_tb, z_tb = 2^E_k,tb 2^E_q (a power of 2, exact; staged
+    // tiles: times the softmax scale) (QJL: 1)
     float zt[4];
 #pragma unroll
-    for (int tb = 0; tb < 4; tb++) zt[tb] = QJL ? 1.f : exp2i(ekt[tb]) * eq_scale;
+    for (int tb = 0; tb < 4; tb++) zt[tb] = QJL ? 1.f : exp2i(ekt[tb]) * eqz;
     float mt = -INFINITY;
 #pragma unroll
     for (int tb = 0; tb < 4; tb++)
