@@ -275,7 +275,8 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
  * that keeps up to 1 GiB between calls; about 71 KB per tile and KV head,
  * 72 KB for TQ);
  * the environment variable
- * TQ_PREFILL_STAGING=0 or 1 forces either path (both within the tolerance;
+ * TQ_PREFILL_STAGING=0 or 1 forces either path (never staged when a KV
+ * head's images would reach 2^31 bytes, about 1.9 M tokens; both within the tolerance;
  * staged tiles hold K inverse-rotated, so the two differ by rounding). */
 int tq_cache_prefill_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                                const uint16_t *k_scales, const uint8_t *v_indices,

@@ -252,13 +252,26 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   constexpr int IMG_ROUNDS = (IMG + 4 * kRows - 1) / (4 * kRows);
   // (native vectors: an array of uint4 structs stays in scratch memory)
   u32x4 img[PH == kStaged ? IMG_ROUNDS : 1];
+  // staged: KV head g's tile images as one buffer resource (scalar registers;
+  // the host bounds a head's images below 2^31 bytes)
+  auto make_img_rsrc = [&]() {
+    const uint64_t p = reinterpret_cast<uint64_t>(a.stage + (long long)g * a.stage_tiles * IMG);
+    const uint64_t ps = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p);
+    const int n = __builtin_amdgcn_readfirstlane(a.stage_tiles * IMG * 16);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(ps), (short)0, n, 0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t img_rsrc = make_img_rsrc();
   auto fetch = [&](int t0) {
     if constexpr (PH == kStaged) {
-      const u32x4 *src =
-          reinterpret_cast<const u32x4 *>(a.stage) + ((long long)g * a.stage_tiles + t0 / kTile) * IMG + tid;
+      // buffer loads: the lane's offset in a vector register (the same for
+      // every tile), the tile's and the round's in a scalar register
+      const uint32_t soff = (uint32_t)(t0 / kTile) * (uint32_t)(IMG * 16);
 #pragma unroll
       for (int r = 0; r < IMG_ROUNDS; r++)
-        if (r + 1 < IMG_ROUNDS || tid + 4 * kRows * r < IMG) img[r] = src[4 * kRows * r];
+        if (r + 1 < IMG_ROUNDS || tid + 4 * kRows * r < IMG)
+          img[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 img_rsrc, (uint32_t)tid * 16u, soff + (uint32_t)(r * 4 * kRows * 16), 0));
       return;
     }
     if constexpr (PH == kStage) {
@@ -692,24 +705,22 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
           dc = mfma(sa, rop[sl][1], dc);
         }
       }
-      auto logits = [&](auto maskc) {
-        constexpr bool MASK = decltype(maskc)::value;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        // without QJL the slice's 2^E_k and the row's 2^E_q are applied in the softmax
+        float v = QJL ? d[i] * (exp2i(ekt[tb]) * eqz) : d[i];
+        if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
+        x[tb][i] = v;
+      }
+      // the mask, in place, for tiles that are not open to every row
+      if (!(open && wave_rows_ok)) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int tp = t0 + 16 * tb + 4 * lg + i;
-          // without QJL the slice's 2^E_k and the row's 2^E_q are applied in the softmax
-          float v = QJL ? d[i] * (exp2i(ekt[tb]) * eqz) : d[i];
-          if constexpr (QJL) v = __builtin_fmaf(dc[i], s_cn[cur][16 * tb + 4 * lg + i] * er_scale, v);
-          if constexpr (MASK) {
-            const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
-            x[tb][i] = ok ? v : -INFINITY;
-          } else {
-            x[tb][i] = v;
-          }
+          const bool ok = my_ok && (open || (tp < a.kv_len && (!a.causal || tp <= qpos)));
+          x[tb][i] = ok ? x[tb][i] : -INFINITY;
         }
-      };
-      if (open && wave_rows_ok) logits(std::false_type{});
-      else logits(std::true_type{});
+      }
     }
     // ---- online softmax of this row (its 64 logits sit in the 4 lanes l16 + 16 k) ----
     // logit = x z_tb, z_tb = 2^E_k,tb 2^E_q (a power of 2, exact; staged
@@ -855,8 +866,12 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 // Whether to decode each tile once into a staging buffer: with q_blocks query
 // blocks per KV head, the workgroups would otherwise decode a tile up to
 // q_blocks times (causal: about half of that on average).  TQ_PREFILL_STAGING
-// = 0 / 1 forces either path.
-bool use_staging(int q_blocks, int kv_len) {
+// = 0 / 1 forces either path, except that a KV head's images must stay below
+// 2^31 bytes (about 1.9 million tokens).
+bool use_staging(int q_blocks, int kv_len, int mode) {
+  // a KV head's images are read through one buffer resource: below 2^31 bytes
+  const long long head_bytes = (long long)((kv_len + kTile - 1) / kTile) * img_chunks(mode) * 16;
+  if (head_bytes >= (1ll << 31)) return false;
   if (const char *e = getenv("TQ_PREFILL_STAGING")) {
     if (e[0] == '0') return false;
     if (e[0] == '1') return true;
@@ -907,7 +922,7 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   const int qb = prefill_rows(MODE) / nr;
   const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
-  if (a.kv_len > 0 && use_staging((int)grid.x, a.kv_len)) {
+  if (a.kv_len > 0 && use_staging((int)grid.x, a.kv_len, MODE)) {
     // staging pass then the attention launch, in stream order; the buffer
     // is released in stream order after the attention launch
     a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
