@@ -249,12 +249,14 @@ def test_staged_prefill_repeats_across_synchronizations(tq, monkeypatch):
     assert torch.equal(first, other)
 
 
-@pytest.mark.parametrize("bits,hq,hkv,ql,t,causal", [
-    (3, 16, 4, 300, 700, True),
-    (4, 8, 8, 200, 333, False),
-    (3, 16, 8, 257, 257, True),
+@pytest.mark.parametrize("bits,hq,hkv,ql,t,causal,qdt", [
+    (3, 16, 4, 300, 700, True, "f32"),
+    (4, 8, 8, 200, 333, False, "f32"),
+    (3, 16, 8, 257, 257, True, "f32"),
+    (3, 16, 8, 300, 1100, True, "bf16"),
+    (4, 16, 4, 260, 600, False, "bf16"),
 ])
-def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, causal):
+def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, causal, qdt):
     """TQ-cache prefill attention (QJL correction inside the key pass) over
     several 128-row workgroups per KV head, GQA 4, 1 and 2, causal and full:
     staged tiles (signs and norms in the image) and in-workgroup decode agree
@@ -265,11 +267,17 @@ def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, 
     v = kv_outlier(rng, hkv, t)
     cache = tq.TqCache(tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1, outlier_blocks=0))
     q = rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D))
+    if qdt == "bf16":
+        # (staged tiles take two products per key slice for a bf16 query)
+        q = bf16_round(q)
+        qd = _dev(bf16_bits(q)).view(torch.bfloat16)[None]
+    else:
+        qd = _dev(q[None])
     cache.prefill(0, _dev(k[None]), _dev(v[None]), _dev(q[None]))
     outs = []
     for mode in ("0", "1"):
         monkeypatch.setenv("TQ_PREFILL_STAGING", mode)
-        outs.append(cache.attend_prefill(0, _dev(q[None]), 1 / math.sqrt(D), causal=causal, out_dtype=torch.float32))
+        outs.append(cache.attend_prefill(0, qd, 1 / math.sqrt(D), causal=causal, out_dtype=torch.float32))
     torch.cuda.synchronize()
     assert float((outs[0] - outs[1]).abs().max()) <= PATHS_TOL
     pk, sk = orc.polar_quantize(bits, 0, k.reshape(-1, D), D)
