@@ -272,8 +272,8 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
  * blocks per KV head over 1024 or more tokens decode each 64-token tile once
  * into a stream-ordered staging buffer (hipMallocFromPoolAsync /
  * hipFreeAsync on stream, from a memory pool of the library's own per device
- * that keeps up to 1 GiB between calls; about 71 KB per tile and KV head,
- * 72 KB for TQ);
+ * that keeps up to 1 GiB between calls; about 72 KB per tile and KV head,
+ * 73 KB for TQ);
  * the environment variable
  * TQ_PREFILL_STAGING=0 or 1 forces either path (never staged when a KV
  * head's images would reach 2^31 bytes, about 1.9 M tokens; both within the tolerance;

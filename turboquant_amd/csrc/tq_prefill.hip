@@ -60,16 +60,18 @@ using namespace tqm;
 // the TQ mode too (its waves fit 244 registers at 8 waves per workgroup)
 constexpr int prefill_rows(int) { return 128; }
 constexpr int kTile = 64;   // tokens per tile
-constexpr int kKStride = 66;  // uint2 per token row of the K tile (32 chunks of 16 bytes + pad)
+constexpr int kKStride = 68;  // uint2 per token row of the K tile (32 chunks of 16 bytes + pad)
 constexpr int kVRow = 144;    // halves per token row of the V tiles (128 elements + pad: the
                               // transposing reads of 4 tokens x 4 element quads hit 32 distinct banks)
 
 // A K tile row holds, per 8-element group g, a 16-byte chunk of hi halves
-// (2 g) and one of lo halves (2 g + 1).  Chunk c sits at c ^ 2 ((c >> 3) & 3):
-// the four lanes of a token, one per qblock (chunks 8 apart), write four
-// distinct bank groups instead of one, and the S^T reads (one chunk of 8
-// consecutive tokens, rows 33 chunks apart) stay distinct.
-__device__ __forceinline__ int kchunk(int c) { return c ^ (2 * ((c >> 3) & 3)); }
+// (2 g) and one of lo halves (2 g + 1).  Chunk c of row r sits at
+// c ^ 2 ((c >> 3) & 3) ^ (r & 1), rows 34 chunks apart: the S^T reads (16
+// rows x 4 chunks per 16-byte read) and the in-workgroup decode's stores (16
+// tokens x 4 qblocks) are both free of LDS bank conflicts on gfx950 (measured
+// with SQ_LDS_BANK_CONFLICT: the previous 33-chunk rows without the row term
+// cost the reads 3.9 conflict cycles each, 2x their 4-cycle minimum).
+__device__ __forceinline__ int kchunk(int c, int row) { return c ^ (2 * ((c >> 3) & 3)) ^ (row & 1); }
 // The V rows' 16-byte chunk c (8 elements of one plane) sits at chunk
 // c ^ ((c >> 3) & 1): rows are 18 chunks apart, and the 16-byte stores of
 // tokens t, t + 1 (qblocks 0-3 each: chunks 0, 4, 8, 12 from the row start)
@@ -412,8 +414,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
         for (int i = 0; i < NP / 4; i++) {
           const int c = 8 * fqb + 2 * (P0 / 4 + i);
-          krow[kchunk(c)] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
-          krow[kchunk(c + 1)] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
+          krow[kchunk(c, ftok)] = make_uint4(hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]);
+          krow[kchunk(c + 1, ftok)] = make_uint4(lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]);
         }
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
@@ -490,8 +492,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       uint4 *krow = reinterpret_cast<uint4 *>(ktile(0) + ftok * kKStride);
 #pragma unroll
       for (int gq = 0; gq < 4; gq++) {
-        krow[kchunk(8 * fqb + 2 * gq)] = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
-        krow[kchunk(8 * fqb + 2 * gq + 1)] = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
+        krow[kchunk(8 * fqb + 2 * gq, ftok)] = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
+        krow[kchunk(8 * fqb + 2 * gq + 1, ftok)] = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
       }
     } else {
 #pragma unroll
@@ -677,7 +679,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
       for (int tb = 0; tb < 4; tb++) {
         const uint4 *krow = reinterpret_cast<const uint4 *>(kt + (16 * tb + l16) * kKStride);
-        const uint4 kh = krow[kchunk(8 * s + 2 * lg)], kl = krow[kchunk(8 * s + 2 * lg + 1)];
+        const uint4 kh = krow[kchunk(8 * s + 2 * lg, l16)], kl = krow[kchunk(8 * s + 2 * lg + 1, l16)];
         ah[tb] = u32x4{kh.x, kh.y, kh.z, kh.w};
         al[tb] = u32x4{kl.x, kl.y, kl.z, kl.w};
       }
