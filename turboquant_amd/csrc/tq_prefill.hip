@@ -182,8 +182,8 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   static_assert(PH == kDecode || NW == 8, "staged tiles: 8 waves");
   static_assert(PH == kDecode || (TILE_WORDS / 4 == kTileChunks && kImgChunksPq == kTileChunks + 3),
                 "the tile image is the LDS tile buffer plus its 12 exponent words (and the TQ arrays)");
-  // (the staging pass decodes straight into the global image)
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[PH == kStage ? 4 : 2 * TILE_WORDS];
+  // (the staging pass decodes into one buffer, then copies it out)
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[PH == kStage ? TILE_WORDS : 2 * TILE_WORDS];
   // per tile, read 4 at a time: [0..3] the K exponent E_k of each 16-token slice, [4 + w] the V
   // exponent E_v of decoding wave w's slice (the exponents folded out of the
   // decoded values)
@@ -309,35 +309,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   };
   // buffer b: K tile at s_tile + b TILE_WORDS, V hi plane after it, lo plane
   // after that
-  // (staging pass: the tile's image in the staging buffer)
-  auto tile_base = [&](int b) -> uint32_t * {
-    if constexpr (PH == kStage)
-      return reinterpret_cast<uint32_t *>(a.stage_out + ((long long)g * a.stage_tiles + qblk) * IMG);
-    else
-      return s_tile + b * TILE_WORDS;
-  };
+  auto tile_base = [&](int b) -> uint32_t * { return s_tile + b * TILE_WORDS; };
   auto ktile = [&](int b) { return reinterpret_cast<uint2 *>(tile_base(b)); };
   auto vhi = [&](int b) { return reinterpret_cast<_Float16 *>(tile_base(b) + K_WORDS); };
-  auto xe = [&](int b) -> int * {
-    if constexpr (PH == kStage)
-      return reinterpret_cast<int *>(tile_base(b) + TILE_WORDS);
-    else
-      return s_xe[b];
-  };
-  // TQ: the tile's sign words and scaled norms (after the exponent words in
-  // the image)
-  auto sgp = [&](int b) -> uint32_t * {
-    if constexpr (PH == kStage)
-      return tile_base(b) + TILE_WORDS + 12;
-    else
-      return s_sg[b];
-  };
-  auto cnp = [&](int b) -> float * {
-    if constexpr (PH == kStage)
-      return reinterpret_cast<float *>(tile_base(b) + TILE_WORDS + 12 + 4 * kTile);
-    else
-      return s_cn[b];
-  };
+  auto xe = [&](int b) -> int * { return s_xe[b]; };
+  // TQ: the tile's sign words and scaled norms
+  auto sgp = [&](int b) -> uint32_t * { return s_sg[b]; };
+  auto cnp = [&](int b) -> float * { return s_cn[b]; };
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
   // (the query and rq staging precedes the tiles and may span both buffers)
   static_assert((QJL ? 2 : 1) * kRows * kQRow <= 2 * (K_WORDS + V_WORDS), "the split query (and rq) fit the tile region");
@@ -441,13 +419,15 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     }
   };
 
-  // ---- staging pass: decode tile qblk of KV head g once, straight
-  // into its image (the K rows' padding words stay unwritten: nothing reads
-  // them), for the attention workgroups of every query block.  Thread
-  // (token, qblock) of waves 0-3 decodes a K record and inverse-rotates it,
-  // k = H (d . c s) / sqrt 32 per 32-element block with d the decode signs
-  // (the transpose of the query's rotation); waves 4-7 decode a V record,
-  // which stays rotated.  One K and one V exponent per 16-token slice. ----
+  // ---- staging pass: decode tile qblk of KV head g once into LDS, then
+  // copy it out as the tile's image (16 contiguous bytes per lane: each store
+  // instruction writes 1 KiB in 16 lines, where the decode's own layout would
+  // touch 64; the K rows' padding words are never read), for the attention
+  // workgroups of every query block.  Thread (token, qblock) of waves 0-3
+  // decodes a K record and inverse-rotates it, k = H (d . c s) / sqrt 32 per
+  // 32-element block with d the decode signs (the transpose of the query's
+  // rotation); waves 4-7 decode a V record, which stays rotated.  One K and
+  // one V exponent per 16-token slice. ----
   if constexpr (PH == kStage) {
     fetch(qblk * kTile);
     __syncthreads();  // codebook staged
@@ -509,6 +489,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
         *reinterpret_cast<uint4 *>(vrh + c) = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
         *reinterpret_cast<uint4 *>(vrl + c) = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
       }
+    }
+    __syncthreads();
+    u32x4 *dst = reinterpret_cast<u32x4 *>(a.stage_out + ((long long)g * a.stage_tiles + qblk) * IMG);
+#pragma unroll
+    for (int r = 0; r < IMG_ROUNDS; r++) {
+      const int c = tid + 4 * kRows * r;
+      if (r + 1 < IMG_ROUNDS || c < IMG) dst[c] = *reinterpret_cast<const u32x4 *>(img_chunk(0, c));
     }
     return;
   }
