@@ -500,6 +500,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     return;
   }
 
+  // the workgroup's tiles; the first tile's records (staged: image) are
+  // requested before the query, so the two latencies overlap
+  const int last_q = min(a.q_len - 1, i0 + QB - 1);
+  const int kv_end = a.causal ? min(a.kv_len, a.kv_len - a.q_len + last_q + 1) : a.kv_len;
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+  if (ntiles > 0) fetch(0);
+
   // ---- query rows: thread (row, quarter) rotates one 32-element block ----
   // (the V tile region holds the split query until the operands are built)
   const int prow = tid >> 2, pq = tid & 3;
@@ -611,11 +618,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   __syncthreads();  // operands built: the tiles may overwrite the query staging
 
   // ---- tiles ----
-  const int last_q = min(a.q_len - 1, i0 + QB - 1);
-  const int kv_end = a.causal ? min(a.kv_len, a.kv_len - a.q_len + last_q + 1) : a.kv_len;
-  const int ntiles = (kv_end + kTile - 1) / kTile;
 
-  if (ntiles > 0) fetch(0);
 
   float m_run = -INFINITY, l_run = 0.f;
   int ev_cur = -1000;
