@@ -87,10 +87,11 @@ constexpr int kORow = 128 + 4;  // floats
 
 // Shapes whose tiles are decoded once, in a staging pass, instead of in every
 // workgroup: at least this many query blocks per KV head and tokens (the
-// pass and its buffer cost 15-20 us, the decode it saves about a fifth of
-// each workgroup's time; 16/8 heads, in-workgroup vs staged, us: 512 x 512
-// causal 36.5 vs 40.2, 1024 x 1024 64.6 vs 62.2, 2048 x 2048 119.9 vs 106.7,
-// 128 queries x 2048 tokens full 115.3 vs 110.6)
+// second launch and its buffer have a fixed cost, the decode it saves is
+// about a fifth of each workgroup's time; 16/8 heads, in-workgroup vs staged,
+// us, measured with a 14-18 us staging pass: 512 x 512 causal 36.5 vs 40.2,
+// 1024 x 1024 64.6 vs 62.2, 2048 x 2048 119.9 vs 106.7, 128 queries x 2048
+// tokens full 115.3 vs 110.6)
 constexpr int kStagingMinQueryBlocks = 2;
 constexpr int kStagingMinTokens = 1024;
 // A staged tile image: the tile buffer's K rows and V planes, then its
@@ -150,8 +151,9 @@ struct PrefillArgs {
   int stage_tiles;
 };
 
-// Kernel phases: decode every tile in the workgroup (kDecode); read the tiles
-// as images that kStage wrote, one per tile and KV head (kStaged)
+// Kernel phases: decode every tile in the workgroup (kDecode); the staging
+// pass, one workgroup per tile and KV head, which writes the tile's image
+// (kStage); read the tiles as those images (kStaged)
 enum PPhase : int { kDecode = 0, kStaged = 1, kStage = 2 };
 
 template <int BITS, int MODE, int NR, int PH>
