@@ -268,8 +268,8 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
  * qjl_signs non-null selects TQ (rq [num_heads][q_len][head_dim] f32 = R q,
  * logits scale * (q.k + correction)).  head_dim 128, GQA 1/2/4, outlier_blocks
  * 0 or all.  Replaces the reference's prefill result (dequantized K/V for
- * SDPA, pqo.rs:184-200, tq.rs:258-273).  Shapes with 2 or more query
- * blocks per KV head over 1024 or more tokens decode each 64-token tile once
+ * SDPA, pqo.rs:184-200, tq.rs:258-273).  Calls over 768 or more tokens
+ * decode each 64-token tile once
  * into a stream-ordered staging buffer (hipMallocFromPoolAsync /
  * hipFreeAsync on stream, from a memory pool of the library's own per device
  * that keeps up to 1 GiB between calls; about 72 KB per tile and KV head,

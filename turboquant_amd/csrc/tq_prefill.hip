@@ -33,9 +33,9 @@
 // decoded while tile t is computed (one barrier per tile), and the records of
 // tile t + 2 are fetched meanwhile.
 //
-// Staged tiles (2 or more query blocks per KV head over 1024 or more
-// tokens): the query blocks of a KV head would each decode every tile again,
-// so a staging pass (the same kernel, one workgroup per tile and KV head)
+// Staged tiles (768 or more tokens): the query blocks of a KV head would
+// each decode every tile again, and a single query block would decode its
+// tiles in only num_kv_heads workgroups, so a staging pass (the same kernel, one workgroup per tile and KV head)
 // decodes each tile once into an image of the tile buffer's LDS contents (TQ:
 // with the sign words and scaled norms), and the attention workgroups copy
 // the images into LDS in place of decoding.  The staging pass inverse-rotates
@@ -86,14 +86,14 @@ constexpr int kQRow = 128 + 8;  // halves
 constexpr int kORow = 128 + 4;  // floats
 
 // Shapes whose tiles are decoded once, in a staging pass, instead of in every
-// workgroup: at least this many query blocks per KV head and tokens (the
-// second launch and its buffer have a fixed cost, the decode it saves is
-// about a fifth of each workgroup's time; 16/8 heads, in-workgroup vs staged,
-// us, measured with a 14-18 us staging pass: 512 x 512 causal 36.5 vs 40.2,
-// 1024 x 1024 64.6 vs 62.2, 2048 x 2048 119.9 vs 106.7, 128 queries x 2048
-// tokens full 115.3 vs 110.6)
-constexpr int kStagingMinQueryBlocks = 2;
-constexpr int kStagingMinTokens = 1024;
+// workgroup: at least this many tokens (the second launch and its buffer
+// have a fixed cost; the staging pass decodes on every compute unit, so it
+// pays even for one query block per KV head, whose attention runs in
+// num_kv_heads workgroups; 16/8 heads, bf16 queries, in-workgroup vs staged,
+// us: 512 x 512 causal 36.1 vs 36.1, 768 x 768 causal 49.1 vs 45.8, 64
+// queries x 512 tokens full 34.3 vs 43.9, 64 x 768 47.3 vs 43.9, 64 x 2048
+// 111.0 vs 91.7, 2048 x 2048 causal 117.3 vs 93.8)
+constexpr int kStagingMinTokens = 768;
 // A staged tile image: the tile buffer's K rows and V planes, then its
 // exponent words (the slices' K exponents, the waves' V exponents), for a TQ
 // cache then the sign words and the scaled residual norms, in 16-byte chunks
@@ -857,12 +857,13 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   }
 }
 
-// Whether to decode each tile once into a staging buffer: with q_blocks query
-// blocks per KV head, the workgroups would otherwise decode a tile up to
-// q_blocks times (causal: about half of that on average).  TQ_PREFILL_STAGING
-// = 0 / 1 forces either path, except that a KV head's images must stay below
-// 2^31 bytes (about 1.9 million tokens).
-bool use_staging(int q_blocks, int kv_len, int mode) {
+// Whether to decode each tile once into a staging buffer: the workgroups of
+// q_blocks query blocks per KV head would otherwise decode a tile up to
+// q_blocks times (causal: about half of that on average), and with one
+// query block the decode would run in num_kv_heads workgroups only.
+// TQ_PREFILL_STAGING = 0 / 1 forces either path, except that a KV head's
+// images must stay below 2^31 bytes (about 1.9 million tokens).
+bool use_staging(int kv_len, int mode) {
   // a KV head's images are read through one buffer resource: below 2^31 bytes
   const long long head_bytes = (long long)((kv_len + kTile - 1) / kTile) * img_chunks(mode) * 16;
   if (head_bytes >= (1ll << 31)) return false;
@@ -870,7 +871,7 @@ bool use_staging(int q_blocks, int kv_len, int mode) {
     if (e[0] == '0') return false;
     if (e[0] == '1') return true;
   }
-  return q_blocks >= kStagingMinQueryBlocks && kv_len >= kStagingMinTokens;
+  return kv_len >= kStagingMinTokens;
 }
 
 // The staging buffers come from a memory pool of the library's own per
@@ -916,7 +917,7 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   const int qb = prefill_rows(MODE) / nr;
   const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
-  if (a.kv_len > 0 && use_staging((int)grid.x, a.kv_len, MODE)) {
+  if (a.kv_len > 0 && use_staging(a.kv_len, MODE)) {
     // staging pass then the attention launch, in stream order; the buffer
     // is released in stream order after the attention launch
     a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
