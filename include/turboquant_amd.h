@@ -277,7 +277,12 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
  * the environment variable
  * TQ_PREFILL_STAGING=0 or 1 forces either path (never staged when a KV
  * head's images would reach 2^31 bytes, about 1.9 M tokens; both within the tolerance;
- * staged tiles hold K inverse-rotated, so the two differ by rounding). */
+ * staged tiles hold K inverse-rotated, so the two differ by rounding).  When
+ * the staged attention's grid (one workgroup per 64 queries' rows and KV
+ * head) would leave compute units idle, each query block's tiles are split
+ * over several workgroups and a third launch merges the splits' partial rows
+ * (132 floats per split, head and query, in the same buffer);
+ * TQ_PREFILL_SPLITS=n forces n splits (1: none). */
 int tq_cache_prefill_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                                const uint16_t *k_scales, const uint8_t *v_indices,
                                const uint16_t *v_scales, const float *rq, const uint8_t *qjl_signs,

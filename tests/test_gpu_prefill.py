@@ -290,3 +290,76 @@ def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, 
     for o in outs:
         err = np.abs(o[0].cpu().numpy() - ref).max()
         assert err <= TOL, err
+
+
+@pytest.mark.parametrize("bits,outlier,hq,hkv,ql,t,causal,splits,odt", [
+    (3, orc.OUTLIER_ALL, 16, 8, 64, 4097, True, None, "f32"),
+    (3, orc.OUTLIER_ALL, 16, 8, 64, 4097, False, None, "bf16"),
+    (4, 0, 16, 4, 1, 2000, True, None, "f32"),
+    (3, orc.OUTLIER_ALL, 32, 8, 100, 1500, True, "7", "f16"),
+    (3, orc.OUTLIER_ALL, 16, 8, 300, 1000, True, "8", "f32"),
+    (4, orc.OUTLIER_ALL, 8, 8, 130, 2500, False, "3", "f32"),
+])
+def test_split_prefill(tq, monkeypatch, bits, outlier, hq, hkv, ql, t, causal, splits, odt):
+    """Staged prefill with its tiles split over several workgroups per query
+    block (automatic when the grid would leave compute units idle, or forced
+    with TQ_PREFILL_SPLITS, uneven and with empty splits for causal blocks that
+    end before a split) and the splits' merge: within PATHS_TOL of one split
+    and TOL of the oracle, in f32, bf16 and f16 outputs."""
+    rng = np.random.default_rng(2600 + t + ql)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    ki, ks, kd = _records(bits, outlier, k, t)
+    vi, vs, vd = _records(bits, outlier, v, t)
+    q = bf16_round(rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D)))
+    qd = _dev(bf16_bits(q)).view(torch.bfloat16)
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[odt]
+    scale = 1 / math.sqrt(D)
+    monkeypatch.setenv("TQ_PREFILL_STAGING", "1")
+    outs = []
+    for sp in ("1", splits):
+        if sp is None:
+            monkeypatch.delenv("TQ_PREFILL_SPLITS", raising=False)
+        else:
+            monkeypatch.setenv("TQ_PREFILL_SPLITS", sp)
+        outs.append(tq.cache_prefill_attention(qd, ki, ks, vi, vs, hkv, bits, t, t, scale, outlier, causal=causal,
+                                               out_dtype=dt).float())
+    torch.cuda.synchronize()
+    rt = PATHS_TOL if odt == "f32" else 1e-2  # (two roundings of the same value to 16 bits may differ by an ulp)
+    assert float((outs[0] - outs[1]).abs().max()) <= rt
+    ref = orc.attention_prefill(q, kd, vd, scale, causal)
+    tol = TOL if odt == "f32" else 1e-2
+    for o in outs:
+        err = np.abs(o.cpu().numpy() - ref).max()
+        assert err <= tol, err
+
+
+def test_split_prefill_tq_cache(tq, monkeypatch):
+    """A TQ cache (QJL correction in the key pass) with few query blocks over a
+    long context: automatic splits against one split and the oracle."""
+    bits, hq, hkv, ql, t = 3, 16, 8, 64, 2100
+    rng = np.random.default_rng(2700)
+    k = kv_outlier(rng, hkv, t)
+    v = kv_outlier(rng, hkv, t)
+    cache = tq.TqCache(tq.CacheConfig(bits=bits, head_dim=D, num_kv_heads=hkv, num_layers=1, outlier_blocks=0))
+    q = rng.standard_normal((hq, ql, D)).astype(np.float32) / np.float32(math.sqrt(D))
+    cache.prefill(0, _dev(k[None]), _dev(v[None]), _dev(q[None]))
+    outs = []
+    for sp in ("1", None):
+        if sp is None:
+            monkeypatch.delenv("TQ_PREFILL_SPLITS", raising=False)
+        else:
+            monkeypatch.setenv("TQ_PREFILL_SPLITS", sp)
+        outs.append(cache.attend_prefill(0, _dev(q[None]), 1 / math.sqrt(D), causal=True, out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    assert float((outs[0] - outs[1]).abs().max()) <= PATHS_TOL
+    pk, sk = orc.polar_quantize(bits, 0, k.reshape(-1, D), D)
+    pv, sv = orc.polar_quantize(bits, 0, v.reshape(-1, D), D)
+    kd = orc.polar_dequantize(bits, 0, pk, sk, D)
+    vd = orc.polar_dequantize(bits, 0, pv, sv, D).reshape(hkv, t, D)
+    sg, nm = orc.tq_signs_norms(k.reshape(-1, D), kd)
+    bias = orc.tq_logit_bias(q, sg.reshape(hkv, t, -1), nm.reshape(hkv, t))
+    ref = orc.attention_prefill(q, kd.reshape(hkv, t, D), vd, 1 / math.sqrt(D), True, bias)
+    for o in outs:
+        err = np.abs(o[0].cpu().numpy() - ref).max()
+        assert err <= TOL, err

@@ -149,7 +149,16 @@ struct PrefillArgs {
   const uint4 *stage;
   uint4 *stage_out;
   int stage_tiles;
+  // split-K over the tiles: workgroup z takes tiles [z tps, (z + 1) tps) of
+  // its query block; with splits > 1 it writes partial rows to part
+  int splits, tps;
+  float *part;
 };
+
+// A partial row of a split: the inverse-rotated output sums (unnormalized,
+// relative to the row maximum) [0, 128), the row maximum m (log2 domain)
+// [128] and the row sum [129], padded to 16 bytes; rows [split][head][query]
+constexpr int kPartRow = 132;
 
 // Kernel phases: decode every tile in the workgroup (kDecode); the staging
 // pass, one workgroup per tile and KV head, which writes the tile's image
@@ -321,7 +330,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   static_assert(2 * V_HALVES <= 2 * V_WORDS, "both V planes fit");
   // (the query and rq staging precedes the tiles and may span both buffers)
   static_assert((QJL ? 2 : 1) * kRows * kQRow <= 2 * (K_WORDS + V_WORDS), "the split query (and rq) fit the tile region");
-  static_assert(kRows * kORow + kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
+  static_assert(kRows * kORow + 2 * kRows <= K_WORDS + V_WORDS, "the output rows fit the tile region");
 
   // chunk c of tile buffer b's image: the K tile and V planes, then the
   // exponent words, then (TQ) the sign words and the scaled norms
@@ -507,7 +516,21 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   const int last_q = min(a.q_len - 1, i0 + QB - 1);
   const int kv_end = a.causal ? min(a.kv_len, a.kv_len - a.q_len + last_q + 1) : a.kv_len;
   const int ntiles = (kv_end + kTile - 1) / kTile;
-  if (ntiles > 0) fetch(0);
+  // this workgroup's split of the tiles
+  const int tile_lo = min(ntiles, (int)blockIdx.z * a.tps), tile_hi = min(ntiles, tile_lo + a.tps);
+  if (a.splits > 1 && tile_hi <= tile_lo) {
+    // an empty split (a causal query block that ends before it): its partial
+    // rows say so, m = -inf (the merge then reads nothing else of them)
+    const int prow = tid >> 2, pq = tid & 3;
+    const int qi = i0 + prow / NR, qh = g * NR + prow % NR;
+    if (qi < a.q_len && pq == 0) {
+      float *pr = a.part + (((long long)blockIdx.z * a.num_heads + qh) * a.q_len + qi) * kPartRow;
+      pr[128] = -INFINITY;
+      pr[129] = 0.f;
+    }
+    return;
+  }
+  if (tile_hi > tile_lo) fetch(tile_lo * kTile);
 
   // ---- query rows: thread (row, quarter) rotates one 32-element block ----
   // (the V tile region holds the split query until the operands are built)
@@ -628,9 +651,9 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 #pragma unroll
   for (int eb = 0; eb < 8; eb++) o[eb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (ntiles > 0) {
+  if (tile_hi > tile_lo) {
     decode_tile(0);
-    if (ntiles > 1) fetch(kTile);  // each tile's records arrive during the tile before
+    if (tile_hi > tile_lo + 1) fetch((tile_lo + 1) * kTile);  // each tile's records arrive during the tile before
   }
   __syncthreads();
   // One barrier per tile: tile + 1 is decoded into the other buffer in the
@@ -638,12 +661,12 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // orders, so that one's decode overlaps the other's matrix products); the
   // barrier then publishes tile + 1 and frees tile's buffer for tile + 2.
   const bool decode_first = (wave >> 2) & 1;
-  for (int tile = 0; tile < ntiles; tile++) {
-    const int t0 = tile * kTile, cur = tile & 1;
-    const bool more = tile + 1 < ntiles;
+  for (int tile = tile_lo; tile < tile_hi; tile++) {
+    const int t0 = tile * kTile, cur = (tile - tile_lo) & 1;
+    const bool more = tile + 1 < tile_hi;
     if (decode_first && more) {
       decode_tile(cur ^ 1);
-      if (tile + 2 < ntiles) fetch(t0 + 2 * kTile);
+      if (tile + 2 < tile_hi) fetch(t0 + 2 * kTile);
     }
     const uint2 *kt = ktile(cur);
     const _Float16 *vth = vhi(cur), *vtl = vth + V_HALVES;
@@ -809,7 +832,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     __builtin_amdgcn_s_setprio(0);
     if (!decode_first && more) {
       decode_tile(cur ^ 1);
-      if (tile + 2 < ntiles) fetch(t0 + 2 * kTile);
+      if (tile + 2 < tile_hi) fetch(t0 + 2 * kTile);
     }
     __syncthreads();
   }
@@ -825,7 +848,11 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     *reinterpret_cast<float4 *>(s_o + myrow * kORow + 16 * eb + 4 * lg) =
         make_float4(o[eb][0] * ofac, o[eb][1] * ofac, o[eb][2] * ofac, o[eb][3] * ofac);
   float *s_rowl = s_o + kRows * kORow;  // [rows] (the tiles are done)
-  if (lg == 0) s_rowl[myrow] = L;
+  float *s_rowm = s_rowl + kRows;
+  if (lg == 0) {
+    s_rowl[myrow] = L;
+    s_rowm[myrow] = m_run;
+  }
   __syncthreads();
   {
     float v[32];
@@ -839,7 +866,19 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     }
     butterfly<32>(v);
     const float Lr = s_rowl[prow];
-    if (row_ok) {
+    if (row_ok && a.splits > 1) {
+      // a split's partial row: the sums unnormalized, its maximum and sum
+      float *pr = a.part + (((long long)blockIdx.z * a.num_heads + qh) * a.q_len + qi) * kPartRow;
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        *reinterpret_cast<float4 *>(pr + 32 * pq + 4 * k) =
+            make_float4(v[4 * k] * kInvSqrt32, v[4 * k + 1] * kInvSqrt32, v[4 * k + 2] * kInvSqrt32,
+                        v[4 * k + 3] * kInvSqrt32);
+      if (pq == 0) {
+        pr[128] = s_rowm[prow];
+        pr[129] = Lr;
+      }
+    } else if (row_ok) {
       const long long ob = ((long long)qh * a.q_len + qi) * HD + 32 * pq;
 #pragma unroll
       for (int j = 0; j < 32; j++) v[j] = Lr > 0.f ? v[j] * kInvSqrt32 / Lr : 0.f;
@@ -855,6 +894,34 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       }
     }
   }
+}
+
+// Split-K merge: out[row] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) L_s
+// over the splits' partial rows (M their maximum; 0 where no split saw a
+// token), one workgroup of 128 lanes per (head, query) row.
+__global__ __launch_bounds__(128) void prefill_merge_kernel(const float *part, int splits, long long rows, void *out,
+                                                            int out_dtype) {
+  const long long row = blockIdx.x;
+  const int e = threadIdx.x;
+  const float *p = part + row * kPartRow;
+  const long long step = rows * kPartRow;
+  float M = -INFINITY;
+  for (int s = 0; s < splits; s++) M = fmaxf(M, p[s * step + 128]);
+  float O = 0.f, L = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < splits; s++) {
+      const float ms = p[s * step + 128];
+      if (ms == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ms - M);
+      O = __builtin_fmaf(p[s * step + e], w, O);
+      L = __builtin_fmaf(p[s * step + 129], w, L);
+    }
+  }
+  const float r = L > 0.f ? O / L : 0.f;
+  const long long oi = row * 128 + e;
+  if (out_dtype == kF32) static_cast<float *>(out)[oi] = r;
+  else if (out_dtype == kBF16) static_cast<uint16_t *>(out)[oi] = f32_to_bf16(r);
+  else static_cast<uint16_t *>(out)[oi] = f32_to_f16(r);
 }
 
 // Whether to decode each tile once into a staging buffer: the workgroups of
@@ -905,8 +972,43 @@ hipMemPool_t staging_pool(int dev) {
   return pools[dev];
 }
 
+// Compute units of device dev (cached; 0 if unknown)
+int cu_count(int dev) {
+  static std::mutex mu;
+  static int n[64] = {};
+  if (dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (n[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      c = -1;
+    }
+    n[dev] = c;
+  }
+  return n[dev] > 0 ? n[dev] : 0;
+}
+
+// Splits of the staged attention's tiles: the attention runs one workgroup
+// per compute unit (its LDS), so a grid of fewer workgroups than compute
+// units (few query blocks per KV head: chunked prefill, multi-token decode)
+// has each workgroup take 1 / splits of its query block's tiles, with
+// floor(CUs / workgroups) splits (one round) of at least 2 tiles each;
+// TQ_PREFILL_SPLITS = n forces n.
+int prefill_splits(int wgs, int ntiles, int dev) {
+  int s = 1;
+  if (const char *e = getenv("TQ_PREFILL_SPLITS")) {
+    s = atoi(e);
+  } else {
+    const int cus = cu_count(dev);
+    if (cus > 0 && wgs > 0 && ntiles >= 4) s = min(cus / wgs, ntiles / 2);
+  }
+  return max(1, min(s, ntiles));
+}
+
 template <int BITS, int MODE, int PH>
 void launch_attn(const PrefillArgs &a, int nr, dim3 grid, dim3 block, hipStream_t st) {
+  grid.z = (unsigned)a.splits;
   if (nr == 1) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, PH>), grid, block, 0, st, a);
   else if (nr == 2) hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 2, PH>), grid, block, 0, st, a);
   else hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 4, PH>), grid, block, 0, st, a);
@@ -917,14 +1019,26 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   const int qb = prefill_rows(MODE) / nr;
   const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
+  const int ntiles = (a.kv_len + kTile - 1) / kTile;
+  a.splits = 1;
+  a.tps = max(ntiles, 1);
+  a.part = nullptr;
   if (a.kv_len > 0 && use_staging(a.kv_len, MODE)) {
-    // staging pass then the attention launch, in stream order; the buffer
-    // is released in stream order after the attention launch
-    a.stage_tiles = (a.kv_len + kTile - 1) / kTile;
-    const size_t bytes = (size_t)a.num_kv_heads * (size_t)a.stage_tiles * img_chunks(MODE) * sizeof(uint4);
-    void *buf = nullptr;
+    // staging pass, the attention launch (split over the tiles when its grid
+    // would leave compute units idle) and the splits' merge, in stream order;
+    // the buffer (tile images, then the splits' partial rows) is released in
+    // stream order after them
     int dev = 0;
     (void)hipGetDevice(&dev);
+    a.stage_tiles = ntiles;
+    const int splits = prefill_splits((int)(grid.x * grid.y), ntiles, dev);
+    a.tps = (ntiles + splits - 1) / splits;
+    a.splits = (ntiles + a.tps - 1) / a.tps;
+    const size_t img_bytes = (size_t)a.num_kv_heads * (size_t)a.stage_tiles * img_chunks(MODE) * sizeof(uint4);
+    const size_t part_at = (img_bytes + 255) & ~(size_t)255;
+    const size_t bytes =
+        part_at + (a.splits > 1 ? (size_t)a.splits * a.num_heads * a.q_len * kPartRow * sizeof(float) : 0);
+    void *buf = nullptr;
     hipMemPool_t pool = staging_pool(dev);
     const hipError_t ae = pool ? hipMallocFromPoolAsync(&buf, bytes, pool, st) : hipMallocAsync(&buf, bytes, st);
     if (ae != hipSuccess) {
@@ -933,9 +1047,15 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
     }
     a.stage = static_cast<const uint4 *>(buf);
     a.stage_out = static_cast<uint4 *>(buf);
+    if (a.splits > 1) a.part = reinterpret_cast<float *>(static_cast<char *>(buf) + part_at);
     hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles * grid.y), block,
                        0, st, a);
     launch_attn<BITS, MODE, kStaged>(a, nr, grid, block, st);
+    if (a.splits > 1) {
+      const long long rows = (long long)a.num_heads * a.q_len;
+      hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)rows), dim3(128), 0, st, a.part, a.splits, rows, a.out,
+                         a.out_dtype);
+    }
     const int rc = tqh::check_launch("prefill_attn_kernel (staged)");
     (void)hipFreeAsync(buf, st);
     return rc;
