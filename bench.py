@@ -508,11 +508,39 @@ def bench_prefill(torch, tq, args):
     flops = 4.0 * h * hd * (t * (t + 1) / 2)
     tflops = flops / (ms * 1e-3) / 1e12
     del x, pk, sk, pv, sv, q, out
+
+    # chunked prefill: a 512-query chunk at the end of a 32768-token context
+    # (8 query blocks per KV head: the tiles are split over 4 workgroups per
+    # block and merged)
+    tc, qc = 32768, 512
+    x = torch.randn((2, hkv * tc, hd), generator=gen, device="cuda")
+    x[:, :, torch.tensor([3, 40, 77, 101], device="cuda")] *= 8.0
+    pk, sk = tq.pqo_quantize(x[0].to(torch.bfloat16), bits)
+    pv, sv = tq.pqo_quantize(x[1].to(torch.bfloat16), bits)
+    del x
+    q = (torch.randn((h, qc, hd), generator=gen, device="cuda") / math.sqrt(hd)).to(torch.bfloat16)
+    out = torch.empty((h, qc, hd), dtype=torch.bfloat16, device="cuda")
+
+    def chunk_step(i):
+        tq.check(tq.lib.tq_cache_prefill_attention(q.data_ptr(), 1, pk.data_ptr(), sk.data_ptr(), pv.data_ptr(),
+                                                   sv.data_ptr(), None, None, None, h, qc, hkv, hd, bits,
+                                                   (1 << 64) - 1, 0, tc, tc, 1, scale, out.data_ptr(), 1,
+                                                   torch.cuda.current_stream().cuda_stream))
+
+    cms, cspread = time_median(torch, chunk_step, warmup=5)
+    cflops = 4.0 * h * hd * (qc * (tc - qc) + qc * (qc + 1) / 2)
+    ctflops = cflops / (cms * 1e-3) / 1e12
+    del pk, sk, pv, sv, q, out
     return {"metric": "causal prefill attention over a PQO3 cache (16/8 heads, d=128, 4096 x 4096)",
             "ms_per_step": round(ms, 4), "useful_tflops": round(tflops, 1),
             "trials_ms": [round(x, 4) for x in spread], "timing": f"median of {TRIALS} trials x {LAUNCHES} launches",
             "roofline": {"bound": "mfma", "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
-                         "note": "f16 dense peak; every product runs as hi/lo parts (3-4 MFMAs per useful one)"}}
+                         "note": "f16 dense peak; each key product runs as two f16 MFMAs (bf16 queries), "
+                                 "each value product as three (hi/lo parts)"},
+            "chunked": {"metric": "chunked prefill: 512 causal queries at the end of a 32768-token PQO3 cache",
+                        "ms_per_step": round(cms, 4), "useful_tflops": round(ctflops, 1),
+                        "trials_ms": [round(x, 4) for x in cspread],
+                        "roofline_frac": round(ctflops / 2500.0, 4)}}
 
 
 def bench_c1(torch, tq, args):
