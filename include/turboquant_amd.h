@@ -268,8 +268,9 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
  * qjl_signs non-null selects TQ (rq [num_heads][q_len][head_dim] f32 = R q,
  * logits scale * (q.k + correction)).  head_dim 128, GQA 1/2/4, outlier_blocks
  * 0 or all.  Replaces the reference's prefill result (dequantized K/V for
- * SDPA, pqo.rs:184-200, tq.rs:258-273).  Calls over 768 or more tokens
- * decode each 64-token tile once
+ * SDPA, pqo.rs:184-200, tq.rs:258-273).  Calls with 6 or more query blocks
+ * (64 queries at GQA 2) per KV head over 768 or more tokens decode each
+ * 64-token tile once
  * into a stream-ordered staging buffer (hipMallocFromPoolAsync /
  * hipFreeAsync on stream, from a memory pool of the library's own per device
  * that keeps up to 1 GiB between calls; about 72 KB per tile and KV head,
@@ -278,10 +279,10 @@ int tq_cache_decode_attention(const void *q, int q_dtype, const uint8_t *k_indic
  * TQ_PREFILL_STAGING=0 or 1 forces either path (never staged when a KV
  * head's images would reach 2^31 bytes, about 1.9 M tokens; both within the tolerance;
  * staged tiles hold K inverse-rotated, so the two differ by rounding).  When
- * the staged attention's grid (one workgroup per 64 queries' rows and KV
+ * the attention's grid (one workgroup per 128 (query, head) rows of a KV
  * head) would leave compute units idle, each query block's tiles are split
- * over several workgroups and a third launch merges the splits' partial rows
- * (132 floats per split, head and query, in the same buffer);
+ * over several workgroups and a last launch merges the splits' partial rows
+ * (132 floats per split, head and query, in a buffer taken the same way);
  * TQ_PREFILL_SPLITS=n forces n splits (1: none). */
 int tq_cache_prefill_attention(const void *q, int q_dtype, const uint8_t *k_indices,
                                const uint16_t *k_scales, const uint8_t *v_indices,

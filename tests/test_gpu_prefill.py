@@ -292,20 +292,24 @@ def test_tq_prefill_several_query_blocks(tq, monkeypatch, bits, hq, hkv, ql, t, 
         assert err <= TOL, err
 
 
-@pytest.mark.parametrize("bits,outlier,hq,hkv,ql,t,causal,splits,odt", [
-    (3, orc.OUTLIER_ALL, 16, 8, 64, 4097, True, None, "f32"),
-    (3, orc.OUTLIER_ALL, 16, 8, 64, 4097, False, None, "bf16"),
-    (4, 0, 16, 4, 1, 2000, True, None, "f32"),
-    (3, orc.OUTLIER_ALL, 32, 8, 100, 1500, True, "7", "f16"),
-    (3, orc.OUTLIER_ALL, 16, 8, 300, 1000, True, "8", "f32"),
-    (4, orc.OUTLIER_ALL, 8, 8, 130, 2500, False, "3", "f32"),
+@pytest.mark.parametrize("bits,outlier,hq,hkv,ql,t,causal,splits,odt,staged", [
+    (3, orc.OUTLIER_ALL, 16, 8, 64, 4097, True, None, "f32", "1"),
+    (3, orc.OUTLIER_ALL, 16, 8, 64, 4097, False, None, "bf16", "1"),
+    (4, 0, 16, 4, 1, 2000, True, None, "f32", "1"),
+    (3, orc.OUTLIER_ALL, 32, 8, 100, 1500, True, "7", "f16", "1"),
+    (3, orc.OUTLIER_ALL, 16, 8, 300, 1000, True, "8", "f32", "1"),
+    (4, orc.OUTLIER_ALL, 8, 8, 130, 2500, False, "3", "f32", "1"),
+    (3, orc.OUTLIER_ALL, 16, 8, 64, 4097, True, None, "f32", "0"),
+    (3, orc.OUTLIER_ALL, 16, 4, 200, 1300, True, "5", "bf16", "0"),
+    (4, 0, 16, 8, 1, 700, False, None, "f32", "0"),
 ])
-def test_split_prefill(tq, monkeypatch, bits, outlier, hq, hkv, ql, t, causal, splits, odt):
-    """Staged prefill with its tiles split over several workgroups per query
-    block (automatic when the grid would leave compute units idle, or forced
-    with TQ_PREFILL_SPLITS, uneven and with empty splits for causal blocks that
-    end before a split) and the splits' merge: within PATHS_TOL of one split
-    and TOL of the oracle, in f32, bf16 and f16 outputs."""
+def test_split_prefill(tq, monkeypatch, bits, outlier, hq, hkv, ql, t, causal, splits, odt, staged):
+    """Prefill with its tiles split over several workgroups per query block
+    (automatic when the grid would leave compute units idle, or forced with
+    TQ_PREFILL_SPLITS, uneven and with empty splits for causal blocks that end
+    before a split), on staged tiles and decoding in the workgroups, and the
+    splits' merge: within PATHS_TOL of one split and TOL of the oracle, in
+    f32, bf16 and f16 outputs."""
     rng = np.random.default_rng(2600 + t + ql)
     k = kv_outlier(rng, hkv, t)
     v = kv_outlier(rng, hkv, t)
@@ -315,7 +319,7 @@ def test_split_prefill(tq, monkeypatch, bits, outlier, hq, hkv, ql, t, causal, s
     qd = _dev(bf16_bits(q)).view(torch.bfloat16)
     dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[odt]
     scale = 1 / math.sqrt(D)
-    monkeypatch.setenv("TQ_PREFILL_STAGING", "1")
+    monkeypatch.setenv("TQ_PREFILL_STAGING", staged)
     outs = []
     for sp in ("1", splits):
         if sp is None:

@@ -33,9 +33,9 @@
 // decoded while tile t is computed (one barrier per tile), and the records of
 // tile t + 2 are fetched meanwhile.
 //
-// Staged tiles (768 or more tokens): the query blocks of a KV head would
-// each decode every tile again, and a single query block would decode its
-// tiles in only num_kv_heads workgroups, so a staging pass (the same kernel, one workgroup per tile and KV head)
+// Staged tiles (6 or more query blocks per KV head over 768 or more tokens):
+// the query blocks of a KV head would each decode every tile again, so a
+// staging pass (the same kernel, one workgroup per tile and KV head)
 // decodes each tile once into an image of the tile buffer's LDS contents (TQ:
 // with the sign words and scaled norms), and the attention workgroups copy
 // the images into LDS in place of decoding.  The staging pass inverse-rotates
@@ -86,13 +86,15 @@ constexpr int kQRow = 128 + 8;  // halves
 constexpr int kORow = 128 + 4;  // floats
 
 // Shapes whose tiles are decoded once, in a staging pass, instead of in every
-// workgroup: at least this many tokens (the second launch and its buffer
-// have a fixed cost; the staging pass decodes on every compute unit, so it
-// pays even for one query block per KV head, whose attention runs in
-// num_kv_heads workgroups; 16/8 heads, bf16 queries, in-workgroup vs staged,
-// us: 512 x 512 causal 36.1 vs 36.1, 768 x 768 causal 49.1 vs 45.8, 64
-// queries x 512 tokens full 34.3 vs 43.9, 64 x 768 47.3 vs 43.9, 64 x 2048
-// 111.0 vs 91.7, 2048 x 2048 causal 117.3 vs 93.8)
+// workgroup: at least this many query blocks per KV head and tokens (the
+// second launch and writing the images have a cost that the decodes saved
+// must repay: each tile is decoded by up to q_blocks workgroups otherwise;
+// 16/8 heads, bf16 queries, both paths split over the tiles where the grid
+// is small, in-workgroup vs staged, us: 128 causal queries at the end of
+// 32768 tokens 135.8 vs 184.5, 256 x 32768 236.6 vs 261.8, 256 x 8192 80.9
+// vs 80.0, 512 x 32768 450.7 vs 428.1; without splits 512 x 512 causal 36.1
+// vs 36.1, 768 x 768 causal 49.1 vs 45.8, 2048 x 2048 causal 117.3 vs 93.8)
+constexpr int kStagingMinQueryBlocks = 6;
 constexpr int kStagingMinTokens = 768;
 // A staged tile image: the tile buffer's K rows and V planes, then its
 // exponent words (the slices' K exponents, the waves' V exponents), for a TQ
@@ -926,11 +928,9 @@ __global__ __launch_bounds__(128) void prefill_merge_kernel(const float *part, i
 
 // Whether to decode each tile once into a staging buffer: the workgroups of
 // q_blocks query blocks per KV head would otherwise decode a tile up to
-// q_blocks times (causal: about half of that on average), and with one
-// query block the decode would run in num_kv_heads workgroups only.
-// TQ_PREFILL_STAGING = 0 / 1 forces either path, except that a KV head's
+// q_blocks times (causal: about half of that on average).  TQ_PREFILL_STAGING = 0 / 1 forces either path, except that a KV head's
 // images must stay below 2^31 bytes (about 1.9 million tokens).
-bool use_staging(int kv_len, int mode) {
+bool use_staging(int q_blocks, int kv_len, int mode) {
   // a KV head's images are read through one buffer resource: below 2^31 bytes
   const long long head_bytes = (long long)((kv_len + kTile - 1) / kTile) * img_chunks(mode) * 16;
   if (head_bytes >= (1ll << 31)) return false;
@@ -938,7 +938,7 @@ bool use_staging(int kv_len, int mode) {
     if (e[0] == '0') return false;
     if (e[0] == '1') return true;
   }
-  return kv_len >= kStagingMinTokens;
+  return q_blocks >= kStagingMinQueryBlocks && kv_len >= kStagingMinTokens;
 }
 
 // The staging buffers come from a memory pool of the library's own per
@@ -989,9 +989,8 @@ int cu_count(int dev) {
   return n[dev] > 0 ? n[dev] : 0;
 }
 
-// Splits of the staged attention's tiles: the attention runs one workgroup
-// per compute unit (its LDS), so a grid of fewer workgroups than compute
-// units (few query blocks per KV head: chunked prefill, multi-token decode)
+// Splits of the attention's tiles: the attention runs one workgroup per
+// compute unit (its LDS), so a grid of fewer workgroups than compute units (few query blocks per KV head: chunked prefill, multi-token decode)
 // has each workgroup take 1 / splits of its query block's tiles, with
 // floor(CUs / workgroups) splits (one round) of at least 2 tiles each;
 // TQ_PREFILL_SPLITS = n forces n.
@@ -1020,48 +1019,49 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   const dim3 block((unsigned)(4 * prefill_rows(MODE)));
   const dim3 grid((unsigned)((a.q_len + qb - 1) / qb), (unsigned)a.num_kv_heads);
   const int ntiles = (a.kv_len + kTile - 1) / kTile;
-  a.splits = 1;
-  a.tps = max(ntiles, 1);
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const bool staged = a.kv_len > 0 && use_staging((int)grid.x, a.kv_len, MODE);
+  // the attention split over the tiles when its grid would leave compute
+  // units idle
+  const int splits = a.kv_len > 0 ? prefill_splits((int)(grid.x * grid.y), ntiles, dev) : 1;
+  a.tps = max((ntiles + splits - 1) / splits, 1);
+  a.splits = max((ntiles + a.tps - 1) / a.tps, 1);
   a.part = nullptr;
-  if (a.kv_len > 0 && use_staging(a.kv_len, MODE)) {
-    // staging pass, the attention launch (split over the tiles when its grid
-    // would leave compute units idle) and the splits' merge, in stream order;
-    // the buffer (tile images, then the splits' partial rows) is released in
-    // stream order after them
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    a.stage_tiles = ntiles;
-    const int splits = prefill_splits((int)(grid.x * grid.y), ntiles, dev);
-    a.tps = (ntiles + splits - 1) / splits;
-    a.splits = (ntiles + a.tps - 1) / a.tps;
-    const size_t img_bytes = (size_t)a.num_kv_heads * (size_t)a.stage_tiles * img_chunks(MODE) * sizeof(uint4);
-    const size_t part_at = (img_bytes + 255) & ~(size_t)255;
-    const size_t bytes =
-        part_at + (a.splits > 1 ? (size_t)a.splits * a.num_heads * a.q_len * kPartRow * sizeof(float) : 0);
-    void *buf = nullptr;
+  a.stage_tiles = ntiles;
+  // one stream-ordered buffer: the tile images (staged), then the splits'
+  // partial rows; released in stream order after the launches
+  const size_t img_bytes =
+      staged ? (size_t)a.num_kv_heads * (size_t)a.stage_tiles * img_chunks(MODE) * sizeof(uint4) : 0;
+  const size_t part_at = (img_bytes + 255) & ~(size_t)255;
+  const size_t bytes = part_at + (a.splits > 1 ? (size_t)a.splits * a.num_heads * a.q_len * kPartRow * sizeof(float) : 0);
+  void *buf = nullptr;
+  if (bytes > 0) {
     hipMemPool_t pool = staging_pool(dev);
     const hipError_t ae = pool ? hipMallocFromPoolAsync(&buf, bytes, pool, st) : hipMallocAsync(&buf, bytes, st);
     if (ae != hipSuccess) {
       (void)hipGetLastError();
       return tqh::fail(TQ_ERR_DEVICE, "prefill staging buffer of %zu bytes not allocated", bytes);
     }
+    if (a.splits > 1) a.part = reinterpret_cast<float *>(static_cast<char *>(buf) + part_at);
+  }
+  if (staged) {
     a.stage = static_cast<const uint4 *>(buf);
     a.stage_out = static_cast<uint4 *>(buf);
-    if (a.splits > 1) a.part = reinterpret_cast<float *>(static_cast<char *>(buf) + part_at);
     hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles * grid.y), block,
                        0, st, a);
     launch_attn<BITS, MODE, kStaged>(a, nr, grid, block, st);
-    if (a.splits > 1) {
-      const long long rows = (long long)a.num_heads * a.q_len;
-      hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)rows), dim3(128), 0, st, a.part, a.splits, rows, a.out,
-                         a.out_dtype);
-    }
-    const int rc = tqh::check_launch("prefill_attn_kernel (staged)");
-    (void)hipFreeAsync(buf, st);
-    return rc;
+  } else {
+    launch_attn<BITS, MODE, kDecode>(a, nr, grid, block, st);
   }
-  launch_attn<BITS, MODE, kDecode>(a, nr, grid, block, st);
-  return tqh::check_launch("prefill_attn_kernel");
+  if (a.splits > 1) {
+    const long long rows = (long long)a.num_heads * a.q_len;
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)rows), dim3(128), 0, st, a.part, a.splits, rows, a.out,
+                       a.out_dtype);
+  }
+  const int rc = tqh::check_launch(staged ? "prefill_attn_kernel (staged)" : "prefill_attn_kernel");
+  if (buf) (void)hipFreeAsync(buf, st);
+  return rc;
 }
 
 }  // namespace
