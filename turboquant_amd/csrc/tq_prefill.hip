@@ -900,24 +900,42 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
 
 // Split-K merge: out[row] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) L_s
 // over the splits' partial rows (M their maximum; 0 where no split saw a
-// token), one workgroup of 128 lanes per (head, query) row.
+// token), one workgroup of 128 lanes per (head, query) row.  The splits go
+// in groups of 8 whose loads are all issued before the group is folded
+// (one memory round trip per group), with a running maximum across groups.
 __global__ __launch_bounds__(128) void prefill_merge_kernel(const float *part, int splits, long long rows, void *out,
                                                             int out_dtype) {
+  constexpr int G = 8;
   const long long row = blockIdx.x;
   const int e = threadIdx.x;
   const float *p = part + row * kPartRow;
   const long long step = rows * kPartRow;
-  float M = -INFINITY;
-  for (int s = 0; s < splits; s++) M = fmaxf(M, p[s * step + 128]);
-  float O = 0.f, L = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < splits; s++) {
-      const float ms = p[s * step + 128];
-      if (ms == -INFINITY) continue;
-      const float w = __builtin_amdgcn_exp2f(ms - M);
-      O = __builtin_fmaf(p[s * step + e], w, O);
-      L = __builtin_fmaf(p[s * step + 129], w, L);
+  float M = -INFINITY, O = 0.f, L = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += G) {
+    float ms[G], ls[G], os[G];
+#pragma unroll
+    for (int k = 0; k < G; k++) {
+      const bool ok = s0 + k < splits;
+      const float *ps = p + (ok ? s0 + k : 0) * step;
+      ms[k] = ok ? ps[128] : -INFINITY;
+      ls[k] = ok ? ps[129] : 0.f;
+      os[k] = ok ? ps[e] : 0.f;
     }
+    float Mg = M;
+#pragma unroll
+    for (int k = 0; k < G; k++) Mg = fmaxf(Mg, ms[k]);
+    if (Mg == -INFINITY) continue;  // nothing seen yet
+    const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mg);
+    O *= f;
+    L *= f;
+#pragma unroll
+    for (int k = 0; k < G; k++) {
+      // (a split that saw no token: m = -inf, weight 0, its sums ignored)
+      const float w = ms[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[k] - Mg);
+      O = __builtin_fmaf(ms[k] == -INFINITY ? 0.f : os[k], w, O);
+      L = __builtin_fmaf(ms[k] == -INFINITY ? 0.f : ls[k], w, L);
+    }
+    M = Mg;
   }
   const float r = L > 0.f ? O / L : 0.f;
   const long long oi = row * 128 + e;
