@@ -151,6 +151,7 @@ struct PrefillArgs {
   const uint4 *stage;
   uint4 *stage_out;
   int stage_tiles;
+  int stage_tpw;  // staging pass: consecutive tiles per workgroup
   // split-K over the tiles: workgroup z takes tiles [z tps, (z + 1) tps) of
   // its query block; with splits > 1 it writes partial rows to part
   int splits, tps;
@@ -277,6 +278,23 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(ps), (short)0, n, 0x00020000);
   };
   const __amdgpu_buffer_rsrc_t img_rsrc = make_img_rsrc();
+  // staging pass: one K (waves 0-3) or V (waves 4-7) record of the tile at
+  // t0 into w, sc (TQ: the sign word and norm)
+  auto load_rec = [&](int t0, uint32_t(&w)[QW], uint16_t &sc, uint32_t &sg, uint16_t &n) {
+    const long long rec = rec0 + min(t0 + ftok, a.kv_len - 1);
+    const bool kwave = wave < 4;
+    const uint32_t *src =
+        reinterpret_cast<const uint32_t *>((kwave ? a.k_idx : a.v_idx) + rec * PACKED + fqb * 4 * QW);
+#pragma unroll
+    for (int i = 0; i < QW; i++) w[i] = src[i];
+    sc = (kwave ? a.k_sc : a.v_sc)[rec * 4 + fqb];
+    if constexpr (QJL) {
+      if (kwave) {
+        sg = a.signs[rec * 4 + fqb];
+        n = a.norms[rec];
+      }
+    }
+  };
   auto fetch = [&](int t0) {
     if constexpr (PH == kStaged) {
       // buffer loads: the lane's offset in a vector register (the same for
@@ -290,20 +308,7 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
       return;
     }
     if constexpr (PH == kStage) {
-      // one K (waves 0-3) or V (waves 4-7) record, into kw and ks
-      const long long rec = rec0 + min(t0 + ftok, a.kv_len - 1);
-      const bool kwave = wave < 4;
-      const uint32_t *src =
-          reinterpret_cast<const uint32_t *>((kwave ? a.k_idx : a.v_idx) + rec * PACKED + fqb * 4 * QW);
-#pragma unroll
-      for (int w = 0; w < QW; w++) kw[w] = src[w];
-      ks = (kwave ? a.k_sc : a.v_sc)[rec * 4 + fqb];
-      if constexpr (QJL) {
-        if (kwave) {
-          sgw = a.signs[rec * 4 + fqb];
-          nm = a.norms[rec];
-        }
-      }
+      load_rec(t0, kw, ks, sgw, nm);
       return;
     }
     const int t = min(t0 + ftok, a.kv_len - 1);
@@ -442,73 +447,92 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // rotation); waves 4-7 decode a V record, which stays rotated.  One K and
   // one V exponent per 16-token slice. ----
   if constexpr (PH == kStage) {
-    fetch(qblk * kTile);
+    // tiles [tile0, tile1) of KV head g; tile + 1's records are requested
+    // before tile's decode
+    const int tile0 = qblk * a.stage_tpw, tile1 = min(a.stage_tiles, tile0 + a.stage_tpw);
+    if (tile0 >= tile1) return;
+    fetch(tile0 * kTile);
     __syncthreads();  // codebook staged
-    const bool kwave = wave < 4;
-    const int slice = wave & 3;
-    const float sc = fabsf(f16_to_f32(ks));
-    const int e = pow2_exponent(wave_max(sc));
-    const float f = sc * exp2i(-e);
-    if (lane == 0) {
+    for (int tile = tile0; tile < tile1; tile++) {
+      uint32_t nkw[QW];
+      uint16_t nks = 0, nnm = 0;
+      uint32_t nsg = 0;
+      const bool more = tile + 1 < tile1;
+      if (more) load_rec((tile + 1) * kTile, nkw, nks, nsg, nnm);
+      const bool kwave = wave < 4;
+      const int slice = wave & 3;
+      const float sc = fabsf(f16_to_f32(ks));
+      const int e = pow2_exponent(wave_max(sc));
+      const float f = sc * exp2i(-e);
+      if (lane == 0) {
+        if (kwave) {
+          xe(0)[slice] = e;
+        } else {
+          xe(0)[4 + 2 * slice] = e;
+          xe(0)[5 + 2 * slice] = e;
+        }
+      }
+      if constexpr (QJL) {
+        if (kwave) {
+          if (fqb == 0) cnp(0)[ftok] = f16_to_f32(nm) * a.qjl_c;
+          sgp(0)[ftok * 4 + fqb] = sgw;
+        }
+      }
+      constexpr uint32_t SM = (1u << BITS) - 1u, CMk = (1u << CB) - 1u;
+      float y[32];
+#pragma unroll
+      for (int pp = 0; pp < 16; pp++) {
+        const uint32_t code = pair_code<BITS>(kw, pp);
+        y[2 * pp] = s_cb[code & SM & CMk];
+        y[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
+      }
+      uint32_t hw[16], lw[16];
       if (kwave) {
-        xe(0)[slice] = e;
+#pragma unroll
+        for (int j = 0; j < 32; j++) y[j] = (y[j] * f) * decode_sign(j);
+        butterfly<32>(y);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const float x0 = y[2 * j] * kInvSqrt32, x1 = y[2 * j + 1] * kInvSqrt32;
+          hw[j] = pack_f16(x0, x1);
+          lw[j] = pack_rem(x0, x1, hw[j], mone);
+        }
+        uint4 *krow = reinterpret_cast<uint4 *>(ktile(0) + ftok * kKStride);
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) {
+          krow[kchunk(8 * fqb + 2 * gq, ftok)] = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
+          krow[kchunk(8 * fqb + 2 * gq + 1, ftok)] = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
+        }
       } else {
-        xe(0)[4 + 2 * slice] = e;
-        xe(0)[5 + 2 * slice] = e;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const float x0 = y[2 * j] * f, x1 = y[2 * j + 1] * f;
+          hw[j] = pack_f16(x0, x1);
+          lw[j] = pack_rem(x0, x1, hw[j], mone);
+        }
+        _Float16 *vrh = vhi(0) + ftok * kVRow, *vrl = vrh + V_HALVES;
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) {
+          const int c = 8 * vchunk(4 * fqb + gq);
+          *reinterpret_cast<uint4 *>(vrh + c) = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
+          *reinterpret_cast<uint4 *>(vrl + c) = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
+        }
       }
-    }
-    if constexpr (QJL) {
-      if (kwave) {
-        if (fqb == 0) cnp(0)[ftok] = f16_to_f32(nm) * a.qjl_c;
-        sgp(0)[ftok * 4 + fqb] = sgw;
+      __syncthreads();
+      u32x4 *dst = reinterpret_cast<u32x4 *>(a.stage_out + ((long long)g * a.stage_tiles + tile) * IMG);
+#pragma unroll
+      for (int r = 0; r < IMG_ROUNDS; r++) {
+        const int c = tid + 4 * kRows * r;
+        if (r + 1 < IMG_ROUNDS || c < IMG) dst[c] = *reinterpret_cast<const u32x4 *>(img_chunk(0, c));
       }
-    }
-    constexpr uint32_t SM = (1u << BITS) - 1u, CMk = (1u << CB) - 1u;
-    float y[32];
+      if (more) {
+        __syncthreads();  // the copy's reads of the buffer are done
 #pragma unroll
-    for (int pp = 0; pp < 16; pp++) {
-      const uint32_t code = pair_code<BITS>(kw, pp);
-      y[2 * pp] = s_cb[code & SM & CMk];
-      y[2 * pp + 1] = s_cb[(code >> BITS) & CMk];
-    }
-    uint32_t hw[16], lw[16];
-    if (kwave) {
-#pragma unroll
-      for (int j = 0; j < 32; j++) y[j] = (y[j] * f) * decode_sign(j);
-      butterfly<32>(y);
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const float x0 = y[2 * j] * kInvSqrt32, x1 = y[2 * j + 1] * kInvSqrt32;
-        hw[j] = pack_f16(x0, x1);
-        lw[j] = pack_rem(x0, x1, hw[j], mone);
+        for (int i = 0; i < QW; i++) kw[i] = nkw[i];
+        ks = nks;
+        sgw = nsg;
+        nm = nnm;
       }
-      uint4 *krow = reinterpret_cast<uint4 *>(ktile(0) + ftok * kKStride);
-#pragma unroll
-      for (int gq = 0; gq < 4; gq++) {
-        krow[kchunk(8 * fqb + 2 * gq, ftok)] = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
-        krow[kchunk(8 * fqb + 2 * gq + 1, ftok)] = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const float x0 = y[2 * j] * f, x1 = y[2 * j + 1] * f;
-        hw[j] = pack_f16(x0, x1);
-        lw[j] = pack_rem(x0, x1, hw[j], mone);
-      }
-      _Float16 *vrh = vhi(0) + ftok * kVRow, *vrl = vrh + V_HALVES;
-#pragma unroll
-      for (int gq = 0; gq < 4; gq++) {
-        const int c = 8 * vchunk(4 * fqb + gq);
-        *reinterpret_cast<uint4 *>(vrh + c) = make_uint4(hw[4 * gq], hw[4 * gq + 1], hw[4 * gq + 2], hw[4 * gq + 3]);
-        *reinterpret_cast<uint4 *>(vrl + c) = make_uint4(lw[4 * gq], lw[4 * gq + 1], lw[4 * gq + 2], lw[4 * gq + 3]);
-      }
-    }
-    __syncthreads();
-    u32x4 *dst = reinterpret_cast<u32x4 *>(a.stage_out + ((long long)g * a.stage_tiles + qblk) * IMG);
-#pragma unroll
-    for (int r = 0; r < IMG_ROUNDS; r++) {
-      const int c = tid + 4 * kRows * r;
-      if (r + 1 < IMG_ROUNDS || c < IMG) dst[c] = *reinterpret_cast<const u32x4 *>(img_chunk(0, c));
     }
     return;
   }
@@ -1066,8 +1090,13 @@ int launch_prefill_m(PrefillArgs &a, int nr, hipStream_t st) {
   if (staged) {
     a.stage = static_cast<const uint4 *>(buf);
     a.stage_out = static_cast<uint4 *>(buf);
-    hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3((unsigned)a.stage_tiles * grid.y), block,
-                       0, st, a);
+    // the staging pass in one round of workgroups (two per compute unit, its
+    // LDS), each taking consecutive tiles of one KV head
+    const int cus = cu_count(dev);
+    const long long units = (long long)a.stage_tiles * grid.y;
+    a.stage_tpw = cus > 0 ? (int)max(1ll, (units + 2ll * cus - 1) / (2ll * cus)) : 1;
+    const unsigned stage_wgs = (unsigned)((a.stage_tiles + a.stage_tpw - 1) / a.stage_tpw) * grid.y;
+    hipLaunchKernelGGL((prefill_attn_kernel<BITS, MODE, 1, kStage>), dim3(stage_wgs), block, 0, st, a);
     launch_attn<BITS, MODE, kStaged>(a, nr, grid, block, st);
   } else {
     launch_attn<BITS, MODE, kDecode>(a, nr, grid, block, st);
