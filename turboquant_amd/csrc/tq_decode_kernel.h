@@ -1087,10 +1087,14 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     if (lane == 0) cml[2 * HG] = exp2i(evrun);
   }
 
-  // ---- combine the waves' records; the workgroup's partial goes out ----
+  // ---- combine the waves' records; the workgroup's partial goes out (a
+  // (sequence, KV head) of one chunk or range: its output, inverse-rotated
+  // and normalized here, with no partial, counter or merge) ----
   if (tid == 0) s_flag = (INLINE_MERGE && (ws_hdr < a.ws_pairs || ws_hdr > a.ws_room)) ? 2 : 0;
   __syncthreads();
   const bool ws_ok = s_flag != 2;
+  const bool direct = INLINE_MERGE && nparts == 1;
+  const float osg = a_sg ? sgl : decode_sign(tid & 31);
   for (int e = tid; e < nh * HD; e += C::THREADS) {
     const int hl = e / HD, d = e - hl * HD;
     float mw[C::WAVES], M = -INFINITY;
@@ -1107,7 +1111,16 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
       A = __builtin_fmaf(cw[C::WC + hl * HD + d], f * cw[C::WM + 2 * HG], A);
       L = __builtin_fmaf(cw[C::WM + HG + hl], f, L);
     }
-    if (ws_ok) {
+    if (direct) {
+      if (ws_ok) {  // (uniform: whole 32-lane blocks of e take the butterfly)
+        const float v = wht32_lanes(A * osg, e & 31);
+        const float res = (L > 0.f) ? v * kInvSqrt32 / L : 0.f;
+        const long long oi = hq0 * HD + e;
+        if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = res;
+        else if (a.out_dtype == kBF16) static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(res);
+        else static_cast<uint16_t *>(a.out)[oi] = f32_to_f16(res);
+      }
+    } else if (ws_ok) {
       const long long bh = hq0 + hl;
       st_agent(&a.po[(bh * a.P + c) * HD + d], A);
       if (d == 0) {
@@ -1131,6 +1144,16 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   // returned and a barrier.  An acq_rel counter would add an L2 writeback and
   // invalidate per workgroup that this needs nowhere. ----
   if constexpr (!INLINE_MERGE) return;
+  if (direct) {
+    if (!ws_ok) {
+      for (int e = tid; e < nh * HD; e += C::THREADS) {
+        const long long oi = hq0 * HD + e;
+        if (a.out_dtype == kF32) static_cast<float *>(a.out)[oi] = __builtin_nanf("");
+        else static_cast<uint16_t *>(a.out)[oi] = 0x7e00;  // quiet NaN in f16 and bf16 alike
+      }
+    }
+    return;
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();
