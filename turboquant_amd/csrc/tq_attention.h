@@ -380,6 +380,11 @@ template <int BITS, int MODE, int NQB, int HG>
 using StreamCfg = DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), stream_waves_c<BITS, MODE, NQB, HG>()>;
 template <int BITS, int MODE, int NQB, int HG>
 using StreamCfg4 = DecCfg<BITS, MODE, NQB, HG, stream_tpw_c(NQB, HG, MODE == kModeTq), 4>;
+// 64 tokens per wave in 8-wave workgroups (512-token chunks): each wave's
+// key and value passes half as long, for grids that fit the compute units
+// in one round even so (a sequence's KV heads over shorter contexts)
+template <int BITS, int MODE, int NQB, int HG>
+using StreamCfg64 = DecCfg<BITS, MODE, NQB, HG, 64, 8>;
 // Compute units of the current device (cached per device).
 int device_cus();
 

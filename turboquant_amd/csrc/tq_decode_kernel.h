@@ -1276,9 +1276,17 @@ template <int BITS, int MODE, int NQB, int HG, bool INLINE>
 void launch_stream_cfg(AttnArgs &a, dim3 grid, hipStream_t st) {
   using C = StreamCfg<BITS, MODE, NQB, HG>;
   using C4 = StreamCfg4<BITS, MODE, NQB, HG>;
+  using C64 = StreamCfg64<BITS, MODE, NQB, HG>;
   if constexpr (INLINE && C::WAVES != 4) {
     const long long wgs = (long long)((a.max_len + C::CHUNK - 1) / C::CHUNK) * grid.y * grid.z;
     if (wgs > device_cus()) return launch_stream_c<C4, INLINE>(a, grid, st);
+    // a grid that leaves compute units idle: 64 tokens per wave when that
+    // grid still fits one round (C3's shape up to 16,384 tokens: 2,048 and
+    // 4,096 tokens 11.8 / 12.0 -> 9.5 us; 32,768 stays at 128)
+    if constexpr (C::TPW == 128 && C64::LDS_FITS) {
+      const long long wgs64 = (long long)((a.max_len + C64::CHUNK - 1) / C64::CHUNK) * grid.y * grid.z;
+      if (wgs64 <= device_cus()) return launch_stream_c<C64, INLINE>(a, grid, st);
+    }
   }
   launch_stream_c<C, INLINE>(a, grid, st);
 }
