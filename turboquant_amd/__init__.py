@@ -30,8 +30,7 @@ __all__ = [
 _DT = {torch.float32: TQ_DTYPE_F32, torch.bfloat16: TQ_DTYPE_BF16, torch.float16: TQ_DTYPE_F16}
 
 
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+from .cache import _stream  # noqa: E402  (the current HIP stream's handle)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
