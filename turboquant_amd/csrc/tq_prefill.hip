@@ -219,7 +219,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
   // work grows with the query block, so the linear index is mapped to the
   // longest blocks first (every KV head's last query block, then the blocks
   // before it): the short blocks fill in at the end instead of the long ones
-  // starting last.
+  // starting last.  Either way KV head = linear index mod KV heads, so (with
+  // 8 heads and workgroups dealt to the XCDs round-robin) a head's query
+  // blocks share the XCD, and L2, that its staged tiles are written from and
+  // read through (full attention, 1024 x 8192: 218.5 -> 210.5 us).
   int g = blockIdx.y, qblk = blockIdx.x;
   if (PH == kStage) {
     // staging pass, a 1-D grid: KV head g = linear index mod num_kv_heads,
@@ -229,10 +232,10 @@ __global__ __launch_bounds__(4 * prefill_rows(MODE)) void prefill_attn_kernel(Pr
     g = (int)blockIdx.x % a.num_kv_heads;
     qblk = (int)blockIdx.x / a.num_kv_heads;
   }
-  if (PH != kStage && a.causal) {
+  if (PH != kStage) {
     const int lin = blockIdx.y * gridDim.x + blockIdx.x;
     g = lin % gridDim.y;
-    qblk = (int)gridDim.x - 1 - lin / (int)gridDim.y;
+    qblk = a.causal ? (int)gridDim.x - 1 - lin / (int)gridDim.y : lin / (int)gridDim.y;
   }
   const int i0 = qblk * QB;
   const long long rec0 = (long long)g * a.kv_head_stride;
