@@ -234,10 +234,12 @@ int tq_pqo_decode_attention_noalloc(const void *q, int q_dtype, const uint8_t *k
 /* tq_cache_decode_attention for TQ records (outlier_blocks 0) with the query
  * projection rq = R q computed inside the decode launch from the sign
  * matrix (tq_qjl_sign_matrix: row j = head_dim / 32 words, bit c set = -1)
- * instead of a separate tq_qjl_project launch.  rq is summed in column order
- * exactly as tq_qjl_project sums it (precompute_query_projections,
- * qjl.rs:196-208), so the outputs are bit-identical to
- * tq_qjl_project + tq_cache_decode_attention.  No reference counterpart as
+ * instead of a separate tq_qjl_project launch.  rq is formed on the matrix
+ * cores from exact products (+-1 times the query cut into bf16 parts that
+ * sum to it); only the f32 accumulation order differs from tq_qjl_project's
+ * serial column-order sum (precompute_query_projections, qjl.rs:196-208),
+ * so the outputs agree with tq_qjl_project + tq_cache_decode_attention to
+ * rounding (within 1e-5 in the tests).  No reference counterpart as
  * one call: replaces the projection and TqCache::decode's attention
  * (tq.rs:185-297). */
 int tq_tq_decode_attention(const void *q, int q_dtype, const uint8_t *k_indices,

@@ -389,12 +389,16 @@ def _f16_bits(x):
     return np.asarray(x, np.float16).view(np.int16)
 
 
+@pytest.mark.parametrize("qdt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("d,nr,bsz", [(64, 2, 1), (128, 8, 1), (256, 4, 1), (128, 2, 24), (256, 2, 40)])
-def test_in_launch_query_projection_bit_identical(tq, d, nr, bsz):
-    """tq_tq_decode_attention (rq = R q computed inside the decode launch from
-    the sign matrix) against tq_qjl_project + tq_cache_decode_attention: the
-    projection is summed in the same column order, so the outputs agree bit
-    for bit (single sequences and ragged batches on the balanced split)."""
+def test_in_launch_query_projection(tq, d, nr, bsz, qdt):
+    """tq_tq_decode_attention (rq = R q computed inside the decode launch, on
+    the matrix cores: +-1 entries times the query cut into exact bf16 parts,
+    one part for bf16 queries, two for f16, three for f32) against
+    tq_qjl_project (a serial f32 sum per element) + tq_cache_decode_attention:
+    every product is exact and only the accumulation order differs, so the
+    outputs agree to rounding, 1e-5 here (single sequences and ragged
+    batches on the balanced split)."""
     hkv, cap, bits = 4 if bsz == 1 else 8, 1800, 3
     h = hkv * nr
     rng = np.random.default_rng(d * 7 + nr + bsz)
@@ -412,7 +416,12 @@ def test_in_launch_query_projection_bit_identical(tq, d, nr, bsz):
     nm = _f16_bits(np.abs(rng.standard_normal((bsz, hkv, cap))) * 0.3)
     lens = rng.integers(0, cap + 1, size=bsz).astype(np.int32) if bsz > 1 else np.array([cap - 5], np.int32)
     q = rng.standard_normal((bsz, h, d)).astype(np.float32) / np.float32(math.sqrt(d))
-    qd = _dev(bf16_bits(bf16_round(q))).view(torch.bfloat16)
+    if qdt == "bf16":
+        qd = _dev(bf16_bits(bf16_round(q))).view(torch.bfloat16)
+    elif qdt == "f16":
+        qd = _dev(q.astype(np.float16))
+    else:
+        qd = _dev(q)
     rmat = tq.qjl_sign_matrix(d, 12345)
     rq = tq.qjl_project(qd.reshape(-1, d), rmat).reshape(bsz, h, d)
     ws = tq.AttentionWorkspace(bsz, h, hkv, d, cap)
@@ -422,5 +431,5 @@ def test_in_launch_query_projection_bit_identical(tq, d, nr, bsz):
     b = tq.cache_decode_attention(*args, qjl_signs=_dev(sg), qjl_norms=_dev(nm), qjl_sign_matrix=rmat)
     torch.cuda.synchronize()
     a, b = a.cpu().numpy(), b.cpu().numpy()
-    assert np.isfinite(a).all()
-    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.isfinite(a).all() and np.isfinite(b).all()
+    assert np.abs(a - b).max() <= 1e-5, np.abs(a - b).max()

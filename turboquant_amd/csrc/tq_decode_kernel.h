@@ -155,7 +155,9 @@ __device__ __forceinline__ float sum_xor16(float v) {
 }
 
 // MULTI: the launch gives workgroups ranges of several chunks (cpr > 1)
-template <class C, bool INLINE_MERGE, bool GRID, bool MULTI>
+// PROJ (TQ only): no rq from the caller, R q is formed in the launch; an
+// instance of its own, so that the launches given rq carry none of its code
+template <class C, bool INLINE_MERGE, bool GRID, bool MULTI, bool PROJ = false>
 #ifndef TQ_DECODE_WPE
 #define TQ_DECODE_WPE 2
 #endif
@@ -291,8 +293,10 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
   constexpr int QIT = (QE + C::THREADS - 1) / C::THREADS;
   uint32_t qbits[QIT];
   float rqv[QIT];
-  // TQ without rq: the sign words of R's row for each of the lane's elements
-  uint32_t rsw[C::QJL ? QIT : 1][C::QJL ? NQB : 1];
+  // TQ without rq: the sign words of the rows of R whose products this lane
+  // computes (row tile wave + WAVES t: row 16 (wave + WAVES t) + l16)
+  constexpr int RT = C::QJL ? (HD / 16 + C::WAVES - 1) / C::WAVES : 1;
+  uint32_t rsw[RT][C::QJL ? NQB : 1];
 #pragma unroll
   for (int k = 0; k < QIT; k++) {
     const int e = tid + C::THREADS * k, hl = e / HD;
@@ -306,11 +310,15 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
         if (a_rq) rqv[k] = a_rq[qi];
       }
     }
-    if constexpr (C::QJL) {
-      if (!a_rq) {
-        const uint32_t *row = a.rmat + (e % HD) * NQB;
+  }
+  if constexpr (C::QJL) {
+    if constexpr (PROJ) {
 #pragma unroll
-        for (int w = 0; w < NQB; w++) rsw[k][w] = e < QE ? row[w] : 0u;
+      for (int t = 0; t < RT; t++) {
+        const int rt = wave + C::WAVES * t;
+        const uint32_t *row = a.rmat + (16 * min(rt, HD / 16 - 1) + l16) * NQB;
+#pragma unroll
+        for (int w = 0; w < NQB; w++) rsw[t][w] = row[w];
       }
     }
   }
@@ -507,37 +515,73 @@ __global__ __launch_bounds__(C::THREADS, TQ_DECODE_WPE) void stream_decode_kerne
     }
   }
   if constexpr (C::QJL) {
-    if (!a_rq) {
+    if constexpr (PROJ) {
       // rq = R q (precompute_query_projections, qjl.rs:196-208) in the
-      // launch: the raw query staged in s_rq (free until the scaled rq is
-      // written below), each element's row summed in column order from -0.0
-      // with exact +-1 products, as tq_qjl_project sums it (bit-identical)
+      // launch, on the matrix cores: R's entries are +-1 (exact in bf16)
+      // and the raw query is cut into bf16 parts that sum to it exactly
+      // (one part for a bf16 query, two for f16, three for f32), so every
+      // product is exact and only the f32 accumulation order differs from
+      // the serial sum of tq_qjl_project (a few ulp).  Wave w takes the row
+      // tiles w, w + WAVES, ..: A, lane (l16, lg), holds R[row][32 s + 8 lg
+      // ..+7] expanded from one byte of sign bits through the nibble table
+      // (f16 +-1 with bit 1 -> +1: its exponent bits flipped to bf16, and
+      // the result negated, since R has bit 1 -> -1); B column h is head
+      // h's query.  The rows land in s_q, which the rotated query below
+      // overwrites element by element in the same lanes.
 #pragma unroll
       for (int k = 0; k < QIT; k++) {
         const int e = tid + C::THREADS * k;
         if (e < QE) s_rq[e] = q_value(qbits[k], a_qdt);
       }
       __syncthreads();
+      const int parts = a_qdt == kBF16 ? 1 : (a_qdt == kF16 ? 2 : 3);
+#pragma unroll
+      for (int t = 0; t < RT; t++) {
+        const int rt = wave + C::WAVES * t;
+        if (rt < HD / 16) {  // uniform per wave
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int sk = 0; sk < HD / 32; sk++) {
+            const uint32_t byte = (rsw[t][sk] >> (8 * lg)) & 0xffu;
+            const uint2 n0 = s_nib[byte & 15u], n1 = s_nib[byte >> 4];
+            const u32x4 am = {n0.x ^ 0x03800380u, n0.y ^ 0x03800380u, n1.x ^ 0x03800380u, n1.y ^ 0x03800380u};
+            float qv[8];
+            if (l16 < HG) {
+              const float4 *src = reinterpret_cast<const float4 *>(s_rq + l16 * HD + 32 * sk + 8 * lg);
+              const float4 v0 = src[0], v1 = src[1];
+              qv[0] = v0.x; qv[1] = v0.y; qv[2] = v0.z; qv[3] = v0.w;
+              qv[4] = v1.x; qv[5] = v1.y; qv[6] = v1.z; qv[7] = v1.w;
+            } else {
+#pragma unroll
+              for (int j = 0; j < 8; j++) qv[j] = 0.f;
+            }
+            for (int p = 0; p < parts; p++) {
+              uint32_t cut[8];
+#pragma unroll
+              for (int j = 0; j < 8; j++) {
+                cut[j] = f2u(qv[j]) & 0xffff0000u;  // the leading 8 significand bits
+                qv[j] -= u2f(cut[j]);                // exact: the rest
+              }
+              const u32x4 bm = {__builtin_amdgcn_perm(cut[1], cut[0], 0x07060302u),
+                                __builtin_amdgcn_perm(cut[3], cut[2], 0x07060302u),
+                                __builtin_amdgcn_perm(cut[5], cut[4], 0x07060302u),
+                                __builtin_amdgcn_perm(cut[7], cut[6], 0x07060302u)};
+              acc = mfma_bf16(am, bm, acc);
+            }
+          }
+          if (l16 < HG) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_q[l16 * HD + 16 * rt + 4 * lg + i] = -acc[i] * a.qjl_inv;
+          }
+        }
+      }
+      __syncthreads();
 #pragma unroll
       for (int k = 0; k < QIT; k++) {
         const int e = tid + C::THREADS * k;
-        if (e < QE) {
-          const float4 *row = reinterpret_cast<const float4 *>(s_rq + (e / HD) * HD);
-          float acc = -0.0f;
-#pragma unroll
-          for (int c4 = 0; c4 < HD / 4; c4++) {
-            const float4 v = row[c4];
-            const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const int col = 4 * c4 + i;
-              acc = __builtin_fmaf(((rsw[k][col >> 5] >> (col & 31)) & 1u) ? -1.0f : 1.0f, vv[i], acc);
-            }
-          }
-          rqv[k] = acc * a.qjl_inv;
-        }
+        if (e < QE) rqv[k] = s_q[e];
       }
-      __syncthreads();  // s_rq is rewritten below
+      __syncthreads();  // s_rq and s_q are rewritten below
     }
   }
   // ---- rotated, scaled query: 32-lane butterflies (elements of a qblock sit
@@ -1210,6 +1254,9 @@ void launch_stream_k(AttnArgs &a, dim3 grid, hipStream_t st, int len_hint) {
   };
   if constexpr (C::BITS == 4 && C::MODE == kModePqo) {
     if (!a.cb_dev && !a.cb_args) return go(stream_decode_kernel<C, INLINE, true, MULTI>);
+  }
+  if constexpr (C::QJL) {
+    if (!a.rq) return go(stream_decode_kernel<C, INLINE, false, MULTI, true>);
   }
   go(stream_decode_kernel<C, INLINE, false, MULTI>);
 }

@@ -202,6 +202,13 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 d) {
                                                 0);
 }
 
+// The same over bf16 operands (two per word, lower k in the low half).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 d) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), d, 0,
+                                                 0, 0);
+}
+
 // Transposing LDS read (ds_read_b64_tr_b16): inside each group of 16 lanes,
 // lane 4 a + b receives item b (16-bit) of the 8-byte rows addressed by
 // lanes a, a + 4, a + 8 and a + 12 of its group, in that order (item 0 in
