@@ -50,6 +50,7 @@ def _decode_cases(n, seed):
 
 @pytest.mark.parametrize("case", _decode_cases(24, 4242), ids=lambda c: f"dec{c[0]}")
 def test_random_decode(tq, case):
+    """QJL cases alternate between rq given and R q formed in the launch."""
     _, qjl, d, bits, bsz, hkv, nr, cap, lens = case
     rng = np.random.default_rng(9000 + case[0])
     h = hkv * nr
@@ -90,8 +91,12 @@ def test_random_decode(tq, case):
     qd = _dev(bf16_bits(q)).view(torch.bfloat16)
     kw = {}
     if qjl:
-        rq = np.stack([[orc.query_projections(q[b, i], 12345) for i in range(h)] for b in range(bsz)])
-        kw = dict(rq=_dev(rq.astype(np.float32)), qjl_signs=_dev(sgb), qjl_norms=_dev(nmb))
+        kw = dict(qjl_signs=_dev(sgb), qjl_norms=_dev(nmb))
+        if case[0] % 2:  # R q formed inside the launch from the sign matrix
+            kw["qjl_sign_matrix"] = tq.qjl_sign_matrix(d, 12345)
+        else:
+            rq = np.stack([[orc.query_projections(q[b, i], 12345) for i in range(h)] for b in range(bsz)])
+            kw["rq"] = _dev(rq.astype(np.float32))
     out = tq.cache_decode_attention(qd, _dev(kp), _dev(ks), _dev(vp), _dev(vs), _dev(np.asarray(lens, np.int32)),
                                     hkv, bits, cap, cap, hkv * cap, 1 / math.sqrt(d), ws, ob, **kw)
     torch.cuda.synchronize()
