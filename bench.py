@@ -355,6 +355,19 @@ def bench_c2_codec(torch, tq, args, x, bits: int):
     dms, dspread = time_median(torch, deq_step)
     code_b = pd + 8
     qb = n * (256 + code_b)
+    copy_ceiling = None
+    if bits == 3:
+        # the rate this GPU sustains for mixed read and write traffic of the
+        # same total bytes: a plain device copy (torch copy_, the runtime's
+        # copy kernel) of half of them, over two buffer pairs in turn
+        m = qb // 8  # float32 elements per buffer: qb / 2 bytes
+        bufs = [(torch.empty(m, dtype=torch.float32, device="cuda"), torch.empty(m, dtype=torch.float32, device="cuda"))
+                for _ in range(2)]
+        cms, _ = time_median(torch, lambda i: bufs[i % 2][1].copy_(bufs[i % 2][0]))
+        del bufs
+        copy_ceiling = {"bytes_read_plus_written": 8 * m, "us": round(cms * 1e3, 3),
+                        "gbs": round(8 * m / (cms * 1e-3) / 1e9, 1), "quantize_frac_of_copy": round(cms / qms, 4),
+                        "kernel": "torch copy_ of qb/2 bytes (the runtime's device copy)"}
     db = n * (code_b + 256)
     q_gbs = qb / (qms * 1e-3) / 1e9
     d_gbs = db / (dms * 1e-3) / 1e9
@@ -368,7 +381,8 @@ def bench_c2_codec(torch, tq, args, x, bits: int):
                      "gbs_out": round(n * code_b / (qms * 1e-3) / 1e9, 2), "algorithmic_bytes_per_step": qb,
                      "roofline": {"bound": "hbm", "achieved": round(q_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(q_gbs / HBM_PEAK_GBS, 4),
-                                  "traffic": traffic("pqo_quant_kernel" if bits == 3 else f"pqo_quant_kernel_pqo{bits}")}},
+                                  "traffic": traffic("pqo_quant_kernel" if bits == 3 else f"pqo_quant_kernel_pqo{bits}")},
+                     "copy_ceiling": copy_ceiling},
         "dequantize": {"metric": f"PQO{bits} dequantize (C2, bf16 out)",
                        "mvec_s": round(n / (dms * 1e-3) / 1e6, 2), "ms_per_step": round(dms, 6),
                        "trials_ms": [round(x, 6) for x in dspread],
