@@ -428,6 +428,11 @@ def bench_c4(torch, tq, args):
     ms, spread = time_median(torch, step, warmup=200)
     ms_graph, _ = time_median(torch, step, 0, graph=True)
     del caches, kv
+    ceiling = None
+    if os.path.exists(os.path.join(ROOT, "libtq_read_probe.so")):
+        # a plain read of the same bytes: the rate any kernel that reads C4's records once can reach
+        ceiling = read_ceiling(torch, step_bytes, args.steps, args.warmup)
+        ceiling["decode_frac_of_read"] = round(ceiling["us"] * 1e-3 / ms, 4)
     return {"metric": "PQO4 batched decode (C4) tokens/s per layer and GB/s",
             "tokens_per_s_per_layer": round(b / (ms * 1e-3), 1), "ms_per_step": round(ms, 6),
             "trials_ms": [round(x, 6) for x in spread], "timing": f"median of {TRIALS} trials x {LAUNCHES} launches",
@@ -436,7 +441,7 @@ def bench_c4(torch, tq, args):
             "roofline": {"bound": "hbm", "achieved": round(step_bytes / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "traffic": traffic("stream_decode_kernel_c4")},
-            "contexts": lens_np.tolist(), "copies": copies}
+            "read_ceiling": ceiling, "contexts": lens_np.tolist(), "copies": copies}
 
 
 def bench_tq_c3(torch, tq, args):
